@@ -1,0 +1,212 @@
+#!/usr/bin/env python3
+"""HFFN layer throughput on one MI355X: tokens/s of the isolated layer and the roofline fraction of its dominant kernel.
+
+Workload (default): the Pythia-410M-shape HFFN layer, d_model 1024, d_ff 4096, 50 % density (512-slot up and down
+supports per neuron, uniform without replacement, sorted), fp32 values ~N(0, 0.02), biases ~N(0, 0.01), x = 2048 tokens
+~N(0, 1), exact-erf GELU. A step is one forward of the whole layer on the 2048 resident tokens. The timed loop rotates
+over enough distinct copies of the layer (different seeds) that their stores exceed the 256 MB Infinity Cache, so
+every step reads its model from HBM.
+
+    python bench.py [--steps K] [--warmup W] [--workload NAME] [--tokens N]
+
+Prints one JSON line. `roofline` is measured live: HIP events around each kernel of the step (on the stream the
+kernels are launched on) give each kernel's average duration; the dominant one is priced against its algorithmic
+bytes or flops. `cpu_baseline` times the reference x86 AVX2 kernel (built from the reference source into
+oracle/_ref) on this host's cores on a bounded sample of the same workload, after checking it against the float64
+oracle on a token sample.
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import math
+import os
+import sys
+import time
+from pathlib import Path
+
+ROOT = Path(__file__).resolve().parent
+sys.path.insert(0, str(ROOT))
+
+import numpy as np  # noqa: E402
+import torch  # noqa: E402
+
+METRIC = "HFFN layer tokens/s + % HBM roofline, Pythia-410M shape @50% density"
+HBM_PEAK = 8.0e12          # bytes/s, MI355X HBM3E
+FP32_PEAK = 157.3e12       # FLOP/s, MI355X fp32 (vector and matrix)
+RIDGE = FP32_PEAK / HBM_PEAK
+MALL_BYTES = 300e6         # rotate over more than the 256 MB Infinity Cache
+
+
+def parse() -> argparse.Namespace:
+    parser = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
+    parser.add_argument("--gpus", type=int, default=1)
+    parser.add_argument("--steps", type=int, default=200)
+    parser.add_argument("--warmup", type=int, default=20)
+    parser.add_argument("--workload", default="pythia410m_d50")
+    parser.add_argument("--tokens", type=int, default=None, help="N (default: the workload's first token count)")
+    parser.add_argument("--copies", type=int, default=None, help="distinct layer copies in the rotation")
+    parser.add_argument("--cpu-seconds", type=float, default=10.0, help="bound of the CPU-baseline sample")
+    parser.add_argument("--cpu-threads", type=int, default=8)
+    parser.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
+    return parser.parse_args()
+
+
+def layer_costs(compact, n: int) -> dict:
+    """Algorithmic bytes and flops of each kernel of one step (model arrays read once, activations once)."""
+    d, h = compact.d_model, compact.d_ff
+    value = 2 if compact.value_dtype == "bf16" else 4
+    nnz_up, nnz_down = int(compact.up_idx.size), int(compact.down_idx.size)
+    up_store = 4 * (h + 1) + (2 + value) * nnz_up + 4 * h
+    down_store = 4 * (d + 1) + (2 + value) * nnz_down + 4 * d
+    return {
+        "transpose_in": {"bytes": 8 * n * d, "flops": 0},
+        "up": {"bytes": up_store + 4 * n * d + 4 * n * h, "flops": 2 * nnz_up * n},
+        "down": {"bytes": down_store + 4 * n * h + 4 * n * d, "flops": 2 * nnz_down * n},
+        "transpose_out": {"bytes": 8 * n * d, "flops": 0},
+        "model_bytes": up_store + down_store,
+        "step_bytes": up_store + down_store + 8 * n * d,
+        "step_flops": 2 * (nnz_up + nnz_down) * n,
+    }
+
+
+def time_kernels(runtime, x: torch.Tensor, steps: int, copies: int) -> dict:
+    """Average duration (s) of each kernel of the step, from HIP events recorded between the launches on the
+    current stream (the stream the C ABI launches on)."""
+    from hffn_amd import _lib
+    from hffn_amd.runtime import leading_dim
+
+    lib = _lib.load()
+    n = x.shape[0]
+    ld = leading_dim(n)
+    up, down = runtime.modes(n)
+    x_t, act, y_t, y = runtime._work
+    stream = torch.cuda.current_stream().cuda_stream
+    names = (["transpose_in"] if up == "rows" else []) + ["up", "down"] + (["transpose_out"] if down == "rows" else [])
+    totals = {name: 0.0 for name in names}
+    for step in range(steps):
+        value_type, up_off, up_idx, up_val, b_up, out_off, out_hid, out_val, b_down = runtime._args[step % copies]
+        events = [torch.cuda.Event(enable_timing=True) for _ in range(len(names) + 1)]
+        events[0].record()
+        k = 1
+        if up == "rows":
+            _lib.check(lib.hffn_transpose(x.data_ptr(), x_t, n, runtime.d_model, runtime.d_model, ld, stream), "transpose")
+            events[k].record(); k += 1
+            _lib.check(lib.hffn_up(_lib.UP_MODES[up], value_type, x_t, up_off, up_idx, up_val, b_up, act, runtime.d_model,
+                                   runtime.d_ff, n, ld, stream), "up")
+        else:
+            _lib.check(lib.hffn_up(_lib.UP_MODES[up], value_type, x.data_ptr(), up_off, up_idx, up_val, b_up, act,
+                                   runtime.d_model, runtime.d_ff, n, ld, stream), "up")
+        events[k].record(); k += 1
+        target = y_t if down == "rows" else y
+        _lib.check(lib.hffn_down(_lib.DOWN_MODES[down], value_type, act, out_off, out_hid, out_val, b_down, target,
+                                 runtime.d_model, runtime.d_ff, n, ld, stream), "down")
+        events[k].record(); k += 1
+        if down == "rows":
+            _lib.check(lib.hffn_transpose(y_t, y, runtime.d_model, n, ld, runtime.d_model, stream), "transpose")
+            events[k].record(); k += 1
+        torch.cuda.synchronize()
+        for i, name in enumerate(names):
+            totals[name] += events[i].elapsed_time(events[i + 1]) * 1e-3
+    return {name: total / steps for name, total in totals.items()}
+
+
+def cpu_baseline(compact, x_np: np.ndarray, seconds: float, threads: int) -> dict | None:
+    """The reference x86 kernel on this host: checked against the float64 oracle on 96 tokens, then timed on whole
+    calls of the workload until `seconds` of work are done (at least 2 calls)."""
+    from oracle import reference, x86_ref
+
+    if not x86_ref.available():
+        return None
+    threads = max(1, min(threads, len(os.sched_getaffinity(0))))
+    kernel = x86_ref.ReferenceKernel(compact, threads=threads)
+    sample = x_np[:96]
+    error = float(np.max(np.abs(kernel.forward(sample) - reference.forward(compact, sample))))
+    if error > 2e-5:
+        raise RuntimeError(f"reference x86 kernel differs from the oracle by {error:.3e}")
+    kernel.forward(x_np)  # warm-up (thread pool, buffers)
+    calls, wall, inside = 0, 0.0, 0
+    while calls < 2 or wall < seconds:
+        start = time.perf_counter()
+        kernel.forward(x_np)
+        wall += time.perf_counter() - start
+        inside += int(kernel.timing.sum())
+        calls += 1
+    n = x_np.shape[0]
+    return {"value": round(n * calls / wall, 1), "unit": "tokens/s", "cores": threads, "kind": "reference",
+            "sample": f"{calls} whole calls of the same layer and {n}-token input ({wall:.1f} s wall, in-kernel "
+                      f"{inside / calls / 1e6:.2f} ms/call); route dual in 96-token chunks, {threads} threads; "
+                      f"checked against the float64 oracle on 96 tokens (max |dy| {error:.1e})"}
+
+
+def main() -> int:
+    args = parse()
+    if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
+        print("bench.py measures one GPU: the HFFN layer runs on a single MI355X here (multi-GPU sharding is design "
+              "only); run it with --gpus 1", file=sys.stderr)
+        return 2
+    from hffn_amd import synth
+    from hffn_amd.ffn import hip_layer
+    from hffn_amd.runtime import HFFNRuntime
+
+    device = torch.device("cuda", 0)
+    workload = synth.WORKLOADS[args.workload]
+    n = args.tokens or workload.tokens[0]
+    base = synth.make_workload_layer(workload)
+    costs = layer_costs(base, n)
+    copies = args.copies or max(1, math.ceil(MALL_BYTES / costs["model_bytes"]))
+    compacts = [base] + [synth.make_workload_layer(workload, seed=workload.seed * 1000 + c) for c in range(1, copies)]
+    runtime = HFFNRuntime([hip_layer(c, device) for c in compacts], device)
+    x_np = synth.make_input(workload, n)
+    x = torch.from_numpy(x_np).to(device)
+
+    for step in range(args.warmup):
+        runtime.forward(step % copies, x)
+    torch.cuda.synchronize()
+    start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    wall = time.perf_counter()
+    start.record()
+    for step in range(args.steps):
+        runtime.forward(step % copies, x)
+    end.record()
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - wall
+    seconds = start.elapsed_time(end) * 1e-3
+    up, down = runtime.modes(n)
+
+    kernels = time_kernels(runtime, x, max(20, min(args.steps, 200)), copies)
+    dominant = max((k for k in kernels if k in ("up", "down")), key=kernels.get)
+    cost = costs[dominant]
+    compute_bound = cost["flops"] / cost["bytes"] > RIDGE
+    if compute_bound:
+        roofline = {"bound": "mfma", "achieved": round(cost["flops"] / kernels[dominant] / 1e12, 3), "peak": FP32_PEAK / 1e12,
+                    "unit": "TFLOP/s"}
+    else:
+        roofline = {"bound": "hbm", "achieved": round(cost["bytes"] / kernels[dominant] / 1e9, 1), "peak": HBM_PEAK / 1e9,
+                    "unit": "GB/s"}
+    roofline["frac"] = round(roofline["achieved"] / roofline["peak"], 4)
+    roofline["traffic"] = None
+    roofline["kernel"] = f"{dominant} ({up if dominant == 'up' else down})"
+    roofline["kernel_us"] = round(kernels[dominant] * 1e6, 2)
+
+    baseline = None if args.no_cpu else cpu_baseline(base, x_np, args.cpu_seconds, args.cpu_threads)
+    line = {
+        "metric": METRIC, "value": round(n * args.steps / seconds, 1), "unit": "tokens/s", "n_gpus": 1,
+        "steps": args.steps, "warmup": args.warmup, "ms_per_step": round(seconds / args.steps * 1e3, 4),
+        "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
+        "dtype": "f32" if base.value_dtype == "float32" else "bf16-weights/f32-accumulate", "data": "synthetic",
+        "config": {"workload": f"{workload.name}: isolated HFFN layer d_model={base.d_model} d_ff={base.d_ff}, "
+                               f"{workload.degree}-slot supports, {n} tokens", "tokens": n, "copies": copies,
+                   "modes": [up, down], "kernel_us": {k: round(v * 1e6, 2) for k, v in kernels.items()},
+                   "step_hbm_fraction": round(costs["step_bytes"] / (seconds / args.steps) / HBM_PEAK, 4),
+                   "step_fp32_fraction": round(costs["step_flops"] / (seconds / args.steps) / FP32_PEAK, 4),
+                   "wall_s": round(wall, 3)},
+        "roofline": roofline,
+        "cpu_baseline": baseline,
+    }
+    print(json.dumps(line), flush=True)
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())

@@ -1,0 +1,71 @@
+"""ctypes binding of ``libhffn_amd.so``, the HIP library built from ``hffn_amd/csrc`` (C ABI: ``include/hffn_amd.h``).
+
+The library is built in-tree by ``hffn_amd.build`` (``python -c "import __graft_entry__ as g; g.build()"``). Loading
+never builds and never falls back to anything: a missing library is an error, so no forward call can run on
+anything but the HIP kernels.
+"""
+from __future__ import annotations
+
+import ctypes
+from pathlib import Path
+
+LIBRARY = Path(__file__).resolve().with_name("libhffn_amd.so")
+ABI_VERSION = 1
+
+OK = 0
+VALUE_F32, VALUE_BF16 = 0, 1
+UP_MODES = {"edges": 1, "rows": 2}
+DOWN_MODES = {"edges": 1, "rows": 2}
+
+_P, _I, _U32, _U64 = ctypes.c_void_p, ctypes.c_int, ctypes.c_uint32, ctypes.c_uint64
+
+# name -> argument types (return type int for every entry but hffn_last_error)
+SIGNATURES = {
+    "hffn_abi_version": [],
+    "hffn_last_error": [],
+    "hffn_edges_supported": [_U32, _U32],
+    "hffn_transpose": [_P, _P, _U32, _U32, _U32, _U32, _P],
+    "hffn_up": [_I, _I, _P, _P, _P, _P, _P, _P, _U32, _U32, _U32, _U32, _P],
+    "hffn_down": [_I, _I, _P, _P, _P, _P, _P, _P, _U32, _U32, _U32, _U32, _P],
+    "hffn_forward": [_I, _I, _I] + [_P] * 13 + [_U32] * 4 + [_P],
+    "hffn_output_major_workspace": [_U32, _U32, ctypes.POINTER(_U64)],
+    "hffn_output_major": [_I, _P, _P, _P, _U32, _U32, _U32, _P, _P, _P, _P, _U64, _P],
+}
+
+
+class HIPError(RuntimeError):
+    """A failure reported by the HIP library (invalid arguments or a refused launch)."""
+
+
+_lib: ctypes.CDLL | None = None
+
+
+def load() -> ctypes.CDLL:
+    """The bound library (loaded once per process). Raises ``RuntimeError`` when it has not been built."""
+    global _lib
+    if _lib is not None:
+        return _lib
+    if not LIBRARY.exists():
+        raise RuntimeError(f"{LIBRARY} is not built: run hffn_amd.build.build() (or __graft_entry__.build()) first; "
+                           "the HFFN forward has no other implementation")
+    lib = ctypes.CDLL(str(LIBRARY))
+    for name, argtypes in SIGNATURES.items():
+        function = getattr(lib, name)
+        function.argtypes = argtypes
+        function.restype = ctypes.c_char_p if name == "hffn_last_error" else ctypes.c_int
+    if lib.hffn_abi_version() != ABI_VERSION:
+        raise RuntimeError(f"{LIBRARY}: ABI version {lib.hffn_abi_version()}, expected {ABI_VERSION}; rebuild it")
+    _lib = lib
+    return lib
+
+
+def check(status: int, what: str) -> None:
+    if status != OK:
+        message = load().hffn_last_error().decode(errors="replace")
+        if status == -1:
+            raise ValueError(f"{what}: {message}")
+        raise HIPError(f"{what}: {message}")
+
+
+def exported_symbols() -> list[str]:
+    return list(SIGNATURES)

@@ -1,0 +1,153 @@
+// C ABI of the HFFN HIP library: plain pointers, sizes and a hipStream_t, a status code per call
+// and a per-thread message for the last failure. Declarations, and the reference interfaces each
+// entry point replaces, are in include/hffn_amd.h.
+#include <hip/hip_runtime.h>
+
+#include <cstdarg>
+#include <cstdio>
+#include <string>
+
+#include "../../include/hffn_amd.h"
+#include "launch.hpp"
+
+namespace {
+
+thread_local std::string g_error;
+
+int fail(int code, const char* format, ...) {
+    char buffer[512];
+    va_list args;
+    va_start(args, format);
+    std::vsnprintf(buffer, sizeof(buffer), format, args);
+    va_end(args);
+    g_error = buffer;
+    return code;
+}
+
+int launched(hipError_t status, const char* what) {
+    if (status != hipSuccess) return fail(HFFN_ERROR_LAUNCH, "%s: %s", what, hipGetErrorString(status));
+    return HFFN_OK;
+}
+
+bool valid_value_type(int vt) { return vt == HFFN_VALUE_F32 || vt == HFFN_VALUE_BF16; }
+
+// Shapes shared by every forward entry: d_model a multiple of 16 (as the reference runtime requires),
+// both widths addressable by the 16-bit indices, 1 <= n <= HFFN_MAX_TOKENS, ld a multiple of 4 covering n.
+int check_shape(uint32_t d, uint32_t h, uint32_t n, uint32_t ld) {
+    if (d == 0 || d % 16 != 0 || d > HFFN_MAX_WIDTH) return fail(HFFN_ERROR_ARGUMENT, "d_model=%u: must be a positive multiple of 16, at most %u", d, HFFN_MAX_WIDTH);
+    if (h == 0 || h > HFFN_MAX_WIDTH) return fail(HFFN_ERROR_ARGUMENT, "d_ff=%u: must be in [1, %u]", h, HFFN_MAX_WIDTH);
+    if (n == 0 || n > HFFN_MAX_TOKENS) return fail(HFFN_ERROR_ARGUMENT, "n=%u: unsupported token count", n);
+    if (ld < n || ld % 4 != 0) return fail(HFFN_ERROR_ARGUMENT, "ld=%u: must be a multiple of 4 and at least n=%u", ld, n);
+    return HFFN_OK;
+}
+
+// EDGES takes its tokens nt at a time: ld must be a multiple of nt, and the up input stage
+// nt * d_model floats must fit the LDS budget.
+int check_edges(uint32_t d, uint32_t n, uint32_t ld, bool stage) {
+    const uint32_t nt = hffn::edges_tokens(n);
+    if (ld % nt != 0) return fail(HFFN_ERROR_ARGUMENT, "edges mode: ld=%u must be a multiple of %u for n=%u", ld, nt, n);
+    if (stage && static_cast<size_t>(nt) * d * sizeof(float) > HFFN_EDGES_MAX_LDS)
+        return fail(HFFN_ERROR_ARGUMENT, "edges mode: %u tokens of d_model=%u exceed the %u-byte LDS stage", nt, d, HFFN_EDGES_MAX_LDS);
+    return HFFN_OK;
+}
+
+}  // namespace
+
+extern "C" {
+
+int hffn_abi_version(void) { return HFFN_ABI_VERSION; }
+
+const char* hffn_last_error(void) { return g_error.c_str(); }
+
+int hffn_edges_supported(uint32_t d_model, uint32_t n) {
+    if (n == 0) return 0;
+    return static_cast<size_t>(hffn::edges_tokens(n)) * d_model * sizeof(float) <= HFFN_EDGES_MAX_LDS ? 1 : 0;
+}
+
+int hffn_transpose(const float* in, float* out, uint32_t rows, uint32_t cols, uint32_t in_ld, uint32_t out_ld,
+                   void* stream) {
+    if (!in || !out) return fail(HFFN_ERROR_ARGUMENT, "transpose: null pointer");
+    if (rows == 0 || cols == 0) return HFFN_OK;
+    if (in_ld < cols || out_ld < rows) return fail(HFFN_ERROR_ARGUMENT, "transpose: strides %u/%u smaller than %ux%u", in_ld, out_ld, rows, cols);
+    return launched(hffn::launch_transpose(in, out, rows, cols, in_ld, out_ld, static_cast<hipStream_t>(stream)), "transpose");
+}
+
+int hffn_up(int mode, int value_type, const float* x, const int32_t* up_offsets, const int16_t* up_idx,
+            const void* up_val, const float* b_up, float* act, uint32_t d_model, uint32_t d_ff, uint32_t n, uint32_t ld,
+            void* stream) {
+    if (int status = check_shape(d_model, d_ff, n, ld)) return status;
+    if (!valid_value_type(value_type)) return fail(HFFN_ERROR_ARGUMENT, "unknown value type %d", value_type);
+    if (!x || !up_offsets || !up_idx || !up_val || !b_up || !act) return fail(HFFN_ERROR_ARGUMENT, "up: null pointer");
+    const hipStream_t s = static_cast<hipStream_t>(stream);
+    if (mode == HFFN_UP_EDGES) {
+        if (int status = check_edges(d_model, n, ld, true)) return status;
+        return launched(hffn::launch_up_edges(value_type, x, up_offsets, up_idx, up_val, b_up, act, d_model, d_ff, n, ld, s), "up edges");
+    }
+    if (mode == HFFN_UP_ROWS)
+        return launched(hffn::launch_up_rows(value_type, x, up_offsets, up_idx, up_val, b_up, act, d_model, d_ff, n, ld, s), "up rows");
+    return fail(HFFN_ERROR_ARGUMENT, "unknown up mode %d", mode);
+}
+
+int hffn_down(int mode, int value_type, const float* act, const int32_t* out_offsets, const int16_t* out_hidden,
+              const void* out_val, const float* b_down, float* y, uint32_t d_model, uint32_t d_ff, uint32_t n,
+              uint32_t ld, void* stream) {
+    if (int status = check_shape(d_model, d_ff, n, ld)) return status;
+    if (!valid_value_type(value_type)) return fail(HFFN_ERROR_ARGUMENT, "unknown value type %d", value_type);
+    if (!act || !out_offsets || !out_hidden || !out_val || !b_down || !y) return fail(HFFN_ERROR_ARGUMENT, "down: null pointer");
+    const hipStream_t s = static_cast<hipStream_t>(stream);
+    if (mode == HFFN_DOWN_EDGES) {
+        if (int status = check_edges(d_model, n, ld, false)) return status;
+        return launched(hffn::launch_down_edges(value_type, act, out_offsets, out_hidden, out_val, b_down, y, d_model, n, ld, s), "down edges");
+    }
+    if (mode == HFFN_DOWN_ROWS)
+        return launched(hffn::launch_down_rows(value_type, act, out_offsets, out_hidden, out_val, b_down, y, d_model, n, ld, s), "down rows");
+    return fail(HFFN_ERROR_ARGUMENT, "unknown down mode %d", mode);
+}
+
+int hffn_forward(int up_mode, int down_mode, int value_type, const float* x, const int32_t* up_offsets,
+                 const int16_t* up_idx, const void* up_val, const float* b_up, const int32_t* out_offsets,
+                 const int16_t* out_hidden, const void* out_val, const float* b_down, float* x_t, float* act,
+                 float* y_t, float* y, uint32_t d_model, uint32_t d_ff, uint32_t n, uint32_t ld, void* stream) {
+    if (int status = check_shape(d_model, d_ff, n, ld)) return status;
+    const hipStream_t s = static_cast<hipStream_t>(stream);
+    if (up_mode == HFFN_UP_ROWS) {
+        if (!x || !x_t) return fail(HFFN_ERROR_ARGUMENT, "forward: null input or x_t workspace");
+        if (int status = hffn_transpose(x, x_t, n, d_model, d_model, ld, stream)) return status;
+        if (int status = hffn_up(up_mode, value_type, x_t, up_offsets, up_idx, up_val, b_up, act, d_model, d_ff, n, ld, stream)) return status;
+    } else {
+        if (int status = hffn_up(up_mode, value_type, x, up_offsets, up_idx, up_val, b_up, act, d_model, d_ff, n, ld, stream)) return status;
+    }
+    if (down_mode == HFFN_DOWN_ROWS) {
+        if (!y_t) return fail(HFFN_ERROR_ARGUMENT, "forward: null y_t workspace");
+        if (int status = hffn_down(down_mode, value_type, act, out_offsets, out_hidden, out_val, b_down, y_t, d_model, d_ff, n, ld, stream)) return status;
+        return launched(hffn::launch_transpose(y_t, y, d_model, n, ld, d_model, s), "output transpose");
+    }
+    return hffn_down(down_mode, value_type, act, out_offsets, out_hidden, out_val, b_down, y, d_model, d_ff, n, ld, stream);
+}
+
+int hffn_output_major_workspace(uint32_t nnz, uint32_t d_model, uint64_t* bytes) {
+    if (!bytes) return fail(HFFN_ERROR_ARGUMENT, "output_major_workspace: null result");
+    *bytes = static_cast<uint64_t>(hffn::output_major_chunks(nnz)) * d_model * sizeof(int32_t);
+    return HFFN_OK;
+}
+
+int hffn_output_major(int value_type, const int32_t* down_offsets, const int16_t* down_idx, const void* down_val,
+                      uint32_t d_model, uint32_t d_ff, uint32_t nnz, int32_t* out_offsets, int16_t* out_hidden,
+                      void* out_val, void* workspace, uint64_t workspace_bytes, void* stream) {
+    if (!valid_value_type(value_type)) return fail(HFFN_ERROR_ARGUMENT, "unknown value type %d", value_type);
+    if (d_model == 0 || d_model > HFFN_MAX_OUTPUT_MAJOR_WIDTH)
+        return fail(HFFN_ERROR_ARGUMENT, "output_major: d_model=%u must be in [1, %u]", d_model, HFFN_MAX_OUTPUT_MAJOR_WIDTH);
+    if (d_ff == 0 || d_ff > HFFN_MAX_WIDTH) return fail(HFFN_ERROR_ARGUMENT, "output_major: d_ff=%u must be in [1, %u]", d_ff, HFFN_MAX_WIDTH);
+    if (!down_offsets || !out_offsets || !workspace || (nnz && (!down_idx || !down_val || !out_hidden || !out_val)))
+        return fail(HFFN_ERROR_ARGUMENT, "output_major: null pointer");
+    uint64_t needed = 0;
+    hffn_output_major_workspace(nnz, d_model, &needed);
+    if (workspace_bytes < needed)
+        return fail(HFFN_ERROR_ARGUMENT, "output_major: workspace of %llu bytes, %llu needed", static_cast<unsigned long long>(workspace_bytes),
+                    static_cast<unsigned long long>(needed));
+    return launched(hffn::launch_output_major(value_type, down_offsets, down_idx, down_val, d_model, d_ff, nnz, out_offsets,
+                                              out_hidden, out_val, static_cast<int32_t*>(workspace), static_cast<hipStream_t>(stream)),
+                    "output_major");
+}
+
+}  // extern "C"

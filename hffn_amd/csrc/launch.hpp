@@ -1,0 +1,47 @@
+// Host-side launchers of the HFFN kernels, shared by the translation units of the library.
+// Every launcher assumes arguments already validated by the C ABI (abi.hip) and returns the
+// hipError_t of its launch.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace hffn {
+
+enum ValueType : int { kF32 = 0, kBF16 = 1 };
+
+// Tokens per pass of the lane-per-slot ("edges") kernels: 1, 2, 4, or 8 for n > 4.
+constexpr uint32_t kEdgesMaxTokens = 8;
+inline uint32_t edges_tokens(uint32_t n) { return n <= 1 ? 1 : n <= 2 ? 2 : n <= 4 ? 4 : 8; }
+
+// x[rows, cols] (row stride in_ld) -> out[cols, rows] (row stride out_ld).
+hipError_t launch_transpose(const float* in, float* out, uint32_t rows, uint32_t cols, uint32_t in_ld,
+                            uint32_t out_ld, hipStream_t stream);
+
+// Up projection + bias + GELU. `edges`: one wave per neuron, lanes over its slots, x token-major
+// [n, d_model]; `rows`: one wave per neuron, lanes over tokens, x feature-major x_t[d_model, ld].
+// Activations hidden-major act[d_ff, ld].
+hipError_t launch_up_edges(int vt, const float* x, const int32_t* off, const int16_t* idx, const void* w,
+                           const float* b, float* act, uint32_t d, uint32_t h, uint32_t n, uint32_t ld,
+                           hipStream_t stream);
+hipError_t launch_up_rows(int vt, const float* x_t, const int32_t* off, const int16_t* idx, const void* w,
+                          const float* b, float* act, uint32_t d, uint32_t h, uint32_t n, uint32_t ld,
+                          hipStream_t stream);
+
+// Down projection over the output-major store. `edges`: one wave per output, lanes over its
+// slots, writes y[n, d_model]; `rows`: one wave per output, lanes over tokens, writes
+// y_t[d_model, ld] (the caller transposes).
+hipError_t launch_down_edges(int vt, const float* act, const int32_t* off, const int16_t* hid, const void* v,
+                             const float* bias, float* y, uint32_t d, uint32_t n, uint32_t ld,
+                             hipStream_t stream);
+hipError_t launch_down_rows(int vt, const float* act, const int32_t* off, const int16_t* hid, const void* v,
+                            const float* bias, float* y_t, uint32_t d, uint32_t n, uint32_t ld,
+                            hipStream_t stream);
+
+// Output-major transpose of the hidden-major down store (stable in slot order).
+uint32_t output_major_chunks(uint32_t nnz);
+hipError_t launch_output_major(int vt, const int32_t* down_offsets, const int16_t* down_idx, const void* down_val,
+                               uint32_t d, uint32_t h, uint32_t nnz, int32_t* out_offsets, int16_t* out_hidden,
+                               void* out_val, int32_t* counts, hipStream_t stream);
+
+}  // namespace hffn

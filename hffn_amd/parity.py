@@ -1,0 +1,44 @@
+"""Parity of the HIP runtime on one FFN against a float64 expectation, as ``hffn_cuda.parity``
+(``runtime/gpu/nvidia/common/kernels/hffn_cuda/parity.py:16-43``).
+
+For one input, the runtime runs with its policy and with each forced (up, down) kernel pair. Criteria: two
+consecutive calls on the same input give the same bits; ``max |y - y64|`` and ``max |y - y64| / max(1, |y64|)`` are
+reported for the caller to compare with its tolerance. Reported without threshold: whether the forced pairs that
+share the lane-per-token shapes (up rows x down rows) agree bitwise with the policy's result of the same shapes.
+"""
+from __future__ import annotations
+
+from dataclasses import dataclass
+
+import torch
+
+from .runtime import DOWN_MODES, UP_MODES, HFFNRuntime
+
+PAIRS = [(None, None)] + [(up, down) for up in UP_MODES for down in DOWN_MODES]
+
+
+@dataclass
+class Parity:
+    error: float           # max |y - y_float64| over the pairs
+    relative: float        # max |y - y_float64| / max(1, |y_float64|) over the pairs
+    repeatable: bool       # every pair gives the same bits on a second call
+    pairs: dict            # (up, down) -> max |y - y_float64| of that pair
+
+
+def check(runtime: HFFNRuntime, index: int, x: torch.Tensor, expected: torch.Tensor, pairs=PAIRS) -> Parity:
+    """``x`` float32 [N, d_model] on the runtime's device, ``expected`` its float64 oracle output (same device)."""
+    scale = expected.abs().clamp(min=1.0)
+    result = Parity(0.0, 0.0, True, {})
+    try:
+        for up, down in pairs:
+            runtime.force(up, down)
+            y = runtime.forward(index, x).clone()
+            result.repeatable &= bool(torch.equal(y, runtime.forward(index, x)))
+            distance = (y.double() - expected).abs()
+            error = float(distance.max())
+            result.pairs[up, down] = error
+            result.error = max(result.error, error)
+            result.relative = max(result.relative, float((distance / scale).max()))
+    finally:
+        runtime.force(None, None)
+    return result

@@ -1,0 +1,224 @@
+"""HFFN forward runtime on MI355X: a stack of FFNs of one shape (the FFNs of one model, or one isolated FFN).
+
+Drop-in for ``hffn_cuda.runtime`` (``runtime/gpu/nvidia/common/kernels/hffn_cuda/runtime.py``): same classes, fields,
+methods, counters and errors. One call runs the whole block of N tokens of one FFN through the HIP library
+(``libhffn_amd.so``, C ABI in ``include/hffn_amd.h``): an up kernel (one wave per hidden neuron, bias and exact GELU
+fused) then a down kernel (one wave per output feature, over the output-major store), with the layout transposes
+the chosen shapes need.
+
+Kernel shapes (the build's own policy, ``up_mode``/``down_mode``):
+
+* ``edges`` - lanes over a row's slots, tokens in registers, input staged in LDS; for decode-sized N (N <= 8).
+* ``rows``  - lanes over tokens (1, 2 or 4 per lane), slots walked in order; for N > 8.
+
+Model arrays stay on the device. Work buffers are dense, shared by all layers, sized for the largest N seen and
+reused. Kernels are queued on PyTorch's current stream of the device, so they run in call order with the PyTorch
+operations around them (the reference requires the default stream; any current stream is accepted here).
+"""
+from __future__ import annotations
+
+from collections import Counter
+from dataclasses import dataclass
+
+import torch
+
+from . import _lib
+
+UP_MODES = ("edges", "rows")
+DOWN_MODES = ("edges", "rows")
+EDGES_MAX_TOKENS = 8      # the policy's last N for the lane-per-slot shapes
+MAX_TOKENS = 1 << 18      # runtime/gpu/nvidia/common/kernels/hffn_cuda/runtime.py:26
+
+_VALUE_TYPES = {torch.float32: _lib.VALUE_F32, torch.bfloat16: _lib.VALUE_BF16}
+
+
+def up_mode(n: int, d_model: int | None = None) -> str:
+    """Up kernel shape for N tokens: ``edges`` up to ``EDGES_MAX_TOKENS`` (when its LDS stage fits), else ``rows``."""
+    if n <= EDGES_MAX_TOKENS and (d_model is None or edges_supported(d_model, n)):
+        return "edges"
+    return "rows"
+
+
+def down_mode(n: int, d_ff: int | None = None) -> str:
+    """Down kernel shape for N tokens (``d_ff`` kept for the reference signature, ``runtime.py:33``)."""
+    return "edges" if n <= EDGES_MAX_TOKENS else "rows"
+
+
+def edges_supported(d_model: int, n: int) -> bool:
+    return bool(_lib.load().hffn_edges_supported(d_model, n))
+
+
+def leading_dim(n: int) -> int:
+    """Leading dimension of the feature-major work buffers for N tokens: a multiple of 4, and of 8 above 4 tokens
+    (the edges shapes read 8-token vectors)."""
+    return (n + 3) // 4 * 4 if n <= 4 else (n + 7) // 8 * 8
+
+
+def _device(device: str | torch.device | None) -> torch.device:
+    device = torch.device("cuda" if device is None else device)
+    if device.type != "cuda" or device.index not in (None, 0):
+        raise ValueError("the HFFN HIP runtime runs on cuda:0")
+    if not torch.cuda.is_available():
+        raise RuntimeError("the HFFN HIP runtime needs a ROCm GPU (torch.cuda.is_available() is False)")
+    return torch.device("cuda", 0)
+
+
+def _value_type(tensor: torch.Tensor, name: str) -> int:
+    try:
+        return _VALUE_TYPES[tensor.dtype]
+    except KeyError:
+        raise ValueError(f"{name} must be float32 or bfloat16, not {tensor.dtype}") from None
+
+
+def _check_side(name: str, offsets: torch.Tensor, index: torch.Tensor, values: torch.Tensor, rows: int, width: int) -> None:
+    """Offsets int32[rows + 1] from 0 to nnz, non-decreasing; int16 indices in [0, width); one value per index."""
+    if offsets.dtype != torch.int32 or offsets.dim() != 1 or offsets.numel() != rows + 1:
+        raise ValueError(f"{name}: offsets must be int32[{rows + 1}]")
+    if index.dtype != torch.int16 or index.dim() != 1 or values.dim() != 1 or values.numel() != index.numel():
+        raise ValueError(f"{name}: expected int16 indices and one value per index")
+    if int(offsets[0]) != 0 or int(offsets[-1]) != index.numel() or bool((offsets.diff() < 0).any()):
+        raise ValueError(f"{name}: offsets must run from 0 to nnz without decreasing")
+    if index.numel() and (int(index.min()) < 0 or int(index.max()) >= width):
+        raise ValueError(f"{name}: index out of [0, {width})")
+
+
+@dataclass(frozen=True)
+class HFFNLayer:
+    """What the kernels read for one FFN: the up arrays per hidden neuron and the down edges in output order
+    (fields of ``runtime/gpu/nvidia/common/kernels/hffn_cuda/runtime.py:41-53``; values float32, or bfloat16 for a
+    bf16 store, the same dtype on both sides)."""
+    d_model: int
+    d_ff: int
+    b_up: torch.Tensor         # float32[d_ff]
+    up_offsets: torch.Tensor   # int32[d_ff + 1]
+    up_idx: torch.Tensor       # int16[nnz_up], input feature of each slot
+    up_val: torch.Tensor       # float32|bfloat16[nnz_up]
+    b_down: torch.Tensor       # float32[d_model]
+    out_offsets: torch.Tensor  # int32[d_model + 1]
+    out_hidden: torch.Tensor   # int16[nnz_down], hidden neuron of each edge (ascending within an output)
+    out_val: torch.Tensor      # float32|bfloat16[nnz_down]
+
+    @classmethod
+    def from_hidden_major(cls, d_model: int, d_ff: int, b_up: torch.Tensor, up_offsets: torch.Tensor, up_idx: torch.Tensor,
+                          up_val: torch.Tensor, b_down: torch.Tensor, down_offsets: torch.Tensor, down_idx: torch.Tensor,
+                          down_val: torch.Tensor, device: str | torch.device | None = None) -> "HFFNLayer":
+        """From the canonical hidden-major storage: for neuron r, its up slots and its down slots (output feature of
+        each slot in ``down_idx``) at ``[offsets[r], offsets[r + 1])``. The up arrays are kept as given (moved to the
+        device); the output-major down store is built on the device by ``hffn_output_major`` (a stable counting sort
+        of the slots by output, bitwise the ``argsort(stable)`` transpose of ``runtime.py:55-67``)."""
+        dev = _device(device)
+        _check_side("up", up_offsets, up_idx, up_val, d_ff, d_model)
+        _check_side("down", down_offsets, down_idx, down_val, d_ff, d_model)
+        if up_val.dtype != down_val.dtype:
+            raise ValueError("up_val and down_val must have the same dtype")
+        value_type = _value_type(down_val, "down_val")
+        if b_up.dtype != torch.float32 or b_up.numel() != d_ff or b_down.dtype != torch.float32 or b_down.numel() != d_model:
+            raise ValueError("b_up must be float32[d_ff] and b_down float32[d_model]")
+        moved = [t.to(dev).contiguous() for t in (b_up, up_offsets, up_idx, up_val, b_down, down_offsets, down_idx, down_val)]
+        b_up, up_offsets, up_idx, up_val, b_down, down_offsets, down_idx, down_val = moved
+        nnz = down_idx.numel()
+        out_offsets = torch.empty(d_model + 1, dtype=torch.int32, device=dev)
+        out_hidden = torch.empty(nnz, dtype=torch.int16, device=dev)
+        out_val = torch.empty(nnz, dtype=down_val.dtype, device=dev)
+        lib = _lib.load()
+        needed = _lib.ctypes.c_uint64(0)
+        _lib.check(lib.hffn_output_major_workspace(nnz, d_model, _lib.ctypes.byref(needed)), "output-major workspace")
+        workspace = torch.empty(max(needed.value, 4), dtype=torch.uint8, device=dev)
+        stream = torch.cuda.current_stream(dev).cuda_stream
+        _lib.check(lib.hffn_output_major(value_type, down_offsets.data_ptr(), down_idx.data_ptr(), down_val.data_ptr(),
+                                         d_model, d_ff, nnz, out_offsets.data_ptr(), out_hidden.data_ptr(),
+                                         out_val.data_ptr(), workspace.data_ptr(), workspace.numel(), stream),
+                   "output-major build")
+        torch.cuda.current_stream(dev).synchronize()  # the workspace is released on return
+        return cls(d_model, d_ff, b_up, up_offsets, up_idx, up_val, b_down, out_offsets, out_hidden, out_val)
+
+    def model_bytes(self) -> int:
+        return sum(value.numel() * value.element_size() for value in vars(self).values() if isinstance(value, torch.Tensor))
+
+
+_ARRAYS = ("b_up", "up_offsets", "up_idx", "up_val", "b_down", "out_offsets", "out_hidden", "out_val")
+
+
+class HFFNRuntime:
+    """``HFFNRuntime`` of ``runtime/gpu/nvidia/common/kernels/hffn_cuda/runtime.py:76-163`` on the HIP library."""
+
+    def __init__(self, layers: list[HFFNLayer], device: str | torch.device = "cuda") -> None:
+        self.device = _device(device)
+        self.layers = layers
+        self.d_model, self.d_ff = layers[0].d_model, layers[0].d_ff
+        if any((layer.d_model, layer.d_ff) != (self.d_model, self.d_ff) for layer in layers):
+            raise ValueError("all layers of a runtime share d_model and d_ff")
+        if self.d_model % 16:
+            raise ValueError("d_model must be a multiple of 16")
+        self._lib = _lib.load()
+        self._tensors = []
+        self._args = []
+        for layer in layers:
+            tensors = {name: getattr(layer, name).to(self.device).contiguous() for name in _ARRAYS}
+            _check_side("up", tensors["up_offsets"], tensors["up_idx"], tensors["up_val"], self.d_ff, self.d_model)
+            _check_side("down", tensors["out_offsets"], tensors["out_hidden"], tensors["out_val"], self.d_model, self.d_ff)
+            if tensors["up_val"].dtype != tensors["out_val"].dtype:
+                raise ValueError("up_val and out_val must have the same dtype")
+            if tensors["b_up"].numel() != self.d_ff or tensors["b_down"].numel() != self.d_model:
+                raise ValueError("bias dimensions do not match d_model/d_ff")
+            self._tensors.append(tensors)
+            self._args.append((_value_type(tensors["up_val"], "up_val"),
+                               *(tensors[name].data_ptr() for name in ("up_offsets", "up_idx", "up_val", "b_up",
+                                                                       "out_offsets", "out_hidden", "out_val", "b_down"))))
+        self.forced_up: str | None = None
+        self.forced_down: str | None = None
+        self.calls: Counter = Counter()
+        self._tokens = 0
+        self._reserve(1)
+
+    def force(self, up: str | None, down: str | None) -> None:
+        """Diagnostic: fix the up and/or the down kernel regardless of N (None: the policy)."""
+        if up not in (None, *UP_MODES) or down not in (None, *DOWN_MODES):
+            raise ValueError("unknown kernel mode")
+        if up == "edges" and not edges_supported(self.d_model, 1):
+            raise ValueError("the edges up shape cannot stage this d_model")
+        self.forced_up, self.forced_down = up, down
+
+    def _reserve(self, n: int) -> None:
+        self._tokens = n
+        ld = leading_dim(n)
+        self._x_t = torch.empty(self.d_model * ld, device=self.device)   # [d_model, ld]
+        self._act = torch.empty(self.d_ff * ld, device=self.device)      # [d_ff, ld]
+        self._y_t = torch.empty(self.d_model * ld, device=self.device)   # [d_model, ld]
+        self._y = torch.empty(n, self.d_model, device=self.device)
+        self._work = (self._x_t.data_ptr(), self._act.data_ptr(), self._y_t.data_ptr(), self._y.data_ptr())
+
+    def workspace_bytes(self) -> int:
+        return 4 * (self._x_t.numel() + self._act.numel() + self._y_t.numel() + self._y.numel())
+
+    def modes(self, n: int) -> tuple[str, str]:
+        """The (up, down) shapes a call of N tokens takes (forced ones first)."""
+        up = self.forced_up or up_mode(n, self.d_model)
+        if up == "edges" and not edges_supported(self.d_model, n):
+            up = "rows"
+        return up, self.forced_down or down_mode(n, self.d_ff)
+
+    def forward(self, index: int, x: torch.Tensor) -> torch.Tensor:
+        """y[N, d_model] of layer ``index`` for x[N, d_model] (contiguous float32 on the device).
+
+        The result is a view of the runtime's output buffer, overwritten by the next call.
+        """
+        if x.dim() != 2 or x.shape[1] != self.d_model or x.dtype != torch.float32 or x.device != self._y.device or not x.is_contiguous():
+            raise ValueError("expected a contiguous float32 [N, d_model] tensor on the runtime's device")
+        n = x.shape[0]
+        if not 1 <= n <= MAX_TOKENS:
+            raise ValueError("unsupported token count")
+        if n > self._tokens:
+            self._reserve(n)
+        up, down = self.modes(n)
+        self._launch(index, x, n, up, down)
+        self.calls[up, down] += 1
+        return self._y[:n]
+
+    def _launch(self, index: int, x: torch.Tensor, n: int, up: str, down: str) -> None:
+        value_type, *model = self._args[index]
+        x_t, act, y_t, y = self._work
+        stream = torch.cuda.current_stream(self.device).cuda_stream
+        _lib.check(self._lib.hffn_forward(_lib.UP_MODES[up], _lib.DOWN_MODES[down], value_type, x.data_ptr(), *model,
+                                          x_t, act, y_t, y, self.d_model, self.d_ff, n, leading_dim(n), stream),
+                   f"forward ({up}, {down})")

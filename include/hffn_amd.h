@@ -1,0 +1,106 @@
+/* C ABI of the MI355X (gfx950) HFFN forward library, libhffn_amd.so.
+ *
+ * One fixed-support sparse FFN  y = W_down gelu(W_up x + b_up) + b_down  stored per hidden
+ * neuron (compact int16 indices, float32 or bfloat16 values, float32 biases, exact-erf GELU).
+ * Every pointer is a device pointer unless stated otherwise; every launch goes on `stream`
+ * (a hipStream_t, NULL for the default stream) and is asynchronous. Every entry point returns
+ * HFFN_OK (0) or a negative HFFN_ERROR_* code; hffn_last_error() then describes the failure
+ * (per calling thread). No entry point allocates memory or synchronises.
+ *
+ * Layouts (n tokens, ld = leading dimension of the feature-major buffers, ld % 4 == 0, ld >= n):
+ *   x      float32 [n, d_model]     token-major input
+ *   x_t    float32 [d_model, ld]    feature-major input (workspace)
+ *   act    float32 [d_ff, ld]       hidden-major activations gelu(z) (workspace)
+ *   y_t    float32 [d_model, ld]    feature-major output (workspace)
+ *   y      float32 [n, d_model]     token-major output
+ *   up store:   up_offsets int32[d_ff + 1], up_idx int16[nnz_up] (input feature of each slot),
+ *               up_val float32|bf16[nnz_up], b_up float32[d_ff]
+ *   down store: out_offsets int32[d_model + 1], out_hidden int16[nnz_down] (hidden neuron of each
+ *               slot, ascending within an output), out_val float32|bf16[nnz_down], b_down float32[d_model]
+ */
+#ifndef HFFN_AMD_H
+#define HFFN_AMD_H
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define HFFN_ABI_VERSION 1
+
+#define HFFN_OK 0
+#define HFFN_ERROR_ARGUMENT (-1) /* invalid shape, mode, pointer or workspace */
+#define HFFN_ERROR_LAUNCH (-2)   /* the HIP runtime refused a launch */
+
+#define HFFN_VALUE_F32 0
+#define HFFN_VALUE_BF16 1
+
+/* Kernel shapes. EDGES: one wave per neuron/output, lanes over its slots, tokens taken nt at a time
+ * (nt = 1, 2, 4 for n <= 4, else 8; ld must be a multiple of nt; the up input of nt tokens is staged
+ * in LDS). ROWS: one wave per neuron/output, lanes over tokens. */
+#define HFFN_UP_EDGES 1
+#define HFFN_UP_ROWS 2
+#define HFFN_DOWN_EDGES 1
+#define HFFN_DOWN_ROWS 2
+
+#define HFFN_MAX_TOKENS (1u << 18)            /* runtime/gpu/nvidia/common/kernels/hffn_cuda/runtime.py:26 */
+#define HFFN_MAX_WIDTH 32768u                 /* widths addressable by the int16 indices */
+#define HFFN_MAX_OUTPUT_MAJOR_WIDTH 16384u    /* d_model of the output-major build (LDS bins) */
+#define HFFN_EDGES_MAX_LDS 65536u             /* bytes of the up input staged by the EDGES shape */
+
+int hffn_abi_version(void);
+const char* hffn_last_error(void);
+
+/* 1 if the EDGES up shape can stage n tokens of width d_model in LDS, else 0 (host-only query). */
+int hffn_edges_supported(uint32_t d_model, uint32_t n);
+
+/* out[c, r] = in[r, c] for r < rows, c < cols (row strides in_ld and out_ld, in floats).
+ * Replaces the `x_t.copy_(x.T)` of runtime/gpu/nvidia/common/kernels/hffn_cuda/runtime.py:150-151. */
+int hffn_transpose(const float* in, float* out, uint32_t rows, uint32_t cols, uint32_t in_ld, uint32_t out_ld,
+                   void* stream);
+
+/* act[r, t] = gelu(b_up[r] + sum_{e in [up_offsets[r], up_offsets[r+1])} up_val[e] * x[t, up_idx[e]]).
+ * mode EDGES reads x token-major [n, d_model]; mode ROWS reads x feature-major [d_model, ld].
+ * Replaces the up kernels `up_coop` / `up_lane` / `up_tile(const float* x, const int* off,
+ * const short* idx, const float* w, const float* b, float* a, unsigned d, unsigned H, unsigned n)`
+ * of runtime/gpu/nvidia/common/kernels/hffn_cuda/kernels.py:102-143 (launch: runtime.py:143-155). */
+int hffn_up(int mode, int value_type, const float* x, const int32_t* up_offsets, const int16_t* up_idx,
+            const void* up_val, const float* b_up, float* act, uint32_t d_model, uint32_t d_ff, uint32_t n, uint32_t ld,
+            void* stream);
+
+/* y[t, o] = sum_{q in [out_offsets[o], out_offsets[o+1])} out_val[q] * act[out_hidden[q], t] + b_down[o].
+ * mode EDGES writes y token-major [n, d_model]; mode ROWS writes y feature-major [d_model, ld].
+ * Replaces `down_coop` / `down_tiled` / `down_blocked(const float* a, const int* off, const short* hid,
+ * const float* v, const float* bias, float* y, unsigned d, unsigned n)` of
+ * runtime/gpu/nvidia/common/kernels/hffn_cuda/kernels.py:145-191 (launch: runtime.py:156-162). */
+int hffn_down(int mode, int value_type, const float* act, const int32_t* out_offsets, const int16_t* out_hidden,
+              const void* out_val, const float* b_down, float* y, uint32_t d_model, uint32_t d_ff, uint32_t n,
+              uint32_t ld, void* stream);
+
+/* The whole layer for x[n, d_model] -> y[n, d_model]: the transposes the modes need, up, down.
+ * x_t and y_t may be NULL when the modes do not use them. Replaces HFFNRuntime._launch
+ * (runtime/gpu/nvidia/common/kernels/hffn_cuda/runtime.py:134-163) and the two driver launches of
+ * PreparedRuntime.forward (runtime/gpu/nvidia/llm/inference/hffn_pythia_cuda/prepared_runtime.py:62-82). */
+int hffn_forward(int up_mode, int down_mode, int value_type, const float* x, const int32_t* up_offsets,
+                 const int16_t* up_idx, const void* up_val, const float* b_up, const int32_t* out_offsets,
+                 const int16_t* out_hidden, const void* out_val, const float* b_down, float* x_t, float* act,
+                 float* y_t, float* y, uint32_t d_model, uint32_t d_ff, uint32_t n, uint32_t ld, void* stream);
+
+/* Bytes of device workspace hffn_output_major needs for nnz down slots (host-only query). */
+int hffn_output_major_workspace(uint32_t nnz, uint32_t d_model, uint64_t* bytes);
+
+/* Output-major transpose of the hidden-major down store, stable in slot order:
+ *   out_offsets = [0, cumsum(bincount(down_idx, d_model))],
+ *   out_hidden[p] = owner neuron of slot order[p], out_val[p] = down_val[order[p]],
+ * with order = the stable argsort of down_idx. Replaces HFFNLayer.from_hidden_major
+ * (runtime/gpu/nvidia/common/kernels/hffn_cuda/runtime.py:55-67), which runs it on the host. */
+int hffn_output_major(int value_type, const int32_t* down_offsets, const int16_t* down_idx, const void* down_val,
+                      uint32_t d_model, uint32_t d_ff, uint32_t nnz, int32_t* out_offsets, int16_t* out_hidden,
+                      void* out_val, void* workspace, uint64_t workspace_bytes, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* HFFN_AMD_H */

@@ -1,0 +1,124 @@
+"""Host-side checks without a GPU: the C-ABI library loads and exports what include/hffn_amd.h declares, its argument
+validation refuses bad shapes before any launch, and the Python boundary keeps the reference's policy and errors."""
+from __future__ import annotations
+
+import ctypes
+import re
+from pathlib import Path
+
+import pytest
+import torch
+
+from hffn_amd import _lib, runtime, synth
+
+ROOT = Path(__file__).resolve().parents[1]
+
+
+def declared_functions() -> list[str]:
+    text = (ROOT / "include" / "hffn_amd.h").read_text()
+    return sorted(set(re.findall(r"^(?:int|const char\*)\s+(hffn_\w+)\(", text, flags=re.M)))
+
+
+def test_library_exports_every_declared_symbol():
+    lib = _lib.load()
+    names = declared_functions()
+    assert len(names) >= 9
+    for name in names:
+        assert hasattr(lib, name), name
+        assert name in _lib.SIGNATURES, f"{name} is declared but not bound"
+    assert lib.hffn_abi_version() == _lib.ABI_VERSION
+
+
+def test_library_is_not_loaded_from_elsewhere():
+    assert _lib.LIBRARY.parent == ROOT / "hffn_amd"
+
+
+def _expect_argument_error(status: int, fragment: str) -> None:
+    assert status == _lib.OK - 1
+    assert fragment in _lib.load().hffn_last_error().decode()
+
+
+@pytest.mark.skipif(torch.cuda.is_available(), reason="uses placeholder pointers: never run where a launch could reach a GPU")
+def test_abi_refuses_bad_shapes_before_launching():
+    lib = _lib.load()
+    p = ctypes.c_void_p(16)  # never dereferenced: every call below fails validation first
+    _expect_argument_error(lib.hffn_up(1, 0, p, p, p, p, p, p, 17, 64, 1, 4, None), "d_model=17")
+    _expect_argument_error(lib.hffn_up(1, 0, p, p, p, p, p, p, 64, 0, 1, 4, None), "d_ff=0")
+    _expect_argument_error(lib.hffn_up(1, 0, p, p, p, p, p, p, 64, 64, 0, 4, None), "n=0")
+    _expect_argument_error(lib.hffn_up(1, 0, p, p, p, p, p, p, 64, 64, (1 << 18) + 1, 1 << 19, None), "unsupported token count")
+    _expect_argument_error(lib.hffn_up(1, 0, p, p, p, p, p, p, 64, 64, 5, 6, None), "ld=6")
+    _expect_argument_error(lib.hffn_up(1, 0, p, p, p, p, p, p, 64, 64, 5, 12, None), "multiple of 8")
+    _expect_argument_error(lib.hffn_up(9, 0, p, p, p, p, p, p, 64, 64, 1, 4, None), "unknown up mode")
+    _expect_argument_error(lib.hffn_up(1, 7, p, p, p, p, p, p, 64, 64, 1, 4, None), "unknown value type")
+    _expect_argument_error(lib.hffn_up(1, 0, None, p, p, p, p, p, 64, 64, 1, 4, None), "null pointer")
+    _expect_argument_error(lib.hffn_up(1, 0, p, p, p, p, p, p, 4096, 64, 8, 8, None), "LDS")
+    _expect_argument_error(lib.hffn_down(3, 0, p, p, p, p, p, p, 64, 64, 1, 4, None), "unknown down mode")
+    _expect_argument_error(lib.hffn_forward(2, 2, 0, p, p, p, p, p, p, p, p, p, None, p, p, p, 64, 64, 1, 4, None), "x_t")
+    needed = ctypes.c_uint64(0)
+    assert lib.hffn_output_major_workspace(2_097_152, 1024, ctypes.byref(needed)) == _lib.OK
+    assert needed.value == 1024 * 1024 * 4
+    _expect_argument_error(lib.hffn_output_major(0, p, p, p, 1024, 4096, 2_097_152, p, p, p, p, needed.value - 1, None), "workspace")
+    _expect_argument_error(lib.hffn_output_major(0, p, p, p, 20000, 4096, 16, p, p, p, p, 1 << 30, None), "d_model=20000")
+
+
+def test_edges_stage_limit():
+    lib = _lib.load()
+    assert lib.hffn_edges_supported(1024, 8) == 1
+    assert lib.hffn_edges_supported(2048, 8) == 1
+    assert lib.hffn_edges_supported(2560, 8) == 0
+    assert lib.hffn_edges_supported(2560, 4) == 1
+
+
+def test_policy():
+    assert [runtime.up_mode(n) for n in (1, 4, 8, 9, 64, 2048)] == ["edges"] * 3 + ["rows"] * 3
+    assert runtime.up_mode(8, 2560) == "rows" and runtime.up_mode(4, 2560) == "edges"
+    assert [runtime.down_mode(n, 4096) for n in (1, 8, 9, 2048)] == ["edges", "edges", "rows", "rows"]
+    assert [runtime.leading_dim(n) for n in (1, 2, 3, 4, 5, 8, 9, 2048, 2049)] == [4, 4, 4, 4, 8, 8, 16, 2048, 2056]
+
+
+def test_runtime_refuses_other_devices():
+    with pytest.raises(ValueError, match="cuda:0"):
+        runtime.HFFNRuntime([], "cuda:1")
+    with pytest.raises(ValueError, match="cuda:0"):
+        runtime.HFFNRuntime([], "cpu")
+
+
+@pytest.mark.skipif(torch.cuda.is_available(), reason="checks the no-GPU error")
+def test_runtime_needs_a_gpu():
+    with pytest.raises(RuntimeError, match="ROCm GPU"):
+        runtime.HFFNRuntime([], "cuda")
+
+
+def test_layer_validation_on_host():
+    """Malformed stores are refused before anything reaches a kernel."""
+    layer = synth.make_layer(synth.CASES["homog_256_1024"])
+    t = torch.from_numpy
+    good = (t(layer.up_offsets), t(layer.up_idx), t(layer.up_val))
+    runtime._check_side("up", *good, layer.d_ff, layer.d_model)
+    bad_index = t(layer.up_idx).clone()
+    bad_index[3] = layer.d_model
+    with pytest.raises(ValueError, match="index out of"):
+        runtime._check_side("up", good[0], bad_index, good[2], layer.d_ff, layer.d_model)
+    bad_offsets = t(layer.up_offsets).clone()
+    bad_offsets[5] = bad_offsets[6] + 1
+    with pytest.raises(ValueError, match="without decreasing"):
+        runtime._check_side("up", bad_offsets, good[1], good[2], layer.d_ff, layer.d_model)
+    with pytest.raises(ValueError, match="int32"):
+        runtime._check_side("up", good[0].long(), good[1], good[2], layer.d_ff, layer.d_model)
+
+
+def test_workload_generator_properties():
+    layer = synth.make_workload_layer("pythia70m_d20")
+    assert layer.up_idx.size == layer.d_ff * 102 and layer.down_idx.size == layer.d_ff * 102
+    for offsets, idx in ((layer.up_offsets, layer.up_idx), (layer.down_offsets, layer.down_idx)):
+        for r in range(0, layer.d_ff, 97):
+            row = idx[offsets[r]:offsets[r + 1]].astype(int)
+            assert (row >= 0).all() and (row < layer.d_model).all() and (row[1:] > row[:-1]).all()
+    assert not layer.b_up.any() and not layer.b_down.any()
+    assert abs(float(layer.up_val.std()) - 0.02) < 0.001
+
+
+def test_bf16_rounding():
+    values = torch.randn(10000).numpy().astype("float32")
+    rounded = synth.round_bf16(values)
+    assert torch.equal(torch.from_numpy(rounded), torch.from_numpy(values).to(torch.bfloat16).float())
