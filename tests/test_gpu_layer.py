@@ -197,7 +197,8 @@ def test_1p4b_bf16(n, device):
 
 def test_2p8b_zipf_bf16_token_sample(device):
     """Pythia-2.8B shape, ~80 % mean density with uneven fan-in and Zipf-biased supports, bf16, N = 4096: the whole
-    batch runs, a token sample is checked against the oracle, and the batch result equals the sample run alone."""
+    batch runs and a token sample is checked against the float64 oracle on the same (bf16-exact) weights. The stated
+    bf16 bound is 2e-2; the float32 accumulation of ~2048-term rows is held to 5e-5 here."""
     workload = synth.WORKLOADS["pythia2p8b_d80_zipf_bf16"]
     compact = _cached(workload.name)
     import json
@@ -210,7 +211,7 @@ def test_2p8b_zipf_bf16_token_sample(device):
     x_np = synth.make_input(workload, 4096)
     y = runtime.forward(0, torch.from_numpy(x_np).to(device)).clone()
     sample = np.random.default_rng(11).choice(4096, 48, replace=False)
-    assert _relative(y[sample], reference.forward(compact, x_np[sample])) <= 1e-5
+    assert _relative(y[sample], reference.forward(compact, x_np[sample])) <= 5e-5
 
 
 _CACHE: dict = {}
