@@ -34,6 +34,7 @@ import torch  # noqa: E402
 METRIC = "HFFN layer tokens/s + % HBM roofline, Pythia-410M shape @50% density"
 HBM_PEAK = 8.0e12          # bytes/s, MI355X HBM3E
 FP32_PEAK = 157.3e12       # FLOP/s, MI355X fp32 (vector and matrix)
+FP16_MFMA_PEAK = 2.5e15    # FLOP/s, MI355X dense fp16 MFMA
 RIDGE = FP32_PEAK / HBM_PEAK
 MALL_BYTES = 300e6         # rotate over more than the 256 MB Infinity Cache
 
@@ -82,6 +83,31 @@ def time_kernels(runtime, x: torch.Tensor, steps: int, copies: int) -> dict:
     up, down = runtime.modes(n)
     x_t, act, y_t, y = runtime._work
     stream = torch.cuda.current_stream().cuda_stream
+    if up == "mfma":
+        names = ["row_binades", "up", "down"]
+        totals = {name: 0.0 for name in names}
+        binades = runtime._binades.data_ptr()
+        act_binades = binades + 4 * n
+        for step in range(steps):
+            index = step % copies
+            value_type = runtime._args[index][0]
+            planes, tensors = runtime._planes[index], runtime._tensors[index]
+            events = [torch.cuda.Event(enable_timing=True) for _ in range(4)]
+            events[0].record()
+            _lib.check(lib.hffn_row_binades(x.data_ptr(), n, runtime.d_model, binades, stream), "row binades")
+            events[1].record()
+            _lib.check(lib.hffn_mfma_up(value_type, x.data_ptr(), binades, planes["up"].data_ptr(),
+                                        planes["up_binades"].data_ptr(), tensors["b_up"].data_ptr(), act, act_binades,
+                                        runtime.d_model, runtime.d_ff, n, stream), "mfma up")
+            events[2].record()
+            _lib.check(lib.hffn_mfma_down(value_type, act, act_binades, planes["down"].data_ptr(),
+                                          planes["down_binades"].data_ptr(), tensors["b_down"].data_ptr(), y,
+                                          runtime.d_model, runtime.d_ff, n, stream), "mfma down")
+            events[3].record()
+            torch.cuda.synchronize()
+            for i, name in enumerate(names):
+                totals[name] += events[i].elapsed_time(events[i + 1]) * 1e-3
+        return {name: total / steps for name, total in totals.items()}
     names = (["transpose_in"] if up == "rows" else []) + ["up", "down"] + (["transpose_out"] if down == "rows" else [])
     totals = {name: 0.0 for name in names}
     for step in range(steps):
@@ -187,6 +213,11 @@ def main() -> int:
     roofline["frac"] = round(roofline["achieved"] / roofline["peak"], 4)
     roofline["traffic"] = None
     roofline["kernel"] = f"{dominant} ({up if dominant == 'up' else down})"
+    if up == "mfma":
+        # what the MFMA units execute: the dense products of the planes, 3 (fp32 values) or 2 (bf16) fp16 MFMAs each
+        products = 2 if base.value_dtype == "bf16" else 3
+        dense = 2 * n * base.d_model * base.d_ff * products
+        roofline["fp16_mfma_issued_frac"] = round(dense / kernels[dominant] / FP16_MFMA_PEAK, 4)
     roofline["kernel_us"] = round(kernels[dominant] * 1e6, 2)
 
     baseline = None if args.no_cpu else cpu_baseline(base, x_np, args.cpu_seconds, args.cpu_threads)

@@ -14,8 +14,8 @@ ABI_VERSION = 1
 
 OK = 0
 VALUE_F32, VALUE_BF16 = 0, 1
-UP_MODES = {"edges": 1, "rows": 2}
-DOWN_MODES = {"edges": 1, "rows": 2}
+UP_MODES = {"edges": 1, "rows": 2, "mfma": 3}
+DOWN_MODES = {"edges": 1, "rows": 2, "mfma": 3}
 
 _P, _I, _U32, _U64 = ctypes.c_void_p, ctypes.c_int, ctypes.c_uint32, ctypes.c_uint64
 
@@ -30,6 +30,14 @@ SIGNATURES = {
     "hffn_forward": [_I, _I, _I] + [_P] * 13 + [_U32] * 4 + [_P],
     "hffn_output_major_workspace": [_U32, _U32, ctypes.POINTER(_U64)],
     "hffn_output_major": [_I, _P, _P, _P, _U32, _U32, _U32, _P, _P, _P, _P, _U64, _P],
+    "hffn_mfma_supported": [_U32, _U32],
+    "hffn_dense_planes_bytes": [_U32, _U32, ctypes.POINTER(_U64)],
+    "hffn_densify": [_I, _P, _P, _P, _U32, _U32, _P, _P, _P],
+    "hffn_mfma_workspace": [_U32, _U32, _U32, ctypes.POINTER(_U64)],
+    "hffn_row_binades": [_P, _U32, _U32, _P, _P],
+    "hffn_mfma_up": [_I, _P, _P, _P, _P, _P, _P, _P, _U32, _U32, _U32, _P],
+    "hffn_mfma_down": [_I, _P, _P, _P, _P, _P, _P, _U32, _U32, _U32, _P],
+    "hffn_forward_mfma": [_I] + [_P] * 10 + [_U32] * 3 + [_P],
 }
 
 
@@ -69,3 +77,10 @@ def check(status: int, what: str) -> None:
 
 def exported_symbols() -> list[str]:
     return list(SIGNATURES)
+
+
+def query_bytes(function, *args) -> int:
+    """Call a host-only size query of the library and return its uint64 result."""
+    result = ctypes.c_uint64(0)
+    check(function(*args, ctypes.byref(result)), function.__name__)
+    return result.value

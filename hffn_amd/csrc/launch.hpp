@@ -44,4 +44,17 @@ hipError_t launch_output_major(int vt, const int32_t* down_offsets, const int16_
                                uint32_t d, uint32_t h, uint32_t nnz, int32_t* out_offsets, int16_t* out_hidden,
                                void* out_val, int32_t* counts, hipStream_t stream);
 
+// Tile-densified MFMA path (mfma.hip). Planes: fp16 hi/lo of a dense [rows, k] matrix, tile-major.
+size_t dense_plane_halves(uint32_t rows, uint32_t k);
+uint32_t mfma_block_cols(uint32_t ncol);
+uint32_t mfma_block_rows(uint32_t m, uint32_t ncol);
+hipError_t launch_row_binades(const float* x, uint32_t rows, uint32_t cols, int32_t* e, hipStream_t stream);
+hipError_t launch_densify(int vt, const int32_t* off, const int16_t* idx, const void* val, uint32_t rows, uint32_t k,
+                          void* planes, int32_t* exps, hipStream_t stream);
+hipError_t launch_mfma_up(int vt, const float* x, const int32_t* x_exp, const void* planes, const int32_t* w_exp,
+                          const float* b_up, float* act, int32_t* act_exp, uint32_t n, uint32_t d, uint32_t h,
+                          hipStream_t stream);
+hipError_t launch_mfma_down(int vt, const float* act, const int32_t* act_exp, const void* planes, const int32_t* v_exp,
+                            const float* b_down, float* y, uint32_t n, uint32_t d, uint32_t h, hipStream_t stream);
+
 }  // namespace hffn

@@ -3,8 +3,8 @@
 
 For one input, the runtime runs with its policy and with each forced (up, down) kernel pair. Criteria: two
 consecutive calls on the same input give the same bits; ``max |y - y64|`` and ``max |y - y64| / max(1, |y64|)`` are
-reported for the caller to compare with its tolerance. Reported without threshold: whether the forced pairs that
-share the lane-per-token shapes (up rows x down rows) agree bitwise with the policy's result of the same shapes.
+reported for the caller to compare with its tolerance. The pairs are the policy, the four gather pairs (edges or
+rows up, edges or rows down) and, when the runtime holds densified planes, the MFMA path.
 """
 from __future__ import annotations
 
@@ -12,9 +12,10 @@ from dataclasses import dataclass
 
 import torch
 
-from .runtime import DOWN_MODES, UP_MODES, HFFNRuntime
+from .runtime import HFFNRuntime
 
-PAIRS = [(None, None)] + [(up, down) for up in UP_MODES for down in DOWN_MODES]
+GATHER = ("edges", "rows")
+PAIRS = [(None, None)] + [(up, down) for up in GATHER for down in GATHER] + [("mfma", "mfma")]
 
 
 @dataclass
@@ -31,6 +32,8 @@ def check(runtime: HFFNRuntime, index: int, x: torch.Tensor, expected: torch.Ten
     result = Parity(0.0, 0.0, True, {})
     try:
         for up, down in pairs:
+            if up == "mfma" and not runtime.mfma_available:
+                continue
             runtime.force(up, down)
             y = runtime.forward(index, x).clone()
             result.repeatable &= bool(torch.equal(y, runtime.forward(index, x)))

@@ -24,9 +24,11 @@ import torch
 
 from . import _lib
 
-UP_MODES = ("edges", "rows")
-DOWN_MODES = ("edges", "rows")
+UP_MODES = ("edges", "rows", "mfma")
+DOWN_MODES = ("edges", "rows", "mfma")
 EDGES_MAX_TOKENS = 8      # the policy's last N for the lane-per-slot shapes
+MFMA_MIN_TOKENS = 64      # the policy's first N for the tile-densified MFMA path
+MFMA_MIN_DENSITY = 0.05   # ... and the lowest support density it takes
 MAX_TOKENS = 1 << 18      # runtime/gpu/nvidia/common/kernels/hffn_cuda/runtime.py:26
 
 _VALUE_TYPES = {torch.float32: _lib.VALUE_F32, torch.bfloat16: _lib.VALUE_BF16}
@@ -68,6 +70,17 @@ def _value_type(tensor: torch.Tensor, name: str) -> int:
         return _VALUE_TYPES[tensor.dtype]
     except KeyError:
         raise ValueError(f"{name} must be float32 or bfloat16, not {tensor.dtype}") from None
+
+
+def _rows_strictly_increasing(offsets: torch.Tensor, index: torch.Tensor) -> bool:
+    """Whether every row's indices increase strictly (distinct, sorted): what the densified planes assume."""
+    if index.numel() < 2:
+        return True
+    step = index[1:].int() - index[:-1].int()
+    starts = offsets[1:-1].long()
+    starts = starts[(starts > 0) & (starts < index.numel())] - 1
+    step[starts] = 1
+    return bool((step > 0).all())
 
 
 def _check_side(name: str, offsets: torch.Tensor, index: torch.Tensor, values: torch.Tensor, rows: int, width: int) -> None:
@@ -142,7 +155,9 @@ _ARRAYS = ("b_up", "up_offsets", "up_idx", "up_val", "b_down", "out_offsets", "o
 class HFFNRuntime:
     """``HFFNRuntime`` of ``runtime/gpu/nvidia/common/kernels/hffn_cuda/runtime.py:76-163`` on the HIP library."""
 
-    def __init__(self, layers: list[HFFNLayer], device: str | torch.device = "cuda") -> None:
+    def __init__(self, layers: list[HFFNLayer], device: str | torch.device = "cuda", dense: bool = True) -> None:
+        """``dense``: also build the densified planes of the MFMA path when the layers qualify (shape a multiple of
+        64, distinct sorted indices per row); without them every call takes the gather kernels."""
         self.device = _device(device)
         self.layers = layers
         self.d_model, self.d_ff = layers[0].d_model, layers[0].d_ff
@@ -165,18 +180,63 @@ class HFFNRuntime:
             self._args.append((_value_type(tensors["up_val"], "up_val"),
                                *(tensors[name].data_ptr() for name in ("up_offsets", "up_idx", "up_val", "b_up",
                                                                        "out_offsets", "out_hidden", "out_val", "b_down"))))
+        self.density = max(layer.up_idx.numel() + layer.out_hidden.numel() for layer in layers) / (2 * self.d_model * self.d_ff)
+        self._planes: list[dict] | None = None
+        if dense and self._mfma_eligible():
+            self._planes = [self._densify(tensors) for tensors in self._tensors]
         self.forced_up: str | None = None
         self.forced_down: str | None = None
         self.calls: Counter = Counter()
         self._tokens = 0
         self._reserve(1)
 
+    # -------------------------------------------------------------------------------- tile-densified MFMA path
+
+    def _mfma_eligible(self) -> bool:
+        if not self._lib.hffn_mfma_supported(self.d_model, self.d_ff):
+            return False
+        return all(_rows_strictly_increasing(t["up_offsets"], t["up_idx"]) and
+                   _rows_strictly_increasing(t["out_offsets"], t["out_hidden"]) for t in self._tensors)
+
+    def _densify(self, tensors: dict) -> dict:
+        """fp16 hi/lo planes (and per-row binades) of W_up [d_ff, d_model] and W_down [d_model, d_ff], built on the
+        device from the compact store."""
+        value_type = _value_type(tensors["up_val"], "up_val")
+        stream = torch.cuda.current_stream(self.device).cuda_stream
+        planes = {}
+        for side, rows, k, names in (("up", self.d_ff, self.d_model, ("up_offsets", "up_idx", "up_val")),
+                                     ("down", self.d_model, self.d_ff, ("out_offsets", "out_hidden", "out_val"))):
+            size = _lib.query_bytes(self._lib.hffn_dense_planes_bytes, rows, k)
+            plane = torch.empty(size // 2, dtype=torch.float16, device=self.device)
+            binades = torch.empty(rows, dtype=torch.int32, device=self.device)
+            offsets, index, values = (tensors[name] for name in names)
+            _lib.check(self._lib.hffn_densify(value_type, offsets.data_ptr(), index.data_ptr(), values.data_ptr(), rows, k,
+                                              plane.data_ptr(), binades.data_ptr(), stream), f"densify {side}")
+            planes[side] = plane
+            planes[f"{side}_binades"] = binades
+        return planes
+
+    @property
+    def mfma_available(self) -> bool:
+        return self._planes is not None
+
+    def dense_bytes(self) -> int:
+        """Bytes of the densified planes held for the MFMA path (0 without it)."""
+        if self._planes is None:
+            return 0
+        return sum(t.numel() * t.element_size() for planes in self._planes for t in planes.values())
+
     def force(self, up: str | None, down: str | None) -> None:
-        """Diagnostic: fix the up and/or the down kernel regardless of N (None: the policy)."""
+        """Diagnostic: fix the up and/or the down kernel regardless of N (None: the policy). The MFMA path runs up and
+        down together (its activations are token-major): ``mfma`` is forced as a pair."""
         if up not in (None, *UP_MODES) or down not in (None, *DOWN_MODES):
             raise ValueError("unknown kernel mode")
         if up == "edges" and not edges_supported(self.d_model, 1):
             raise ValueError("the edges up shape cannot stage this d_model")
+        if (up == "mfma") != (down == "mfma"):
+            raise ValueError("the mfma path runs up and down together: force ('mfma', 'mfma')")
+        if up == "mfma" and self._planes is None:
+            raise ValueError("the mfma path is not available for these layers")
         self.forced_up, self.forced_down = up, down
 
     def _reserve(self, n: int) -> None:
@@ -186,13 +246,20 @@ class HFFNRuntime:
         self._act = torch.empty(self.d_ff * ld, device=self.device)      # [d_ff, ld]
         self._y_t = torch.empty(self.d_model * ld, device=self.device)   # [d_model, ld]
         self._y = torch.empty(n, self.d_model, device=self.device)
+        binades = 0
+        if self._planes is not None:
+            binades = _lib.query_bytes(self._lib.hffn_mfma_workspace, n, self.d_model, self.d_ff) // 4
+        self._binades = torch.empty(max(binades, 1), dtype=torch.int32, device=self.device)
         self._work = (self._x_t.data_ptr(), self._act.data_ptr(), self._y_t.data_ptr(), self._y.data_ptr())
 
     def workspace_bytes(self) -> int:
-        return 4 * (self._x_t.numel() + self._act.numel() + self._y_t.numel() + self._y.numel())
+        return 4 * (self._x_t.numel() + self._act.numel() + self._y_t.numel() + self._y.numel() + self._binades.numel())
 
     def modes(self, n: int) -> tuple[str, str]:
         """The (up, down) shapes a call of N tokens takes (forced ones first)."""
+        if self.forced_up is None and self.forced_down is None and self._planes is not None \
+                and n >= MFMA_MIN_TOKENS and self.density >= MFMA_MIN_DENSITY:
+            return "mfma", "mfma"
         up = self.forced_up or up_mode(n, self.d_model)
         if up == "edges" and not edges_supported(self.d_model, n):
             up = "rows"
@@ -219,6 +286,14 @@ class HFFNRuntime:
         value_type, *model = self._args[index]
         x_t, act, y_t, y = self._work
         stream = torch.cuda.current_stream(self.device).cuda_stream
+        if up == "mfma":
+            planes, tensors = self._planes[index], self._tensors[index]
+            _lib.check(self._lib.hffn_forward_mfma(value_type, x.data_ptr(), planes["up"].data_ptr(),
+                                                   planes["up_binades"].data_ptr(), tensors["b_up"].data_ptr(),
+                                                   planes["down"].data_ptr(), planes["down_binades"].data_ptr(),
+                                                   tensors["b_down"].data_ptr(), act, self._binades.data_ptr(), y,
+                                                   self.d_model, self.d_ff, n, stream), "forward (mfma, mfma)")
+            return
         _lib.check(self._lib.hffn_forward(_lib.UP_MODES[up], _lib.DOWN_MODES[down], value_type, x.data_ptr(), *model,
                                           x_t, act, y_t, y, self.d_model, self.d_ff, n, leading_dim(n), stream),
                    f"forward ({up}, {down})")

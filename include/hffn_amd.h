@@ -99,6 +99,46 @@ int hffn_output_major(int value_type, const int32_t* down_offsets, const int16_t
                       uint32_t d_model, uint32_t d_ff, uint32_t nnz, int32_t* out_offsets, int16_t* out_hidden,
                       void* out_val, void* workspace, uint64_t workspace_bytes, void* stream);
 
+/* ---- Tile-densified MFMA path (high density, large n). No reference counterpart: the reference runs every shape on
+ * the gather kernels (runtime/gpu/nvidia/common/kernels/hffn_cuda/kernels.py). Weights are densified at load into
+ * fp16 hi/lo "planes" with one power-of-two scale per row (binade); activations are split the same way on the fly;
+ * each product is hi*hi + hi*lo + lo*hi (hi*hi + lo*hi for bf16 weights) on v_mfma_f32_32x32x16_f16 with fp32
+ * accumulation. Activations are token-major act[n, d_ff] on this path. */
+
+/* 1 if the MFMA path takes this shape (d_model and d_ff multiples of 64), else 0 (host-only query). */
+int hffn_mfma_supported(uint32_t d_model, uint32_t d_ff);
+
+/* Bytes of the planes of a dense [rows, k] matrix (host-only query). */
+int hffn_dense_planes_bytes(uint32_t rows, uint32_t k, uint64_t* bytes);
+
+/* Densify one side: row r holds slots [offsets[r], offsets[r+1]) at columns idx[] (distinct within a row, in [0, k)).
+ * The up side is rows = d_ff over k = d_model from (up_offsets, up_idx, up_val); the down side is rows = d_model over
+ * k = d_ff from the output-major (out_offsets, out_hidden, out_val). Writes every byte of `planes` and binades[rows]. */
+int hffn_densify(int value_type, const int32_t* offsets, const int16_t* idx, const void* val, uint32_t rows, uint32_t k,
+                 void* planes, int32_t* binades, void* stream);
+
+/* Bytes of the int32 binade workspace of hffn_forward_mfma for n tokens (host-only query). */
+int hffn_mfma_workspace(uint32_t n, uint32_t d_model, uint32_t d_ff, uint64_t* bytes);
+
+/* binades[r] = floor(log2(max_c |x[r, c]|)) (0 for a zero row), x row-major [rows, cols]. */
+int hffn_row_binades(const float* x, uint32_t rows, uint32_t cols, int32_t* binades, void* stream);
+
+/* act[t, r] = gelu(b_up[r] + sum_i W_up[r, i] x[t, i]) (token-major), and act_binades[t, block] the binade of the
+ * largest |act| of token t in each block of the up kernel's neuron tile (d_ff / 128 or d_ff / 64 blocks). */
+int hffn_mfma_up(int value_type, const float* x, const int32_t* x_binades, const void* up_planes, const int32_t* up_binades,
+                 const float* b_up, float* act, int32_t* act_binades, uint32_t d_model, uint32_t d_ff, uint32_t n, void* stream);
+
+/* y[t, o] = sum_r W_down[o, r] act[t, r] + b_down[o], y token-major [n, d_model]. */
+int hffn_mfma_down(int value_type, const float* act, const int32_t* act_binades, const void* down_planes,
+                   const int32_t* down_binades, const float* b_down, float* y, uint32_t d_model, uint32_t d_ff, uint32_t n,
+                   void* stream);
+
+/* The whole layer on the MFMA path: row binades of x, up, down. `binades` is the workspace of hffn_mfma_workspace,
+ * act a float32 [n, d_ff] workspace. */
+int hffn_forward_mfma(int value_type, const float* x, const void* up_planes, const int32_t* up_binades, const float* b_up,
+                      const void* down_planes, const int32_t* down_binades, const float* b_down, float* act,
+                      int32_t* binades, float* y, uint32_t d_model, uint32_t d_ff, uint32_t n, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -97,7 +97,35 @@ def test_shared_buffers_between_calls(test_layers, device):
     assert torch.equal(runtime.forward(0, x8), first)
 
 
-@pytest.mark.parametrize("up,down", [("edges", "edges"), ("rows", "rows"), ("rows", "edges"), ("edges", "rows")])
+def _planes_to_dense(plane: torch.Tensor, binades: torch.Tensor, rows: int, k: int) -> np.ndarray:
+    """float64 [rows, k] = (hi + lo) * 2^binade from the tile-major planes [k/32][rows][hi 32 | lo 32]."""
+    tiles = plane.float().cpu().numpy().astype(np.float64).reshape(k // 32, rows, 2, 32)
+    dense = (tiles[:, :, 0, :] + tiles[:, :, 1, :]).transpose(1, 0, 2).reshape(rows, k)
+    return dense * np.exp2(binades.cpu().numpy().astype(np.float64))[:, None]
+
+
+@pytest.mark.parametrize("name", sorted(synth.CASES))
+def test_densified_planes_reconstruct_the_weights(name, test_layers, device):
+    """hi + lo of each plane entry, rescaled by its row's power of two, is the weight to 2^-22 of the row's largest
+    entry, and exactly zero outside the support."""
+    compact, _, layer = test_layers[name]
+    runtime = HFFNRuntime([layer], device)
+    assert runtime.mfma_available
+    planes = runtime._planes[0]
+    w_up, w_down = reference.dense_weights(compact)
+    for side, expected in (("up", w_up), ("down", w_down)):
+        rows, k = expected.shape
+        got = _planes_to_dense(planes[side], planes[f"{side}_binades"], rows, k)
+        bound = np.abs(expected).max(axis=1, keepdims=True) * 2.0**-22
+        assert np.all(np.abs(got - expected) <= bound), side
+        assert np.all(got[expected == 0] == 0), side
+        rowmax = np.abs(expected).max(axis=1)
+        top = np.exp2(planes[f"{side}_binades"].cpu().numpy().astype(np.float64))
+        assert np.all((rowmax == 0) | ((top <= rowmax) & (rowmax < 2 * top))), side
+
+
+@pytest.mark.parametrize("up,down", [("edges", "edges"), ("rows", "rows"), ("rows", "edges"), ("edges", "rows"),
+                                     ("mfma", "mfma")])
 def test_token_result_does_not_depend_on_the_batch(up, down, test_layers, device):
     compact, case, layer = test_layers["homog_512_2048"]
     runtime = HFFNRuntime([layer], device)
@@ -164,7 +192,7 @@ def test_410m_relative_error(n, w410m, device):
     runtime = HFFNRuntime([layer], device)
     x_np = synth.make_input(workload, n)
     expected = reference.forward(compact, x_np)
-    pairs = parity.PAIRS if n <= 32 else [(None, None), ("rows", "rows")]
+    pairs = parity.PAIRS if n <= 32 else [(None, None), ("rows", "rows"), ("mfma", "mfma")]
     result = parity.check(runtime, 0, torch.from_numpy(x_np).to(device), torch.from_numpy(expected).to(device), pairs)
     assert result.repeatable
     assert result.relative <= 1e-5, result.pairs
