@@ -84,26 +84,23 @@ def time_kernels(runtime, x: torch.Tensor, steps: int, copies: int) -> dict:
     x_t, act, y_t, y = runtime._work
     stream = torch.cuda.current_stream().cuda_stream
     if up == "mfma":
-        names = ["row_binades", "up", "down"]
+        names = ["up", "down"]
         totals = {name: 0.0 for name in names}
-        binades = runtime._binades.data_ptr()
-        act_binades = binades + 4 * n
+        work = runtime._mfma_work.data_ptr()
         for step in range(steps):
             index = step % copies
             value_type = runtime._args[index][0]
             planes, tensors = runtime._planes[index], runtime._tensors[index]
-            events = [torch.cuda.Event(enable_timing=True) for _ in range(4)]
+            events = [torch.cuda.Event(enable_timing=True) for _ in range(3)]
             events[0].record()
-            _lib.check(lib.hffn_row_binades(x.data_ptr(), n, runtime.d_model, binades, stream), "row binades")
+            _lib.check(lib.hffn_mfma_up(value_type, x.data_ptr(), planes["up"].data_ptr(), planes["up_binades"].data_ptr(),
+                                        tensors["b_up"].data_ptr(), act, work, runtime.d_model, runtime.d_ff, n, stream),
+                       "mfma up")
             events[1].record()
-            _lib.check(lib.hffn_mfma_up(value_type, x.data_ptr(), binades, planes["up"].data_ptr(),
-                                        planes["up_binades"].data_ptr(), tensors["b_up"].data_ptr(), act, act_binades,
-                                        runtime.d_model, runtime.d_ff, n, stream), "mfma up")
+            _lib.check(lib.hffn_mfma_down(value_type, act, planes["down"].data_ptr(), planes["down_binades"].data_ptr(),
+                                          tensors["b_down"].data_ptr(), y, work, runtime.d_model, runtime.d_ff, n, stream),
+                       "mfma down")
             events[2].record()
-            _lib.check(lib.hffn_mfma_down(value_type, act, act_binades, planes["down"].data_ptr(),
-                                          planes["down_binades"].data_ptr(), tensors["b_down"].data_ptr(), y,
-                                          runtime.d_model, runtime.d_ff, n, stream), "mfma down")
-            events[3].record()
             torch.cuda.synchronize()
             for i, name in enumerate(names):
                 totals[name] += events[i].elapsed_time(events[i + 1]) * 1e-3

@@ -34,8 +34,7 @@ SIGNATURES = {
     "hffn_dense_planes_bytes": [_U32, _U32, ctypes.POINTER(_U64)],
     "hffn_densify": [_I, _P, _P, _P, _U32, _U32, _P, _P, _P],
     "hffn_mfma_workspace": [_U32, _U32, _U32, ctypes.POINTER(_U64)],
-    "hffn_row_binades": [_P, _U32, _U32, _P, _P],
-    "hffn_mfma_up": [_I, _P, _P, _P, _P, _P, _P, _P, _U32, _U32, _U32, _P],
+    "hffn_mfma_up": [_I, _P, _P, _P, _P, _P, _P, _U32, _U32, _U32, _P],
     "hffn_mfma_down": [_I, _P, _P, _P, _P, _P, _P, _U32, _U32, _U32, _P],
     "hffn_forward_mfma": [_I] + [_P] * 10 + [_U32] * 3 + [_P],
 }

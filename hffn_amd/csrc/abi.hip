@@ -151,7 +151,7 @@ int hffn_output_major(int value_type, const int32_t* down_offsets, const int16_t
 }
 
 int hffn_mfma_supported(uint32_t d_model, uint32_t d_ff) {
-    return d_model % 64 == 0 && d_ff % 64 == 0 && d_model <= HFFN_MAX_WIDTH && d_ff <= HFFN_MAX_WIDTH ? 1 : 0;
+    return d_model <= HFFN_MAX_WIDTH && d_ff <= HFFN_MAX_WIDTH && hffn::mfma_shape_supported(d_model, d_ff) ? 1 : 0;
 }
 
 int hffn_dense_planes_bytes(uint32_t rows, uint32_t k, uint64_t* bytes) {
@@ -161,58 +161,53 @@ int hffn_dense_planes_bytes(uint32_t rows, uint32_t k, uint64_t* bytes) {
 }
 
 int hffn_densify(int value_type, const int32_t* offsets, const int16_t* idx, const void* val, uint32_t rows, uint32_t k,
-                 void* planes, int32_t* exps, void* stream) {
+                 void* planes, int32_t* binades, void* stream) {
     if (!valid_value_type(value_type)) return fail(HFFN_ERROR_ARGUMENT, "unknown value type %d", value_type);
     if (rows == 0 || rows > HFFN_MAX_WIDTH || k == 0 || k % 32 != 0 || k > HFFN_MAX_WIDTH)
         return fail(HFFN_ERROR_ARGUMENT, "densify: rows=%u k=%u (k must be a positive multiple of 32)", rows, k);
-    if (!offsets || !idx || !val || !planes || !exps) return fail(HFFN_ERROR_ARGUMENT, "densify: null pointer");
-    return launched(hffn::launch_densify(value_type, offsets, idx, val, rows, k, planes, exps, static_cast<hipStream_t>(stream)),
+    if (!offsets || !idx || !val || !planes || !binades) return fail(HFFN_ERROR_ARGUMENT, "densify: null pointer");
+    return launched(hffn::launch_densify(value_type, offsets, idx, val, rows, k, planes, binades, static_cast<hipStream_t>(stream)),
                     "densify");
 }
 
+namespace {
+int check_mfma(int value_type, uint32_t d_model, uint32_t d_ff, uint32_t n) {
+    if (int status = check_shape(d_model, d_ff, n, (n + 3) / 4 * 4)) return status;
+    if (!valid_value_type(value_type)) return fail(HFFN_ERROR_ARGUMENT, "unknown value type %d", value_type);
+    if (!hffn_mfma_supported(d_model, d_ff))
+        return fail(HFFN_ERROR_ARGUMENT, "mfma path: d_model=%u and d_ff=%u must be multiples of 128", d_model, d_ff);
+    return HFFN_OK;
+}
+}  // namespace
+
 int hffn_mfma_workspace(uint32_t n, uint32_t d_model, uint32_t d_ff, uint64_t* bytes) {
     if (!bytes) return fail(HFFN_ERROR_ARGUMENT, "mfma_workspace: null result");
-    if (!hffn_mfma_supported(d_model, d_ff)) return fail(HFFN_ERROR_ARGUMENT, "mfma path: d_model=%u, d_ff=%u must be multiples of 64", d_model, d_ff);
-    *bytes = static_cast<uint64_t>(n) * (1 + d_ff / hffn::mfma_block_cols(d_ff)) * sizeof(int32_t);
+    if (int status = check_mfma(HFFN_VALUE_F32, d_model, d_ff, n)) return status;
+    *bytes = hffn::mfma_workspace_bytes(n, d_model, d_ff);
     return HFFN_OK;
 }
 
-int hffn_row_binades(const float* x, uint32_t rows, uint32_t cols, int32_t* binades, void* stream) {
-    if (!x || !binades) return fail(HFFN_ERROR_ARGUMENT, "row_binades: null pointer");
-    if (rows == 0 || cols == 0) return HFFN_OK;
-    return launched(hffn::launch_row_binades(x, rows, cols, binades, static_cast<hipStream_t>(stream)), "row_binades");
-}
-
-int hffn_mfma_up(int value_type, const float* x, const int32_t* x_binades, const void* up_planes, const int32_t* up_binades,
-                 const float* b_up, float* act, int32_t* act_binades, uint32_t d_model, uint32_t d_ff, uint32_t n, void* stream) {
-    if (int status = check_shape(d_model, d_ff, n, (n + 3) / 4 * 4)) return status;
-    if (!valid_value_type(value_type)) return fail(HFFN_ERROR_ARGUMENT, "unknown value type %d", value_type);
-    if (!hffn_mfma_supported(d_model, d_ff)) return fail(HFFN_ERROR_ARGUMENT, "mfma path: d_model=%u, d_ff=%u must be multiples of 64", d_model, d_ff);
-    if (!x || !x_binades || !up_planes || !up_binades || !b_up || !act || !act_binades) return fail(HFFN_ERROR_ARGUMENT, "mfma_up: null pointer");
-    return launched(hffn::launch_mfma_up(value_type, x, x_binades, up_planes, up_binades, b_up, act, act_binades, n, d_model, d_ff,
+int hffn_mfma_up(int value_type, const float* x, const void* up_planes, const int32_t* up_binades, const float* b_up,
+                 float* act, void* workspace, uint32_t d_model, uint32_t d_ff, uint32_t n, void* stream) {
+    if (int status = check_mfma(value_type, d_model, d_ff, n)) return status;
+    if (!x || !up_planes || !up_binades || !b_up || !act || !workspace) return fail(HFFN_ERROR_ARGUMENT, "mfma_up: null pointer");
+    return launched(hffn::launch_mfma_up(value_type, x, up_planes, up_binades, b_up, act, workspace, n, d_model, d_ff,
                                          static_cast<hipStream_t>(stream)), "mfma up");
 }
 
-int hffn_mfma_down(int value_type, const float* act, const int32_t* act_binades, const void* down_planes, const int32_t* down_binades,
-                   const float* b_down, float* y, uint32_t d_model, uint32_t d_ff, uint32_t n, void* stream) {
-    if (int status = check_shape(d_model, d_ff, n, (n + 3) / 4 * 4)) return status;
-    if (!valid_value_type(value_type)) return fail(HFFN_ERROR_ARGUMENT, "unknown value type %d", value_type);
-    if (!hffn_mfma_supported(d_model, d_ff)) return fail(HFFN_ERROR_ARGUMENT, "mfma path: d_model=%u, d_ff=%u must be multiples of 64", d_model, d_ff);
-    if (!act || !act_binades || !down_planes || !down_binades || !b_down || !y) return fail(HFFN_ERROR_ARGUMENT, "mfma_down: null pointer");
-    return launched(hffn::launch_mfma_down(value_type, act, act_binades, down_planes, down_binades, b_down, y, n, d_model, d_ff,
+int hffn_mfma_down(int value_type, const float* act, const void* down_planes, const int32_t* down_binades, const float* b_down,
+                   float* y, void* workspace, uint32_t d_model, uint32_t d_ff, uint32_t n, void* stream) {
+    if (int status = check_mfma(value_type, d_model, d_ff, n)) return status;
+    if (!act || !down_planes || !down_binades || !b_down || !y || !workspace) return fail(HFFN_ERROR_ARGUMENT, "mfma_down: null pointer");
+    return launched(hffn::launch_mfma_down(value_type, act, down_planes, down_binades, b_down, y, workspace, n, d_model, d_ff,
                                            static_cast<hipStream_t>(stream)), "mfma down");
 }
 
 int hffn_forward_mfma(int value_type, const float* x, const void* up_planes, const int32_t* up_binades, const float* b_up,
-                      const void* down_planes, const int32_t* down_binades, const float* b_down, float* act,
-                      int32_t* binades, float* y, uint32_t d_model, uint32_t d_ff, uint32_t n, void* stream) {
-    if (int status = check_shape(d_model, d_ff, n, (n + 3) / 4 * 4)) return status;
-    if (!binades) return fail(HFFN_ERROR_ARGUMENT, "forward_mfma: null binade workspace");
-    int32_t* x_binades = binades;
-    int32_t* act_binades = binades + n;
-    if (int status = hffn_row_binades(x, n, d_model, x_binades, stream)) return status;
-    if (int status = hffn_mfma_up(value_type, x, x_binades, up_planes, up_binades, b_up, act, act_binades, d_model, d_ff, n, stream)) return status;
-    return hffn_mfma_down(value_type, act, act_binades, down_planes, down_binades, b_down, y, d_model, d_ff, n, stream);
+                      const void* down_planes, const int32_t* down_binades, const float* b_down, float* act, void* workspace,
+                      float* y, uint32_t d_model, uint32_t d_ff, uint32_t n, void* stream) {
+    if (int status = hffn_mfma_up(value_type, x, up_planes, up_binades, b_up, act, workspace, d_model, d_ff, n, stream)) return status;
+    return hffn_mfma_down(value_type, act, down_planes, down_binades, b_down, y, workspace, d_model, d_ff, n, stream);
 }
 
 }  // extern "C"

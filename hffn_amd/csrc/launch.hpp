@@ -10,6 +10,8 @@ namespace hffn {
 
 enum ValueType : int { kF32 = 0, kBF16 = 1 };
 
+constexpr uint32_t kMaxTokens = 1u << 18;  // largest n of any entry point
+
 // Tokens per pass of the lane-per-slot ("edges") kernels: 1, 2, 4, or 8 for n > 4.
 constexpr uint32_t kEdgesMaxTokens = 8;
 inline uint32_t edges_tokens(uint32_t n) { return n <= 1 ? 1 : n <= 2 ? 2 : n <= 4 ? 4 : 8; }
@@ -45,16 +47,16 @@ hipError_t launch_output_major(int vt, const int32_t* down_offsets, const int16_
                                void* out_val, int32_t* counts, hipStream_t stream);
 
 // Tile-densified MFMA path (mfma.hip). Planes: fp16 hi/lo of a dense [rows, k] matrix, tile-major.
+// The workspace holds the token binades, the activation block binades, the split-K counters (zero between calls)
+// and the split-K partial sums; it must be zero-filled before its first use.
 size_t dense_plane_halves(uint32_t rows, uint32_t k);
-uint32_t mfma_block_cols(uint32_t ncol);
-uint32_t mfma_block_rows(uint32_t m, uint32_t ncol);
-hipError_t launch_row_binades(const float* x, uint32_t rows, uint32_t cols, int32_t* e, hipStream_t stream);
+bool mfma_shape_supported(uint32_t d, uint32_t h);
+size_t mfma_workspace_bytes(uint32_t n, uint32_t d, uint32_t h);
 hipError_t launch_densify(int vt, const int32_t* off, const int16_t* idx, const void* val, uint32_t rows, uint32_t k,
                           void* planes, int32_t* exps, hipStream_t stream);
-hipError_t launch_mfma_up(int vt, const float* x, const int32_t* x_exp, const void* planes, const int32_t* w_exp,
-                          const float* b_up, float* act, int32_t* act_exp, uint32_t n, uint32_t d, uint32_t h,
-                          hipStream_t stream);
-hipError_t launch_mfma_down(int vt, const float* act, const int32_t* act_exp, const void* planes, const int32_t* v_exp,
-                            const float* b_down, float* y, uint32_t n, uint32_t d, uint32_t h, hipStream_t stream);
+hipError_t launch_mfma_up(int vt, const float* x, const void* planes, const int32_t* w_exp, const float* b_up, float* act,
+                          void* workspace, uint32_t n, uint32_t d, uint32_t h, hipStream_t stream);
+hipError_t launch_mfma_down(int vt, const float* act, const void* planes, const int32_t* v_exp, const float* b_down, float* y,
+                            void* workspace, uint32_t n, uint32_t d, uint32_t h, hipStream_t stream);
 
 }  // namespace hffn

@@ -8,14 +8,23 @@
 // by the MFMA units (the lo*lo term, ~2^-22 relative, is dropped; bf16 weights are exact in the hi plane and take
 // the first two terms). The powers of two are undone exactly in the epilogue.
 //
-// Plane layout (tile-major, for 128-byte transactions): for k-tile kt (32 wide) and row n, 32 hi halves then 32 lo
-// halves, i.e. planes[((kt * rows + n) * 2 + part) * 32 + k % 32]; a block's B tile of BN rows is one contiguous
-// run of BN * 128 bytes.
+// Plane layout (K-chunk-major): k is cut into 32-wide k-tiles and each k-tile into four 16-byte chunks of 8 halves;
+// for k-tile kt, part p (0 hi, 1 lo) and chunk c, the chunks of all rows follow one another:
+//   planes[((((kt * 2 + p) * 4 + c) * rows + n) * 8 + k % 8]   with c = (k % 32) / 8.
+// A block's B tile of BN rows is 8 runs of BN * 16 contiguous bytes, and LDS keeps the same order, so the MFMA
+// operand reads (32 lanes on 32 consecutive rows of one chunk) and the staging writes touch consecutive 16-byte
+// blocks: no LDS bank conflicts, no padding.
 //
-// Kernels: row_binade (per-row power of two of the fp32 input), densify (load time), gemm_split<Up|Down>.
+// GEMM blocks: 4 waves in 2 x 2, each wave a (32 MI) x (32 NI) tile of 32x32 MFMA accumulators; the k loop stages
+// 32-wide k-tiles through double-buffered LDS (one barrier per k-tile, the next tile's global loads in flight during
+// the current tile's MFMAs). The grid is one-dimensional and remapped so that each of the 8 XCDs works on one compact
+// group of output tiles (its L2 then holds the A rows and B columns those tiles share). A down projection with very
+// few output tiles splits K over 2 blocks per tile; the block that finishes a tile last (an integer counter per tile)
+// adds the partials in split order, so the result does not depend on which block ends first.
+//
 // The up epilogue applies bias and exact GELU, writes the activations token-major [N, d_ff] in fp32, and, per token
-// row and block of BN neurons, the binade of the largest activation; the down kernel takes, per token, the largest
-// of those binades as its row scale. No atomics: every output is written by one lane.
+// row and block of BN neurons, the binade of the largest activation; the down kernel takes, per token, the largest of
+// those binades as its row scale.
 #include "common.hpp"
 #include "launch.hpp"
 
@@ -27,7 +36,9 @@ typedef float floatx16 __attribute__((ext_vector_type(16)));
 
 constexpr int kThreads = 256;
 constexpr int kBK = 32;          // k per staged step, one plane k-tile
-constexpr int kRow = kBK + 8;    // halves per LDS row: 80-byte stride keeps 16-byte lane reads conflict-free
+constexpr int kRuns = 8;         // (part, chunk) runs of a k-tile
+constexpr uint32_t kXcds = 8;    // MI355X: 8 XCDs, workgroups dispatched round-robin over them
+constexpr uint32_t kGroupM = 4;  // output-tile rows per group of the tile order
 
 // floor(log2(m)) of a non-negative float given by its bits; 0 for zero (any scale is exact for zeros).
 __device__ __forceinline__ int binade_of_bits(uint32_t bits) {
@@ -72,12 +83,10 @@ __global__ __launch_bounds__(kThreads) void densify_kernel(const int32_t* __rest
 #pragma unroll
     for (int s = 32; s >= 1; s >>= 1) m = max(m, static_cast<uint32_t>(__shfl_xor(static_cast<int>(m), s, kWave)));
     if (threadIdx.x % kWave == 0) part[threadIdx.x / kWave] = m;
-    // zero this row in every k-tile (64 halves per tile: hi then lo)
-    const uint32_t tiles = k / kBK;
-    for (uint32_t i = threadIdx.x; i < tiles * 64; i += kThreads) {
-        const uint32_t kt = i / 64, j = i % 64;
-        planes[(static_cast<size_t>(kt) * rows + n) * 64 + j] = static_cast<_Float16>(0.0f);
-    }
+    // zero this row's 16-byte chunk in every (k-tile, part, chunk) run
+    const uint32_t runs = k / kBK * kRuns;
+    for (uint32_t i = threadIdx.x; i < runs; i += kThreads)
+        *reinterpret_cast<uint4*>(planes + (static_cast<size_t>(i) * rows + n) * 8) = make_uint4(0, 0, 0, 0);
     __syncthreads();
     uint32_t mx = 0;
 #pragma unroll
@@ -87,9 +96,9 @@ __global__ __launch_bounds__(kThreads) void densify_kernel(const int32_t* __rest
         const uint32_t c = static_cast<uint16_t>(idx[s]);
         _Float16 hi, lo;
         split(ldexpf(widen(val[s]), -e), hi, lo);
-        _Float16* row = planes + (static_cast<size_t>(c / kBK) * rows + n) * 64 + c % kBK;
-        row[0] = hi;
-        row[32] = lo;
+        const size_t run = static_cast<size_t>(c / kBK) * kRuns + (c % kBK) / 8;  // part 0
+        planes[(run * rows + n) * 8 + c % 8] = hi;
+        planes[((run + 4) * rows + n) * 8 + c % 8] = lo;
     }
     if (threadIdx.x == 0) exps[n] = e;
 }
@@ -97,7 +106,80 @@ __global__ __launch_bounds__(kThreads) void densify_kernel(const int32_t* __rest
 // ------------------------------------------------------------------------------------------------ GEMM
 enum class Epi { Up, Down };
 
-template <Epi EPI, int BM, int BN, bool LO_B>
+struct Tile {
+    uint32_t m, n, split;
+};
+
+// Workgroup id -> (row tile, column tile, k split). The first 8 * floor(T / 8) ids are dealt so that XCD j (ids
+// j, j + 8, ...) takes the j-th contiguous run of the tile order; the tile order walks groups of kGroupM tile rows
+// column by column, so a run is a compact block of tiles.
+__device__ __forceinline__ Tile tile_of(uint32_t id, uint32_t tiles_m, uint32_t tiles_n, uint32_t splits) {
+    const uint32_t total = tiles_m * tiles_n * splits;
+    const uint32_t per = total / kXcds;
+    uint32_t t = id < kXcds * per ? (id % kXcds) * per + id / kXcds : id;
+    const uint32_t per_split = tiles_m * tiles_n;
+    Tile tile;
+    tile.split = t / per_split;
+    t %= per_split;
+    const uint32_t group = t / (kGroupM * tiles_n);
+    const uint32_t first = group * kGroupM;
+    const uint32_t rows = min(tiles_m - first, kGroupM);
+    const uint32_t within = t % (kGroupM * tiles_n);
+    tile.m = first + within % rows;
+    tile.n = within / rows;
+    return tile;
+}
+
+template <int ARPT, int BRPT>
+struct StageRegs {
+    float4 a[ARPT][2];
+    uint4 b[BRPT];
+};
+
+// Global loads of k-tile kt: 8 floats of A from rows row0 + 16 j (zeros past M), BRPT 16-byte chunks of B.
+template <int ARPT, int BRPT>
+__device__ __forceinline__ void load_stage(StageRegs<ARPT, BRPT>& r, const float* a_src, uint32_t row0, uint32_t M, uint32_t K,
+                                           const _Float16* b_src, size_t b_stride, uint32_t kt) {
+#pragma unroll
+    for (int j = 0; j < ARPT; ++j) {
+        if (row0 + 16 * j < M) {
+            const float* p = a_src + static_cast<size_t>(16 * j) * K + kt * kBK;
+            r.a[j][0] = *reinterpret_cast<const float4*>(p);
+            r.a[j][1] = *reinterpret_cast<const float4*>(p + 4);
+        } else {
+            r.a[j][0] = make_float4(0.f, 0.f, 0.f, 0.f);
+            r.a[j][1] = make_float4(0.f, 0.f, 0.f, 0.f);
+        }
+    }
+#pragma unroll
+    for (int j = 0; j < BRPT; ++j) r.b[j] = *reinterpret_cast<const uint4*>(b_src + kt * b_stride + 32 * j * 8);
+}
+
+// LDS stores of a staged k-tile: A split into hi/lo halves with its row's power of two, B copied.
+template <int BM, int BN, int ARPT, int BRPT>
+__device__ __forceinline__ void store_stage(const StageRegs<ARPT, BRPT>& r, _Float16* s_a, _Float16* s_b, uint32_t a_chunk,
+                                            uint32_t a_row0, const int32_t* row_e, uint32_t b_run, uint32_t b_row) {
+#pragma unroll
+    for (int j = 0; j < ARPT; ++j) {
+        const uint32_t row = a_row0 + 16 * j;
+        const float scale = ldexpf(1.0f, -row_e[row]);
+        const float v[8] = {r.a[j][0].x, r.a[j][0].y, r.a[j][0].z, r.a[j][0].w, r.a[j][1].x, r.a[j][1].y, r.a[j][1].z, r.a[j][1].w};
+        half8 h, l;
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+            _Float16 hh, ll;
+            split(v[e] * scale, hh, ll);
+            h[e] = hh;
+            l[e] = ll;
+        }
+        *reinterpret_cast<half8*>(s_a + (a_chunk * BM + row) * 8) = h;
+        *reinterpret_cast<half8*>(s_a + ((4 + a_chunk) * BM + row) * 8) = l;
+    }
+#pragma unroll
+    for (int j = 0; j < BRPT; ++j) *reinterpret_cast<uint4*>(s_b + (b_run * BN + b_row + 32 * j) * 8) = r.b[j];
+}
+
+template <Epi EPI, int MI, int NI, bool LO_B, int SPLITS>
 __global__ __launch_bounds__(kThreads) void gemm_split_kernel(
     const float* __restrict__ a,          // [M, K] fp32 row-major
     const int32_t* __restrict__ a_exp,    // Up: [M] row binades; Down: [M, a_blocks] block binades (max taken here)
@@ -107,21 +189,27 @@ __global__ __launch_bounds__(kThreads) void gemm_split_kernel(
     const float* __restrict__ bias,       // [Ncol]
     float* __restrict__ out,              // [M, Ncol] fp32 row-major
     int32_t* __restrict__ out_exp,        // Up: [M, Ncol / BN] activation block binades
+    float* __restrict__ partials,         // SPLITS > 1: [SPLITS, M, Ncol] scaled partial sums
+    int32_t* __restrict__ counters,       // SPLITS > 1: [tiles], zero between calls
     uint32_t M, uint32_t Ncol, uint32_t K) {
-    static_assert(BM == 64 || BM == 128, "BM");
-    static_assert(BN == 64 || BN == 128, "BN");
-    constexpr int MI = BM / 64, NI = BN / 64;        // 32x32 MFMA tiles per wave (2x2 waves)
-    constexpr int TPR = kThreads / BM;               // staging threads per A row
-    constexpr int FPT = kBK / TPR;                   // floats per staging thread (16 or 8)
-    constexpr int BBYTES = BN * 128 / kThreads;      // bytes of B per staging thread (64 or 32)
+    constexpr int BM = 64 * MI, BN = 64 * NI;
+    constexpr int ARPT = BM / 64;                    // A rows per staging thread (16 rows x 4 chunks per wave pass)
+    constexpr int BRPT = BN / 32;                    // B rows per staging thread (32 rows x 8 runs per block pass)
 
-    __shared__ __attribute__((aligned(16))) _Float16 a_hi[BM * kRow], a_lo[BM * kRow], b_hi[BN * kRow], b_lo[BN * kRow];
+    // [buffer][part][chunk][row][8 halves]
+    __shared__ __attribute__((aligned(16))) _Float16 s_a[2][kRuns * BM * 8];
+    __shared__ __attribute__((aligned(16))) _Float16 s_b[2][kRuns * BN * 8];
     __shared__ int32_t row_e[BM];
     __shared__ uint32_t row_max[2][BM];
+    __shared__ int32_t last;
 
     const uint32_t tid = threadIdx.x, lane = tid % kWave, wave = tid / kWave;
     const uint32_t wm = wave / 2, wn = wave % 2;
-    const uint32_t m0 = blockIdx.y * BM, n0 = blockIdx.x * BN;
+    const uint32_t tiles_m = (M + BM - 1) / BM, tiles_n = Ncol / BN;
+    const Tile tile = tile_of(blockIdx.x, tiles_m, tiles_n, SPLITS);
+    const uint32_t m0 = tile.m * BM, n0 = tile.n * BN;
+    const uint32_t ktiles = K / kBK;
+    const uint32_t k_begin = tile.split * ktiles / SPLITS, k_end = (tile.split + 1) * ktiles / SPLITS;
 
     if (tid < BM) {
         const uint32_t row = m0 + tid;
@@ -138,55 +226,14 @@ __global__ __launch_bounds__(kThreads) void gemm_split_kernel(
     }
     __syncthreads();
 
-    // staging assignments
-    const uint32_t a_row = tid / TPR, a_col = (tid % TPR) * FPT;
-    const bool a_valid = m0 + a_row < M;
-    const float* a_src = a + static_cast<size_t>(m0 + (a_valid ? a_row : 0)) * K + a_col;
-    const float a_scale = ldexpf(1.0f, -row_e[a_row]);
-    const char* b_base = reinterpret_cast<const char*>(planes) + static_cast<size_t>(n0) * 128 + tid * BBYTES;
-    const size_t b_stride = static_cast<size_t>(Ncol) * 128;  // bytes per k-tile
-    // B staging target: BN=128 -> row tid/2, part tid%2, 32 halves; BN=64 -> row tid/4, part (tid/2)%2, 16 halves at (tid%2)*16
-    const uint32_t b_row = BN == 128 ? tid / 2 : tid / 4;
-    const uint32_t b_part = BN == 128 ? tid % 2 : (tid / 2) % 2;
-    const uint32_t b_col = BN == 128 ? 0 : (tid % 2) * 16;
-    _Float16* b_dst = (b_part == 0 ? b_hi : b_lo) + b_row * kRow + b_col;
-
-    float4 a_reg[FPT / 4];
-    uint4 b_reg[BBYTES / 16];
-
-    auto load = [&](uint32_t kt) {
-        if (a_valid) {
-#pragma unroll
-            for (int i = 0; i < FPT / 4; ++i) a_reg[i] = *reinterpret_cast<const float4*>(a_src + kt * kBK + 4 * i);
-        } else {
-#pragma unroll
-            for (int i = 0; i < FPT / 4; ++i) a_reg[i] = make_float4(0.f, 0.f, 0.f, 0.f);
-        }
-        const uint4* src = reinterpret_cast<const uint4*>(b_base + kt * b_stride);
-#pragma unroll
-        for (int i = 0; i < BBYTES / 16; ++i) b_reg[i] = src[i];
-    };
-    auto stage = [&]() {
-        _Float16* hi_dst = a_hi + a_row * kRow + a_col;
-        _Float16* lo_dst = a_lo + a_row * kRow + a_col;
-#pragma unroll
-        for (int i = 0; i < FPT / 8; ++i) {
-            half8 h, l;
-            const float v[8] = {a_reg[2 * i].x, a_reg[2 * i].y, a_reg[2 * i].z, a_reg[2 * i].w,
-                                a_reg[2 * i + 1].x, a_reg[2 * i + 1].y, a_reg[2 * i + 1].z, a_reg[2 * i + 1].w};
-#pragma unroll
-            for (int j = 0; j < 8; ++j) {
-                _Float16 hh, ll;
-                split(v[j] * a_scale, hh, ll);
-                h[j] = hh;
-                l[j] = ll;
-            }
-            *reinterpret_cast<half8*>(hi_dst + 8 * i) = h;
-            *reinterpret_cast<half8*>(lo_dst + 8 * i) = l;
-        }
-#pragma unroll
-        for (int i = 0; i < BBYTES / 16; ++i) *reinterpret_cast<uint4*>(b_dst + 8 * i) = b_reg[i];
-    };
+    // staging assignments. A: lane l of wave w converts chunk l / 16 (8 floats) of rows w * 16 * ARPT + l % 16 + 16 j;
+    // B: thread t copies run t / 32 of rows t % 32 + 32 j.
+    const uint32_t a_chunk = lane / 16, a_row0 = wave * 16 * ARPT + lane % 16;
+    const float* a_src = a + static_cast<size_t>(m0 + a_row0) * K + a_chunk * 8;
+    const uint32_t b_run = tid / 32, b_row = tid % 32;
+    const _Float16* b_src = planes + (static_cast<size_t>(b_run) * Ncol + n0 + b_row) * 8;
+    const size_t b_stride = static_cast<size_t>(kRuns) * Ncol * 8;  // halves per k-tile
+    StageRegs<ARPT, BRPT> regs;
 
     floatx16 acc[MI][NI];
 #pragma unroll
@@ -196,27 +243,29 @@ __global__ __launch_bounds__(kThreads) void gemm_split_kernel(
 #pragma unroll
             for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.0f;
 
-    const uint32_t ktiles = K / kBK;
-    load(0);
-    for (uint32_t kt = 0; kt < ktiles; ++kt) {
-        stage();
+    if (k_begin < k_end) {
+        load_stage<ARPT, BRPT>(regs, a_src, m0 + a_row0, M, K, b_src, b_stride, k_begin);
+        store_stage<BM, BN, ARPT, BRPT>(regs, s_a[0], s_b[0], a_chunk, a_row0, row_e, b_run, b_row);
+        if (k_begin + 1 < k_end) load_stage<ARPT, BRPT>(regs, a_src, m0 + a_row0, M, K, b_src, b_stride, k_begin + 1);
         __syncthreads();
-        if (kt + 1 < ktiles) load(kt + 1);
+    }
+    for (uint32_t kt = k_begin; kt < k_end; ++kt) {
+        const int buf = (kt - k_begin) & 1;
 #pragma unroll
         for (int kk = 0; kk < 2; ++kk) {
-            const uint32_t koff = kk * 16 + 8 * (lane / 32);
+            const uint32_t chunk = kk * 2 + lane / 32;
             half8 ah[MI], al[MI], bh[NI], bl[NI];
 #pragma unroll
             for (int i = 0; i < MI; ++i) {
                 const uint32_t r = wm * (BM / 2) + i * 32 + lane % 32;
-                ah[i] = *reinterpret_cast<const half8*>(a_hi + r * kRow + koff);
-                al[i] = *reinterpret_cast<const half8*>(a_lo + r * kRow + koff);
+                ah[i] = *reinterpret_cast<const half8*>(s_a[buf] + (chunk * BM + r) * 8);
+                al[i] = *reinterpret_cast<const half8*>(s_a[buf] + ((4 + chunk) * BM + r) * 8);
             }
 #pragma unroll
             for (int j = 0; j < NI; ++j) {
                 const uint32_t r = wn * (BN / 2) + j * 32 + lane % 32;
-                bh[j] = *reinterpret_cast<const half8*>(b_hi + r * kRow + koff);
-                if constexpr (LO_B) bl[j] = *reinterpret_cast<const half8*>(b_lo + r * kRow + koff);
+                bh[j] = *reinterpret_cast<const half8*>(s_b[buf] + (chunk * BN + r) * 8);
+                if constexpr (LO_B) bl[j] = *reinterpret_cast<const half8*>(s_b[buf] + ((4 + chunk) * BN + r) * 8);
             }
 #pragma unroll
             for (int i = 0; i < MI; ++i)
@@ -227,34 +276,35 @@ __global__ __launch_bounds__(kThreads) void gemm_split_kernel(
                     acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(al[i], bh[j], acc[i][j], 0, 0, 0);
                 }
         }
+        if (kt + 1 < k_end) {
+            store_stage<BM, BN, ARPT, BRPT>(regs, s_a[buf ^ 1], s_b[buf ^ 1], a_chunk, a_row0, row_e, b_run, b_row);
+            if (kt + 2 < k_end) load_stage<ARPT, BRPT>(regs, a_src, m0 + a_row0, M, K, b_src, b_stride, kt + 2);
+        }
         __syncthreads();
     }
 
     // epilogue: accumulator r of lane l of tile (i, j) holds row 8 (r / 4) + 4 (l / 32) + r % 4, column l % 32
-    uint32_t lane_max[MI][16];
-#pragma unroll
-    for (int i = 0; i < MI; ++i)
-#pragma unroll
-        for (int r = 0; r < 16; ++r) lane_max[i][r] = 0;
-#pragma unroll
-    for (int j = 0; j < NI; ++j) {
-        const uint32_t col = n0 + wn * (BN / 2) + j * 32 + lane % 32;
-        const int ce = b_exp[col];
-        const float cb = bias[col];
+    if constexpr (EPI == Epi::Up) {
+        uint32_t lane_max[MI][16];
 #pragma unroll
         for (int i = 0; i < MI; ++i)
 #pragma unroll
-            for (int r = 0; r < 16; ++r) {
-                const uint32_t m = wm * (BM / 2) + i * 32 + 8 * (r / 4) + 4 * (lane / 32) + r % 4;
-                float v = ldexpf(acc[i][j][r], row_e[m] + ce) + cb;
-                if constexpr (EPI == Epi::Up) {
-                    v = gelu(v);
+            for (int r = 0; r < 16; ++r) lane_max[i][r] = 0;
+#pragma unroll
+        for (int j = 0; j < NI; ++j) {
+            const uint32_t col = n0 + wn * (BN / 2) + j * 32 + lane % 32;
+            const int ce = b_exp[col];
+            const float cb = bias[col];
+#pragma unroll
+            for (int i = 0; i < MI; ++i)
+#pragma unroll
+                for (int r = 0; r < 16; ++r) {
+                    const uint32_t m = wm * (BM / 2) + i * 32 + 8 * (r / 4) + 4 * (lane / 32) + r % 4;
+                    const float v = gelu(ldexpf(acc[i][j][r], row_e[m] + ce) + cb);
                     lane_max[i][r] = max(lane_max[i][r], abs_bits(v));
+                    if (m0 + m < M) out[static_cast<size_t>(m0 + m) * Ncol + col] = v;
                 }
-                if (m0 + m < M) out[static_cast<size_t>(m0 + m) * Ncol + col] = v;
-            }
-    }
-    if constexpr (EPI == Epi::Up) {
+        }
 #pragma unroll
         for (int i = 0; i < MI; ++i)
 #pragma unroll
@@ -266,44 +316,158 @@ __global__ __launch_bounds__(kThreads) void gemm_split_kernel(
             }
         __syncthreads();
         if (tid < BM && m0 + tid < M)
-            out_exp[static_cast<size_t>(m0 + tid) * (Ncol / BN) + blockIdx.x] = binade_of_bits(max(row_max[0][tid], row_max[1][tid]));
+            out_exp[static_cast<size_t>(m0 + tid) * tiles_n + tile.n] = binade_of_bits(max(row_max[0][tid], row_max[1][tid]));
+    } else if constexpr (SPLITS == 1) {
+#pragma unroll
+        for (int j = 0; j < NI; ++j) {
+            const uint32_t col = n0 + wn * (BN / 2) + j * 32 + lane % 32;
+            const int ce = b_exp[col];
+            const float cb = bias[col];
+#pragma unroll
+            for (int i = 0; i < MI; ++i)
+#pragma unroll
+                for (int r = 0; r < 16; ++r) {
+                    const uint32_t m = wm * (BM / 2) + i * 32 + 8 * (r / 4) + 4 * (lane / 32) + r % 4;
+                    if (m0 + m < M) out[static_cast<size_t>(m0 + m) * Ncol + col] = ldexpf(acc[i][j][r], row_e[m] + ce) + cb;
+                }
+        }
+    } else {
+        // every split writes its scaled partial, then the block that completes the tile adds them in split order
+        const size_t plane_size = static_cast<size_t>(M) * Ncol;
+#pragma unroll
+        for (int j = 0; j < NI; ++j) {
+            const uint32_t col = n0 + wn * (BN / 2) + j * 32 + lane % 32;
+            const int ce = b_exp[col];
+#pragma unroll
+            for (int i = 0; i < MI; ++i)
+#pragma unroll
+                for (int r = 0; r < 16; ++r) {
+                    const uint32_t m = wm * (BM / 2) + i * 32 + 8 * (r / 4) + 4 * (lane / 32) + r % 4;
+                    acc[i][j][r] = ldexpf(acc[i][j][r], row_e[m] + ce);
+                    if (m0 + m < M) partials[tile.split * plane_size + static_cast<size_t>(m0 + m) * Ncol + col] = acc[i][j][r];
+                }
+        }
+        __threadfence();
+        __syncthreads();
+        if (tid == 0) {
+            const uint32_t counter = tile.m * tiles_n + tile.n;
+            const int32_t arrived = atomicAdd(&counters[counter], 1);
+            last = arrived == SPLITS - 1;
+            if (last) counters[counter] = 0;  // every split of this tile has arrived: ready for the next call
+        }
+        __syncthreads();
+        if (!last) return;
+        __threadfence();
+#pragma unroll
+        for (int j = 0; j < NI; ++j) {
+            const uint32_t col = n0 + wn * (BN / 2) + j * 32 + lane % 32;
+            const float cb = bias[col];
+#pragma unroll
+            for (int i = 0; i < MI; ++i)
+#pragma unroll
+                for (int r = 0; r < 16; ++r) {
+                    const uint32_t m = wm * (BM / 2) + i * 32 + 8 * (r / 4) + 4 * (lane / 32) + r % 4;
+                    if (m0 + m >= M) continue;
+                    const size_t at = static_cast<size_t>(m0 + m) * Ncol + col;
+                    float total = 0.0f;
+#pragma unroll
+                    for (int s = 0; s < SPLITS; ++s) {
+                        const float p = s == static_cast<int>(tile.split)
+                                            ? acc[i][j][r]
+                                            : __hip_atomic_load(partials + s * plane_size + at, __ATOMIC_RELAXED,
+                                                                __HIP_MEMORY_SCOPE_AGENT);
+                        total = s == 0 ? p : total + p;
+                    }
+                    out[at] = total + cb;
+                }
+        }
     }
 }
 
 uint32_t ceil_div(uint32_t a, uint32_t b) { return (a + b - 1) / b; }
 
-template <Epi EPI, bool LO_B>
-hipError_t gemm(int bm, int bn, const float* a, const int32_t* a_exp, uint32_t a_blocks, const _Float16* planes, const int32_t* b_exp,
-                const float* bias, float* out, int32_t* out_exp, uint32_t M, uint32_t Ncol, uint32_t K, hipStream_t stream) {
-    const dim3 block(kThreads);
-    const dim3 grid(Ncol / bn, ceil_div(M, bm));
-    if (bm == 128 && bn == 128)
-        hipLaunchKernelGGL((gemm_split_kernel<EPI, 128, 128, LO_B>), grid, block, 0, stream, a, a_exp, a_blocks, planes, b_exp, bias, out, out_exp, M, Ncol, K);
-    else if (bm == 64 && bn == 128)
-        hipLaunchKernelGGL((gemm_split_kernel<EPI, 64, 128, LO_B>), grid, block, 0, stream, a, a_exp, a_blocks, planes, b_exp, bias, out, out_exp, M, Ncol, K);
-    else if (bm == 128 && bn == 64)
-        hipLaunchKernelGGL((gemm_split_kernel<EPI, 128, 64, LO_B>), grid, block, 0, stream, a, a_exp, a_blocks, planes, b_exp, bias, out, out_exp, M, Ncol, K);
-    else
-        hipLaunchKernelGGL((gemm_split_kernel<EPI, 64, 64, LO_B>), grid, block, 0, stream, a, a_exp, a_blocks, planes, b_exp, bias, out, out_exp, M, Ncol, K);
+struct Shape {
+    int mi, ni, splits;  // wave tile (32 mi) x (32 ni), block tile (64 mi) x (64 ni), k splits
+};
+
+constexpr int kMaxSplits = 4;
+
+// Measured on the Pythia-410M layer at N = 2048: up 128 x 128 blocks (80 us); down 64 x 128 blocks without a k
+// split (91 us; 128 x 128 with 2 splits: 131 us, the fixup's device-scope fences write back the L2). K is split only
+// when a down projection has fewer than 64 blocks.
+Shape up_shape(uint32_t, uint32_t) { return {2, 2, 1}; }
+
+Shape down_shape(uint32_t m, uint32_t ncol, uint32_t k) {
+    const uint32_t tiles = ceil_div(m, 64) * (ncol / 128);
+    return {1, 2, tiles < 64 && k >= 2048 ? 2 : 1};
+}
+
+template <Epi EPI, bool LO_B, int MI, int NI, int SPLITS>
+hipError_t launch_gemm(const float* a, const int32_t* a_exp, uint32_t a_blocks, const _Float16* planes, const int32_t* b_exp,
+                       const float* bias, float* out, int32_t* out_exp, float* partials, int32_t* counters, uint32_t M,
+                       uint32_t Ncol, uint32_t K, hipStream_t stream) {
+    const uint32_t tiles = ceil_div(M, 64 * MI) * (Ncol / (64 * NI));
+    hipLaunchKernelGGL((gemm_split_kernel<EPI, MI, NI, LO_B, SPLITS>), dim3(tiles * SPLITS), dim3(kThreads), 0, stream, a, a_exp,
+                       a_blocks, planes, b_exp, bias, out, out_exp, partials, counters, M, Ncol, K);
     return hipGetLastError();
+}
+
+// The instantiated shapes: up (mi, ni) in {(2,2), (2,4), (4,2), (1,2)} without splits; down (2,2) and (1,2) with
+// 1, 2 or 4 splits and (2,4) with 1 or 2.
+template <Epi EPI, bool LO_B>
+hipError_t gemm(Shape shape, const float* a, const int32_t* a_exp, uint32_t a_blocks, const _Float16* planes, const int32_t* b_exp,
+                const float* bias, float* out, int32_t* out_exp, float* partials, int32_t* counters, uint32_t M, uint32_t Ncol,
+                uint32_t K, hipStream_t stream) {
+#define HFFN_GEMM(MI, NI, S)                                                                                                \
+    if (shape.mi == MI && shape.ni == NI && shape.splits == S)                                                              \
+        return launch_gemm<EPI, LO_B, MI, NI, S>(a, a_exp, a_blocks, planes, b_exp, bias, out, out_exp, partials, counters, \
+                                                 M, Ncol, K, stream);
+    if constexpr (EPI == Epi::Up) {
+        HFFN_GEMM(2, 2, 1)
+        HFFN_GEMM(2, 4, 1)
+        HFFN_GEMM(4, 2, 1)
+        HFFN_GEMM(1, 2, 1)
+    } else {
+        HFFN_GEMM(2, 2, 1)
+        HFFN_GEMM(2, 2, 2)
+        HFFN_GEMM(2, 2, 4)
+        HFFN_GEMM(1, 2, 1)
+        HFFN_GEMM(1, 2, 2)
+        HFFN_GEMM(1, 2, 4)
+        HFFN_GEMM(2, 4, 1)
+        HFFN_GEMM(2, 4, 2)
+    }
+#undef HFFN_GEMM
+    return hipErrorInvalidValue;
+}
+
+// Workspace layout (int32 words unless stated): split counters [down tiles of the largest token count, 64 x 64 tiles]
+// | x binades [M] | activation block binades [M, d_ff / 64] | (256-byte aligned) float partials [4, M, d_model].
+// The counters come first and are sized for every M and tile shape, so a call at any M finds them where the previous
+// call, at any other M, left them (at zero).
+struct Workspace {
+    size_t counters, x_binades, act_binades, partials, bytes;
+};
+
+Workspace workspace_layout(uint32_t m, uint32_t d, uint32_t h) {
+    Workspace w{};
+    w.counters = 0;
+    const size_t counter_words = static_cast<size_t>(ceil_div(kMaxTokens, 64)) * (d / 64);
+    w.x_binades = w.counters + counter_words;
+    w.act_binades = w.x_binades + m;
+    const size_t partial_start = (w.act_binades + static_cast<size_t>(m) * (h / 64)) * 4;
+    w.partials = (partial_start + 255) / 256 * 256;  // bytes
+    w.bytes = w.partials + static_cast<size_t>(kMaxSplits) * m * d * 4;
+    return w;
 }
 
 }  // namespace
 
 size_t dense_plane_halves(uint32_t rows, uint32_t k) { return static_cast<size_t>(rows) * k * 2; }
 
-uint32_t mfma_block_cols(uint32_t ncol) { return ncol % 128 == 0 ? 128 : 64; }
+bool mfma_shape_supported(uint32_t d, uint32_t h) { return d % 256 == 0 && h % 256 == 0; }
 
-uint32_t mfma_block_rows(uint32_t m, uint32_t ncol) {
-    // 128-row tiles unless that leaves most of the 256 CUs without a block
-    const uint32_t bn = mfma_block_cols(ncol);
-    return ceil_div(m, 128) * (ncol / bn) >= 256 ? 128 : 64;
-}
-
-hipError_t launch_row_binades(const float* x, uint32_t rows, uint32_t cols, int32_t* e, hipStream_t stream) {
-    hipLaunchKernelGGL(row_binade_kernel, dim3(ceil_div(rows, kThreads / kWave)), dim3(kThreads), 0, stream, x, rows, cols, e);
-    return hipGetLastError();
-}
+size_t mfma_workspace_bytes(uint32_t n, uint32_t d, uint32_t h) { return workspace_layout(n, d, h).bytes; }
 
 hipError_t launch_densify(int vt, const int32_t* off, const int16_t* idx, const void* val, uint32_t rows, uint32_t k,
                           void* planes, int32_t* exps, hipStream_t stream) {
@@ -316,22 +480,35 @@ hipError_t launch_densify(int vt, const int32_t* off, const int16_t* idx, const 
     return hipGetLastError();
 }
 
-hipError_t launch_mfma_up(int vt, const float* x, const int32_t* x_exp, const void* planes, const int32_t* w_exp,
-                          const float* b_up, float* act, int32_t* act_exp, uint32_t n, uint32_t d, uint32_t h,
-                          hipStream_t stream) {
-    const uint32_t bn = mfma_block_cols(h), bm = mfma_block_rows(n, h);
+hipError_t launch_mfma_up(int vt, const float* x, const void* planes, const int32_t* w_exp, const float* b_up, float* act,
+                          void* workspace, uint32_t n, uint32_t d, uint32_t h, hipStream_t stream) {
+    const Workspace w = workspace_layout(n, d, h);
+    int32_t* words = static_cast<int32_t*>(workspace);
+    hipLaunchKernelGGL(row_binade_kernel, dim3(ceil_div(n, kThreads / kWave)), dim3(kThreads), 0, stream, x, n, d,
+                       words + w.x_binades);
+    if (hipError_t status = hipGetLastError(); status != hipSuccess) return status;
     const auto* p = static_cast<const _Float16*>(planes);
-    if (vt == kBF16) return gemm<Epi::Up, false>(bm, bn, x, x_exp, 1, p, w_exp, b_up, act, act_exp, n, h, d, stream);
-    return gemm<Epi::Up, true>(bm, bn, x, x_exp, 1, p, w_exp, b_up, act, act_exp, n, h, d, stream);
+    const Shape shape = up_shape(n, h);
+    if (vt == kBF16)
+        return gemm<Epi::Up, false>(shape, x, words + w.x_binades, 1, p, w_exp, b_up, act, words + w.act_binades, nullptr,
+                                    nullptr, n, h, d, stream);
+    return gemm<Epi::Up, true>(shape, x, words + w.x_binades, 1, p, w_exp, b_up, act, words + w.act_binades, nullptr, nullptr,
+                               n, h, d, stream);
 }
 
-hipError_t launch_mfma_down(int vt, const float* act, const int32_t* act_exp, const void* planes, const int32_t* v_exp,
-                            const float* b_down, float* y, uint32_t n, uint32_t d, uint32_t h, hipStream_t stream) {
-    const uint32_t bn = mfma_block_cols(d), bm = mfma_block_rows(n, d);
-    const uint32_t blocks = h / mfma_block_cols(h);
+hipError_t launch_mfma_down(int vt, const float* act, const void* planes, const int32_t* v_exp, const float* b_down, float* y,
+                            void* workspace, uint32_t n, uint32_t d, uint32_t h, hipStream_t stream) {
+    const Workspace w = workspace_layout(n, d, h);
+    int32_t* words = static_cast<int32_t*>(workspace);
+    float* partials = reinterpret_cast<float*>(static_cast<char*>(workspace) + w.partials);
     const auto* p = static_cast<const _Float16*>(planes);
-    if (vt == kBF16) return gemm<Epi::Down, false>(bm, bn, act, act_exp, blocks, p, v_exp, b_down, y, nullptr, n, d, h, stream);
-    return gemm<Epi::Down, true>(bm, bn, act, act_exp, blocks, p, v_exp, b_down, y, nullptr, n, d, h, stream);
+    const Shape shape = down_shape(n, d, h);
+    const uint32_t blocks = h / (64 * up_shape(n, h).ni);
+    if (vt == kBF16)
+        return gemm<Epi::Down, false>(shape, act, words + w.act_binades, blocks, p, v_exp, b_down, y, nullptr, partials,
+                                      words + w.counters, n, d, h, stream);
+    return gemm<Epi::Down, true>(shape, act, words + w.act_binades, blocks, p, v_exp, b_down, y, nullptr, partials,
+                                 words + w.counters, n, d, h, stream);
 }
 
 }  // namespace hffn

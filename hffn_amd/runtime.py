@@ -246,14 +246,15 @@ class HFFNRuntime:
         self._act = torch.empty(self.d_ff * ld, device=self.device)      # [d_ff, ld]
         self._y_t = torch.empty(self.d_model * ld, device=self.device)   # [d_model, ld]
         self._y = torch.empty(n, self.d_model, device=self.device)
-        binades = 0
+        words = 1
         if self._planes is not None:
-            binades = _lib.query_bytes(self._lib.hffn_mfma_workspace, n, self.d_model, self.d_ff) // 4
-        self._binades = torch.empty(max(binades, 1), dtype=torch.int32, device=self.device)
+            words = (_lib.query_bytes(self._lib.hffn_mfma_workspace, n, self.d_model, self.d_ff) + 3) // 4
+        # zero-filled once: the split-K counters it holds start at zero and every call leaves them at zero
+        self._mfma_work = torch.zeros(words, dtype=torch.int32, device=self.device)
         self._work = (self._x_t.data_ptr(), self._act.data_ptr(), self._y_t.data_ptr(), self._y.data_ptr())
 
     def workspace_bytes(self) -> int:
-        return 4 * (self._x_t.numel() + self._act.numel() + self._y_t.numel() + self._y.numel() + self._binades.numel())
+        return 4 * (self._x_t.numel() + self._act.numel() + self._y_t.numel() + self._y.numel() + self._mfma_work.numel())
 
     def modes(self, n: int) -> tuple[str, str]:
         """The (up, down) shapes a call of N tokens takes (forced ones first)."""
@@ -291,7 +292,7 @@ class HFFNRuntime:
             _lib.check(self._lib.hffn_forward_mfma(value_type, x.data_ptr(), planes["up"].data_ptr(),
                                                    planes["up_binades"].data_ptr(), tensors["b_up"].data_ptr(),
                                                    planes["down"].data_ptr(), planes["down_binades"].data_ptr(),
-                                                   tensors["b_down"].data_ptr(), act, self._binades.data_ptr(), y,
+                                                   tensors["b_down"].data_ptr(), act, self._mfma_work.data_ptr(), y,
                                                    self.d_model, self.d_ff, n, stream), "forward (mfma, mfma)")
             return
         _lib.check(self._lib.hffn_forward(_lib.UP_MODES[up], _lib.DOWN_MODES[down], value_type, x.data_ptr(), *model,

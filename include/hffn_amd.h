@@ -105,7 +105,7 @@ int hffn_output_major(int value_type, const int32_t* down_offsets, const int16_t
  * each product is hi*hi + hi*lo + lo*hi (hi*hi + lo*hi for bf16 weights) on v_mfma_f32_32x32x16_f16 with fp32
  * accumulation. Activations are token-major act[n, d_ff] on this path. */
 
-/* 1 if the MFMA path takes this shape (d_model and d_ff multiples of 64), else 0 (host-only query). */
+/* 1 if the MFMA path takes this shape (d_model and d_ff multiples of 128), else 0 (host-only query). */
 int hffn_mfma_supported(uint32_t d_model, uint32_t d_ff);
 
 /* Bytes of the planes of a dense [rows, k] matrix (host-only query). */
@@ -117,27 +117,26 @@ int hffn_dense_planes_bytes(uint32_t rows, uint32_t k, uint64_t* bytes);
 int hffn_densify(int value_type, const int32_t* offsets, const int16_t* idx, const void* val, uint32_t rows, uint32_t k,
                  void* planes, int32_t* binades, void* stream);
 
-/* Bytes of the int32 binade workspace of hffn_forward_mfma for n tokens (host-only query). */
+/* Bytes of the device workspace of the MFMA entry points for n tokens (host-only query). The workspace holds the
+ * token and activation binades, the split-K partial sums and one counter per output tile of the down projection;
+ * it must be zero-filled before its first use, and every call leaves the counters at zero. Calls that share a
+ * workspace must be ordered (one stream). */
 int hffn_mfma_workspace(uint32_t n, uint32_t d_model, uint32_t d_ff, uint64_t* bytes);
 
-/* binades[r] = floor(log2(max_c |x[r, c]|)) (0 for a zero row), x row-major [rows, cols]. */
-int hffn_row_binades(const float* x, uint32_t rows, uint32_t cols, int32_t* binades, void* stream);
+/* act[t, r] = gelu(b_up[r] + sum_i W_up[r, i] x[t, i]), token-major act[n, d_ff]; also records in the workspace the
+ * binade of each token of x and of each token's activations per 128-neuron block (read by hffn_mfma_down). */
+int hffn_mfma_up(int value_type, const float* x, const void* up_planes, const int32_t* up_binades, const float* b_up,
+                 float* act, void* workspace, uint32_t d_model, uint32_t d_ff, uint32_t n, void* stream);
 
-/* act[t, r] = gelu(b_up[r] + sum_i W_up[r, i] x[t, i]) (token-major), and act_binades[t, block] the binade of the
- * largest |act| of token t in each block of the up kernel's neuron tile (d_ff / 128 or d_ff / 64 blocks). */
-int hffn_mfma_up(int value_type, const float* x, const int32_t* x_binades, const void* up_planes, const int32_t* up_binades,
-                 const float* b_up, float* act, int32_t* act_binades, uint32_t d_model, uint32_t d_ff, uint32_t n, void* stream);
+/* y[t, o] = sum_r W_down[o, r] act[t, r] + b_down[o], y token-major [n, d_model]; act and the workspace as left by
+ * hffn_mfma_up. */
+int hffn_mfma_down(int value_type, const float* act, const void* down_planes, const int32_t* down_binades, const float* b_down,
+                   float* y, void* workspace, uint32_t d_model, uint32_t d_ff, uint32_t n, void* stream);
 
-/* y[t, o] = sum_r W_down[o, r] act[t, r] + b_down[o], y token-major [n, d_model]. */
-int hffn_mfma_down(int value_type, const float* act, const int32_t* act_binades, const void* down_planes,
-                   const int32_t* down_binades, const float* b_down, float* y, uint32_t d_model, uint32_t d_ff, uint32_t n,
-                   void* stream);
-
-/* The whole layer on the MFMA path: row binades of x, up, down. `binades` is the workspace of hffn_mfma_workspace,
- * act a float32 [n, d_ff] workspace. */
+/* The whole layer on the MFMA path (hffn_mfma_up then hffn_mfma_down); act is a float32 [n, d_ff] workspace. */
 int hffn_forward_mfma(int value_type, const float* x, const void* up_planes, const int32_t* up_binades, const float* b_up,
-                      const void* down_planes, const int32_t* down_binades, const float* b_down, float* act,
-                      int32_t* binades, float* y, uint32_t d_model, uint32_t d_ff, uint32_t n, void* stream);
+                      const void* down_planes, const int32_t* down_binades, const float* b_down, float* act, void* workspace,
+                      float* y, uint32_t d_model, uint32_t d_ff, uint32_t n, void* stream);
 
 #ifdef __cplusplus
 }

@@ -98,9 +98,9 @@ def test_shared_buffers_between_calls(test_layers, device):
 
 
 def _planes_to_dense(plane: torch.Tensor, binades: torch.Tensor, rows: int, k: int) -> np.ndarray:
-    """float64 [rows, k] = (hi + lo) * 2^binade from the tile-major planes [k/32][rows][hi 32 | lo 32]."""
-    tiles = plane.float().cpu().numpy().astype(np.float64).reshape(k // 32, rows, 2, 32)
-    dense = (tiles[:, :, 0, :] + tiles[:, :, 1, :]).transpose(1, 0, 2).reshape(rows, k)
+    """float64 [rows, k] = (hi + lo) * 2^binade from the K-chunk-major planes [k/32][part][chunk][rows][8]."""
+    tiles = plane.float().cpu().numpy().astype(np.float64).reshape(k // 32, 2, 4, rows, 8).transpose(3, 0, 1, 2, 4)
+    dense = (tiles[:, :, 0] + tiles[:, :, 1]).reshape(rows, k)
     return dense * np.exp2(binades.cpu().numpy().astype(np.float64))[:, None]
 
 
@@ -134,6 +134,18 @@ def test_token_result_does_not_depend_on_the_batch(up, down, test_layers, device
     whole = runtime.forward(0, x).clone()
     for start, size in ((0, 1), (7, 5), (64, 129), (299, 1)):
         assert torch.equal(runtime.forward(0, x[start:start + size].contiguous()), whole[start:start + size])
+
+
+def test_mfma_workspace_reused_at_shrinking_token_counts(test_layers, device):
+    """The MFMA path's workspace (split-K counters, binades, partials) is shared by calls of any N: calls at falling N
+    after a large one stay correct."""
+    compact, case, layer = test_layers["homog_512_2048"]
+    runtime = HFFNRuntime([layer], device)
+    runtime.force("mfma", "mfma")
+    for n in (300, 129, 64, 5, 1, 300):
+        x_np = synth.make_input(case, n)
+        y = runtime.forward(0, torch.from_numpy(x_np).to(device))
+        assert float((y.double().cpu() - torch.from_numpy(reference.forward(compact, x_np))).abs().max()) <= ATOL, n
 
 
 def test_stack_of_layers(test_layers, device):
