@@ -50,7 +50,22 @@ def parse() -> argparse.Namespace:
     parser.add_argument("--cpu-seconds", type=float, default=10.0, help="bound of the CPU-baseline sample")
     parser.add_argument("--cpu-threads", type=int, default=8)
     parser.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
+    parser.add_argument("--copy-probe-mb", type=int, default=0,
+                        help="after the run, copy a buffer of this many MiB 3 times (the plain copy kernel that "
+                             "calibrates rocprofv3 FETCH_SIZE/WRITE_SIZE)")
     return parser.parse_args()
+
+
+TRAFFIC = ROOT / "profiles" / "traffic.json"
+
+
+def measured_traffic(workload: str, n: int, kernel: str) -> int | None:
+    """Memory-side bytes per launch of `kernel` ("up (mfma)", ...), from the committed rocprofv3 FETCH_SIZE/WRITE_SIZE
+    summary of this workload (each counter scaled by its copy-kernel calibration), or None when none matches."""
+    if not TRAFFIC.exists():
+        return None
+    record = json.loads(TRAFFIC.read_text()).get("workloads", {}).get(f"{workload}/n{n}", {}).get(kernel)
+    return int(record["traffic_bytes"]) if record else None
 
 
 def layer_costs(compact, n: int) -> dict:
@@ -208,8 +223,8 @@ def main() -> int:
         roofline = {"bound": "hbm", "achieved": round(cost["bytes"] / kernels[dominant] / 1e9, 1), "peak": HBM_PEAK / 1e9,
                     "unit": "GB/s"}
     roofline["frac"] = round(roofline["achieved"] / roofline["peak"], 4)
-    roofline["traffic"] = None
     roofline["kernel"] = f"{dominant} ({up if dominant == 'up' else down})"
+    roofline["traffic"] = measured_traffic(workload.name, n, roofline["kernel"])
     if up == "mfma":
         # what the MFMA units execute: the dense products of the planes, 3 (fp32 values) or 2 (bf16) fp16 MFMAs each
         products = 2 if base.value_dtype == "bf16" else 3
@@ -233,6 +248,12 @@ def main() -> int:
         "cpu_baseline": baseline,
     }
     print(json.dumps(line), flush=True)
+    if args.copy_probe_mb:
+        source = torch.empty(args.copy_probe_mb << 18, device=device)
+        target = torch.empty_like(source)
+        for _ in range(3):
+            target.copy_(source)
+        torch.cuda.synchronize()
     return 0
 
 
