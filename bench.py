@@ -124,6 +124,7 @@ def time_kernels(runtime, x: torch.Tensor, steps: int, copies: int) -> dict:
     totals = {name: 0.0 for name in names}
     for step in range(steps):
         value_type, up_off, up_idx, up_val, b_up, out_off, out_hid, out_val, b_down = runtime._args[step % copies]
+        nnz_up, nnz_down = runtime._nnz[step % copies]
         events = [torch.cuda.Event(enable_timing=True) for _ in range(len(names) + 1)]
         events[0].record()
         k = 1
@@ -131,14 +132,14 @@ def time_kernels(runtime, x: torch.Tensor, steps: int, copies: int) -> dict:
             _lib.check(lib.hffn_transpose(x.data_ptr(), x_t, n, runtime.d_model, runtime.d_model, ld, stream), "transpose")
             events[k].record(); k += 1
             _lib.check(lib.hffn_up(_lib.UP_MODES[up], value_type, x_t, up_off, up_idx, up_val, b_up, act, runtime.d_model,
-                                   runtime.d_ff, n, ld, stream), "up")
+                                   runtime.d_ff, nnz_up, n, ld, stream), "up")
         else:
             _lib.check(lib.hffn_up(_lib.UP_MODES[up], value_type, x.data_ptr(), up_off, up_idx, up_val, b_up, act,
-                                   runtime.d_model, runtime.d_ff, n, ld, stream), "up")
+                                   runtime.d_model, runtime.d_ff, nnz_up, n, ld, stream), "up")
         events[k].record(); k += 1
         target = y_t if down == "rows" else y
         _lib.check(lib.hffn_down(_lib.DOWN_MODES[down], value_type, act, out_off, out_hid, out_val, b_down, target,
-                                 runtime.d_model, runtime.d_ff, n, ld, stream), "down")
+                                 runtime.d_model, runtime.d_ff, nnz_down, n, ld, stream), "down")
         events[k].record(); k += 1
         if down == "rows":
             _lib.check(lib.hffn_transpose(y_t, y, runtime.d_model, n, ld, runtime.d_model, stream), "transpose")

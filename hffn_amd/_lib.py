@@ -25,9 +25,9 @@ SIGNATURES = {
     "hffn_last_error": [],
     "hffn_edges_supported": [_U32, _U32],
     "hffn_transpose": [_P, _P, _U32, _U32, _U32, _U32, _P],
-    "hffn_up": [_I, _I, _P, _P, _P, _P, _P, _P, _U32, _U32, _U32, _U32, _P],
-    "hffn_down": [_I, _I, _P, _P, _P, _P, _P, _P, _U32, _U32, _U32, _U32, _P],
-    "hffn_forward": [_I, _I, _I] + [_P] * 13 + [_U32] * 4 + [_P],
+    "hffn_up": [_I, _I, _P, _P, _P, _P, _P, _P, _U32, _U32, _U32, _U32, _U32, _P],
+    "hffn_down": [_I, _I, _P, _P, _P, _P, _P, _P, _U32, _U32, _U32, _U32, _U32, _P],
+    "hffn_forward": [_I, _I, _I] + [_P] * 13 + [_U32] * 6 + [_P],
     "hffn_output_major_workspace": [_U32, _U32, ctypes.POINTER(_U64)],
     "hffn_output_major": [_I, _P, _P, _P, _U32, _U32, _U32, _P, _P, _P, _P, _U64, _P],
     "hffn_mfma_supported": [_U32, _U32],

@@ -46,7 +46,7 @@ int check_shape(uint32_t d, uint32_t h, uint32_t n, uint32_t ld) {
 int check_edges(uint32_t d, uint32_t n, uint32_t ld, bool stage) {
     const uint32_t nt = hffn::edges_tokens(n);
     if (ld % nt != 0) return fail(HFFN_ERROR_ARGUMENT, "edges mode: ld=%u must be a multiple of %u for n=%u", ld, nt, n);
-    if (stage && static_cast<size_t>(nt) * d * sizeof(float) > HFFN_EDGES_MAX_LDS)
+    if (stage && static_cast<size_t>(nt) * (d + 4) * sizeof(float) > HFFN_EDGES_MAX_LDS)
         return fail(HFFN_ERROR_ARGUMENT, "edges mode: %u tokens of d_model=%u exceed the %u-byte LDS stage", nt, d, HFFN_EDGES_MAX_LDS);
     return HFFN_OK;
 }
@@ -61,7 +61,7 @@ const char* hffn_last_error(void) { return g_error.c_str(); }
 
 int hffn_edges_supported(uint32_t d_model, uint32_t n) {
     if (n == 0) return 0;
-    return static_cast<size_t>(hffn::edges_tokens(n)) * d_model * sizeof(float) <= HFFN_EDGES_MAX_LDS ? 1 : 0;
+    return static_cast<size_t>(hffn::edges_tokens(n)) * (d_model + 4) * sizeof(float) <= HFFN_EDGES_MAX_LDS ? 1 : 0;
 }
 
 int hffn_transpose(const float* in, float* out, uint32_t rows, uint32_t cols, uint32_t in_ld, uint32_t out_ld,
@@ -72,16 +72,28 @@ int hffn_transpose(const float* in, float* out, uint32_t rows, uint32_t cols, ui
     return launched(hffn::launch_transpose(in, out, rows, cols, in_ld, out_ld, static_cast<hipStream_t>(stream)), "transpose");
 }
 
+namespace {
+// The edges kernels read 4 slots at a time: 8-byte aligned indices, 16-byte (fp32) or 8-byte (bf16) aligned values.
+int check_store_alignment(const int16_t* idx, const void* val, int value_type) {
+    const uintptr_t value_align = value_type == HFFN_VALUE_BF16 ? 8 : 16;
+    if (reinterpret_cast<uintptr_t>(idx) % 8 != 0 || reinterpret_cast<uintptr_t>(val) % value_align != 0)
+        return fail(HFFN_ERROR_ARGUMENT, "edges mode: index/value arrays must be 8/%u-byte aligned", static_cast<unsigned>(value_align));
+    return HFFN_OK;
+}
+}  // namespace
+
 int hffn_up(int mode, int value_type, const float* x, const int32_t* up_offsets, const int16_t* up_idx,
-            const void* up_val, const float* b_up, float* act, uint32_t d_model, uint32_t d_ff, uint32_t n, uint32_t ld,
-            void* stream) {
+            const void* up_val, const float* b_up, float* act, uint32_t d_model, uint32_t d_ff, uint32_t nnz_up, uint32_t n,
+            uint32_t ld, void* stream) {
     if (int status = check_shape(d_model, d_ff, n, ld)) return status;
     if (!valid_value_type(value_type)) return fail(HFFN_ERROR_ARGUMENT, "unknown value type %d", value_type);
     if (!x || !up_offsets || !up_idx || !up_val || !b_up || !act) return fail(HFFN_ERROR_ARGUMENT, "up: null pointer");
     const hipStream_t s = static_cast<hipStream_t>(stream);
     if (mode == HFFN_UP_EDGES) {
         if (int status = check_edges(d_model, n, ld, true)) return status;
-        return launched(hffn::launch_up_edges(value_type, x, up_offsets, up_idx, up_val, b_up, act, d_model, d_ff, n, ld, s), "up edges");
+        if (int status = check_store_alignment(up_idx, up_val, value_type)) return status;
+        return launched(hffn::launch_up_edges(value_type, x, up_offsets, up_idx, up_val, b_up, act, d_model, d_ff, n, ld, nnz_up, s),
+                        "up edges");
     }
     if (mode == HFFN_UP_ROWS)
         return launched(hffn::launch_up_rows(value_type, x, up_offsets, up_idx, up_val, b_up, act, d_model, d_ff, n, ld, s), "up rows");
@@ -89,15 +101,18 @@ int hffn_up(int mode, int value_type, const float* x, const int32_t* up_offsets,
 }
 
 int hffn_down(int mode, int value_type, const float* act, const int32_t* out_offsets, const int16_t* out_hidden,
-              const void* out_val, const float* b_down, float* y, uint32_t d_model, uint32_t d_ff, uint32_t n,
-              uint32_t ld, void* stream) {
+              const void* out_val, const float* b_down, float* y, uint32_t d_model, uint32_t d_ff, uint32_t nnz_down,
+              uint32_t n, uint32_t ld, void* stream) {
     if (int status = check_shape(d_model, d_ff, n, ld)) return status;
     if (!valid_value_type(value_type)) return fail(HFFN_ERROR_ARGUMENT, "unknown value type %d", value_type);
     if (!act || !out_offsets || !out_hidden || !out_val || !b_down || !y) return fail(HFFN_ERROR_ARGUMENT, "down: null pointer");
     const hipStream_t s = static_cast<hipStream_t>(stream);
     if (mode == HFFN_DOWN_EDGES) {
         if (int status = check_edges(d_model, n, ld, false)) return status;
-        return launched(hffn::launch_down_edges(value_type, act, out_offsets, out_hidden, out_val, b_down, y, d_model, n, ld, s), "down edges");
+        if (int status = check_store_alignment(out_hidden, out_val, value_type)) return status;
+        return launched(hffn::launch_down_edges(value_type, act, out_offsets, out_hidden, out_val, b_down, y, d_model, d_ff, n, ld,
+                                                nnz_down, s),
+                        "down edges");
     }
     if (mode == HFFN_DOWN_ROWS)
         return launched(hffn::launch_down_rows(value_type, act, out_offsets, out_hidden, out_val, b_down, y, d_model, n, ld, s), "down rows");
@@ -107,22 +122,27 @@ int hffn_down(int mode, int value_type, const float* act, const int32_t* out_off
 int hffn_forward(int up_mode, int down_mode, int value_type, const float* x, const int32_t* up_offsets,
                  const int16_t* up_idx, const void* up_val, const float* b_up, const int32_t* out_offsets,
                  const int16_t* out_hidden, const void* out_val, const float* b_down, float* x_t, float* act,
-                 float* y_t, float* y, uint32_t d_model, uint32_t d_ff, uint32_t n, uint32_t ld, void* stream) {
+                 float* y_t, float* y, uint32_t d_model, uint32_t d_ff, uint32_t nnz_up, uint32_t nnz_down, uint32_t n,
+                 uint32_t ld, void* stream) {
     if (int status = check_shape(d_model, d_ff, n, ld)) return status;
     const hipStream_t s = static_cast<hipStream_t>(stream);
     if (up_mode == HFFN_UP_ROWS) {
         if (!x || !x_t) return fail(HFFN_ERROR_ARGUMENT, "forward: null input or x_t workspace");
         if (int status = hffn_transpose(x, x_t, n, d_model, d_model, ld, stream)) return status;
-        if (int status = hffn_up(up_mode, value_type, x_t, up_offsets, up_idx, up_val, b_up, act, d_model, d_ff, n, ld, stream)) return status;
+        if (int status = hffn_up(up_mode, value_type, x_t, up_offsets, up_idx, up_val, b_up, act, d_model, d_ff, nnz_up, n, ld, stream))
+            return status;
     } else {
-        if (int status = hffn_up(up_mode, value_type, x, up_offsets, up_idx, up_val, b_up, act, d_model, d_ff, n, ld, stream)) return status;
+        if (int status = hffn_up(up_mode, value_type, x, up_offsets, up_idx, up_val, b_up, act, d_model, d_ff, nnz_up, n, ld, stream))
+            return status;
     }
     if (down_mode == HFFN_DOWN_ROWS) {
         if (!y_t) return fail(HFFN_ERROR_ARGUMENT, "forward: null y_t workspace");
-        if (int status = hffn_down(down_mode, value_type, act, out_offsets, out_hidden, out_val, b_down, y_t, d_model, d_ff, n, ld, stream)) return status;
+        if (int status = hffn_down(down_mode, value_type, act, out_offsets, out_hidden, out_val, b_down, y_t, d_model, d_ff, nnz_down,
+                                   n, ld, stream))
+            return status;
         return launched(hffn::launch_transpose(y_t, y, d_model, n, ld, d_model, s), "output transpose");
     }
-    return hffn_down(down_mode, value_type, act, out_offsets, out_hidden, out_val, b_down, y, d_model, d_ff, n, ld, stream);
+    return hffn_down(down_mode, value_type, act, out_offsets, out_hidden, out_val, b_down, y, d_model, d_ff, nnz_down, n, ld, stream);
 }
 
 int hffn_output_major_workspace(uint32_t nnz, uint32_t d_model, uint64_t* bytes) {

@@ -1,0 +1,374 @@
+// Decode-shaped ("edges") kernels of the HFFN forward on CDNA4: lanes over a row's slots, tokens in registers.
+//
+// Up:   act[r, t] = gelu(b_up[r] + sum_e w[e] x[t, idx[e]]),   one row per neuron r (up store).
+// Down: y[t, o]   = b_down[o] + sum_q v[q] act[hid[q], t],     one row per output o (output-major store).
+//
+// A row is read as groups of 4 consecutive slots per lane (16-byte value and 8-byte index loads, i.e. 1 KB and
+// 512 B per wave instruction; groups are aligned to 4 slots, so a group may straddle the row's ends and its outside
+// slots are skipped). A wave requests its first 3 groups per lane (768 slots) before its block stages the inputs in
+// LDS, so the store streams while the block waits: at decode sizes these kernels are HBM-bound on the store.
+// Long rows are split over P waves of the block (each takes a contiguous segment cut on the 4-slot grid); the P
+// partial sums are added in segment order. Within a wave the 64 lane partials are added by a fixed xor butterfly. Inputs are
+// staged in LDS when they fit (x for up, act for down at small n), otherwise act is gathered from L2.
+// Tokens are processed NT at a time (NT = 1, 2, 4 or 8); every activation and output is written by one lane: no
+// atomics, bitwise repeatable, and a token's result does not depend on the other tokens of the call.
+#include "common.hpp"
+#include "launch.hpp"
+
+namespace hffn {
+namespace {
+
+constexpr uint32_t kBlock = 256;
+constexpr uint32_t kWaves = kBlock / kWave;
+
+template <typename V> struct Group;
+template <> struct Group<float> {
+    using type = float4;
+    __device__ static float at(const float4& g, int s) { return s == 0 ? g.x : s == 1 ? g.y : s == 2 ? g.z : g.w; }
+};
+template <> struct Group<uint16_t> {
+    using type = uint2;
+    __device__ static float at(const uint2& g, int s) {
+        const uint32_t word = s < 2 ? g.x : g.y;
+        return __uint_as_float((s % 2 == 0 ? word << 16 : word & 0xffff0000u));
+    }
+};
+
+__device__ __forceinline__ uint32_t index_at(const uint2& g, int s) {
+    const uint32_t word = s < 2 ? g.x : g.y;
+    return s % 2 == 0 ? (word & 0xffffu) : (word >> 16);
+}
+
+// Where a token's input for feature i lives: LDS [i][NT] (staged) or global [i * ld] + t (act of the down kernel).
+struct StagedInput {
+    const float* lds;
+    template <int NT> __device__ void load(uint32_t i, float (&v)[NT]) const { load_vec<NT>(lds + i * NT, v); }
+};
+struct GlobalInput {
+    const float* base;  // act + c0
+    uint32_t ld;
+    template <int NT> __device__ void load(uint32_t i, float (&v)[NT]) const {
+        load_vec<NT>(base + static_cast<size_t>(i) * ld, v);
+    }
+};
+
+// A wave's slots of one row segment [pb, pe), held in registers: up to G groups of 4 slots per lane, loaded before
+// the inputs are staged so that the store's bytes are in flight while the block waits for its inputs.
+template <typename V, int G>
+struct Segment {
+    typename Group<V>::type vals[G];
+    uint2 ids[G];
+    int32_t first;  // slot of this lane's group 0
+};
+
+// Issues the loads of groups [chunk * G, chunk * G + G) of this lane (4-slot groups strided by the wave); groups
+// that cross nnz, or lie past pe, are loaded slot by slot or left empty.
+template <typename V, int G>
+__device__ __forceinline__ void load_segment(Segment<V, G>& seg, const int16_t* __restrict__ idx, const V* __restrict__ val,
+                                             int32_t pb, int32_t pe, int32_t nnz, uint32_t lane, uint32_t chunk) {
+    seg.first = (pb & ~3) + 4 * static_cast<int32_t>(lane) + static_cast<int32_t>(chunk) * G * 4 * kWave;
+#pragma unroll
+    for (int k = 0; k < G; ++k) {
+        const int32_t g = seg.first + k * 4 * kWave;
+        if (g < pe && g + 4 <= nnz) {
+            seg.vals[k] = *reinterpret_cast<const typename Group<V>::type*>(val + g);
+            seg.ids[k] = *reinterpret_cast<const uint2*>(idx + g);
+        } else if (g < pe) {
+            // the store's last group: pack the slots below nnz by hand
+            uint16_t i4[4] = {0, 0, 0, 0};
+            V v4[4] = {V(0), V(0), V(0), V(0)};
+            for (int s = 0; s < 4; ++s)
+                if (g + s < nnz) {
+                    i4[s] = static_cast<uint16_t>(idx[g + s]);
+                    v4[s] = val[g + s];
+                }
+            seg.ids[k] = make_uint2(i4[0] | (static_cast<uint32_t>(i4[1]) << 16), i4[2] | (static_cast<uint32_t>(i4[3]) << 16));
+            seg.vals[k] = *reinterpret_cast<const typename Group<V>::type*>(v4);
+        }
+    }
+}
+
+template <int NT, typename V, int G, typename Input>
+__device__ __forceinline__ void accumulate_segment(const Segment<V, G>& seg, int32_t pb, int32_t pe, const Input& input,
+                                                   float (&acc)[NT]) {
+#pragma unroll
+    for (int k = 0; k < G; ++k) {
+        const int32_t g = seg.first + k * 4 * kWave;
+        if (g < pe) {
+#pragma unroll
+            for (int s = 0; s < 4; ++s) {
+                if (g + s >= pb && g + s < pe) {
+                    float xv[NT];
+                    input.template load<NT>(index_at(seg.ids[k], s), xv);
+                    const float w = Group<V>::at(seg.vals[k], s);
+#pragma unroll
+                    for (int t = 0; t < NT; ++t) acc[t] = fmaf(w, xv[t], acc[t]);
+                }
+            }
+        }
+    }
+}
+
+// Groups per lane held at once (768 slots per wave); longer segments take several chunks.
+constexpr int kGroups = 3;
+
+// Partial sums of one wave over slots [pb, pe) of a row, NT tokens: the first chunk's loads come from `first`
+// (issued by the caller before the inputs were staged); the next chunks are loaded here.
+template <int NT, typename V, typename Input>
+__device__ __forceinline__ void row_partials(const Segment<V, kGroups>& first, const int16_t* __restrict__ idx,
+                                             const V* __restrict__ val, int32_t pb, int32_t pe, int32_t nnz,
+                                             const Input& input, uint32_t lane, float (&acc)[NT]) {
+#pragma unroll
+    for (int t = 0; t < NT; ++t) acc[t] = 0.0f;
+    accumulate_segment<NT>(first, pb, pe, input, acc);
+    const int32_t span = kGroups * 4 * kWave;
+    for (uint32_t chunk = 1; (pb & ~3) + static_cast<int32_t>(chunk) * span < pe; ++chunk) {
+        Segment<V, kGroups> seg;
+        load_segment(seg, idx, val, pb, pe, nnz, lane, chunk);
+        accumulate_segment<NT>(seg, pb, pe, input, acc);
+    }
+}
+
+// Adds the wave's lane partials, then (P > 1) the block's P segment totals of the row in segment order; returns, in
+// lane t < NT of the row's first wave, the row total of token t (other lanes: unspecified).
+template <int NT, int P>
+__device__ __forceinline__ float row_total(float (&acc)[NT], uint32_t lane, uint32_t part, uint32_t row_in_block,
+                                           float* __restrict__ totals /* LDS [kWaves][NT] */) {
+    float mine = 0.0f;
+#pragma unroll
+    for (int t = 0; t < NT; ++t) {
+        const float s = wave_sum(acc[t]);
+        if (lane == static_cast<uint32_t>(t)) mine = s;
+    }
+    if constexpr (P > 1) {
+        const uint32_t wave = row_in_block * P + part;
+        if (lane < NT) totals[wave * NT + lane] = mine;
+        __syncthreads();
+        if (part == 0 && lane < NT) {
+            float s = totals[(row_in_block * P) * NT + lane];
+#pragma unroll
+            for (int p = 1; p < P; ++p) s += totals[(row_in_block * P + p) * NT + lane];
+            mine = s;
+        }
+        __syncthreads();
+    }
+    return mine;
+}
+
+// Segment [pb, pe) of part `part` of a row [begin, end) split in P: the parts cut the row on the 4-slot grid, so
+// each starts on a group boundary and no group is shared by two waves.
+template <int P>
+__device__ __forceinline__ void segment(int32_t begin, int32_t end, uint32_t part, int32_t& pb, int32_t& pe) {
+    if constexpr (P == 1) {
+        pb = begin;
+        pe = end;
+    } else {
+        const int32_t base = begin & ~3;
+        const int32_t seg = ((end - base + P - 1) / P + 3) & ~3;
+        const int32_t start = base + static_cast<int32_t>(part) * seg;
+        pb = max(begin, min(end, start));
+        pe = min(end, start + seg);
+    }
+}
+
+// ------------------------------------------------------------------------------------------------- up
+template <int NT, int P, typename V>
+__global__ __launch_bounds__(kBlock) void up_edges_kernel(const float* __restrict__ x, const int32_t* __restrict__ off,
+                                                         const int16_t* __restrict__ idx, const V* __restrict__ w,
+                                                         const float* __restrict__ b, float* __restrict__ act, uint32_t d,
+                                                         uint32_t h, uint32_t n, uint32_t ld, int32_t nnz, uint32_t per_block) {
+    extern __shared__ float smem[];  // x of NT tokens, [d][NT]; then the segment totals [kWaves][NT]
+    float* xs = smem;
+    float* totals = smem + static_cast<size_t>(d) * NT;
+    constexpr uint32_t kRowsPerPass = kWaves / P;
+    const uint32_t wave = uniform(threadIdx.x / kWave), lane = threadIdx.x % kWave;
+    const uint32_t row_in_pass = wave / P, part = wave % P;
+    const uint32_t r0 = blockIdx.x * per_block;
+    const uint32_t r1 = min(h, r0 + per_block);
+    for (uint32_t c0 = 0; c0 < n; c0 += NT) {
+        const uint32_t tokens = min(n - c0, static_cast<uint32_t>(NT));
+        // the first row's slots are requested before the block stages x and waits for it
+        int32_t pb = 0, pe = 0;
+        Segment<V, kGroups> first;
+        if (r0 + row_in_pass < r1) {
+            segment<P>(off[r0 + row_in_pass], off[r0 + row_in_pass + 1], part, pb, pe);
+            load_segment(first, idx, w, pb, pe, nnz, lane, 0);
+        }
+        if (c0) __syncthreads();
+        for (uint32_t i = threadIdx.x; i < d * NT; i += kBlock) {
+            const uint32_t feature = i / NT, t = i % NT;
+            xs[i] = t < tokens ? x[static_cast<size_t>(c0 + t) * d + feature] : 0.0f;
+        }
+        __syncthreads();
+        const StagedInput input{xs};
+        for (uint32_t base = r0; base < r1; base += kRowsPerPass) {  // uniform trip count across the block
+            const uint32_t r = base + row_in_pass;
+            float acc[NT];
+            if (r < r1) {
+                if (base != r0) {
+                    segment<P>(off[r], off[r + 1], part, pb, pe);
+                    load_segment(first, idx, w, pb, pe, nnz, lane, 0);
+                }
+                row_partials<NT>(first, idx, w, pb, pe, nnz, input, lane, acc);
+            } else {
+#pragma unroll
+                for (int t = 0; t < NT; ++t) acc[t] = 0.0f;
+            }
+            const float total = row_total<NT, P>(acc, lane, part, row_in_pass, totals);
+            if (r < r1 && part == 0 && lane < tokens) act[static_cast<size_t>(r) * ld + c0 + lane] = gelu(b[r] + total);
+        }
+    }
+}
+
+// ----------------------------------------------------------------------------------------------- down
+template <int NT, int P, typename V, bool STAGE, int WAVES>
+__global__ __launch_bounds__(WAVES * kWave) void down_edges_kernel(const float* __restrict__ act, const int32_t* __restrict__ off,
+                                                           const int16_t* __restrict__ hid, const V* __restrict__ v,
+                                                           const float* __restrict__ bias, float* __restrict__ y, uint32_t d,
+                                                           uint32_t h, uint32_t n, uint32_t ld, int32_t nnz, uint32_t per_block) {
+    extern __shared__ float smem[];  // STAGE: act of NT tokens, [h][NT]; then the segment totals [WAVES][NT]
+    float* as = smem;
+    float* totals = smem + (STAGE ? static_cast<size_t>(h) * NT : 0);
+    constexpr uint32_t kRowsPerPass = WAVES / P;
+    const uint32_t wave = uniform(threadIdx.x / kWave), lane = threadIdx.x % kWave;
+    const uint32_t row_in_pass = wave / P, part = wave % P;
+    const uint32_t o0 = blockIdx.x * per_block;
+    const uint32_t o1 = min(d, o0 + per_block);
+    for (uint32_t c0 = 0; c0 < n; c0 += NT) {
+        const uint32_t tokens = min(n - c0, static_cast<uint32_t>(NT));
+        int32_t pb = 0, pe = 0;
+        Segment<V, kGroups> first;
+        if (o0 + row_in_pass < o1) {
+            segment<P>(off[o0 + row_in_pass], off[o0 + row_in_pass + 1], part, pb, pe);
+            load_segment(first, hid, v, pb, pe, nnz, lane, 0);
+        }
+        if constexpr (STAGE) {
+            if (c0) __syncthreads();
+            for (uint32_t i = threadIdx.x; i < h * NT; i += WAVES * kWave) {
+                const uint32_t r = i / NT, t = i % NT;
+                as[i] = t < tokens ? act[static_cast<size_t>(r) * ld + c0 + t] : 0.0f;
+            }
+            __syncthreads();
+        }
+        for (uint32_t base = o0; base < o1; base += kRowsPerPass) {
+            const uint32_t o = base + row_in_pass;
+            float acc[NT];
+            if (o < o1) {
+                if (base != o0) {
+                    segment<P>(off[o], off[o + 1], part, pb, pe);
+                    load_segment(first, hid, v, pb, pe, nnz, lane, 0);
+                }
+                if constexpr (STAGE) row_partials<NT>(first, hid, v, pb, pe, nnz, StagedInput{as}, lane, acc);
+                else row_partials<NT>(first, hid, v, pb, pe, nnz, GlobalInput{act + c0, ld}, lane, acc);
+            } else {
+#pragma unroll
+                for (int t = 0; t < NT; ++t) acc[t] = 0.0f;
+            }
+            const float total = row_total<NT, P>(acc, lane, part, row_in_pass, totals);
+            if (o < o1 && part == 0 && lane < tokens) y[static_cast<size_t>(c0 + lane) * d + o] = total + bias[o];
+        }
+    }
+}
+
+uint32_t ceil_div(uint32_t a, uint32_t b) { return (a + b - 1) / b; }
+
+// Waves per row: one per 512 slots of the average row, at most 4.
+int parts_for(uint32_t nnz, uint32_t rows) {
+    const uint32_t average = rows ? nnz / rows : 0;
+    return average >= 1536 ? 4 : average >= 768 ? 2 : 1;
+}
+
+// Rows per block: about `blocks` blocks, a multiple of the rows one pass of the block takes.
+uint32_t rows_per_block(uint32_t rows, int parts, uint32_t waves = kWaves, uint32_t blocks = 1024) {
+    const uint32_t pass = waves / parts;
+    const uint32_t per = max(1u, ceil_div(rows, blocks));
+    return ceil_div(per, pass) * pass;
+}
+
+template <int NT, int P, typename V>
+hipError_t up_shape(const float* x, const int32_t* off, const int16_t* idx, const V* w, const float* b, float* act, uint32_t d,
+                    uint32_t h, uint32_t n, uint32_t ld, uint32_t nnz, hipStream_t stream) {
+    const uint32_t per = rows_per_block(h, P);
+    const size_t lds = (static_cast<size_t>(d) * NT + kWaves * NT) * sizeof(float);
+    hipLaunchKernelGGL((up_edges_kernel<NT, P, V>), dim3(ceil_div(h, per)), dim3(kBlock), lds, stream, x, off, idx, w, b, act, d,
+                       h, n, ld, static_cast<int32_t>(nnz), per);
+    return hipGetLastError();
+}
+
+// With act staged in LDS (small n), blocks of 16 waves take 4x the rows of 4-wave blocks, so each block's staging
+// of the whole act serves 4x the slots.
+template <int NT, int P, typename V>
+hipError_t down_shape(const float* act, const int32_t* off, const int16_t* hid, const V* v, const float* bias, float* y,
+                      uint32_t d, uint32_t h, uint32_t n, uint32_t ld, uint32_t nnz, hipStream_t stream) {
+    const bool stage = static_cast<size_t>(h) * NT * sizeof(float) <= kEdgesStageBytes;
+    if (stage) {
+        constexpr uint32_t waves = 16;
+        const uint32_t per = rows_per_block(d, P, waves, 256);
+        const size_t lds = (static_cast<size_t>(h) * NT + waves * NT) * sizeof(float);
+        hipLaunchKernelGGL((down_edges_kernel<NT, P, V, true, waves>), dim3(ceil_div(d, per)), dim3(waves * kWave), lds, stream,
+                           act, off, hid, v, bias, y, d, h, n, ld, static_cast<int32_t>(nnz), per);
+    } else {
+        const uint32_t per = rows_per_block(d, P);
+        const size_t lds = static_cast<size_t>(kWaves) * NT * sizeof(float);
+        hipLaunchKernelGGL((down_edges_kernel<NT, P, V, false, kWaves>), dim3(ceil_div(d, per)), dim3(kBlock), lds, stream, act,
+                           off, hid, v, bias, y, d, h, n, ld, static_cast<int32_t>(nnz), per);
+    }
+    return hipGetLastError();
+}
+
+template <int NT, typename V>
+hipError_t up_parts(int parts, const float* x, const int32_t* off, const int16_t* idx, const V* w, const float* b, float* act,
+                    uint32_t d, uint32_t h, uint32_t n, uint32_t ld, uint32_t nnz, hipStream_t stream) {
+    if (parts == 4) return up_shape<NT, 4>(x, off, idx, w, b, act, d, h, n, ld, nnz, stream);
+    if (parts == 2) return up_shape<NT, 2>(x, off, idx, w, b, act, d, h, n, ld, nnz, stream);
+    return up_shape<NT, 1>(x, off, idx, w, b, act, d, h, n, ld, nnz, stream);
+}
+
+template <int NT, typename V>
+hipError_t down_parts(int parts, const float* act, const int32_t* off, const int16_t* hid, const V* v, const float* bias,
+                      float* y, uint32_t d, uint32_t h, uint32_t n, uint32_t ld, uint32_t nnz, hipStream_t stream) {
+    if (parts == 4) return down_shape<NT, 4>(act, off, hid, v, bias, y, d, h, n, ld, nnz, stream);
+    if (parts == 2) return down_shape<NT, 2>(act, off, hid, v, bias, y, d, h, n, ld, nnz, stream);
+    return down_shape<NT, 1>(act, off, hid, v, bias, y, d, h, n, ld, nnz, stream);
+}
+
+template <typename V>
+hipError_t up_typed(const float* x, const int32_t* off, const int16_t* idx, const V* w, const float* b, float* act, uint32_t d,
+                    uint32_t h, uint32_t n, uint32_t ld, uint32_t nnz, hipStream_t stream) {
+    const int parts = parts_for(nnz, h);
+    switch (edges_tokens(n)) {
+        case 1: return up_parts<1>(parts, x, off, idx, w, b, act, d, h, n, ld, nnz, stream);
+        case 2: return up_parts<2>(parts, x, off, idx, w, b, act, d, h, n, ld, nnz, stream);
+        case 4: return up_parts<4>(parts, x, off, idx, w, b, act, d, h, n, ld, nnz, stream);
+        default: return up_parts<8>(parts, x, off, idx, w, b, act, d, h, n, ld, nnz, stream);
+    }
+}
+
+template <typename V>
+hipError_t down_typed(const float* act, const int32_t* off, const int16_t* hid, const V* v, const float* bias, float* y,
+                      uint32_t d, uint32_t h, uint32_t n, uint32_t ld, uint32_t nnz, hipStream_t stream) {
+    const int parts = parts_for(nnz, d);
+    switch (edges_tokens(n)) {
+        case 1: return down_parts<1>(parts, act, off, hid, v, bias, y, d, h, n, ld, nnz, stream);
+        case 2: return down_parts<2>(parts, act, off, hid, v, bias, y, d, h, n, ld, nnz, stream);
+        case 4: return down_parts<4>(parts, act, off, hid, v, bias, y, d, h, n, ld, nnz, stream);
+        default: return down_parts<8>(parts, act, off, hid, v, bias, y, d, h, n, ld, nnz, stream);
+    }
+}
+
+}  // namespace
+
+hipError_t launch_up_edges(int vt, const float* x, const int32_t* off, const int16_t* idx, const void* w, const float* b,
+                           float* act, uint32_t d, uint32_t h, uint32_t n, uint32_t ld, uint32_t nnz, hipStream_t stream) {
+    if (vt == kBF16) return up_typed(x, off, idx, static_cast<const uint16_t*>(w), b, act, d, h, n, ld, nnz, stream);
+    return up_typed(x, off, idx, static_cast<const float*>(w), b, act, d, h, n, ld, nnz, stream);
+}
+
+hipError_t launch_down_edges(int vt, const float* act, const int32_t* off, const int16_t* hid, const void* v,
+                             const float* bias, float* y, uint32_t d, uint32_t h, uint32_t n, uint32_t ld, uint32_t nnz,
+                             hipStream_t stream) {
+    if (vt == kBF16) return down_typed(act, off, hid, static_cast<const uint16_t*>(v), bias, y, d, h, n, ld, nnz, stream);
+    return down_typed(act, off, hid, static_cast<const float*>(v), bias, y, d, h, n, ld, nnz, stream);
+}
+
+}  // namespace hffn

@@ -15,6 +15,8 @@ constexpr uint32_t kMaxTokens = 1u << 18;  // largest n of any entry point
 // Tokens per pass of the lane-per-slot ("edges") kernels: 1, 2, 4, or 8 for n > 4.
 constexpr uint32_t kEdgesMaxTokens = 8;
 inline uint32_t edges_tokens(uint32_t n) { return n <= 1 ? 1 : n <= 2 ? 2 : n <= 4 ? 4 : 8; }
+// The down edges kernel stages act of its tokens in LDS up to this many bytes (else gathers it from L2).
+constexpr size_t kEdgesStageBytes = 32768;
 
 // x[rows, cols] (row stride in_ld) -> out[cols, rows] (row stride out_ld).
 hipError_t launch_transpose(const float* in, float* out, uint32_t rows, uint32_t cols, uint32_t in_ld,
@@ -24,7 +26,7 @@ hipError_t launch_transpose(const float* in, float* out, uint32_t rows, uint32_t
 // [n, d_model]; `rows`: one wave per neuron, lanes over tokens, x feature-major x_t[d_model, ld].
 // Activations hidden-major act[d_ff, ld].
 hipError_t launch_up_edges(int vt, const float* x, const int32_t* off, const int16_t* idx, const void* w,
-                           const float* b, float* act, uint32_t d, uint32_t h, uint32_t n, uint32_t ld,
+                           const float* b, float* act, uint32_t d, uint32_t h, uint32_t n, uint32_t ld, uint32_t nnz,
                            hipStream_t stream);
 hipError_t launch_up_rows(int vt, const float* x_t, const int32_t* off, const int16_t* idx, const void* w,
                           const float* b, float* act, uint32_t d, uint32_t h, uint32_t n, uint32_t ld,
@@ -34,7 +36,7 @@ hipError_t launch_up_rows(int vt, const float* x_t, const int32_t* off, const in
 // slots, writes y[n, d_model]; `rows`: one wave per output, lanes over tokens, writes
 // y_t[d_model, ld] (the caller transposes).
 hipError_t launch_down_edges(int vt, const float* act, const int32_t* off, const int16_t* hid, const void* v,
-                             const float* bias, float* y, uint32_t d, uint32_t n, uint32_t ld,
+                             const float* bias, float* y, uint32_t d, uint32_t h, uint32_t n, uint32_t ld, uint32_t nnz,
                              hipStream_t stream);
 hipError_t launch_down_rows(int vt, const float* act, const int32_t* off, const int16_t* hid, const void* v,
                             const float* bias, float* y_t, uint32_t d, uint32_t n, uint32_t ld,

@@ -72,6 +72,12 @@ def _value_type(tensor: torch.Tensor, name: str) -> int:
         raise ValueError(f"{name} must be float32 or bfloat16, not {tensor.dtype}") from None
 
 
+def _aligned(tensor: torch.Tensor, alignment: int = 16) -> torch.Tensor:
+    """The tensor itself when its data starts on an `alignment`-byte boundary (the edges kernels load 4 slots at a
+    time), else an aligned copy."""
+    return tensor if tensor.data_ptr() % alignment == 0 else tensor.clone()
+
+
 def _rows_strictly_increasing(offsets: torch.Tensor, index: torch.Tensor) -> bool:
     """Whether every row's indices increase strictly (distinct, sorted): what the densified planes assume."""
     if index.numel() < 2:
@@ -168,8 +174,9 @@ class HFFNRuntime:
         self._lib = _lib.load()
         self._tensors = []
         self._args = []
+        self._nnz = []
         for layer in layers:
-            tensors = {name: getattr(layer, name).to(self.device).contiguous() for name in _ARRAYS}
+            tensors = {name: _aligned(getattr(layer, name).to(self.device).contiguous()) for name in _ARRAYS}
             _check_side("up", tensors["up_offsets"], tensors["up_idx"], tensors["up_val"], self.d_ff, self.d_model)
             _check_side("down", tensors["out_offsets"], tensors["out_hidden"], tensors["out_val"], self.d_model, self.d_ff)
             if tensors["up_val"].dtype != tensors["out_val"].dtype:
@@ -180,6 +187,7 @@ class HFFNRuntime:
             self._args.append((_value_type(tensors["up_val"], "up_val"),
                                *(tensors[name].data_ptr() for name in ("up_offsets", "up_idx", "up_val", "b_up",
                                                                        "out_offsets", "out_hidden", "out_val", "b_down"))))
+            self._nnz.append((tensors["up_idx"].numel(), tensors["out_hidden"].numel()))
         self.density = max(layer.up_idx.numel() + layer.out_hidden.numel() for layer in layers) / (2 * self.d_model * self.d_ff)
         self._planes: list[dict] | None = None
         if dense and self._mfma_eligible():
@@ -296,5 +304,6 @@ class HFFNRuntime:
                                                    self.d_model, self.d_ff, n, stream), "forward (mfma, mfma)")
             return
         _lib.check(self._lib.hffn_forward(_lib.UP_MODES[up], _lib.DOWN_MODES[down], value_type, x.data_ptr(), *model,
-                                          x_t, act, y_t, y, self.d_model, self.d_ff, n, leading_dim(n), stream),
+                                          x_t, act, y_t, y, self.d_model, self.d_ff, *self._nnz[index], n, leading_dim(n),
+                                          stream),
                    f"forward ({up}, {down})")

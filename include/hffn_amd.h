@@ -36,9 +36,10 @@ extern "C" {
 #define HFFN_VALUE_F32 0
 #define HFFN_VALUE_BF16 1
 
-/* Kernel shapes. EDGES: one wave per neuron/output, lanes over its slots, tokens taken nt at a time
- * (nt = 1, 2, 4 for n <= 4, else 8; ld must be a multiple of nt; the up input of nt tokens is staged
- * in LDS). ROWS: one wave per neuron/output, lanes over tokens. */
+/* Kernel shapes. EDGES: lanes over a row's slots, 4 slots per lane per load (index arrays 8-byte aligned, value
+ * arrays 16-byte (fp32) or 8-byte (bf16) aligned; nnz bounds the grouped loads), long rows split over up to 4 waves,
+ * tokens taken nt at a time (nt = 1, 2, 4 for n <= 4, else 8; ld must be a multiple of nt; the up input of nt tokens
+ * is staged in LDS). ROWS: one wave per neuron/output, lanes over tokens. nnz_up / nnz_down: slots of each store. */
 #define HFFN_UP_EDGES 1
 #define HFFN_UP_ROWS 2
 #define HFFN_DOWN_EDGES 1
@@ -66,8 +67,8 @@ int hffn_transpose(const float* in, float* out, uint32_t rows, uint32_t cols, ui
  * const short* idx, const float* w, const float* b, float* a, unsigned d, unsigned H, unsigned n)`
  * of runtime/gpu/nvidia/common/kernels/hffn_cuda/kernels.py:102-143 (launch: runtime.py:143-155). */
 int hffn_up(int mode, int value_type, const float* x, const int32_t* up_offsets, const int16_t* up_idx,
-            const void* up_val, const float* b_up, float* act, uint32_t d_model, uint32_t d_ff, uint32_t n, uint32_t ld,
-            void* stream);
+            const void* up_val, const float* b_up, float* act, uint32_t d_model, uint32_t d_ff, uint32_t nnz_up, uint32_t n,
+            uint32_t ld, void* stream);
 
 /* y[t, o] = sum_{q in [out_offsets[o], out_offsets[o+1])} out_val[q] * act[out_hidden[q], t] + b_down[o].
  * mode EDGES writes y token-major [n, d_model]; mode ROWS writes y feature-major [d_model, ld].
@@ -75,8 +76,8 @@ int hffn_up(int mode, int value_type, const float* x, const int32_t* up_offsets,
  * const float* v, const float* bias, float* y, unsigned d, unsigned n)` of
  * runtime/gpu/nvidia/common/kernels/hffn_cuda/kernels.py:145-191 (launch: runtime.py:156-162). */
 int hffn_down(int mode, int value_type, const float* act, const int32_t* out_offsets, const int16_t* out_hidden,
-              const void* out_val, const float* b_down, float* y, uint32_t d_model, uint32_t d_ff, uint32_t n,
-              uint32_t ld, void* stream);
+              const void* out_val, const float* b_down, float* y, uint32_t d_model, uint32_t d_ff, uint32_t nnz_down,
+              uint32_t n, uint32_t ld, void* stream);
 
 /* The whole layer for x[n, d_model] -> y[n, d_model]: the transposes the modes need, up, down.
  * x_t and y_t may be NULL when the modes do not use them. Replaces HFFNRuntime._launch
@@ -85,7 +86,8 @@ int hffn_down(int mode, int value_type, const float* act, const int32_t* out_off
 int hffn_forward(int up_mode, int down_mode, int value_type, const float* x, const int32_t* up_offsets,
                  const int16_t* up_idx, const void* up_val, const float* b_up, const int32_t* out_offsets,
                  const int16_t* out_hidden, const void* out_val, const float* b_down, float* x_t, float* act,
-                 float* y_t, float* y, uint32_t d_model, uint32_t d_ff, uint32_t n, uint32_t ld, void* stream);
+                 float* y_t, float* y, uint32_t d_model, uint32_t d_ff, uint32_t nnz_up, uint32_t nnz_down, uint32_t n,
+                 uint32_t ld, void* stream);
 
 /* Bytes of device workspace hffn_output_major needs for nnz down slots (host-only query). */
 int hffn_output_major_workspace(uint32_t nnz, uint32_t d_model, uint64_t* bytes);

@@ -42,18 +42,21 @@ def _expect_argument_error(status: int, fragment: str) -> None:
 def test_abi_refuses_bad_shapes_before_launching():
     lib = _lib.load()
     p = ctypes.c_void_p(16)  # never dereferenced: every call below fails validation first
-    _expect_argument_error(lib.hffn_up(1, 0, p, p, p, p, p, p, 17, 64, 1, 4, None), "d_model=17")
-    _expect_argument_error(lib.hffn_up(1, 0, p, p, p, p, p, p, 64, 0, 1, 4, None), "d_ff=0")
-    _expect_argument_error(lib.hffn_up(1, 0, p, p, p, p, p, p, 64, 64, 0, 4, None), "n=0")
-    _expect_argument_error(lib.hffn_up(1, 0, p, p, p, p, p, p, 64, 64, (1 << 18) + 1, 1 << 19, None), "unsupported token count")
-    _expect_argument_error(lib.hffn_up(1, 0, p, p, p, p, p, p, 64, 64, 5, 6, None), "ld=6")
-    _expect_argument_error(lib.hffn_up(1, 0, p, p, p, p, p, p, 64, 64, 5, 12, None), "multiple of 8")
-    _expect_argument_error(lib.hffn_up(9, 0, p, p, p, p, p, p, 64, 64, 1, 4, None), "unknown up mode")
-    _expect_argument_error(lib.hffn_up(1, 7, p, p, p, p, p, p, 64, 64, 1, 4, None), "unknown value type")
-    _expect_argument_error(lib.hffn_up(1, 0, None, p, p, p, p, p, 64, 64, 1, 4, None), "null pointer")
-    _expect_argument_error(lib.hffn_up(1, 0, p, p, p, p, p, p, 4096, 64, 8, 8, None), "LDS")
-    _expect_argument_error(lib.hffn_down(3, 0, p, p, p, p, p, p, 64, 64, 1, 4, None), "unknown down mode")
-    _expect_argument_error(lib.hffn_forward(2, 2, 0, p, p, p, p, p, p, p, p, p, None, p, p, p, 64, 64, 1, 4, None), "x_t")
+    _expect_argument_error(lib.hffn_up(1, 0, p, p, p, p, p, p, 17, 64, 64, 1, 4, None), "d_model=17")
+    _expect_argument_error(lib.hffn_up(1, 0, p, p, p, p, p, p, 64, 0, 64, 1, 4, None), "d_ff=0")
+    _expect_argument_error(lib.hffn_up(1, 0, p, p, p, p, p, p, 64, 64, 64, 0, 4, None), "n=0")
+    _expect_argument_error(lib.hffn_up(1, 0, p, p, p, p, p, p, 64, 64, 64, (1 << 18) + 1, 1 << 19, None), "unsupported token count")
+    _expect_argument_error(lib.hffn_up(1, 0, p, p, p, p, p, p, 64, 64, 64, 5, 6, None), "ld=6")
+    _expect_argument_error(lib.hffn_up(1, 0, p, p, p, p, p, p, 64, 64, 64, 5, 12, None), "multiple of 8")
+    _expect_argument_error(lib.hffn_up(9, 0, p, p, p, p, p, p, 64, 64, 64, 1, 4, None), "unknown up mode")
+    _expect_argument_error(lib.hffn_up(1, 7, p, p, p, p, p, p, 64, 64, 64, 1, 4, None), "unknown value type")
+    _expect_argument_error(lib.hffn_up(1, 0, None, p, p, p, p, p, 64, 64, 64, 1, 4, None), "null pointer")
+    _expect_argument_error(lib.hffn_up(1, 0, p, p, p, p, p, p, 4096, 64, 64, 8, 8, None), "LDS")
+    _expect_argument_error(lib.hffn_down(3, 0, p, p, p, p, p, p, 64, 64, 64, 1, 4, None), "unknown down mode")
+    odd = ctypes.c_void_p(18)
+    _expect_argument_error(lib.hffn_up(1, 0, p, p, odd, p, p, p, 64, 64, 64, 1, 4, None), "aligned")
+    _expect_argument_error(lib.hffn_down(1, 0, p, p, p, ctypes.c_void_p(24), p, p, 64, 64, 64, 1, 4, None), "aligned")
+    _expect_argument_error(lib.hffn_forward(2, 2, 0, p, p, p, p, p, p, p, p, p, None, p, p, p, 64, 64, 64, 64, 1, 4, None), "x_t")
     needed = ctypes.c_uint64(0)
     assert lib.hffn_output_major_workspace(2_097_152, 1024, ctypes.byref(needed)) == _lib.OK
     assert needed.value == 1024 * 1024 * 4
@@ -64,7 +67,8 @@ def test_abi_refuses_bad_shapes_before_launching():
 def test_edges_stage_limit():
     lib = _lib.load()
     assert lib.hffn_edges_supported(1024, 8) == 1
-    assert lib.hffn_edges_supported(2048, 8) == 1
+    assert lib.hffn_edges_supported(2048, 4) == 1
+    assert lib.hffn_edges_supported(2048, 8) == 0
     assert lib.hffn_edges_supported(2560, 8) == 0
     assert lib.hffn_edges_supported(2560, 4) == 1
 
