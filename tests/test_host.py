@@ -74,9 +74,9 @@ def test_edges_stage_limit():
 
 
 def test_policy():
-    assert [runtime.up_mode(n) for n in (1, 4, 8, 9, 64, 2048)] == ["edges"] * 3 + ["rows"] * 3
+    assert [runtime.up_mode(n) for n in (1, 4, 8, 9, 32, 33, 64, 2048)] == ["edges"] * 5 + ["rows"] * 3
     assert runtime.up_mode(8, 2560) == "rows" and runtime.up_mode(4, 2560) == "edges"
-    assert [runtime.down_mode(n, 4096) for n in (1, 8, 9, 2048)] == ["edges", "edges", "rows", "rows"]
+    assert [runtime.down_mode(n, 4096) for n in (1, 8, 32, 33, 2048)] == ["edges"] * 3 + ["rows"] * 2
     assert [runtime.leading_dim(n) for n in (1, 2, 3, 4, 5, 8, 9, 2048, 2049)] == [4, 4, 4, 4, 8, 8, 16, 2048, 2056]
 
 
