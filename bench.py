@@ -101,7 +101,7 @@ def time_kernels(runtime, x: torch.Tensor, steps: int, copies: int) -> dict:
     if up == "mfma":
         names = ["up", "down"]
         totals = {name: 0.0 for name in names}
-        work = runtime._mfma_work.data_ptr()
+        work, work_bytes = runtime._mfma_work.data_ptr(), 4 * runtime._mfma_work.numel()
         for step in range(steps):
             index = step % copies
             value_type = runtime._args[index][0]
@@ -109,11 +109,11 @@ def time_kernels(runtime, x: torch.Tensor, steps: int, copies: int) -> dict:
             events = [torch.cuda.Event(enable_timing=True) for _ in range(3)]
             events[0].record()
             _lib.check(lib.hffn_mfma_up(value_type, x.data_ptr(), planes["up"].data_ptr(), planes["up_binades"].data_ptr(),
-                                        tensors["b_up"].data_ptr(), act, work, runtime.d_model, runtime.d_ff, n, stream),
+                                        tensors["b_up"].data_ptr(), work, work_bytes, runtime.d_model, runtime.d_ff, n, stream),
                        "mfma up")
             events[1].record()
-            _lib.check(lib.hffn_mfma_down(value_type, act, planes["down"].data_ptr(), planes["down_binades"].data_ptr(),
-                                          tensors["b_down"].data_ptr(), y, work, runtime.d_model, runtime.d_ff, n, stream),
+            _lib.check(lib.hffn_mfma_down(value_type, planes["down"].data_ptr(), planes["down_binades"].data_ptr(),
+                                          tensors["b_down"].data_ptr(), y, work, work_bytes, runtime.d_model, runtime.d_ff, n, stream),
                        "mfma down")
             events[2].record()
             torch.cuda.synchronize()

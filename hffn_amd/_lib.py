@@ -10,7 +10,7 @@ import ctypes
 from pathlib import Path
 
 LIBRARY = Path(__file__).resolve().with_name("libhffn_amd.so")
-ABI_VERSION = 1
+ABI_VERSION = 2
 
 OK = 0
 VALUE_F32, VALUE_BF16 = 0, 1
@@ -34,9 +34,9 @@ SIGNATURES = {
     "hffn_dense_planes_bytes": [_U32, _U32, ctypes.POINTER(_U64)],
     "hffn_densify": [_I, _P, _P, _P, _U32, _U32, _P, _P, _P],
     "hffn_mfma_workspace": [_U32, _U32, _U32, ctypes.POINTER(_U64)],
-    "hffn_mfma_up": [_I, _P, _P, _P, _P, _P, _P, _U32, _U32, _U32, _P],
-    "hffn_mfma_down": [_I, _P, _P, _P, _P, _P, _P, _U32, _U32, _U32, _P],
-    "hffn_forward_mfma": [_I] + [_P] * 10 + [_U32] * 3 + [_P],
+    "hffn_mfma_up": [_I, _P, _P, _P, _P, _P, _U64, _U32, _U32, _U32, _P],
+    "hffn_mfma_down": [_I, _P, _P, _P, _P, _P, _U64, _U32, _U32, _U32, _P],
+    "hffn_forward_mfma": [_I] + [_P] * 8 + [_U64, _P] + [_U32] * 3 + [_P],
 }
 
 

@@ -195,7 +195,7 @@ int check_mfma(int value_type, uint32_t d_model, uint32_t d_ff, uint32_t n) {
     if (int status = check_shape(d_model, d_ff, n, (n + 3) / 4 * 4)) return status;
     if (!valid_value_type(value_type)) return fail(HFFN_ERROR_ARGUMENT, "unknown value type %d", value_type);
     if (!hffn_mfma_supported(d_model, d_ff))
-        return fail(HFFN_ERROR_ARGUMENT, "mfma path: d_model=%u and d_ff=%u must be multiples of 128", d_model, d_ff);
+        return fail(HFFN_ERROR_ARGUMENT, "mfma path: d_model=%u and d_ff=%u must be multiples of 256", d_model, d_ff);
     return HFFN_OK;
 }
 }  // namespace
@@ -207,27 +207,41 @@ int hffn_mfma_workspace(uint32_t n, uint32_t d_model, uint32_t d_ff, uint64_t* b
     return HFFN_OK;
 }
 
+namespace {
+int check_workspace(uint64_t bytes, uint32_t d_model, uint32_t d_ff, uint32_t n, const char* what) {
+    const uint64_t needed = hffn::mfma_workspace_bytes(n, d_model, d_ff);
+    if (bytes < needed)
+        return fail(HFFN_ERROR_ARGUMENT, "%s: workspace of %llu bytes, %llu needed for n=%u", what, static_cast<unsigned long long>(bytes),
+                    static_cast<unsigned long long>(needed), n);
+    return HFFN_OK;
+}
+}  // namespace
+
 int hffn_mfma_up(int value_type, const float* x, const void* up_planes, const int32_t* up_binades, const float* b_up,
-                 float* act, void* workspace, uint32_t d_model, uint32_t d_ff, uint32_t n, void* stream) {
+                 void* workspace, uint64_t workspace_bytes, uint32_t d_model, uint32_t d_ff, uint32_t n, void* stream) {
     if (int status = check_mfma(value_type, d_model, d_ff, n)) return status;
-    if (!x || !up_planes || !up_binades || !b_up || !act || !workspace) return fail(HFFN_ERROR_ARGUMENT, "mfma_up: null pointer");
-    return launched(hffn::launch_mfma_up(value_type, x, up_planes, up_binades, b_up, act, workspace, n, d_model, d_ff,
+    if (!x || !up_planes || !up_binades || !b_up || !workspace) return fail(HFFN_ERROR_ARGUMENT, "mfma_up: null pointer");
+    if (reinterpret_cast<uintptr_t>(x) % 16 != 0) return fail(HFFN_ERROR_ARGUMENT, "mfma_up: x must be 16-byte aligned");
+    if (int status = check_workspace(workspace_bytes, d_model, d_ff, n, "mfma_up")) return status;
+    return launched(hffn::launch_mfma_up(value_type, x, up_planes, up_binades, b_up, workspace, n, d_model, d_ff,
                                          static_cast<hipStream_t>(stream)), "mfma up");
 }
 
-int hffn_mfma_down(int value_type, const float* act, const void* down_planes, const int32_t* down_binades, const float* b_down,
-                   float* y, void* workspace, uint32_t d_model, uint32_t d_ff, uint32_t n, void* stream) {
+int hffn_mfma_down(int value_type, const void* down_planes, const int32_t* down_binades, const float* b_down, float* y,
+                   void* workspace, uint64_t workspace_bytes, uint32_t d_model, uint32_t d_ff, uint32_t n, void* stream) {
     if (int status = check_mfma(value_type, d_model, d_ff, n)) return status;
-    if (!act || !down_planes || !down_binades || !b_down || !y || !workspace) return fail(HFFN_ERROR_ARGUMENT, "mfma_down: null pointer");
-    return launched(hffn::launch_mfma_down(value_type, act, down_planes, down_binades, b_down, y, workspace, n, d_model, d_ff,
+    if (!down_planes || !down_binades || !b_down || !y || !workspace) return fail(HFFN_ERROR_ARGUMENT, "mfma_down: null pointer");
+    if (int status = check_workspace(workspace_bytes, d_model, d_ff, n, "mfma_down")) return status;
+    return launched(hffn::launch_mfma_down(value_type, down_planes, down_binades, b_down, y, workspace, n, d_model, d_ff,
                                            static_cast<hipStream_t>(stream)), "mfma down");
 }
 
 int hffn_forward_mfma(int value_type, const float* x, const void* up_planes, const int32_t* up_binades, const float* b_up,
-                      const void* down_planes, const int32_t* down_binades, const float* b_down, float* act, void* workspace,
-                      float* y, uint32_t d_model, uint32_t d_ff, uint32_t n, void* stream) {
-    if (int status = hffn_mfma_up(value_type, x, up_planes, up_binades, b_up, act, workspace, d_model, d_ff, n, stream)) return status;
-    return hffn_mfma_down(value_type, act, down_planes, down_binades, b_down, y, workspace, d_model, d_ff, n, stream);
+                      const void* down_planes, const int32_t* down_binades, const float* b_down, void* workspace,
+                      uint64_t workspace_bytes, float* y, uint32_t d_model, uint32_t d_ff, uint32_t n, void* stream) {
+    if (int status = hffn_mfma_up(value_type, x, up_planes, up_binades, b_up, workspace, workspace_bytes, d_model, d_ff, n, stream))
+        return status;
+    return hffn_mfma_down(value_type, down_planes, down_binades, b_down, y, workspace, workspace_bytes, d_model, d_ff, n, stream);
 }
 
 }  // extern "C"

@@ -48,17 +48,18 @@ hipError_t launch_output_major(int vt, const int32_t* down_offsets, const int16_
                                uint32_t d, uint32_t h, uint32_t nnz, int32_t* out_offsets, int16_t* out_hidden,
                                void* out_val, int32_t* counts, hipStream_t stream);
 
-// Tile-densified MFMA path (mfma.hip). Planes: fp16 hi/lo of a dense [rows, k] matrix, tile-major.
-// The workspace holds the token binades, the activation block binades, the split-K counters (zero between calls)
-// and the split-K partial sums; it must be zero-filled before its first use.
+// Tile-densified MFMA path (mfma.hip). Planes: fp16 hi/lo of a dense [rows, k] matrix, K-chunk-major.
+// The workspace holds the split-K counters (zero between calls), the token and activation binades, the input and
+// activation planes and the split-K partial sums; it must be zero-filled before its first use. The up launcher
+// leaves the activations in the workspace, where the down launcher reads them.
 size_t dense_plane_halves(uint32_t rows, uint32_t k);
 bool mfma_shape_supported(uint32_t d, uint32_t h);
 size_t mfma_workspace_bytes(uint32_t n, uint32_t d, uint32_t h);
 hipError_t launch_densify(int vt, const int32_t* off, const int16_t* idx, const void* val, uint32_t rows, uint32_t k,
                           void* planes, int32_t* exps, hipStream_t stream);
-hipError_t launch_mfma_up(int vt, const float* x, const void* planes, const int32_t* w_exp, const float* b_up, float* act,
-                          void* workspace, uint32_t n, uint32_t d, uint32_t h, hipStream_t stream);
-hipError_t launch_mfma_down(int vt, const float* act, const void* planes, const int32_t* v_exp, const float* b_down, float* y,
-                            void* workspace, uint32_t n, uint32_t d, uint32_t h, hipStream_t stream);
+hipError_t launch_mfma_up(int vt, const float* x, const void* planes, const int32_t* w_exp, const float* b_up, void* workspace,
+                          uint32_t n, uint32_t d, uint32_t h, hipStream_t stream);
+hipError_t launch_mfma_down(int vt, const void* planes, const int32_t* v_exp, const float* b_down, float* y, void* workspace,
+                            uint32_t n, uint32_t d, uint32_t h, hipStream_t stream);
 
 }  // namespace hffn

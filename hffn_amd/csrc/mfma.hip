@@ -2,29 +2,29 @@
 //
 // At high density and large token counts a tile of neurons has a nearly dense union support, so the layer is two
 // contractions: Z[N, d_ff] = X[N, d_model] W_up^T, A = gelu(Z + b_up), Y[N, d_model] = A W_down^T + b_down.
-// The weights are densified once at load into fp16 "planes" (hi and lo parts, each row scaled by a power of two so
-// that its largest entry lies in [1, 2)); activations are split the same way on the fly while they are staged in
-// LDS, with one power of two per token row. Each product is  a_hi b_hi + a_hi b_lo + a_lo b_hi  accumulated in fp32
-// by the MFMA units (the lo*lo term, ~2^-22 relative, is dropped; bf16 weights are exact in the hi plane and take
-// the first two terms). The powers of two are undone exactly in the epilogue.
+// Every operand enters the MFMA units as a pair of fp16 "planes" (hi and lo parts) scaled by powers of two: the
+// weights are densified once at load (one power of two per row, so that its largest entry lies in [1, 2)); the input
+// X is split by a small kernel before the up GEMM (one power of two per token); the activations are split by the up
+// GEMM's epilogue (one power of two per token and 128-neuron block). Each product is  a_hi b_hi + a_hi b_lo +
+// a_lo b_hi  accumulated in fp32 (the lo*lo term, ~2^-22 relative, is dropped; bf16 weights are exact in the hi
+// plane and take the first and last terms). The powers of two are undone exactly: the down GEMM rescales its
+// accumulators at each 128-wide k block by the ratio of the blocks' powers of two, and the epilogues apply the last.
 //
 // Plane layout (K-chunk-major): k is cut into 32-wide k-tiles and each k-tile into four 16-byte chunks of 8 halves;
 // for k-tile kt, part p (0 hi, 1 lo) and chunk c, the chunks of all rows follow one another:
 //   planes[((((kt * 2 + p) * 4 + c) * rows + n) * 8 + k % 8]   with c = (k % 32) / 8.
-// A block's B tile of BN rows is 8 runs of BN * 16 contiguous bytes, and LDS keeps the same order, so the MFMA
-// operand reads (32 lanes on 32 consecutive rows of one chunk) and the staging writes touch consecutive 16-byte
-// blocks: no LDS bank conflicts, no padding.
+// A block's tile of B rows is 8 runs of B * 16 contiguous bytes, and LDS keeps the same order, so the MFMA operand
+// reads (32 lanes on 32 consecutive rows of one chunk) and the staging writes touch consecutive 16-byte blocks: no
+// LDS bank conflicts, no padding. Token planes have a row count padded to kRowPad (rows past N are zeros in X and
+// hold gelu(b_up) in A; their outputs are never stored).
 //
 // GEMM blocks: 4 waves in 2 x 2, each wave a (32 MI) x (32 NI) tile of 32x32 MFMA accumulators; the k loop stages
-// 32-wide k-tiles through double-buffered LDS (one barrier per k-tile, the next tile's global loads in flight during
-// the current tile's MFMAs). The grid is one-dimensional and remapped so that each of the 8 XCDs works on one compact
-// group of output tiles (its L2 then holds the A rows and B columns those tiles share). A down projection with very
-// few output tiles splits K over 2 blocks per tile; the block that finishes a tile last (an integer counter per tile)
-// adds the partials in split order, so the result does not depend on which block ends first.
-//
-// The up epilogue applies bias and exact GELU, writes the activations token-major [N, d_ff] in fp32, and, per token
-// row and block of BN neurons, the binade of the largest activation; the down kernel takes, per token, the largest of
-// those binades as its row scale.
+// 32-wide k-tiles of both planes through double-buffered LDS with plain 16-byte copies (one barrier per k-tile, the
+// next tile's global loads in flight during the current tile's MFMAs). The grid is one-dimensional and remapped so
+// that each of the 8 XCDs works on one compact group of output tiles (its L2 then holds the A rows and B columns
+// those tiles share). A down projection with very few output tiles splits K over 2 blocks per tile; the block that
+// finishes a tile last (an integer counter per tile) adds the partials in split order, so the result does not depend
+// on which block ends first.
 #include "common.hpp"
 #include "launch.hpp"
 
@@ -33,12 +33,16 @@ namespace {
 
 typedef _Float16 half8 __attribute__((ext_vector_type(8)));
 typedef float floatx16 __attribute__((ext_vector_type(16)));
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));  // 16 bytes of plane: 8 halves
 
 constexpr int kThreads = 256;
 constexpr int kBK = 32;          // k per staged step, one plane k-tile
 constexpr int kRuns = 8;         // (part, chunk) runs of a k-tile
 constexpr uint32_t kXcds = 8;    // MI355X: 8 XCDs, workgroups dispatched round-robin over them
 constexpr uint32_t kGroupM = 4;  // output-tile rows per group of the tile order
+constexpr uint32_t kRowPad = 256;  // token planes hold a multiple of this many rows
+constexpr uint32_t kActBlock = 128;  // neurons per activation power of two (the up GEMM's column tile)
+constexpr uint32_t kKtPerActBlock = kActBlock / kBK;
 
 // floor(log2(m)) of a non-negative float given by its bits; 0 for zero (any scale is exact for zeros).
 __device__ __forceinline__ int binade_of_bits(uint32_t bits) {
@@ -52,19 +56,48 @@ __device__ __forceinline__ void split(float v, _Float16& hi, _Float16& lo) {
     lo = static_cast<_Float16>(v - static_cast<float>(hi));
 }
 
-// ------------------------------------------------------------------------------------------ row binades
-// e[row] = binade of max |x[row, :]| ; one wave per row.
-__global__ __launch_bounds__(kThreads) void row_binade_kernel(const float* __restrict__ x, uint32_t rows, uint32_t cols,
-                                                             int32_t* __restrict__ e) {
-    const uint32_t row = blockIdx.x * (kThreads / kWave) + threadIdx.x / kWave;
-    if (row >= rows) return;
-    const uint32_t lane = threadIdx.x % kWave;
-    const float* p = x + static_cast<size_t>(row) * cols;
+// Index of element (row, k) of part p (0 hi, 1 lo) in planes of `rows` rows.
+__device__ __forceinline__ size_t plane_at(uint32_t rows, uint32_t row, uint32_t k, uint32_t p) {
+    return ((static_cast<size_t>(k / kBK) * kRuns + p * 4 + (k % kBK) / 8) * rows + row) * 8 + k % 8;
+}
+
+// ------------------------------------------------------------------------------------------ input planes
+// X [M, K] fp32 -> planes of X [rows_pad, K] and e[row] = binade of max |x[row, :]| (rows past M: zeros, e = 0).
+// One wave per row: the row's largest |x|, then each lane splits 8 consecutive k per step (a 16-byte chunk per part;
+// the 4 rows of a block fill 64 contiguous bytes of each chunk run).
+constexpr uint32_t kSplitRows = kThreads / kWave;
+__global__ __launch_bounds__(kThreads) void split_rows_kernel(const float* __restrict__ x, uint32_t M, uint32_t rows_pad,
+                                                             uint32_t K, _Float16* __restrict__ planes, int32_t* __restrict__ e) {
+    const uint32_t lane = threadIdx.x % kWave, row = blockIdx.x * kSplitRows + threadIdx.x / kWave;
+    const float* p = x + static_cast<size_t>(row) * K;
     uint32_t m = 0;
-    for (uint32_t c = lane; c < cols; c += kWave) m = max(m, abs_bits(p[c]));
+    if (row < M)
+        for (uint32_t c = lane * 4; c < K; c += kWave * 4) {
+            const float4 u = *reinterpret_cast<const float4*>(p + c);
+            m = max(max(m, max(abs_bits(u.x), abs_bits(u.y))), max(abs_bits(u.z), abs_bits(u.w)));
+        }
 #pragma unroll
     for (int s = 32; s >= 1; s >>= 1) m = max(m, static_cast<uint32_t>(__shfl_xor(static_cast<int>(m), s, kWave)));
-    if (lane == 0) e[row] = binade_of_bits(m);
+    const int be = binade_of_bits(m);
+    if (lane == 0) e[row] = be;
+    const float scale = ldexpf(1.0f, -be);
+    for (uint32_t q = lane; q < K / 8; q += kWave) {
+        float v[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+        if (row < M) {
+            const float4 u = *reinterpret_cast<const float4*>(p + q * 8), w = *reinterpret_cast<const float4*>(p + q * 8 + 4);
+            v[0] = u.x; v[1] = u.y; v[2] = u.z; v[3] = u.w; v[4] = w.x; v[5] = w.y; v[6] = w.z; v[7] = w.w;
+        }
+        half8 h, l;
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+            _Float16 hh, ll;
+            split(v[i] * scale, hh, ll);
+            h[i] = hh;
+            l[i] = ll;
+        }
+        *reinterpret_cast<half8*>(planes + plane_at(rows_pad, row, q * 8, 0)) = h;
+        *reinterpret_cast<half8*>(planes + plane_at(rows_pad, row, q * 8, 1)) = l;
+    }
 }
 
 // --------------------------------------------------------------------------------------------- densify
@@ -130,109 +163,84 @@ __device__ __forceinline__ Tile tile_of(uint32_t id, uint32_t tiles_m, uint32_t 
     return tile;
 }
 
+// One k-tile of a block's operands in flight: ARPT 16-byte chunks of the A planes and BRPT of the B planes per thread.
 template <int ARPT, int BRPT>
 struct StageRegs {
-    float4 a[ARPT][2];
-    uint4 b[BRPT];
+    u32x4 a[ARPT];
+    u32x4 b[BRPT];
 };
 
-// Global loads of k-tile kt: 8 floats of A from rows row0 + 16 j (zeros past M), BRPT 16-byte chunks of B.
+// Global loads of k-tile kt: thread t copies run t / 32 (part, chunk) of rows t % 32 + 32 j of each operand.
 template <int ARPT, int BRPT>
-__device__ __forceinline__ void load_stage(StageRegs<ARPT, BRPT>& r, const float* a_src, uint32_t row0, uint32_t M, uint32_t K,
-                                           const _Float16* b_src, size_t b_stride, uint32_t kt) {
+__device__ __forceinline__ void load_stage(StageRegs<ARPT, BRPT>& r, const _Float16* a_src, size_t a_stride, const _Float16* b_src,
+                                           size_t b_stride, uint32_t kt) {
 #pragma unroll
-    for (int j = 0; j < ARPT; ++j) {
-        if (row0 + 16 * j < M) {
-            const float* p = a_src + static_cast<size_t>(16 * j) * K + kt * kBK;
-            r.a[j][0] = *reinterpret_cast<const float4*>(p);
-            r.a[j][1] = *reinterpret_cast<const float4*>(p + 4);
-        } else {
-            r.a[j][0] = make_float4(0.f, 0.f, 0.f, 0.f);
-            r.a[j][1] = make_float4(0.f, 0.f, 0.f, 0.f);
-        }
-    }
+    for (int j = 0; j < ARPT; ++j) r.a[j] = *reinterpret_cast<const u32x4*>(a_src + kt * a_stride + 32 * j * 8);
 #pragma unroll
-    for (int j = 0; j < BRPT; ++j) r.b[j] = *reinterpret_cast<const uint4*>(b_src + kt * b_stride + 32 * j * 8);
+    for (int j = 0; j < BRPT; ++j) r.b[j] = *reinterpret_cast<const u32x4*>(b_src + kt * b_stride + 32 * j * 8);
 }
 
-// LDS stores of a staged k-tile: A split into hi/lo halves with its row's power of two, B copied.
 template <int BM, int BN, int ARPT, int BRPT>
-__device__ __forceinline__ void store_stage(const StageRegs<ARPT, BRPT>& r, _Float16* s_a, _Float16* s_b, uint32_t a_chunk,
-                                            uint32_t a_row0, const int32_t* row_e, uint32_t b_run, uint32_t b_row) {
+__device__ __forceinline__ void store_stage(const StageRegs<ARPT, BRPT>& r, _Float16* s_a, _Float16* s_b, uint32_t run,
+                                            uint32_t row) {
 #pragma unroll
-    for (int j = 0; j < ARPT; ++j) {
-        const uint32_t row = a_row0 + 16 * j;
-        const float scale = ldexpf(1.0f, -row_e[row]);
-        const float v[8] = {r.a[j][0].x, r.a[j][0].y, r.a[j][0].z, r.a[j][0].w, r.a[j][1].x, r.a[j][1].y, r.a[j][1].z, r.a[j][1].w};
-        half8 h, l;
+    for (int j = 0; j < ARPT; ++j) *reinterpret_cast<u32x4*>(s_a + (run * BM + row + 32 * j) * 8) = r.a[j];
 #pragma unroll
-        for (int e = 0; e < 8; ++e) {
-            _Float16 hh, ll;
-            split(v[e] * scale, hh, ll);
-            h[e] = hh;
-            l[e] = ll;
-        }
-        *reinterpret_cast<half8*>(s_a + (a_chunk * BM + row) * 8) = h;
-        *reinterpret_cast<half8*>(s_a + ((4 + a_chunk) * BM + row) * 8) = l;
-    }
-#pragma unroll
-    for (int j = 0; j < BRPT; ++j) *reinterpret_cast<uint4*>(s_b + (b_run * BN + b_row + 32 * j) * 8) = r.b[j];
+    for (int j = 0; j < BRPT; ++j) *reinterpret_cast<u32x4*>(s_b + (run * BN + row + 32 * j) * 8) = r.b[j];
 }
 
-template <Epi EPI, int MI, int NI, bool LO_B, int SPLITS>
-__global__ __launch_bounds__(kThreads) void gemm_split_kernel(
-    const float* __restrict__ a,          // [M, K] fp32 row-major
-    const int32_t* __restrict__ a_exp,    // Up: [M] row binades; Down: [M, a_blocks] block binades (max taken here)
-    uint32_t a_blocks,
-    const _Float16* __restrict__ planes,  // tile-major planes of B [Ncol, K]
-    const int32_t* __restrict__ b_exp,    // [Ncol]
-    const float* __restrict__ bias,       // [Ncol]
-    float* __restrict__ out,              // [M, Ncol] fp32 row-major
-    int32_t* __restrict__ out_exp,        // Up: [M, Ncol / BN] activation block binades
-    float* __restrict__ partials,         // SPLITS > 1: [SPLITS, M, Ncol] scaled partial sums
-    int32_t* __restrict__ counters,       // SPLITS > 1: [tiles], zero between calls
-    uint32_t M, uint32_t Ncol, uint32_t K) {
-    constexpr int BM = 64 * MI, BN = 64 * NI;
-    constexpr int ARPT = BM / 64;                    // A rows per staging thread (16 rows x 4 chunks per wave pass)
-    constexpr int BRPT = BN / 32;                    // B rows per staging thread (32 rows x 8 runs per block pass)
+// Row m (within the block tile) of accumulator register r of tile row i of wave row wm, lane `lane`: accumulator r
+// of a 32x32 tile holds row 8 (r / 4) + 4 (lane / 32) + r % 4 and column lane % 32.
+template <int BM>
+__device__ __forceinline__ uint32_t acc_row(uint32_t wm, int i, int r, uint32_t lane) {
+    return wm * (BM / 2) + i * 32 + 8 * (r / 4) + 4 * (lane / 32) + r % 4;
+}
 
-    // [buffer][part][chunk][row][8 halves]
-    __shared__ __attribute__((aligned(16))) _Float16 s_a[2][kRuns * BM * 8];
-    __shared__ __attribute__((aligned(16))) _Float16 s_b[2][kRuns * BN * 8];
-    __shared__ int32_t row_e[BM];
+// C[M, Ncol] = A[M, K] B[Ncol, K]^T from planes. Up: A = X planes (power of two per row), epilogue bias + GELU,
+// writes the activation planes (K-chunk-major over the d_ff neurons) and one power of two per (row, BN block).
+// Down: A = activation planes (power of two per row and kActBlock-wide k block), epilogue bias, writes Y fp32.
+template <Epi EPI, int MI, int NI, bool LO_B, int SPLITS>
+__global__ __launch_bounds__(kThreads) void gemm_planes_kernel(
+    const _Float16* __restrict__ a_planes,  // [K / 32][8][rows_pad][8]
+    const int32_t* __restrict__ a_exp,      // Up: [rows_pad]; Down: [rows_pad, K / kActBlock]
+    const _Float16* __restrict__ b_planes,  // [K / 32][8][Ncol][8]
+    const int32_t* __restrict__ b_exp,      // [Ncol]
+    const float* __restrict__ bias,         // [Ncol]
+    float* __restrict__ out,                // Down: [M, Ncol] fp32 row-major
+    _Float16* __restrict__ out_planes,      // Up: activation planes [Ncol / 32][8][rows_pad][8]
+    int32_t* __restrict__ out_exp,          // Up: [rows_pad, Ncol / BN] activation block binades
+    float* __restrict__ partials,           // SPLITS > 1: [SPLITS, M, Ncol] partial sums
+    int32_t* __restrict__ counters,         // SPLITS > 1: [tiles], zero between calls
+    uint32_t M, uint32_t rows_pad, uint32_t Ncol, uint32_t K) {
+    constexpr int BM = 64 * MI, BN = 64 * NI;
+    constexpr int ARPT = BM / 32, BRPT = BN / 32;  // chunks per thread and k-tile (8 runs x 32 rows per block pass)
+
+    // staged k-tiles, [buffer][part][chunk][row][8 halves] of A then of B; the up epilogue reuses it for its output
+    __shared__ __attribute__((aligned(16))) _Float16 smem[2 * kRuns * (BM + BN) * 8];
+    const auto s_a = [&](uint32_t buffer) { return smem + buffer * (kRuns * BM * 8); };
+    const auto s_b = [&](uint32_t buffer) { return smem + 2 * kRuns * BM * 8 + buffer * (kRuns * BN * 8); };
+    __shared__ int32_t row_e[2][BM];  // Up: [0] the row binades; Down: the row binades of the current / next k block
     __shared__ uint32_t row_max[2][BM];
     __shared__ int32_t last;
 
     const uint32_t tid = threadIdx.x, lane = tid % kWave, wave = tid / kWave;
     const uint32_t wm = wave / 2, wn = wave % 2;
-    const uint32_t tiles_m = (M + BM - 1) / BM, tiles_n = Ncol / BN;
+    const uint32_t tiles_m = rows_pad / BM, tiles_n = Ncol / BN;
     const Tile tile = tile_of(blockIdx.x, tiles_m, tiles_n, SPLITS);
     const uint32_t m0 = tile.m * BM, n0 = tile.n * BN;
     const uint32_t ktiles = K / kBK;
     const uint32_t k_begin = tile.split * ktiles / SPLITS, k_end = (tile.split + 1) * ktiles / SPLITS;
+    const uint32_t a_kblocks = K / kActBlock;
 
     if (tid < BM) {
-        const uint32_t row = m0 + tid;
-        int e = 0;
-        if (row < M) {
-            if constexpr (EPI == Epi::Up) {
-                e = a_exp[row];
-            } else {
-                e = -1000;
-                for (uint32_t b = 0; b < a_blocks; ++b) e = max(e, a_exp[static_cast<size_t>(row) * a_blocks + b]);
-            }
-        }
-        row_e[tid] = e;
+        if constexpr (EPI == Epi::Up) row_e[0][tid] = a_exp[m0 + tid];
+        else row_e[(k_begin / kKtPerActBlock) & 1][tid] = a_exp[static_cast<size_t>(m0 + tid) * a_kblocks + k_begin / kKtPerActBlock];
     }
-    __syncthreads();
 
-    // staging assignments. A: lane l of wave w converts chunk l / 16 (8 floats) of rows w * 16 * ARPT + l % 16 + 16 j;
-    // B: thread t copies run t / 32 of rows t % 32 + 32 j.
-    const uint32_t a_chunk = lane / 16, a_row0 = wave * 16 * ARPT + lane % 16;
-    const float* a_src = a + static_cast<size_t>(m0 + a_row0) * K + a_chunk * 8;
-    const uint32_t b_run = tid / 32, b_row = tid % 32;
-    const _Float16* b_src = planes + (static_cast<size_t>(b_run) * Ncol + n0 + b_row) * 8;
-    const size_t b_stride = static_cast<size_t>(kRuns) * Ncol * 8;  // halves per k-tile
+    const uint32_t run = tid / 32, row = tid % 32;
+    const _Float16* a_src = a_planes + (static_cast<size_t>(run) * rows_pad + m0 + row) * 8;
+    const _Float16* b_src = b_planes + (static_cast<size_t>(run) * Ncol + n0 + row) * 8;
+    const size_t a_stride = static_cast<size_t>(kRuns) * rows_pad * 8, b_stride = static_cast<size_t>(kRuns) * Ncol * 8;
     StageRegs<ARPT, BRPT> regs;
 
     floatx16 acc[MI][NI];
@@ -243,14 +251,36 @@ __global__ __launch_bounds__(kThreads) void gemm_split_kernel(
 #pragma unroll
             for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.0f;
 
+    int32_t next_e = 0;  // Down: binades of the activation block of the k-tile in flight, when it starts one
     if (k_begin < k_end) {
-        load_stage<ARPT, BRPT>(regs, a_src, m0 + a_row0, M, K, b_src, b_stride, k_begin);
-        store_stage<BM, BN, ARPT, BRPT>(regs, s_a[0], s_b[0], a_chunk, a_row0, row_e, b_run, b_row);
-        if (k_begin + 1 < k_end) load_stage<ARPT, BRPT>(regs, a_src, m0 + a_row0, M, K, b_src, b_stride, k_begin + 1);
-        __syncthreads();
+        load_stage<ARPT, BRPT>(regs, a_src, a_stride, b_src, b_stride, k_begin);
+        store_stage<BM, BN, ARPT, BRPT>(regs, s_a(0), s_b(0), run, row);
+        if (k_begin + 1 < k_end) {
+            load_stage<ARPT, BRPT>(regs, a_src, a_stride, b_src, b_stride, k_begin + 1);
+            if constexpr (EPI == Epi::Down) {
+                if ((k_begin + 1) % kKtPerActBlock == 0 && tid < BM)
+                    next_e = a_exp[static_cast<size_t>(m0 + tid) * a_kblocks + (k_begin + 1) / kKtPerActBlock];
+            }
+        }
     }
+    __syncthreads();
     for (uint32_t kt = k_begin; kt < k_end; ++kt) {
         const int buf = (kt - k_begin) & 1;
+        if constexpr (EPI == Epi::Down) {
+            // a new activation block: bring the accumulators to its power of two (exact), and fetch the next one's
+            if (kt % kKtPerActBlock == 0 && kt != k_begin) {
+                const uint32_t kb = kt / kKtPerActBlock;
+#pragma unroll
+                for (int i = 0; i < MI; ++i)
+#pragma unroll
+                    for (int r = 0; r < 16; ++r) {
+                        const uint32_t m = acc_row<BM>(wm, i, r, lane);
+                        const float f = ldexpf(1.0f, row_e[(kb - 1) & 1][m] - row_e[kb & 1][m]);
+#pragma unroll
+                        for (int j = 0; j < NI; ++j) acc[i][j][r] *= f;
+                    }
+            }
+        }
 #pragma unroll
         for (int kk = 0; kk < 2; ++kk) {
             const uint32_t chunk = kk * 2 + lane / 32;
@@ -258,14 +288,14 @@ __global__ __launch_bounds__(kThreads) void gemm_split_kernel(
 #pragma unroll
             for (int i = 0; i < MI; ++i) {
                 const uint32_t r = wm * (BM / 2) + i * 32 + lane % 32;
-                ah[i] = *reinterpret_cast<const half8*>(s_a[buf] + (chunk * BM + r) * 8);
-                al[i] = *reinterpret_cast<const half8*>(s_a[buf] + ((4 + chunk) * BM + r) * 8);
+                ah[i] = *reinterpret_cast<const half8*>(s_a(buf) + (chunk * BM + r) * 8);
+                al[i] = *reinterpret_cast<const half8*>(s_a(buf) + ((4 + chunk) * BM + r) * 8);
             }
 #pragma unroll
             for (int j = 0; j < NI; ++j) {
                 const uint32_t r = wn * (BN / 2) + j * 32 + lane % 32;
-                bh[j] = *reinterpret_cast<const half8*>(s_b[buf] + (chunk * BN + r) * 8);
-                if constexpr (LO_B) bl[j] = *reinterpret_cast<const half8*>(s_b[buf] + ((4 + chunk) * BN + r) * 8);
+                bh[j] = *reinterpret_cast<const half8*>(s_b(buf) + (chunk * BN + r) * 8);
+                if constexpr (LO_B) bl[j] = *reinterpret_cast<const half8*>(s_b(buf) + ((4 + chunk) * BN + r) * 8);
             }
 #pragma unroll
             for (int i = 0; i < MI; ++i)
@@ -277,46 +307,97 @@ __global__ __launch_bounds__(kThreads) void gemm_split_kernel(
                 }
         }
         if (kt + 1 < k_end) {
-            store_stage<BM, BN, ARPT, BRPT>(regs, s_a[buf ^ 1], s_b[buf ^ 1], a_chunk, a_row0, row_e, b_run, b_row);
-            if (kt + 2 < k_end) load_stage<ARPT, BRPT>(regs, a_src, m0 + a_row0, M, K, b_src, b_stride, kt + 2);
+            store_stage<BM, BN, ARPT, BRPT>(regs, s_a(buf ^ 1), s_b(buf ^ 1), run, row);
+            if constexpr (EPI == Epi::Down) {
+                // the next activation block's binades travel with the stage loads: requested with k-tile 4 kb, they
+                // reach LDS with its store, one barrier before the rescale at k-tile 4 kb reads them
+                if ((kt + 1) % kKtPerActBlock == 0 && tid < BM) row_e[((kt + 1) / kKtPerActBlock) & 1][tid] = next_e;
+            }
+            if (kt + 2 < k_end) {
+                load_stage<ARPT, BRPT>(regs, a_src, a_stride, b_src, b_stride, kt + 2);
+                if constexpr (EPI == Epi::Down) {
+                    if ((kt + 2) % kKtPerActBlock == 0 && tid < BM)
+                        next_e = a_exp[static_cast<size_t>(m0 + tid) * a_kblocks + (kt + 2) / kKtPerActBlock];
+                }
+            }
         }
         __syncthreads();
     }
+    const int e_last = EPI == Epi::Up ? 0 : static_cast<int>(((k_end - 1) / kKtPerActBlock) & 1);
 
-    // epilogue: accumulator r of lane l of tile (i, j) holds row 8 (r / 4) + 4 (l / 32) + r % 4, column l % 32
     if constexpr (EPI == Epi::Up) {
-        uint32_t lane_max[MI][16];
+        // v = gelu(z + b): first its largest |v| per row over the tile's BN neurons (one tile row at a time, to keep
+        // few registers live), then v again, split with that row's power of two into the activation planes
 #pragma unroll
-        for (int i = 0; i < MI; ++i)
+        for (int i = 0; i < MI; ++i) {
+            uint32_t lane_max[16];
 #pragma unroll
-            for (int r = 0; r < 16; ++r) lane_max[i][r] = 0;
+            for (int r = 0; r < 16; ++r) lane_max[r] = 0;
 #pragma unroll
-        for (int j = 0; j < NI; ++j) {
-            const uint32_t col = n0 + wn * (BN / 2) + j * 32 + lane % 32;
-            const int ce = b_exp[col];
-            const float cb = bias[col];
+            for (int j = 0; j < NI; ++j) {
+                const uint32_t col = n0 + wn * (BN / 2) + j * 32 + lane % 32;
+                const int ce = b_exp[col];
+                const float cb = bias[col];
 #pragma unroll
-            for (int i = 0; i < MI; ++i)
-#pragma unroll
-                for (int r = 0; r < 16; ++r) {
-                    const uint32_t m = wm * (BM / 2) + i * 32 + 8 * (r / 4) + 4 * (lane / 32) + r % 4;
-                    const float v = gelu(ldexpf(acc[i][j][r], row_e[m] + ce) + cb);
-                    lane_max[i][r] = max(lane_max[i][r], abs_bits(v));
-                    if (m0 + m < M) out[static_cast<size_t>(m0 + m) * Ncol + col] = v;
-                }
-        }
-#pragma unroll
-        for (int i = 0; i < MI; ++i)
+                for (int r = 0; r < 16; ++r)
+                    lane_max[r] = max(lane_max[r],
+                                      abs_bits(gelu(ldexpf(acc[i][j][r], row_e[0][acc_row<BM>(wm, i, r, lane)] + ce) + cb)));
+            }
 #pragma unroll
             for (int r = 0; r < 16; ++r) {
-                uint32_t v = lane_max[i][r];
+                uint32_t v = lane_max[r];
 #pragma unroll
                 for (int s = 16; s >= 1; s >>= 1) v = max(v, static_cast<uint32_t>(__shfl_xor(static_cast<int>(v), s, kWave)));
-                if (lane % 32 == 0) row_max[wn][wm * (BM / 2) + i * 32 + 8 * (r / 4) + 4 * (lane / 32) + r % 4] = v;
+                if (lane % 32 == 0) row_max[wn][acc_row<BM>(wm, i, r, lane)] = v;
             }
+        }
         __syncthreads();
-        if (tid < BM && m0 + tid < M)
-            out_exp[static_cast<size_t>(m0 + tid) * tiles_n + tile.n] = binade_of_bits(max(row_max[0][tid], row_max[1][tid]));
+        if (tid < BM) {
+            const int e = binade_of_bits(max(row_max[0][tid], row_max[1][tid]));
+            row_e[1][tid] = e;
+            out_exp[static_cast<size_t>(m0 + tid) * tiles_n + tile.n] = e;
+        }
+        // the planes go out through LDS, half the block's rows (one wave row) at a time: the waves of that row store
+        // v as fp32 [row][col], then every thread splits 8 consecutive columns of one row and writes 16 bytes per
+        // part, 64 consecutive rows of one chunk per wave (1 KB contiguous)
+        constexpr uint32_t R = BM / 2, kLd = BN + 8;
+        static_assert(R * kLd * sizeof(float) <= sizeof(smem), "the epilogue tile fits the staging LDS");
+        float* tile_v = reinterpret_cast<float*>(smem);
+#pragma unroll
+        for (uint32_t half = 0; half < 2; ++half) {
+            __syncthreads();
+            if (wm == half) {
+#pragma unroll
+                for (int j = 0; j < NI; ++j) {
+                    const uint32_t c = wn * (BN / 2) + j * 32 + lane % 32;
+                    const int ce = b_exp[n0 + c];
+                    const float cb = bias[n0 + c];
+#pragma unroll
+                    for (int i = 0; i < MI; ++i)
+#pragma unroll
+                        for (int r = 0; r < 16; ++r) {
+                            const uint32_t m = acc_row<BM>(wm, i, r, lane);
+                            tile_v[(m - half * R) * kLd + c] = gelu(ldexpf(acc[i][j][r], row_e[0][m] + ce) + cb);
+                        }
+                }
+            }
+            __syncthreads();
+            for (uint32_t q = tid; q < R * (BN / 8); q += kThreads) {
+                const uint32_t m = q % R, chunk = q / R, k = n0 + chunk * 8;
+                const float scale = ldexpf(1.0f, -row_e[1][half * R + m]);
+                const float* src = tile_v + m * kLd + chunk * 8;
+                half8 h, l;
+#pragma unroll
+                for (int e = 0; e < 8; ++e) {
+                    _Float16 hh, ll;
+                    split(src[e] * scale, hh, ll);
+                    h[e] = hh;
+                    l[e] = ll;
+                }
+                *reinterpret_cast<half8*>(out_planes + plane_at(rows_pad, m0 + half * R + m, k, 0)) = h;
+                *reinterpret_cast<half8*>(out_planes + plane_at(rows_pad, m0 + half * R + m, k, 1)) = l;
+            }
+        }
     } else if constexpr (SPLITS == 1) {
 #pragma unroll
         for (int j = 0; j < NI; ++j) {
@@ -327,12 +408,13 @@ __global__ __launch_bounds__(kThreads) void gemm_split_kernel(
             for (int i = 0; i < MI; ++i)
 #pragma unroll
                 for (int r = 0; r < 16; ++r) {
-                    const uint32_t m = wm * (BM / 2) + i * 32 + 8 * (r / 4) + 4 * (lane / 32) + r % 4;
-                    if (m0 + m < M) out[static_cast<size_t>(m0 + m) * Ncol + col] = ldexpf(acc[i][j][r], row_e[m] + ce) + cb;
+                    const uint32_t m = acc_row<BM>(wm, i, r, lane);
+                    if (m0 + m < M) out[static_cast<size_t>(m0 + m) * Ncol + col] = ldexpf(acc[i][j][r], row_e[e_last][m] + ce) + cb;
                 }
         }
     } else {
-        // every split writes its scaled partial, then the block that completes the tile adds them in split order
+        // every split writes its partial (powers of two undone), then the block that completes the tile adds them in
+        // split order
         const size_t plane_size = static_cast<size_t>(M) * Ncol;
 #pragma unroll
         for (int j = 0; j < NI; ++j) {
@@ -342,8 +424,8 @@ __global__ __launch_bounds__(kThreads) void gemm_split_kernel(
             for (int i = 0; i < MI; ++i)
 #pragma unroll
                 for (int r = 0; r < 16; ++r) {
-                    const uint32_t m = wm * (BM / 2) + i * 32 + 8 * (r / 4) + 4 * (lane / 32) + r % 4;
-                    acc[i][j][r] = ldexpf(acc[i][j][r], row_e[m] + ce);
+                    const uint32_t m = acc_row<BM>(wm, i, r, lane);
+                    acc[i][j][r] = ldexpf(acc[i][j][r], row_e[e_last][m] + ce);
                     if (m0 + m < M) partials[tile.split * plane_size + static_cast<size_t>(m0 + m) * Ncol + col] = acc[i][j][r];
                 }
         }
@@ -366,7 +448,7 @@ __global__ __launch_bounds__(kThreads) void gemm_split_kernel(
             for (int i = 0; i < MI; ++i)
 #pragma unroll
                 for (int r = 0; r < 16; ++r) {
-                    const uint32_t m = wm * (BM / 2) + i * 32 + 8 * (r / 4) + 4 * (lane / 32) + r % 4;
+                    const uint32_t m = acc_row<BM>(wm, i, r, lane);
                     if (m0 + m >= M) continue;
                     const size_t at = static_cast<size_t>(m0 + m) * Ncol + col;
                     float total = 0.0f;
@@ -384,6 +466,250 @@ __global__ __launch_bounds__(kThreads) void gemm_split_kernel(
     }
 }
 
+// ------------------------------------------------------------------------------- streamed GEMM (LDS DMA)
+// The large-N GEMM: 256 x 128 block tiles (4 waves of 128 x 64), one block per CU, and k-tiles streamed straight
+// from global memory into a ring of kDmaStages LDS stages by global_load_lds (16 bytes per lane, no registers on
+// the way): at k-tile kt the block waits for stage kt, meets at a barrier, requests stage kt + kDmaStages - 1 into
+// the slot read at kt - 1, and multiplies stage kt; each stage is thus requested kDmaStages - 1 k-tiles before its
+// use. The down GEMM reads the activation binades of its rows and k range into LDS before the first k-tile. Same
+// products and order as gemm_planes_kernel.
+constexpr int kDmaStages = 3;
+constexpr int kDmaBM = 256, kDmaBN = 128;
+constexpr uint32_t kDmaMaxActBlocks = 40;  // activation blocks of one down split held in LDS (int8 binades)
+
+// s_waitcnt vmcnt(N) lgkmcnt(0): at most N vector-memory loads of this wave still in flight, its LDS accesses done.
+template <int N>
+__device__ __forceinline__ void wait_loads() {
+    static_assert(N >= 0 && N < 64, "vmcnt is 6 bits");
+    __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | (7 << 4));
+}
+
+// 16 bytes per lane from global memory straight into LDS: lane l's bytes land at lds + 16 l (lds wave-uniform). Written
+// as inline assembly so that the compiler, which cannot tell the ring slots apart, does not wait for every transfer
+// in flight before each LDS read; the kernel orders them itself (wait_loads, then a barrier).
+__device__ __forceinline__ void dma16(const _Float16* src, const _Float16* lds) {
+    const uint32_t offset = static_cast<uint32_t>(__builtin_amdgcn_readfirstlane(
+        static_cast<int>(static_cast<uint32_t>(reinterpret_cast<uintptr_t>(lds)))));  // low 32 bits: the LDS address
+    asm volatile("s_mov_b32 m0, %1\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, off" ::"v"(src), "s"(offset) : "memory", "m0");
+}
+
+// Workgroup barrier without the memory fence of __syncthreads (whose release would also wait for every LDS DMA in
+// flight); LDS visibility is ensured by the wait_loads before it.
+__device__ __forceinline__ void block_barrier() {
+    asm volatile("" ::: "memory");
+    __builtin_amdgcn_s_barrier();
+    asm volatile("" ::: "memory");
+}
+
+template <Epi EPI, bool LO_B, int SPLITS>
+__global__ __launch_bounds__(kThreads) void gemm_dma_kernel(
+    const _Float16* __restrict__ a_planes,  // [K / 32][8][rows_pad][8]
+    const int32_t* __restrict__ a_exp,      // Up: [rows_pad]; Down: [rows_pad, K / kActBlock]
+    const _Float16* __restrict__ b_planes,  // [K / 32][8][Ncol][8]
+    const int32_t* __restrict__ b_exp,      // [Ncol]
+    const float* __restrict__ bias,         // [Ncol]
+    float* __restrict__ out,                // Down: y [M, Ncol] (SPLITS == 1) or partials [SPLITS, M, Ncol]
+    _Float16* __restrict__ out_planes,      // Up: activation planes [Ncol / 32][8][rows_pad][8]
+    int32_t* __restrict__ out_exp,          // Up: [rows_pad, Ncol / BN] activation block binades
+    uint32_t M, uint32_t rows_pad, uint32_t Ncol, uint32_t K) {
+    constexpr int MI = 4, NI = 2, BM = kDmaBM, BN = kDmaBN, S = kDmaStages;
+    static_assert(BM == kThreads, "one thread per block row for the binade tables");
+    constexpr uint32_t kStage = kRuns * (BM + BN) * 8;  // halves per stage
+    constexpr int kLoadsA = BM * kRuns / kWave / 4, kLoadsB = BN * kRuns / kWave / 4;  // DMA instructions per wave
+    constexpr int kLoads = kLoadsA + kLoadsB;
+
+    __shared__ __attribute__((aligned(16))) _Float16 smem[S * kStage];
+    __shared__ int32_t e_row[2][BM];  // Up: [0] x binades, [1] activation block binades
+    __shared__ uint32_t row_max[2][BM];
+    __shared__ int8_t e_tab[EPI == Epi::Down ? BM : 1][EPI == Epi::Down ? kDmaMaxActBlocks : 1];  // Down: [row][block]
+
+    const uint32_t tid = threadIdx.x, lane = tid % kWave, wave = uniform(tid / kWave);
+    const uint32_t wm = wave / 2, wn = wave % 2;
+    const uint32_t tiles_m = rows_pad / BM, tiles_n = Ncol / BN;
+    const Tile tile = tile_of(blockIdx.x, tiles_m, tiles_n, SPLITS);
+    const uint32_t m0 = tile.m * BM, n0 = tile.n * BN;
+    const uint32_t ktiles = K / kBK;
+    const uint32_t k_begin = tile.split * ktiles / SPLITS, k_end = (tile.split + 1) * ktiles / SPLITS;
+    const uint32_t a_kblocks = K / kActBlock, kb0 = k_begin / kKtPerActBlock;
+    if constexpr (EPI == Epi::Up) {
+        e_row[0][tid] = a_exp[m0 + tid];
+    } else {
+        for (uint32_t kb = kb0; kb * kKtPerActBlock < k_end; ++kb)
+            e_tab[tid][kb - kb0] = static_cast<int8_t>(a_exp[static_cast<size_t>(m0 + tid) * a_kblocks + kb]);
+    }
+    __syncthreads();
+
+    // stage kt into ring slot `slot`: wave w copies runs of 64 rows (1 KB each) of A, then of B
+    const auto issue = [&](uint32_t kt, uint32_t slot) {
+#pragma unroll
+        for (int q = 0; q < kLoadsA; ++q) {
+            const uint32_t at = wave * kLoadsA + q, run = at / (BM / 64), rb = at % (BM / 64);
+            dma16(a_planes + ((static_cast<size_t>(kt) * kRuns + run) * rows_pad + m0 + rb * 64 + lane) * 8,
+                  smem + slot * kStage + (run * BM + rb * 64) * 8);
+        }
+#pragma unroll
+        for (int q = 0; q < kLoadsB; ++q) {
+            const uint32_t at = wave * kLoadsB + q, run = at / (BN / 64), rb = at % (BN / 64);
+            dma16(b_planes + ((static_cast<size_t>(kt) * kRuns + run) * Ncol + n0 + rb * 64 + lane) * 8,
+                  smem + slot * kStage + kRuns * BM * 8 + (run * BN + rb * 64) * 8);
+        }
+    };
+
+    floatx16 acc[MI][NI];
+#pragma unroll
+    for (int i = 0; i < MI; ++i)
+#pragma unroll
+        for (int j = 0; j < NI; ++j)
+#pragma unroll
+            for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.0f;
+
+#pragma unroll
+    for (int s = 0; s < S - 1; ++s)
+        if (k_begin + s < k_end) issue(k_begin + s, s);
+    for (uint32_t kt = k_begin; kt < k_end; ++kt) {
+        const uint32_t it = kt - k_begin, slot = it % S;
+        if (kt + 1 < k_end) wait_loads<kLoads>();  // stage kt has landed; stage kt + 1 may still be in flight
+        else wait_loads<0>();
+        block_barrier();
+        if (kt + S - 1 < k_end) issue(kt + S - 1, (it + S - 1) % S);
+        if constexpr (EPI == Epi::Down) {
+            if (kt % kKtPerActBlock == 0 && kt != k_begin) {
+                // a new activation block: bring the accumulators to its power of two (exact)
+                const uint32_t kb = kt / kKtPerActBlock - kb0;
+#pragma unroll
+                for (int i = 0; i < MI; ++i)
+#pragma unroll
+                    for (int r = 0; r < 16; ++r) {
+                        const uint32_t m = acc_row<BM>(wm, i, r, lane);
+                        const float f = ldexpf(1.0f, e_tab[m][kb - 1] - e_tab[m][kb]);
+#pragma unroll
+                        for (int j = 0; j < NI; ++j) acc[i][j][r] *= f;
+                    }
+            }
+        }
+        const _Float16* s_a = smem + slot * kStage;
+        const _Float16* s_b = s_a + kRuns * BM * 8;
+#pragma unroll
+        for (int kk = 0; kk < 2; ++kk) {
+            const uint32_t chunk = kk * 2 + lane / 32;
+            half8 ah[MI], al[MI], bh[NI], bl[NI];
+#pragma unroll
+            for (int i = 0; i < MI; ++i) {
+                const uint32_t r = wm * (BM / 2) + i * 32 + lane % 32;
+                ah[i] = *reinterpret_cast<const half8*>(s_a + (chunk * BM + r) * 8);
+                al[i] = *reinterpret_cast<const half8*>(s_a + ((4 + chunk) * BM + r) * 8);
+            }
+#pragma unroll
+            for (int j = 0; j < NI; ++j) {
+                const uint32_t r = wn * (BN / 2) + j * 32 + lane % 32;
+                bh[j] = *reinterpret_cast<const half8*>(s_b + (chunk * BN + r) * 8);
+                if constexpr (LO_B) bl[j] = *reinterpret_cast<const half8*>(s_b + ((4 + chunk) * BN + r) * 8);
+            }
+#pragma unroll
+            for (int i = 0; i < MI; ++i)
+#pragma unroll
+                for (int j = 0; j < NI; ++j) {
+                    acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(ah[i], bh[j], acc[i][j], 0, 0, 0);
+                    if constexpr (LO_B) acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(ah[i], bl[j], acc[i][j], 0, 0, 0);
+                    acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(al[i], bh[j], acc[i][j], 0, 0, 0);
+                }
+        }
+    }
+    __syncthreads();
+
+    if constexpr (EPI == Epi::Up) {
+        // v = gelu(z + b) once per element into an fp32 [BM][BN] tile in LDS, with the largest |v| per row over the
+        // tile's BN neurons; then every thread splits 8 consecutive columns of one row with that row's power of two
+        // and writes 16 bytes per part (64 consecutive rows of one chunk per wave: 1 KB contiguous)
+        constexpr uint32_t kLd = BN + 8;
+        static_assert(BM * kLd * sizeof(float) <= sizeof(smem), "the epilogue tile fits the staging LDS");
+        float* tile_v = reinterpret_cast<float*>(smem);
+#pragma unroll
+        for (int i = 0; i < MI; ++i) {
+            uint32_t lane_max[16];
+#pragma unroll
+            for (int r = 0; r < 16; ++r) lane_max[r] = 0;
+#pragma unroll
+            for (int j = 0; j < NI; ++j) {
+                const uint32_t c = wn * (BN / 2) + j * 32 + lane % 32;
+                const int ce = b_exp[n0 + c];
+                const float cb = bias[n0 + c];
+#pragma unroll
+                for (int r = 0; r < 16; ++r) {
+                    const uint32_t m = acc_row<BM>(wm, i, r, lane);
+                    const float v = gelu(ldexpf(acc[i][j][r], e_row[0][m] + ce) + cb);
+                    tile_v[m * kLd + c] = v;
+                    lane_max[r] = max(lane_max[r], abs_bits(v));
+                }
+            }
+#pragma unroll
+            for (int r = 0; r < 16; ++r) {
+                uint32_t v = lane_max[r];
+#pragma unroll
+                for (int s = 16; s >= 1; s >>= 1) v = max(v, static_cast<uint32_t>(__shfl_xor(static_cast<int>(v), s, kWave)));
+                if (lane % 32 == 0) row_max[wn][acc_row<BM>(wm, i, r, lane)] = v;
+            }
+        }
+        __syncthreads();
+        {
+            const int e = binade_of_bits(max(row_max[0][tid], row_max[1][tid]));
+            e_row[1][tid] = e;
+            out_exp[static_cast<size_t>(m0 + tid) * tiles_n + tile.n] = e;
+        }
+        __syncthreads();
+        for (uint32_t q = tid; q < BM * (BN / 8); q += kThreads) {
+            const uint32_t m = q % BM, chunk = q / BM, k = n0 + chunk * 8;
+            const float scale = ldexpf(1.0f, -e_row[1][m]);
+            const float* src = tile_v + m * kLd + chunk * 8;
+            half8 h, l;
+#pragma unroll
+            for (int e = 0; e < 8; ++e) {
+                _Float16 hh, ll;
+                split(src[e] * scale, hh, ll);
+                h[e] = hh;
+                l[e] = ll;
+            }
+            *reinterpret_cast<half8*>(out_planes + plane_at(rows_pad, m0 + m, k, 0)) = h;
+            *reinterpret_cast<half8*>(out_planes + plane_at(rows_pad, m0 + m, k, 1)) = l;
+        }
+    } else {
+        // y (one split) or this split's partial, powers of two undone
+        const uint32_t kb_last = (k_end - 1) / kKtPerActBlock - kb0;
+        float* target = out + (SPLITS > 1 ? static_cast<size_t>(tile.split) * M * Ncol : 0);
+#pragma unroll
+        for (int j = 0; j < NI; ++j) {
+            const uint32_t col = n0 + wn * (BN / 2) + j * 32 + lane % 32;
+            const int ce = b_exp[col];
+            const float cb = SPLITS > 1 ? 0.0f : bias[col];
+#pragma unroll
+            for (int i = 0; i < MI; ++i)
+#pragma unroll
+                for (int r = 0; r < 16; ++r) {
+                    const uint32_t m = acc_row<BM>(wm, i, r, lane);
+                    const float v = ldexpf(acc[i][j][r], e_tab[m][kb_last] + ce);
+                    if (m0 + m < M) target[static_cast<size_t>(m0 + m) * Ncol + col] = SPLITS > 1 ? v : v + cb;
+                }
+        }
+    }
+}
+
+// y[m, :] = sum over splits (in split order) of partials[s, m, :] + bias; 4 columns per thread.
+__global__ __launch_bounds__(kThreads) void reduce_splits_kernel(const float* __restrict__ partials, const float* __restrict__ bias,
+                                                                float* __restrict__ y, uint32_t M, uint32_t Ncol, uint32_t splits) {
+    const size_t quads = static_cast<size_t>(M) * Ncol / 4;
+    const size_t i = static_cast<size_t>(blockIdx.x) * kThreads + threadIdx.x;
+    if (i >= quads) return;
+    const float4* p = reinterpret_cast<const float4*>(partials);
+    float4 t = p[i];
+    for (uint32_t s = 1; s < splits; ++s) {
+        const float4 u = p[s * quads + i];
+        t.x += u.x; t.y += u.y; t.z += u.z; t.w += u.w;
+    }
+    const float4 b = *reinterpret_cast<const float4*>(bias + (i * 4) % Ncol);
+    t.x += b.x; t.y += b.y; t.z += b.z; t.w += b.w;
+    reinterpret_cast<float4*>(y)[i] = t;
+}
+
 uint32_t ceil_div(uint32_t a, uint32_t b) { return (a + b - 1) / b; }
 
 struct Shape {
@@ -392,39 +718,41 @@ struct Shape {
 
 constexpr int kMaxSplits = 4;
 
-// Measured on the Pythia-410M layer at N = 2048: up 128 x 128 blocks (80 us); down 64 x 128 blocks without a k
-// split (91 us; 128 x 128 with 2 splits: 131 us, the fixup's device-scope fences write back the L2). K is split only
-// when a down projection has fewer than 64 blocks.
+uint32_t rows_padded(uint32_t m) { return ceil_div(m, kRowPad) * kRowPad; }
+
+// Up: 128 x 128 blocks (the column tile is the activation block). Down: 64 x 128 blocks without a k split; K is
+// split only when a down projection has fewer than 64 blocks (the fixup's device-scope fences write back the L2).
 Shape up_shape(uint32_t, uint32_t) { return {2, 2, 1}; }
 
 Shape down_shape(uint32_t m, uint32_t ncol, uint32_t k) {
-    const uint32_t tiles = ceil_div(m, 64) * (ncol / 128);
+    const uint32_t tiles = rows_padded(m) / 64 * (ncol / 128);
     return {1, 2, tiles < 64 && k >= 2048 ? 2 : 1};
 }
 
 template <Epi EPI, bool LO_B, int MI, int NI, int SPLITS>
-hipError_t launch_gemm(const float* a, const int32_t* a_exp, uint32_t a_blocks, const _Float16* planes, const int32_t* b_exp,
-                       const float* bias, float* out, int32_t* out_exp, float* partials, int32_t* counters, uint32_t M,
-                       uint32_t Ncol, uint32_t K, hipStream_t stream) {
-    const uint32_t tiles = ceil_div(M, 64 * MI) * (Ncol / (64 * NI));
-    hipLaunchKernelGGL((gemm_split_kernel<EPI, MI, NI, LO_B, SPLITS>), dim3(tiles * SPLITS), dim3(kThreads), 0, stream, a, a_exp,
-                       a_blocks, planes, b_exp, bias, out, out_exp, partials, counters, M, Ncol, K);
+hipError_t launch_gemm(const _Float16* a_planes, const int32_t* a_exp, const _Float16* b_planes, const int32_t* b_exp,
+                       const float* bias, float* out, _Float16* out_planes, int32_t* out_exp, float* partials, int32_t* counters,
+                       uint32_t M, uint32_t Ncol, uint32_t K, hipStream_t stream) {
+    static_assert(EPI == Epi::Down || 64 * NI == kActBlock, "the up GEMM's column tile is the activation block");
+    const uint32_t rows_pad = rows_padded(M);
+    const uint32_t tiles = rows_pad / (64 * MI) * (Ncol / (64 * NI));
+    hipLaunchKernelGGL((gemm_planes_kernel<EPI, MI, NI, LO_B, SPLITS>), dim3(tiles * SPLITS), dim3(kThreads), 0, stream, a_planes,
+                       a_exp, b_planes, b_exp, bias, out, out_planes, out_exp, partials, counters, M, rows_pad, Ncol, K);
     return hipGetLastError();
 }
 
-// The instantiated shapes: up (mi, ni) in {(2,2), (2,4), (4,2), (1,2)} without splits; down (2,2) and (1,2) with
-// 1, 2 or 4 splits and (2,4) with 1 or 2.
+// The instantiated shapes: up (mi, ni) in {(2,2), (4,2), (1,2)} without splits; down (2,2) and (1,2) with 1, 2 or 4
+// splits and (2,4) with 1 or 2.
 template <Epi EPI, bool LO_B>
-hipError_t gemm(Shape shape, const float* a, const int32_t* a_exp, uint32_t a_blocks, const _Float16* planes, const int32_t* b_exp,
-                const float* bias, float* out, int32_t* out_exp, float* partials, int32_t* counters, uint32_t M, uint32_t Ncol,
-                uint32_t K, hipStream_t stream) {
-#define HFFN_GEMM(MI, NI, S)                                                                                                \
-    if (shape.mi == MI && shape.ni == NI && shape.splits == S)                                                              \
-        return launch_gemm<EPI, LO_B, MI, NI, S>(a, a_exp, a_blocks, planes, b_exp, bias, out, out_exp, partials, counters, \
-                                                 M, Ncol, K, stream);
+hipError_t gemm(Shape shape, const _Float16* a_planes, const int32_t* a_exp, const _Float16* b_planes, const int32_t* b_exp,
+                const float* bias, float* out, _Float16* out_planes, int32_t* out_exp, float* partials, int32_t* counters,
+                uint32_t M, uint32_t Ncol, uint32_t K, hipStream_t stream) {
+#define HFFN_GEMM(MI, NI, S)                                                                                                   \
+    if (shape.mi == MI && shape.ni == NI && shape.splits == S)                                                                 \
+        return launch_gemm<EPI, LO_B, MI, NI, S>(a_planes, a_exp, b_planes, b_exp, bias, out, out_planes, out_exp, partials,   \
+                                                 counters, M, Ncol, K, stream);
     if constexpr (EPI == Epi::Up) {
         HFFN_GEMM(2, 2, 1)
-        HFFN_GEMM(2, 4, 1)
         HFFN_GEMM(4, 2, 1)
         HFFN_GEMM(1, 2, 1)
     } else {
@@ -441,22 +769,65 @@ hipError_t gemm(Shape shape, const float* a, const int32_t* a_exp, uint32_t a_bl
     return hipErrorInvalidValue;
 }
 
-// Workspace layout (int32 words unless stated): split counters [down tiles of the largest token count, 64 x 64 tiles]
-// | x binades [M] | activation block binades [M, d_ff / 64] | (256-byte aligned) float partials [4, M, d_model].
-// The counters come first and are sized for every M and tile shape, so a call at any M finds them where the previous
-// call, at any other M, left them (at zero).
+// The streamed kernel takes a GEMM when its 256 x 128 tiles (times the k splits of a down projection) give at least
+// 128 blocks; a down projection splits K in 2 or 4 to reach about 256 blocks (each split a whole number of
+// activation blocks), its partials added by reduce_splits_kernel.
+constexpr uint32_t kDmaMinBlocks = 128;
+
+uint32_t dma_tiles(uint32_t m, uint32_t ncol) { return rows_padded(m) / kDmaBM * (ncol / kDmaBN); }
+
+uint32_t dma_down_splits(uint32_t m, uint32_t ncol, uint32_t k) {
+    const uint32_t tiles = dma_tiles(m, ncol);
+    uint32_t splits = tiles >= 192 ? 1 : tiles >= 96 ? 2 : 4;
+    while (splits > 1 && k % (kActBlock * splits) != 0) splits /= 2;
+    if (k / kActBlock / splits > kDmaMaxActBlocks) return 0;  // 0: not streamed
+    return tiles * splits >= kDmaMinBlocks ? splits : 0;
+}
+
+template <Epi EPI, bool LO_B, int SPLITS>
+hipError_t launch_dma(const _Float16* a_planes, const int32_t* a_exp, const _Float16* b_planes, const int32_t* b_exp,
+                      const float* bias, float* out, _Float16* out_planes, int32_t* out_exp, uint32_t M, uint32_t Ncol, uint32_t K,
+                      hipStream_t stream) {
+    hipLaunchKernelGGL((gemm_dma_kernel<EPI, LO_B, SPLITS>), dim3(dma_tiles(M, Ncol) * SPLITS), dim3(kThreads), 0, stream, a_planes,
+                       a_exp, b_planes, b_exp, bias, out, out_planes, out_exp, M, rows_padded(M), Ncol, K);
+    return hipGetLastError();
+}
+
+template <bool LO_B>
+hipError_t dma_down(uint32_t splits, const _Float16* a_planes, const int32_t* a_exp, const _Float16* b_planes, const int32_t* b_exp,
+                    const float* bias, float* y, float* partials, uint32_t M, uint32_t Ncol, uint32_t K, hipStream_t stream) {
+    if (splits == 1)
+        return launch_dma<Epi::Down, LO_B, 1>(a_planes, a_exp, b_planes, b_exp, bias, y, nullptr, nullptr, M, Ncol, K, stream);
+    const hipError_t status =
+        splits == 2 ? launch_dma<Epi::Down, LO_B, 2>(a_planes, a_exp, b_planes, b_exp, bias, partials, nullptr, nullptr, M, Ncol, K, stream)
+                    : launch_dma<Epi::Down, LO_B, 4>(a_planes, a_exp, b_planes, b_exp, bias, partials, nullptr, nullptr, M, Ncol, K, stream);
+    if (status != hipSuccess) return status;
+    const size_t quads = static_cast<size_t>(M) * Ncol / 4;
+    hipLaunchKernelGGL(reduce_splits_kernel, dim3(static_cast<uint32_t>((quads + kThreads - 1) / kThreads)), dim3(kThreads), 0, stream,
+                       partials, bias, y, M, Ncol, splits);
+    return hipGetLastError();
+}
+
+// Workspace layout (int32 words unless stated; rows = M padded to kRowPad): split counters [down tiles of the
+// largest token count, 64 x 64 tiles] | x binades [rows] | activation block binades [rows, d_ff / kActBlock] |
+// (256-byte aligned, bytes) x planes [rows * d_model * 2 halves] | activation planes [rows * d_ff * 2 halves] |
+// float partials [4, M, d_model]. The counters come first and are sized for every M and tile shape, so a call at
+// any M finds them where the previous call, at any other M, left them (at zero).
 struct Workspace {
-    size_t counters, x_binades, act_binades, partials, bytes;
+    size_t counters, x_binades, act_binades, x_planes, act_planes, partials, bytes;
 };
 
 Workspace workspace_layout(uint32_t m, uint32_t d, uint32_t h) {
+    const size_t rows = rows_padded(m);
     Workspace w{};
     w.counters = 0;
     const size_t counter_words = static_cast<size_t>(ceil_div(kMaxTokens, 64)) * (d / 64);
     w.x_binades = w.counters + counter_words;
-    w.act_binades = w.x_binades + m;
-    const size_t partial_start = (w.act_binades + static_cast<size_t>(m) * (h / 64)) * 4;
-    w.partials = (partial_start + 255) / 256 * 256;  // bytes
+    w.act_binades = w.x_binades + rows;
+    const size_t words_end = (w.act_binades + rows * (h / kActBlock)) * 4;
+    w.x_planes = (words_end + 255) / 256 * 256;  // bytes from here on
+    w.act_planes = w.x_planes + rows * d * 4;
+    w.partials = w.act_planes + rows * h * 4;
     w.bytes = w.partials + static_cast<size_t>(kMaxSplits) * m * d * 4;
     return w;
 }
@@ -480,34 +851,50 @@ hipError_t launch_densify(int vt, const int32_t* off, const int16_t* idx, const 
     return hipGetLastError();
 }
 
-hipError_t launch_mfma_up(int vt, const float* x, const void* planes, const int32_t* w_exp, const float* b_up, float* act,
-                          void* workspace, uint32_t n, uint32_t d, uint32_t h, hipStream_t stream) {
+hipError_t launch_mfma_up(int vt, const float* x, const void* planes, const int32_t* w_exp, const float* b_up, void* workspace,
+                          uint32_t n, uint32_t d, uint32_t h, hipStream_t stream) {
     const Workspace w = workspace_layout(n, d, h);
     int32_t* words = static_cast<int32_t*>(workspace);
-    hipLaunchKernelGGL(row_binade_kernel, dim3(ceil_div(n, kThreads / kWave)), dim3(kThreads), 0, stream, x, n, d,
-                       words + w.x_binades);
+    char* bytes = static_cast<char*>(workspace);
+    auto* x_planes = reinterpret_cast<_Float16*>(bytes + w.x_planes);
+    auto* act_planes = reinterpret_cast<_Float16*>(bytes + w.act_planes);
+    hipLaunchKernelGGL(split_rows_kernel, dim3(rows_padded(n) / kSplitRows), dim3(kThreads), 0, stream, x, n, rows_padded(n), d,
+                       x_planes, words + w.x_binades);  // one wave per padded row
     if (hipError_t status = hipGetLastError(); status != hipSuccess) return status;
     const auto* p = static_cast<const _Float16*>(planes);
+    if (dma_tiles(n, h) >= kDmaMinBlocks) {
+        if (vt == kBF16)
+            return launch_dma<Epi::Up, false, 1>(x_planes, words + w.x_binades, p, w_exp, b_up, nullptr, act_planes, words + w.act_binades,
+                                                 n, h, d, stream);
+        return launch_dma<Epi::Up, true, 1>(x_planes, words + w.x_binades, p, w_exp, b_up, nullptr, act_planes, words + w.act_binades, n,
+                                            h, d, stream);
+    }
     const Shape shape = up_shape(n, h);
     if (vt == kBF16)
-        return gemm<Epi::Up, false>(shape, x, words + w.x_binades, 1, p, w_exp, b_up, act, words + w.act_binades, nullptr,
-                                    nullptr, n, h, d, stream);
-    return gemm<Epi::Up, true>(shape, x, words + w.x_binades, 1, p, w_exp, b_up, act, words + w.act_binades, nullptr, nullptr,
-                               n, h, d, stream);
+        return gemm<Epi::Up, false>(shape, x_planes, words + w.x_binades, p, w_exp, b_up, nullptr, act_planes, words + w.act_binades,
+                                    nullptr, nullptr, n, h, d, stream);
+    return gemm<Epi::Up, true>(shape, x_planes, words + w.x_binades, p, w_exp, b_up, nullptr, act_planes, words + w.act_binades,
+                               nullptr, nullptr, n, h, d, stream);
 }
 
-hipError_t launch_mfma_down(int vt, const float* act, const void* planes, const int32_t* v_exp, const float* b_down, float* y,
-                            void* workspace, uint32_t n, uint32_t d, uint32_t h, hipStream_t stream) {
+hipError_t launch_mfma_down(int vt, const void* planes, const int32_t* v_exp, const float* b_down, float* y, void* workspace,
+                            uint32_t n, uint32_t d, uint32_t h, hipStream_t stream) {
     const Workspace w = workspace_layout(n, d, h);
     int32_t* words = static_cast<int32_t*>(workspace);
-    float* partials = reinterpret_cast<float*>(static_cast<char*>(workspace) + w.partials);
+    char* bytes = static_cast<char*>(workspace);
+    const auto* act_planes = reinterpret_cast<const _Float16*>(bytes + w.act_planes);
+    float* partials = reinterpret_cast<float*>(bytes + w.partials);
     const auto* p = static_cast<const _Float16*>(planes);
+    if (const uint32_t splits = dma_down_splits(n, d, h)) {
+        if (vt == kBF16)
+            return dma_down<false>(splits, act_planes, words + w.act_binades, p, v_exp, b_down, y, partials, n, d, h, stream);
+        return dma_down<true>(splits, act_planes, words + w.act_binades, p, v_exp, b_down, y, partials, n, d, h, stream);
+    }
     const Shape shape = down_shape(n, d, h);
-    const uint32_t blocks = h / (64 * up_shape(n, h).ni);
     if (vt == kBF16)
-        return gemm<Epi::Down, false>(shape, act, words + w.act_binades, blocks, p, v_exp, b_down, y, nullptr, partials,
+        return gemm<Epi::Down, false>(shape, act_planes, words + w.act_binades, p, v_exp, b_down, y, nullptr, nullptr, partials,
                                       words + w.counters, n, d, h, stream);
-    return gemm<Epi::Down, true>(shape, act, words + w.act_binades, blocks, p, v_exp, b_down, y, nullptr, partials,
+    return gemm<Epi::Down, true>(shape, act_planes, words + w.act_binades, p, v_exp, b_down, y, nullptr, nullptr, partials,
                                  words + w.counters, n, d, h, stream);
 }
 

@@ -240,7 +240,7 @@ class HFFNRuntime:
 
     def force(self, up: str | None, down: str | None) -> None:
         """Diagnostic: fix the up and/or the down kernel regardless of N (None: the policy). The MFMA path runs up and
-        down together (its activations are token-major): ``mfma`` is forced as a pair."""
+        down together (its activations stay in its own workspace as fp16 planes): ``mfma`` is forced as a pair."""
         if up not in (None, *UP_MODES) or down not in (None, *DOWN_MODES):
             raise ValueError("unknown kernel mode")
         if up == "edges" and not edges_supported(self.d_model, 1):
@@ -300,11 +300,13 @@ class HFFNRuntime:
         x_t, act, y_t, y = self._work
         stream = torch.cuda.current_stream(self.device).cuda_stream
         if up == "mfma":
+            x = _aligned(x)  # the MFMA path reads x 16 bytes at a time
             planes, tensors = self._planes[index], self._tensors[index]
             _lib.check(self._lib.hffn_forward_mfma(value_type, x.data_ptr(), planes["up"].data_ptr(),
                                                    planes["up_binades"].data_ptr(), tensors["b_up"].data_ptr(),
                                                    planes["down"].data_ptr(), planes["down_binades"].data_ptr(),
-                                                   tensors["b_down"].data_ptr(), act, self._mfma_work.data_ptr(), y,
+                                                   tensors["b_down"].data_ptr(), self._mfma_work.data_ptr(),
+                                                   4 * self._mfma_work.numel(), y,
                                                    self.d_model, self.d_ff, n, stream), "forward (mfma, mfma)")
             return
         _lib.check(self._lib.hffn_forward(_lib.UP_MODES[up], _lib.DOWN_MODES[down], value_type, x.data_ptr(), *model,

@@ -27,7 +27,7 @@
 extern "C" {
 #endif
 
-#define HFFN_ABI_VERSION 1
+#define HFFN_ABI_VERSION 2
 
 #define HFFN_OK 0
 #define HFFN_ERROR_ARGUMENT (-1) /* invalid shape, mode, pointer or workspace */
@@ -102,12 +102,13 @@ int hffn_output_major(int value_type, const int32_t* down_offsets, const int16_t
                       void* out_val, void* workspace, uint64_t workspace_bytes, void* stream);
 
 /* ---- Tile-densified MFMA path (high density, large n). No reference counterpart: the reference runs every shape on
- * the gather kernels (runtime/gpu/nvidia/common/kernels/hffn_cuda/kernels.py). Weights are densified at load into
- * fp16 hi/lo "planes" with one power-of-two scale per row (binade); activations are split the same way on the fly;
- * each product is hi*hi + hi*lo + lo*hi (hi*hi + lo*hi for bf16 weights) on v_mfma_f32_32x32x16_f16 with fp32
- * accumulation. Activations are token-major act[n, d_ff] on this path. */
+ * the gather kernels (runtime/gpu/nvidia/common/kernels/hffn_cuda/kernels.py). Every operand is a pair of fp16 hi/lo
+ * "planes" scaled by powers of two (binades): the weights are densified at load (one binade per row); x is split
+ * before the up GEMM (one binade per token); the activations are split by the up GEMM (one binade per token and
+ * 128-neuron block) and stay in the workspace. Each product is hi*hi + hi*lo + lo*hi (hi*hi + lo*hi for bf16
+ * weights) on v_mfma_f32_32x32x16_f16 with fp32 accumulation; the binades are undone exactly. */
 
-/* 1 if the MFMA path takes this shape (d_model and d_ff multiples of 128), else 0 (host-only query). */
+/* 1 if the MFMA path takes this shape (d_model and d_ff multiples of 256), else 0 (host-only query). */
 int hffn_mfma_supported(uint32_t d_model, uint32_t d_ff);
 
 /* Bytes of the planes of a dense [rows, k] matrix (host-only query). */
@@ -119,26 +120,27 @@ int hffn_dense_planes_bytes(uint32_t rows, uint32_t k, uint64_t* bytes);
 int hffn_densify(int value_type, const int32_t* offsets, const int16_t* idx, const void* val, uint32_t rows, uint32_t k,
                  void* planes, int32_t* binades, void* stream);
 
-/* Bytes of the device workspace of the MFMA entry points for n tokens (host-only query). The workspace holds the
- * token and activation binades, the split-K partial sums and one counter per output tile of the down projection;
- * it must be zero-filled before its first use, and every call leaves the counters at zero. Calls that share a
- * workspace must be ordered (one stream). */
+/* Bytes of the device workspace of the MFMA entry points for n tokens (host-only query; the entry points refuse a
+ * smaller workspace_bytes). The workspace holds one
+ * counter per output tile of the down projection, the token and activation binades, the planes of x and of the
+ * activations (n padded to 256 rows) and the split-K partial sums; it must be zero-filled before its first use, and
+ * every call leaves the counters at zero. Calls that share a workspace must be ordered (one stream). */
 int hffn_mfma_workspace(uint32_t n, uint32_t d_model, uint32_t d_ff, uint64_t* bytes);
 
-/* act[t, r] = gelu(b_up[r] + sum_i W_up[r, i] x[t, i]), token-major act[n, d_ff]; also records in the workspace the
- * binade of each token of x and of each token's activations per 128-neuron block (read by hffn_mfma_down). */
+/* act[t, r] = gelu(b_up[r] + sum_i W_up[r, i] x[t, i]), left in the workspace as planes with one binade per token and
+ * 128-neuron block (read by hffn_mfma_down); also splits x (16-byte aligned) into the workspace. */
 int hffn_mfma_up(int value_type, const float* x, const void* up_planes, const int32_t* up_binades, const float* b_up,
-                 float* act, void* workspace, uint32_t d_model, uint32_t d_ff, uint32_t n, void* stream);
+                 void* workspace, uint64_t workspace_bytes, uint32_t d_model, uint32_t d_ff, uint32_t n, void* stream);
 
-/* y[t, o] = sum_r W_down[o, r] act[t, r] + b_down[o], y token-major [n, d_model]; act and the workspace as left by
- * hffn_mfma_up. */
-int hffn_mfma_down(int value_type, const float* act, const void* down_planes, const int32_t* down_binades, const float* b_down,
-                   float* y, void* workspace, uint32_t d_model, uint32_t d_ff, uint32_t n, void* stream);
+/* y[t, o] = sum_r W_down[o, r] act[t, r] + b_down[o], y token-major [n, d_model]; the activations as left in the
+ * workspace by hffn_mfma_up for the same n. */
+int hffn_mfma_down(int value_type, const void* down_planes, const int32_t* down_binades, const float* b_down, float* y,
+                   void* workspace, uint64_t workspace_bytes, uint32_t d_model, uint32_t d_ff, uint32_t n, void* stream);
 
-/* The whole layer on the MFMA path (hffn_mfma_up then hffn_mfma_down); act is a float32 [n, d_ff] workspace. */
+/* The whole layer on the MFMA path (hffn_mfma_up then hffn_mfma_down). */
 int hffn_forward_mfma(int value_type, const float* x, const void* up_planes, const int32_t* up_binades, const float* b_up,
-                      const void* down_planes, const int32_t* down_binades, const float* b_down, float* act, void* workspace,
-                      float* y, uint32_t d_model, uint32_t d_ff, uint32_t n, void* stream);
+                      const void* down_planes, const int32_t* down_binades, const float* b_down, void* workspace,
+                      uint64_t workspace_bytes, float* y, uint32_t d_model, uint32_t d_ff, uint32_t n, void* stream);
 
 #ifdef __cplusplus
 }

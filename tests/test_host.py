@@ -57,6 +57,14 @@ def test_abi_refuses_bad_shapes_before_launching():
     _expect_argument_error(lib.hffn_up(1, 0, p, p, odd, p, p, p, 64, 64, 64, 1, 4, None), "aligned")
     _expect_argument_error(lib.hffn_down(1, 0, p, p, p, ctypes.c_void_p(24), p, p, 64, 64, 64, 1, 4, None), "aligned")
     _expect_argument_error(lib.hffn_forward(2, 2, 0, p, p, p, p, p, p, p, p, p, None, p, p, p, 64, 64, 64, 64, 1, 4, None), "x_t")
+    mfma_needed = ctypes.c_uint64(0)
+    assert lib.hffn_mfma_workspace(2048, 1024, 4096, ctypes.byref(mfma_needed)) == _lib.OK
+    small = mfma_needed.value - 1
+    _expect_argument_error(lib.hffn_mfma_up(0, p, p, p, p, p, small, 1024, 4096, 2048, None), "workspace")
+    _expect_argument_error(lib.hffn_mfma_down(0, p, p, p, p, p, small, 1024, 4096, 2048, None), "workspace")
+    _expect_argument_error(lib.hffn_forward_mfma(0, p, p, p, p, p, p, p, p, small, p, 1024, 4096, 2048, None), "workspace")
+    _expect_argument_error(lib.hffn_mfma_up(0, p, p, p, p, p, 1 << 40, 1024, 4000, 2048, None), "multiples")
+    _expect_argument_error(lib.hffn_mfma_up(0, ctypes.c_void_p(20), p, p, p, p, 1 << 40, 1024, 4096, 2048, None), "aligned")
     needed = ctypes.c_uint64(0)
     assert lib.hffn_output_major_workspace(2_097_152, 1024, ctypes.byref(needed)) == _lib.OK
     assert needed.value == 1024 * 1024 * 4
