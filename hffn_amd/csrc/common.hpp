@@ -8,10 +8,28 @@ namespace hffn {
 
 constexpr int kWave = 64;
 
-// Exact GELU (erf form, PyTorch's approximate="none"), with the device erff of the ROCm math
-// library (OCML). Matches `gelu` of runtime/gpu/nvidia/common/kernels/hffn_cuda/kernels.py:87-89.
+// Exact GELU (erf form, PyTorch's approximate="none"; `gelu` of
+// runtime/gpu/nvidia/common/kernels/hffn_cuda/kernels.py:87-89), written as z/2 erfc(-z/sqrt 2) so that negative z
+// keep their relative accuracy (no 1 + erf cancellation), with erfc from the Chebyshev fit of Press, Teukolsky,
+// Vetterling and Flannery, Numerical Recipes (2nd ed., section 6.2, "erfcc"; fractional error below 1.2e-7 for
+// every argument): for x >= 0, erfc(x) = t exp(-x^2 + P(t)) with t = 1 / (1 + x / 2), and erfc(-x) = 2 - erfc(x).
+// Branch-free, so that a wave evaluates many independent GELUs back to back.
 __device__ __forceinline__ float gelu(float z) {
-    return 0.5f * z * (1.0f + erff(z * 0.70710678118654752f));
+    const float x = -z * 0.70710678118654752f;
+    const float a = fabsf(x);
+    const float t = 1.0f / fmaf(0.5f, a, 1.0f);
+    float p = 0.17087277f;
+    p = fmaf(p, t, -0.82215223f);
+    p = fmaf(p, t, 1.48851587f);
+    p = fmaf(p, t, -1.13520398f);
+    p = fmaf(p, t, 0.27886807f);
+    p = fmaf(p, t, -0.18628806f);
+    p = fmaf(p, t, 0.09678418f);
+    p = fmaf(p, t, 0.37409196f);
+    p = fmaf(p, t, 1.00002368f);
+    p = fmaf(p, t, -1.26551223f);
+    const float tail = t * expf(fmaf(-a, a, p));  // erfc(|x|)
+    return 0.5f * z * (x >= 0.0f ? tail : 2.0f - tail);
 }
 
 // Value loads: float32 store, or bfloat16 bits widened exactly to float32.

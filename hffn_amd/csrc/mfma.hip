@@ -519,9 +519,8 @@ __global__ __launch_bounds__(kThreads) void gemm_dma_kernel(
     constexpr int kLoads = kLoadsA + kLoadsB;
 
     __shared__ __attribute__((aligned(16))) _Float16 smem[S * kStage];
-    __shared__ int32_t e_row[2][BM];  // Up: [0] x binades, [1] activation block binades
-    __shared__ uint32_t row_max[2][BM];
-    __shared__ int8_t e_tab[EPI == Epi::Down ? BM : 1][EPI == Epi::Down ? kDmaMaxActBlocks : 1];  // Down: [row][block]
+    __shared__ int32_t e_row[1][BM];  // Up: x binades
+    __shared__ __attribute__((aligned(4))) int8_t e_tab[EPI == Epi::Down ? kDmaMaxActBlocks : 1][EPI == Epi::Down ? BM : 1];  // Down: [block][row]
 
     const uint32_t tid = threadIdx.x, lane = tid % kWave, wave = uniform(tid / kWave);
     const uint32_t wm = wave / 2, wn = wave % 2;
@@ -535,7 +534,7 @@ __global__ __launch_bounds__(kThreads) void gemm_dma_kernel(
         e_row[0][tid] = a_exp[m0 + tid];
     } else {
         for (uint32_t kb = kb0; kb * kKtPerActBlock < k_end; ++kb)
-            e_tab[tid][kb - kb0] = static_cast<int8_t>(a_exp[static_cast<size_t>(m0 + tid) * a_kblocks + kb]);
+            e_tab[kb - kb0][tid] = static_cast<int8_t>(a_exp[static_cast<size_t>(m0 + tid) * a_kblocks + kb]);
     }
     __syncthreads();
 
@@ -575,15 +574,22 @@ __global__ __launch_bounds__(kThreads) void gemm_dma_kernel(
         if constexpr (EPI == Epi::Down) {
             if (kt % kKtPerActBlock == 0 && kt != k_begin) {
                 // a new activation block: bring the accumulators to its power of two (exact)
+                // accumulator registers 4g .. 4g + 3 hold 4 consecutive rows: one 4-byte read per block and group
                 const uint32_t kb = kt / kKtPerActBlock - kb0;
 #pragma unroll
                 for (int i = 0; i < MI; ++i)
 #pragma unroll
-                    for (int r = 0; r < 16; ++r) {
-                        const uint32_t m = acc_row<BM>(wm, i, r, lane);
-                        const float f = ldexpf(1.0f, e_tab[m][kb - 1] - e_tab[m][kb]);
+                    for (int g = 0; g < 4; ++g) {
+                        const uint32_t m = acc_row<BM>(wm, i, 4 * g, lane);
+                        const uint32_t before = *reinterpret_cast<const uint32_t*>(&e_tab[kb - 1][m]);
+                        const uint32_t now = *reinterpret_cast<const uint32_t*>(&e_tab[kb][m]);
 #pragma unroll
-                        for (int j = 0; j < NI; ++j) acc[i][j][r] *= f;
+                        for (int b = 0; b < 4; ++b) {
+                            const int d = static_cast<int8_t>(before >> (8 * b)) - static_cast<int8_t>(now >> (8 * b));
+                            const float f = ldexpf(1.0f, d);
+#pragma unroll
+                            for (int j = 0; j < NI; ++j) acc[i][j][4 * g + b] *= f;
+                        }
                     }
             }
         }
@@ -618,77 +624,82 @@ __global__ __launch_bounds__(kThreads) void gemm_dma_kernel(
     __syncthreads();
 
     if constexpr (EPI == Epi::Up) {
-        // v = gelu(z + b) once per element into an fp32 [BM][BN] tile in LDS, with the largest |v| per row over the
-        // tile's BN neurons; then every thread splits 8 consecutive columns of one row with that row's power of two
-        // and writes 16 bytes per part (64 consecutive rows of one chunk per wave: 1 KB contiguous)
-        constexpr uint32_t kLd = BN + 8;
+        // v = gelu(z + b) once per element into an fp32 [BM][BN] tile in LDS; then thread t takes block row t: the
+        // largest |v| of the row over the tile's BN neurons gives its power of two, and the row goes out split, 16
+        // bytes per part and chunk (the 256 threads write 256 consecutive rows of one chunk: 4 KB contiguous)
+        constexpr uint32_t kLd = BN + 4;
         static_assert(BM * kLd * sizeof(float) <= sizeof(smem), "the epilogue tile fits the staging LDS");
         float* tile_v = reinterpret_cast<float*>(smem);
 #pragma unroll
-        for (int i = 0; i < MI; ++i) {
-            uint32_t lane_max[16];
-#pragma unroll
-            for (int r = 0; r < 16; ++r) lane_max[r] = 0;
-#pragma unroll
-            for (int j = 0; j < NI; ++j) {
-                const uint32_t c = wn * (BN / 2) + j * 32 + lane % 32;
-                const int ce = b_exp[n0 + c];
-                const float cb = bias[n0 + c];
-#pragma unroll
-                for (int r = 0; r < 16; ++r) {
-                    const uint32_t m = acc_row<BM>(wm, i, r, lane);
-                    const float v = gelu(ldexpf(acc[i][j][r], e_row[0][m] + ce) + cb);
-                    tile_v[m * kLd + c] = v;
-                    lane_max[r] = max(lane_max[r], abs_bits(v));
-                }
-            }
-#pragma unroll
-            for (int r = 0; r < 16; ++r) {
-                uint32_t v = lane_max[r];
-#pragma unroll
-                for (int s = 16; s >= 1; s >>= 1) v = max(v, static_cast<uint32_t>(__shfl_xor(static_cast<int>(v), s, kWave)));
-                if (lane % 32 == 0) row_max[wn][acc_row<BM>(wm, i, r, lane)] = v;
-            }
-        }
-        __syncthreads();
-        {
-            const int e = binade_of_bits(max(row_max[0][tid], row_max[1][tid]));
-            e_row[1][tid] = e;
-            out_exp[static_cast<size_t>(m0 + tid) * tiles_n + tile.n] = e;
-        }
-        __syncthreads();
-        for (uint32_t q = tid; q < BM * (BN / 8); q += kThreads) {
-            const uint32_t m = q % BM, chunk = q / BM, k = n0 + chunk * 8;
-            const float scale = ldexpf(1.0f, -e_row[1][m]);
-            const float* src = tile_v + m * kLd + chunk * 8;
-            half8 h, l;
-#pragma unroll
-            for (int e = 0; e < 8; ++e) {
-                _Float16 hh, ll;
-                split(src[e] * scale, hh, ll);
-                h[e] = hh;
-                l[e] = ll;
-            }
-            *reinterpret_cast<half8*>(out_planes + plane_at(rows_pad, m0 + m, k, 0)) = h;
-            *reinterpret_cast<half8*>(out_planes + plane_at(rows_pad, m0 + m, k, 1)) = l;
-        }
-    } else {
-        // y (one split) or this split's partial, powers of two undone
-        const uint32_t kb_last = (k_end - 1) / kKtPerActBlock - kb0;
-        float* target = out + (SPLITS > 1 ? static_cast<size_t>(tile.split) * M * Ncol : 0);
-#pragma unroll
         for (int j = 0; j < NI; ++j) {
-            const uint32_t col = n0 + wn * (BN / 2) + j * 32 + lane % 32;
-            const int ce = b_exp[col];
-            const float cb = SPLITS > 1 ? 0.0f : bias[col];
+            const uint32_t c = wn * (BN / 2) + j * 32 + lane % 32;
+            const int ce = b_exp[n0 + c];
+            const float cb = bias[n0 + c];
 #pragma unroll
             for (int i = 0; i < MI; ++i)
 #pragma unroll
                 for (int r = 0; r < 16; ++r) {
                     const uint32_t m = acc_row<BM>(wm, i, r, lane);
-                    const float v = ldexpf(acc[i][j][r], e_tab[m][kb_last] + ce);
-                    if (m0 + m < M) target[static_cast<size_t>(m0 + m) * Ncol + col] = SPLITS > 1 ? v : v + cb;
+                    tile_v[m * kLd + c] = gelu(ldexpf(acc[i][j][r], e_row[0][m] + ce) + cb);
                 }
+        }
+        __syncthreads();
+        const float* row_v = tile_v + tid * kLd;
+        uint32_t largest = 0;
+#pragma unroll 8
+        for (uint32_t c = 0; c < BN; c += 4) {
+            const float4 v = *reinterpret_cast<const float4*>(row_v + c);
+            largest = max(largest, max(max(abs_bits(v.x), abs_bits(v.y)), max(abs_bits(v.z), abs_bits(v.w))));
+        }
+        const int e = binade_of_bits(largest);
+        out_exp[static_cast<size_t>(m0 + tid) * tiles_n + tile.n] = e;
+        const float scale = ldexpf(1.0f, -e);
+#pragma unroll 4
+        for (uint32_t chunk = 0; chunk < BN / 8; ++chunk) {
+            const float4 u = *reinterpret_cast<const float4*>(row_v + chunk * 8);
+            const float4 w = *reinterpret_cast<const float4*>(row_v + chunk * 8 + 4);
+            const float v[8] = {u.x, u.y, u.z, u.w, w.x, w.y, w.z, w.w};
+            half8 h, l;
+#pragma unroll
+            for (int q = 0; q < 8; ++q) {
+                _Float16 hh, ll;
+                split(v[q] * scale, hh, ll);
+                h[q] = hh;
+                l[q] = ll;
+            }
+            *reinterpret_cast<half8*>(out_planes + plane_at(rows_pad, m0 + tid, n0 + chunk * 8, 0)) = h;
+            *reinterpret_cast<half8*>(out_planes + plane_at(rows_pad, m0 + tid, n0 + chunk * 8, 1)) = l;
+        }
+    } else {
+        // y (one split) or this split's partial, powers of two undone: through an fp32 [BM][BN] tile in LDS, so that
+        // every thread writes 16 bytes (a wave: two rows of BN columns)
+        constexpr uint32_t kLd = BN + 4;
+        static_assert(BM * kLd * sizeof(float) <= sizeof(smem), "the epilogue tile fits the staging LDS");
+        float* tile_v = reinterpret_cast<float*>(smem);
+        const uint32_t kb_last = (k_end - 1) / kKtPerActBlock - kb0;
+#pragma unroll
+        for (int j = 0; j < NI; ++j) {
+            const uint32_t c = wn * (BN / 2) + j * 32 + lane % 32;
+            const int ce = b_exp[n0 + c];
+#pragma unroll
+            for (int i = 0; i < MI; ++i)
+#pragma unroll
+                for (int r = 0; r < 16; ++r) {
+                    const uint32_t m = acc_row<BM>(wm, i, r, lane);
+                    tile_v[m * kLd + c] = ldexpf(acc[i][j][r], e_tab[kb_last][m] + ce);
+                }
+        }
+        __syncthreads();
+        float* target = out + (SPLITS > 1 ? static_cast<size_t>(tile.split) * M * Ncol : 0);
+        for (uint32_t q = tid; q < BM * (BN / 4); q += kThreads) {
+            const uint32_t m = q / (BN / 4), c = (q % (BN / 4)) * 4;
+            if (m0 + m >= M) break;  // rows ascend with q
+            float4 v = *reinterpret_cast<const float4*>(tile_v + m * kLd + c);
+            if constexpr (SPLITS == 1) {
+                const float4 b = *reinterpret_cast<const float4*>(bias + n0 + c);
+                v.x += b.x; v.y += b.y; v.z += b.z; v.w += b.w;
+            }
+            *reinterpret_cast<float4*>(target + static_cast<size_t>(m0 + m) * Ncol + n0 + c) = v;
         }
     }
 }

@@ -73,6 +73,35 @@ def test_output_major_duplicates_and_empty_rows(device):
     _bitwise_store(hip_layer(compact), compact)
 
 
+def test_gelu_against_float64(device):
+    """The device GELU (z/2 erfc(-z/sqrt 2), erfc by the Numerical Recipes Chebyshev fit) through the edges up kernel
+    on a layer whose neuron r reads input r with weight 1: act[r, t] = gelu(x[t, r]) for 2048 arguments in [-12, 12],
+    against float64 (relative 2e-6 where |gelu| > 1e-6, absolute 4e-7 max(1, |z|) everywhere)."""
+    import ctypes
+    import math
+    from hffn_amd import _lib
+    d = h = 256
+    n = 8
+    z = torch.linspace(-12.0, 12.0, n * d, dtype=torch.float64)
+    x = z.float().reshape(n, d).to(device)
+    offsets = torch.arange(h + 1, dtype=torch.int32, device=device)
+    index = torch.arange(h, dtype=torch.int16, device=device)
+    values = torch.ones(h, device=device)
+    bias = torch.zeros(h, device=device)
+    act = torch.empty(h, n, device=device)
+    lib = _lib.load()
+    _lib.check(lib.hffn_up(_lib.UP_MODES["edges"], _lib.VALUE_F32, x.data_ptr(), offsets.data_ptr(), index.data_ptr(),
+                           values.data_ptr(), bias.data_ptr(), act.data_ptr(), d, h, h, n, n,
+                           torch.cuda.current_stream(device).cuda_stream), "up")
+    got = act.T.double().cpu().reshape(-1)
+    zf = x.double().cpu().reshape(-1)
+    expected = torch.tensor([0.5 * v * math.erfc(-v / math.sqrt(2.0)) for v in zf.tolist()], dtype=torch.float64)
+    error = (got - expected).abs()
+    assert bool((error <= 4e-7 * zf.abs().clamp(min=1.0)).all()), float(error.max())
+    big = expected.abs() > 1e-6
+    assert float((error[big] / expected[big].abs()).max()) <= 2e-6
+
+
 @pytest.mark.parametrize("name", sorted(synth.CASES))
 def test_forced_pairs_match_the_oracle(name, test_layers, device):
     compact, case, layer = test_layers[name]
