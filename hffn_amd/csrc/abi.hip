@@ -46,7 +46,7 @@ int check_shape(uint32_t d, uint32_t h, uint32_t n, uint32_t ld) {
 int check_edges(uint32_t d, uint32_t n, uint32_t ld, bool stage) {
     const uint32_t nt = hffn::edges_tokens(n);
     if (ld % nt != 0) return fail(HFFN_ERROR_ARGUMENT, "edges mode: ld=%u must be a multiple of %u for n=%u", ld, nt, n);
-    if (stage && static_cast<size_t>(nt) * (d + 4) * sizeof(float) > HFFN_EDGES_MAX_LDS)
+    if (stage && static_cast<size_t>(nt) * (d + 16) * sizeof(float) > HFFN_EDGES_MAX_LDS)
         return fail(HFFN_ERROR_ARGUMENT, "edges mode: %u tokens of d_model=%u exceed the %u-byte LDS stage", nt, d, HFFN_EDGES_MAX_LDS);
     return HFFN_OK;
 }
@@ -61,7 +61,7 @@ const char* hffn_last_error(void) { return g_error.c_str(); }
 
 int hffn_edges_supported(uint32_t d_model, uint32_t n) {
     if (n == 0) return 0;
-    return static_cast<size_t>(hffn::edges_tokens(n)) * (d_model + 4) * sizeof(float) <= HFFN_EDGES_MAX_LDS ? 1 : 0;
+    return static_cast<size_t>(hffn::edges_tokens(n)) * (d_model + 16) * sizeof(float) <= HFFN_EDGES_MAX_LDS ? 1 : 0;
 }
 
 int hffn_transpose(const float* in, float* out, uint32_t rows, uint32_t cols, uint32_t in_ld, uint32_t out_ld,

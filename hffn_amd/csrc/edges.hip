@@ -172,15 +172,15 @@ __device__ __forceinline__ void segment(int32_t begin, int32_t end, uint32_t par
 }
 
 // ------------------------------------------------------------------------------------------------- up
-template <int NT, int P, typename V>
-__global__ __launch_bounds__(kBlock) void up_edges_kernel(const float* __restrict__ x, const int32_t* __restrict__ off,
-                                                         const int16_t* __restrict__ idx, const V* __restrict__ w,
-                                                         const float* __restrict__ b, float* __restrict__ act, uint32_t d,
-                                                         uint32_t h, uint32_t n, uint32_t ld, int32_t nnz, uint32_t per_block) {
-    extern __shared__ float smem[];  // x of NT tokens, [d][NT]; then the segment totals [kWaves][NT]
+template <int NT, int P, typename V, int WAVES>
+__global__ __launch_bounds__(WAVES * kWave) void up_edges_kernel(const float* __restrict__ x, const int32_t* __restrict__ off,
+                                                                const int16_t* __restrict__ idx, const V* __restrict__ w,
+                                                                const float* __restrict__ b, float* __restrict__ act, uint32_t d,
+                                                                uint32_t h, uint32_t n, uint32_t ld, int32_t nnz, uint32_t per_block) {
+    extern __shared__ float smem[];  // x of NT tokens, [d][NT]; then the segment totals [WAVES][NT]
     float* xs = smem;
     float* totals = smem + static_cast<size_t>(d) * NT;
-    constexpr uint32_t kRowsPerPass = kWaves / P;
+    constexpr uint32_t kRowsPerPass = WAVES / P;
     const uint32_t wave = uniform(threadIdx.x / kWave), lane = threadIdx.x % kWave;
     const uint32_t row_in_pass = wave / P, part = wave % P;
     const uint32_t r0 = blockIdx.x * per_block;
@@ -195,7 +195,7 @@ __global__ __launch_bounds__(kBlock) void up_edges_kernel(const float* __restric
             load_segment(first, idx, w, pb, pe, nnz, lane, 0);
         }
         if (c0) __syncthreads();
-        for (uint32_t i = threadIdx.x; i < d * NT; i += kBlock) {
+        for (uint32_t i = threadIdx.x; i < d * NT; i += WAVES * kWave) {
             const uint32_t feature = i / NT, t = i % NT;
             xs[i] = t < tokens ? x[static_cast<size_t>(c0 + t) * d + feature] : 0.0f;
         }
@@ -285,14 +285,36 @@ uint32_t rows_per_block(uint32_t rows, int parts, uint32_t waves = kWaves, uint3
     return ceil_div(per, pass) * pass;
 }
 
+// Up stages of more than 64 KB (wide d_model at 8 tokens) need the kernel's dynamic LDS limit raised (once per
+// kernel: the limit is remembered per instantiation).
+template <auto Kernel>
+hipError_t allow_lds(size_t lds) {
+    static size_t allowed = 65536;
+    if (lds <= allowed) return hipSuccess;
+    const hipError_t status = hipFuncSetAttribute(reinterpret_cast<const void*>(Kernel), hipFuncAttributeMaxDynamicSharedMemorySize,
+                                                  static_cast<int>(lds));
+    if (status == hipSuccess) allowed = lds;
+    return status;
+}
+
+// Every block stages x of its NT tokens (d * NT floats from L2): from 4 tokens on, blocks of 16 waves (a quarter as
+// many blocks) cut that traffic by 4.
+template <int NT, int P, typename V, int WAVES>
+hipError_t up_waves(const float* x, const int32_t* off, const int16_t* idx, const V* w, const float* b, float* act, uint32_t d,
+                    uint32_t h, uint32_t n, uint32_t ld, uint32_t nnz, hipStream_t stream) {
+    const uint32_t per = rows_per_block(h, P, WAVES, WAVES == kWaves ? 1024 : 256);
+    const size_t lds = (static_cast<size_t>(d) * NT + WAVES * NT) * sizeof(float);
+    if (const hipError_t status = allow_lds<up_edges_kernel<NT, P, V, WAVES>>(lds); status != hipSuccess) return status;
+    hipLaunchKernelGGL((up_edges_kernel<NT, P, V, WAVES>), dim3(ceil_div(h, per)), dim3(WAVES * kWave), lds, stream, x, off, idx, w, b,
+                       act, d, h, n, ld, static_cast<int32_t>(nnz), per);
+    return hipGetLastError();
+}
+
 template <int NT, int P, typename V>
 hipError_t up_shape(const float* x, const int32_t* off, const int16_t* idx, const V* w, const float* b, float* act, uint32_t d,
                     uint32_t h, uint32_t n, uint32_t ld, uint32_t nnz, hipStream_t stream) {
-    const uint32_t per = rows_per_block(h, P);
-    const size_t lds = (static_cast<size_t>(d) * NT + kWaves * NT) * sizeof(float);
-    hipLaunchKernelGGL((up_edges_kernel<NT, P, V>), dim3(ceil_div(h, per)), dim3(kBlock), lds, stream, x, off, idx, w, b, act, d,
-                       h, n, ld, static_cast<int32_t>(nnz), per);
-    return hipGetLastError();
+    if constexpr (NT >= 4) return up_waves<NT, P, V, 16>(x, off, idx, w, b, act, d, h, n, ld, nnz, stream);
+    else return up_waves<NT, P, V, kWaves>(x, off, idx, w, b, act, d, h, n, ld, nnz, stream);
 }
 
 // With act staged in LDS (small n), blocks of 16 waves take 4x the rows of 4-wave blocks, so each block's staging
@@ -305,6 +327,7 @@ hipError_t down_shape(const float* act, const int32_t* off, const int16_t* hid, 
         constexpr uint32_t waves = 16;
         const uint32_t per = rows_per_block(d, P, waves, 256);
         const size_t lds = (static_cast<size_t>(h) * NT + waves * NT) * sizeof(float);
+        if (const hipError_t status = allow_lds<down_edges_kernel<NT, P, V, true, waves>>(lds); status != hipSuccess) return status;
         hipLaunchKernelGGL((down_edges_kernel<NT, P, V, true, waves>), dim3(ceil_div(d, per)), dim3(waves * kWave), lds, stream,
                            act, off, hid, v, bias, y, d, h, n, ld, static_cast<int32_t>(nnz), per);
     } else {

@@ -781,8 +781,9 @@ hipError_t gemm(Shape shape, const _Float16* a_planes, const int32_t* a_exp, con
 }
 
 // The streamed kernel takes a GEMM when its 256 x 128 tiles (times the k splits of a down projection) give at least
-// 128 blocks; a down projection splits K in 2 or 4 to reach about 256 blocks (each split a whole number of
-// activation blocks), its partials added by reduce_splits_kernel.
+// 128 blocks; a down projection splits K in 2 or 4 to reach about 256 blocks, or to bring a split's activation
+// binades within kDmaMaxActBlocks (each split a whole number of activation blocks); its partials are added by
+// reduce_splits_kernel.
 constexpr uint32_t kDmaMinBlocks = 128;
 
 uint32_t dma_tiles(uint32_t m, uint32_t ncol) { return rows_padded(m) / kDmaBM * (ncol / kDmaBN); }
@@ -790,6 +791,7 @@ uint32_t dma_tiles(uint32_t m, uint32_t ncol) { return rows_padded(m) / kDmaBM *
 uint32_t dma_down_splits(uint32_t m, uint32_t ncol, uint32_t k) {
     const uint32_t tiles = dma_tiles(m, ncol);
     uint32_t splits = tiles >= 192 ? 1 : tiles >= 96 ? 2 : 4;
+    while (splits < 4 && k / kActBlock / splits > kDmaMaxActBlocks) splits *= 2;  // the split's binades must fit LDS
     while (splits > 1 && k % (kActBlock * splits) != 0) splits /= 2;
     if (k / kActBlock / splits > kDmaMaxActBlocks) return 0;  // 0: not streamed
     return tiles * splits >= kDmaMinBlocks ? splits : 0;

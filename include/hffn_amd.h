@@ -48,7 +48,7 @@ extern "C" {
 #define HFFN_MAX_TOKENS (1u << 18)            /* runtime/gpu/nvidia/common/kernels/hffn_cuda/runtime.py:26 */
 #define HFFN_MAX_WIDTH 32768u                 /* widths addressable by the int16 indices */
 #define HFFN_MAX_OUTPUT_MAJOR_WIDTH 16384u    /* d_model of the output-major build (LDS bins) */
-#define HFFN_EDGES_MAX_LDS 65536u             /* bytes of the up input staged by the EDGES shape */
+#define HFFN_EDGES_MAX_LDS 131072u            /* bytes of the up input staged by the EDGES shape */
 
 int hffn_abi_version(void);
 const char* hffn_last_error(void);

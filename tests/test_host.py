@@ -52,6 +52,7 @@ def test_abi_refuses_bad_shapes_before_launching():
     _expect_argument_error(lib.hffn_up(1, 7, p, p, p, p, p, p, 64, 64, 64, 1, 4, None), "unknown value type")
     _expect_argument_error(lib.hffn_up(1, 0, None, p, p, p, p, p, 64, 64, 64, 1, 4, None), "null pointer")
     _expect_argument_error(lib.hffn_up(1, 0, p, p, p, p, p, p, 4096, 64, 64, 8, 8, None), "LDS")
+    _expect_argument_error(lib.hffn_up(1, 0, p, p, p, p, p, p, 8192, 64, 64, 4, 4, None), "LDS")
     _expect_argument_error(lib.hffn_down(3, 0, p, p, p, p, p, p, 64, 64, 64, 1, 4, None), "unknown down mode")
     odd = ctypes.c_void_p(18)
     _expect_argument_error(lib.hffn_up(1, 0, p, p, odd, p, p, p, 64, 64, 64, 1, 4, None), "aligned")
@@ -75,15 +76,17 @@ def test_abi_refuses_bad_shapes_before_launching():
 def test_edges_stage_limit():
     lib = _lib.load()
     assert lib.hffn_edges_supported(1024, 8) == 1
-    assert lib.hffn_edges_supported(2048, 4) == 1
-    assert lib.hffn_edges_supported(2048, 8) == 0
-    assert lib.hffn_edges_supported(2560, 8) == 0
-    assert lib.hffn_edges_supported(2560, 4) == 1
+    assert lib.hffn_edges_supported(2048, 8) == 1
+    assert lib.hffn_edges_supported(2560, 8) == 1
+    assert lib.hffn_edges_supported(4080, 8) == 1
+    assert lib.hffn_edges_supported(4096, 4) == 1
+    assert lib.hffn_edges_supported(4096, 8) == 0
+    assert lib.hffn_edges_supported(4096, 4) == 1
 
 
 def test_policy():
     assert [runtime.up_mode(n) for n in (1, 4, 8, 9, 32, 33, 64, 2048)] == ["edges"] * 5 + ["rows"] * 3
-    assert runtime.up_mode(8, 2560) == "rows" and runtime.up_mode(4, 2560) == "edges"
+    assert runtime.up_mode(8, 4096) == "rows" and runtime.up_mode(4, 4096) == "edges" and runtime.up_mode(8, 2560) == "edges"
     assert [runtime.down_mode(n, 4096) for n in (1, 8, 32, 33, 2048)] == ["edges"] * 3 + ["rows"] * 2
     assert [runtime.leading_dim(n) for n in (1, 2, 3, 4, 5, 8, 9, 2048, 2049)] == [4, 4, 4, 4, 8, 8, 16, 2048, 2056]
 
