@@ -231,18 +231,13 @@ def pythia_config(**overrides):
     return config
 
 
-def write_random_pythia(model_dir: str | Path, export_dir: str | Path, density: float = 0.5, seed: int = 104,
-                        **config_overrides) -> None:
-    """Write a random-init Pythia-shaped checkpoint (``config.json`` + ``model.safetensors`` of the non-FFN tensors,
-    initialised by the model class from ``torch.manual_seed(seed)``) and one export per layer: every neuron's up and
-    down supports are ``round(density * d_model)`` indices drawn uniformly without replacement and sorted, values
-    ~N(0, initializer_range), biases zero (layer l draws from seed ``seed * 100 + l``)."""
+def write_random_checkpoint(model_dir: str | Path, seed: int = 104, **config_overrides):
+    """Write a random-init Pythia-shaped checkpoint: ``config.json`` + ``model.safetensors`` of the non-FFN tensors,
+    initialised by the model class from ``torch.manual_seed(seed)``. Returns the config."""
     from safetensors.torch import save_file
     from transformers import AutoModelForCausalLM
-
-    from .synth import Workload, make_workload_layer
     config = pythia_config(**config_overrides)
-    model_dir, export_dir = Path(model_dir), Path(export_dir)
+    model_dir = Path(model_dir)
     model_dir.mkdir(parents=True, exist_ok=True)
     config.save_pretrained(str(model_dir))
     torch.manual_seed(seed)
@@ -250,11 +245,40 @@ def write_random_pythia(model_dir: str | Path, export_dir: str | Path, density: 
         model = AutoModelForCausalLM.from_config(config, dtype=torch.float32)
     state = {name: tensor.contiguous() for name, tensor in model.state_dict().items() if ".mlp." not in name}
     save_file(state, str(model_dir / "model.safetensors"))
+    return config
+
+
+def write_random_exports(export_dir: str | Path, config, density: float = 0.5, seed: int = 104) -> None:
+    """One export per layer of ``config``: every neuron's up and down supports are ``round(density * d_model)``
+    indices drawn uniformly without replacement and sorted, values ~N(0, initializer_range), biases zero (layer l
+    draws from seed ``seed * 100 + l``)."""
+    from .synth import Workload, make_workload_layer
     d, f = config.hidden_size, config.intermediate_size
-    degree = int(round(density * d))
+    degree = max(1, int(round(density * d)))
     for index in range(config.num_hidden_layers):
         workload = Workload(f"pythia_layer{index}", d, f, degree, seed * 100 + index, w_std=config.initializer_range)
         write_layer(layer_path(export_dir, index), export_of_compact(make_workload_layer(workload)))
+
+
+def write_random_pythia(model_dir: str | Path, export_dir: str | Path, density: float = 0.5, seed: int = 104,
+                        **config_overrides) -> None:
+    """A random-init checkpoint (``write_random_checkpoint``) and its exports at one density
+    (``write_random_exports``)."""
+    config = write_random_checkpoint(model_dir, seed, **config_overrides)
+    write_random_exports(export_dir, config, density, seed)
+
+
+@torch.no_grad()
+def share_non_ffn(model: nn.Module, source: nn.Module) -> None:
+    """Make ``model`` read the non-FFN parameters of ``source`` (both loaded from the same checkpoint) instead of its
+    own copy, so that two arms in one process differ by their FFNs only (``runtime/common/pythia/hffn_pythia/
+    model.py:114-124``)."""
+    owned = dict(source.named_parameters())
+    for prefix, module in model.named_modules():
+        for key, parameter in list(module._parameters.items()):
+            name = f"{prefix}.{key}" if prefix else key
+            if parameter is not None and ".mlp." not in name:
+                module._parameters[key] = owned[name]
 
 
 def synthetic_prompts(batch: int, length: int, vocab: int, seed: int = 1041) -> torch.Tensor:
