@@ -13,11 +13,16 @@ constexpr int kWave = 64;
 // keep their relative accuracy (no 1 + erf cancellation), with erfc from the Chebyshev fit of Press, Teukolsky,
 // Vetterling and Flannery, Numerical Recipes (2nd ed., section 6.2, "erfcc"; fractional error below 1.2e-7 for
 // every argument): for x >= 0, erfc(x) = t exp(-x^2 + P(t)) with t = 1 / (1 + x / 2), and erfc(-x) = 2 - erfc(x).
-// Branch-free, so that a wave evaluates many independent GELUs back to back.
+// Branch-free, so that a wave evaluates many independent GELUs back to back. The reciprocal is the hardware one
+// (1 ulp) refined by a Newton step; exp(y) is the hardware base-2 exponential of y log2(e) carried in two floats
+// (the product's rounding error and the tail of log2(e) are put back by a first-order factor), so that it loses
+// nothing against expf to the rounding of a large |y|.
 __device__ __forceinline__ float gelu(float z) {
     const float x = -z * 0.70710678118654752f;
     const float a = fabsf(x);
-    const float t = 1.0f / fmaf(0.5f, a, 1.0f);
+    const float d = fmaf(0.5f, a, 1.0f);
+    const float t0 = __builtin_amdgcn_rcpf(d);
+    const float t = fmaf(t0, fmaf(-d, t0, 1.0f), t0);
     float p = 0.17087277f;
     p = fmaf(p, t, -0.82215223f);
     p = fmaf(p, t, 1.48851587f);
@@ -28,7 +33,11 @@ __device__ __forceinline__ float gelu(float z) {
     p = fmaf(p, t, 0.37409196f);
     p = fmaf(p, t, 1.00002368f);
     p = fmaf(p, t, -1.26551223f);
-    const float tail = t * expf(fmaf(-a, a, p));  // erfc(|x|)
+    const float y = fmaf(-a, a, p);
+    constexpr float kLog2e = 1.44269502162933349609375f, kLog2eTail = 1.925963033500011e-8f, kLn2 = 0.69314718055994531f;
+    const float h = y * kLog2e;
+    const float l = fmaf(y, kLog2eTail, fmaf(y, kLog2e, -h));  // y log2(e) = h + l to about 2^-48 |h|
+    const float tail = t * (__builtin_amdgcn_exp2f(h) * fmaf(l, kLn2, 1.0f));  // erfc(|x|)
     return 0.5f * z * (x >= 0.0f ? tail : 2.0f - tail);
 }
 

@@ -469,9 +469,9 @@ __global__ __launch_bounds__(kThreads) void gemm_planes_kernel(
 // ------------------------------------------------------------------------------- streamed GEMM (LDS DMA)
 // The large-N GEMM: 256 x 128 block tiles (4 waves of 128 x 64), one block per CU, and k-tiles streamed straight
 // from global memory into a ring of kDmaStages LDS stages by global_load_lds (16 bytes per lane, no registers on
-// the way): at k-tile kt the block waits for stage kt, meets at a barrier, requests stage kt + kDmaStages - 1 into
-// the slot read at kt - 1, and multiplies stage kt; each stage is thus requested kDmaStages - 1 k-tiles before its
-// use. The down GEMM reads the activation binades of its rows and k range into LDS before the first k-tile. Same
+// the way). In the middle of k-tile kt (its first 16-wide step multiplied, its second read into registers) the block
+// waits for stage kt + 1, meets at a barrier and requests stage kt + kDmaStages into the slot of kt; each stage is
+// thus requested kDmaStages - 1 k-tiles before its wait, and the MFMAs never wait for LDS reads. The down GEMM reads the activation binades of its rows and k range into LDS before the first k-tile. Same
 // products and order as gemm_planes_kernel.
 constexpr int kDmaStages = 3;
 constexpr int kDmaBM = 256, kDmaBN = 128;
@@ -484,13 +484,15 @@ __device__ __forceinline__ void wait_loads() {
     __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | (7 << 4));
 }
 
-// 16 bytes per lane from global memory straight into LDS: lane l's bytes land at lds + 16 l (lds wave-uniform). Written
-// as inline assembly so that the compiler, which cannot tell the ring slots apart, does not wait for every transfer
-// in flight before each LDS read; the kernel orders them itself (wait_loads, then a barrier).
-__device__ __forceinline__ void dma16(const _Float16* src, const _Float16* lds) {
-    const uint32_t offset = static_cast<uint32_t>(__builtin_amdgcn_readfirstlane(
+// 16 bytes per lane from global memory straight into LDS: lane l reads base + 16 l (base wave-uniform, in scalar
+// registers, so that a transfer costs no vector address arithmetic) and its bytes land at lds + 16 l. Written as
+// inline assembly so that the compiler, which cannot tell the ring slots apart, does not wait for every transfer in
+// flight before each LDS read; the kernel orders them itself (wait_loads, then a barrier).
+__device__ __forceinline__ void dma16(const _Float16* base, uint32_t lane, const _Float16* lds) {
+    const uint32_t to = static_cast<uint32_t>(__builtin_amdgcn_readfirstlane(
         static_cast<int>(static_cast<uint32_t>(reinterpret_cast<uintptr_t>(lds)))));  // low 32 bits: the LDS address
-    asm volatile("s_mov_b32 m0, %1\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, off" ::"v"(src), "s"(offset) : "memory", "m0");
+    asm volatile("s_mov_b32 m0, %2\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, %1" ::"v"(lane * 16), "s"(base), "s"(to)
+                 : "memory", "m0");
 }
 
 // Workgroup barrier without the memory fence of __syncthreads (whose release would also wait for every LDS DMA in
@@ -533,25 +535,36 @@ __global__ __launch_bounds__(kThreads) void gemm_dma_kernel(
     if constexpr (EPI == Epi::Up) {
         e_row[0][tid] = a_exp[m0 + tid];
     } else {
-        for (uint32_t kb = kb0; kb * kKtPerActBlock < k_end; ++kb)
-            e_tab[kb - kb0][tid] = static_cast<int8_t>(a_exp[static_cast<size_t>(m0 + tid) * a_kblocks + kb]);
+        // the row's binades of this split (whole activation blocks), eight loads in flight at a time
+        const uint32_t blocks = (k_end - k_begin) / kKtPerActBlock;
+        const int32_t* row_exp = a_exp + static_cast<size_t>(m0 + tid) * a_kblocks + kb0;
+        for (uint32_t b0 = 0; b0 < blocks; b0 += 8) {
+            int32_t v[8];
+#pragma unroll
+            for (uint32_t q = 0; q < 8; ++q) v[q] = b0 + q < blocks ? row_exp[b0 + q] : 0;
+#pragma unroll
+            for (uint32_t q = 0; q < 8; ++q)
+                if (b0 + q < blocks) e_tab[b0 + q][tid] = static_cast<int8_t>(v[q]);
+        }
     }
     __syncthreads();
 
-    // stage kt into ring slot `slot`: wave w copies runs of 64 rows (1 KB each) of A, then of B
-    const auto issue = [&](uint32_t kt, uint32_t slot) {
-#pragma unroll
-        for (int q = 0; q < kLoadsA; ++q) {
+    // piece q of stage kt into ring slot `slot`: wave w copies runs of 64 rows (1 KB each) of A (pieces below
+    // kLoadsA), then of B
+    const auto issue_piece = [&](uint32_t kt, uint32_t slot, int q) {
+        if (q < kLoadsA) {
             const uint32_t at = wave * kLoadsA + q, run = at / (BM / 64), rb = at % (BM / 64);
-            dma16(a_planes + ((static_cast<size_t>(kt) * kRuns + run) * rows_pad + m0 + rb * 64 + lane) * 8,
+            dma16(a_planes + ((static_cast<size_t>(kt) * kRuns + run) * rows_pad + m0 + rb * 64) * 8, lane,
                   smem + slot * kStage + (run * BM + rb * 64) * 8);
-        }
-#pragma unroll
-        for (int q = 0; q < kLoadsB; ++q) {
-            const uint32_t at = wave * kLoadsB + q, run = at / (BN / 64), rb = at % (BN / 64);
-            dma16(b_planes + ((static_cast<size_t>(kt) * kRuns + run) * Ncol + n0 + rb * 64 + lane) * 8,
+        } else {
+            const uint32_t at = wave * kLoadsB + (q - kLoadsA), run = at / (BN / 64), rb = at % (BN / 64);
+            dma16(b_planes + ((static_cast<size_t>(kt) * kRuns + run) * Ncol + n0 + rb * 64) * 8, lane,
                   smem + slot * kStage + kRuns * BM * 8 + (run * BN + rb * 64) * 8);
         }
+    };
+    const auto issue = [&](uint32_t kt, uint32_t slot) {
+#pragma unroll
+        for (int q = 0; q < kLoads; ++q) issue_piece(kt, slot, q);
     };
 
     floatx16 acc[MI][NI];
@@ -562,19 +575,77 @@ __global__ __launch_bounds__(kThreads) void gemm_dma_kernel(
 #pragma unroll
             for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.0f;
 
+    // operand fragments of one 16-wide k step (chunk pair kk of a k-tile)
+    struct Frags {
+        half8 ah[MI], al[MI], bh[NI], bl[NI];
+    };
+    const auto load = [&](Frags& f, uint32_t slot, int kk) {
+        const _Float16* s_a = smem + slot * kStage;
+        const _Float16* s_b = s_a + kRuns * BM * 8;
+        const uint32_t chunk = kk * 2 + lane / 32;
 #pragma unroll
-    for (int s = 0; s < S - 1; ++s)
-        if (k_begin + s < k_end) issue(k_begin + s, s);
-    for (uint32_t kt = k_begin; kt < k_end; ++kt) {
-        const uint32_t it = kt - k_begin, slot = it % S;
-        if (kt + 1 < k_end) wait_loads<kLoads>();  // stage kt has landed; stage kt + 1 may still be in flight
-        else wait_loads<0>();
-        block_barrier();
-        if (kt + S - 1 < k_end) issue(kt + S - 1, (it + S - 1) % S);
+        for (int i = 0; i < MI; ++i) {
+            const uint32_t r = wm * (BM / 2) + i * 32 + lane % 32;
+            f.ah[i] = *reinterpret_cast<const half8*>(s_a + (chunk * BM + r) * 8);
+            f.al[i] = *reinterpret_cast<const half8*>(s_a + ((4 + chunk) * BM + r) * 8);
+        }
+#pragma unroll
+        for (int j = 0; j < NI; ++j) {
+            const uint32_t r = wn * (BN / 2) + j * 32 + lane % 32;
+            f.bh[j] = *reinterpret_cast<const half8*>(s_b + (chunk * BN + r) * 8);
+            if constexpr (LO_B) f.bl[j] = *reinterpret_cast<const half8*>(s_b + ((4 + chunk) * BN + r) * 8);
+        }
+    };
+    const auto multiply = [&](const Frags& f) {
+#pragma unroll
+        for (int i = 0; i < MI; ++i)
+#pragma unroll
+            for (int j = 0; j < NI; ++j) {
+                acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(f.ah[i], f.bh[j], acc[i][j], 0, 0, 0);
+                if constexpr (LO_B) acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(f.ah[i], f.bl[j], acc[i][j], 0, 0, 0);
+                acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(f.al[i], f.bh[j], acc[i][j], 0, 0, 0);
+            }
+    };
+    // The same products with stage kt's transfers spread among them, one after every few MFMAs: a transfer's issue
+    // holds the wave while the CU's address unit takes the other waves' transfers, and in-order issue would
+    // otherwise keep the MFMA unit idle behind a burst of them. sched_barrier pins the order.
+    constexpr int kProducts = LO_B ? 3 : 2, kMfmas = MI * NI * kProducts;
+    static_assert(kMfmas >= kLoads, "at most one transfer per MFMA");
+    const auto multiply_issuing = [&](const Frags& f, uint32_t kt, uint32_t slot, bool transfer) {
+#pragma unroll
+        for (int p = 0; p < kProducts; ++p)  // product-major: consecutive MFMAs accumulate into different tiles
+#pragma unroll
+            for (int i = 0; i < MI; ++i)
+#pragma unroll
+                for (int j = 0; j < NI; ++j) {
+                    const half8& a = p == kProducts - 1 ? f.al[i] : f.ah[i];
+                    const half8& b = (LO_B && p == 1) ? f.bl[j] : f.bh[j];
+                    acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a, b, acc[i][j], 0, 0, 0);
+                    const int m = (p * MI + i) * NI + j;  // MFMAs issued so far, less one
+                    if ((m + 1) * kLoads % kMfmas < kLoads) {   // kLoads transfers evenly over kMfmas MFMAs
+                        __builtin_amdgcn_sched_barrier(0);
+                        if (transfer) issue_piece(kt, slot, (m + 1) * kLoads / kMfmas - 1);
+                        __builtin_amdgcn_sched_barrier(0);
+                    }
+                }
+    };
+
+    // Software pipeline over half k-tiles: the fragments of the next 16-wide step are read from LDS while the MFMAs
+    // of the current one run, and the block meets once per k-tile, between its two steps (after every wave has read
+    // all of k-tile kt and before anyone reads k-tile kt + 1), where the slot of kt is refilled with kt + kDmaStages.
+    const uint32_t steps = k_end - k_begin;  // at least 1
+#pragma unroll
+    for (int s = 0; s < S; ++s)
+        if (static_cast<uint32_t>(s) < steps) issue(k_begin + s, s);
+    if (steps >= 3) wait_loads<2 * kLoads>();  // stage k_begin has landed; the two after it may be in flight
+    else if (steps == 2) wait_loads<kLoads>();
+    else wait_loads<0>();
+    block_barrier();
+    // a new activation block at k-tile kt: bring the accumulators to its power of two (exact); accumulator
+    // registers 4g .. 4g + 3 hold 4 consecutive rows, so one 4-byte read per block and group
+    const auto rescale = [&](uint32_t kt) {
         if constexpr (EPI == Epi::Down) {
             if (kt % kKtPerActBlock == 0 && kt != k_begin) {
-                // a new activation block: bring the accumulators to its power of two (exact)
-                // accumulator registers 4g .. 4g + 3 hold 4 consecutive rows: one 4-byte read per block and group
                 const uint32_t kb = kt / kKtPerActBlock - kb0;
 #pragma unroll
                 for (int i = 0; i < MI; ++i)
@@ -593,34 +664,33 @@ __global__ __launch_bounds__(kThreads) void gemm_dma_kernel(
                     }
             }
         }
-        const _Float16* s_a = smem + slot * kStage;
-        const _Float16* s_b = s_a + kRuns * BM * 8;
-#pragma unroll
-        for (int kk = 0; kk < 2; ++kk) {
-            const uint32_t chunk = kk * 2 + lane / 32;
-            half8 ah[MI], al[MI], bh[NI], bl[NI];
-#pragma unroll
-            for (int i = 0; i < MI; ++i) {
-                const uint32_t r = wm * (BM / 2) + i * 32 + lane % 32;
-                ah[i] = *reinterpret_cast<const half8*>(s_a + (chunk * BM + r) * 8);
-                al[i] = *reinterpret_cast<const half8*>(s_a + ((4 + chunk) * BM + r) * 8);
-            }
-#pragma unroll
-            for (int j = 0; j < NI; ++j) {
-                const uint32_t r = wn * (BN / 2) + j * 32 + lane % 32;
-                bh[j] = *reinterpret_cast<const half8*>(s_b + (chunk * BN + r) * 8);
-                if constexpr (LO_B) bl[j] = *reinterpret_cast<const half8*>(s_b + ((4 + chunk) * BN + r) * 8);
-            }
-#pragma unroll
-            for (int i = 0; i < MI; ++i)
-#pragma unroll
-                for (int j = 0; j < NI; ++j) {
-                    acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(ah[i], bh[j], acc[i][j], 0, 0, 0);
-                    if constexpr (LO_B) acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(ah[i], bl[j], acc[i][j], 0, 0, 0);
-                    acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(al[i], bh[j], acc[i][j], 0, 0, 0);
-                }
-        }
+    };
+    Frags f0, f1;
+    load(f0, 0, 0);
+    // every k-tile but the last (peeled, so that no path reaches the second step's MFMAs without the barrier's wait
+    // for the first step's reads: the compiler's own LDS waits then never hold them for the reads just issued)
+    // (sched_barrier keeps each step's LDS reads ahead of the MFMAs they overlap)
+    for (uint32_t kt = k_begin; kt + 1 < k_end; ++kt) {
+        const uint32_t it = kt - k_begin, slot = it % S;
+        rescale(kt);
+        wait_loads<63>();  // this step's reads, issued a step ago, are in: the next reads do not hold its MFMAs
+        load(f1, slot, 1);
+        __builtin_amdgcn_sched_barrier(0);
+        multiply(f0);
+        if (kt + 2 < k_end) wait_loads<kLoads>();  // stage kt + 1 has landed, kt + 2 may be in flight
+        else wait_loads<0>();
+        wait_loads<63>();  // the same LDS wait on every path, where the compiler's wait tracking sees it
+        block_barrier();
+        load(f0, (it + 1) % S, 0);
+        __builtin_amdgcn_sched_barrier(0);
+        multiply_issuing(f1, kt + S, slot, kt + S < k_end);  // straight-line MFMAs: one set of accumulators
     }
+    rescale(k_end - 1);
+    wait_loads<63>();
+    load(f1, (steps - 1) % S, 1);
+    __builtin_amdgcn_sched_barrier(0);
+    multiply(f0);
+    multiply(f1);
     __syncthreads();
 
     if constexpr (EPI == Epi::Up) {
