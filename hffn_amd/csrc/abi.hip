@@ -5,7 +5,9 @@
 
 #include <cstdarg>
 #include <cstdio>
+#include <mutex>
 #include <string>
+#include <unordered_map>
 
 #include "../../include/hffn_amd.h"
 #include "launch.hpp"
@@ -82,41 +84,124 @@ int check_store_alignment(const int16_t* idx, const void* val, int value_type) {
 }
 }  // namespace
 
-int hffn_up(int mode, int value_type, const float* x, const int32_t* up_offsets, const int16_t* up_idx,
-            const void* up_val, const float* b_up, float* act, uint32_t d_model, uint32_t d_ff, uint32_t nnz_up, uint32_t n,
-            uint32_t ld, void* stream) {
+}  // extern "C"
+
+namespace {
+
+// Argument checks of hffn_up / hffn_down (everything a launch relies on), apart from the launch itself.
+int check_up(int mode, int value_type, const float* x, const int32_t* up_offsets, const int16_t* up_idx, const void* up_val,
+             const float* b_up, const float* act, uint32_t d_model, uint32_t d_ff, uint32_t n, uint32_t ld) {
     if (int status = check_shape(d_model, d_ff, n, ld)) return status;
     if (!valid_value_type(value_type)) return fail(HFFN_ERROR_ARGUMENT, "unknown value type %d", value_type);
     if (!x || !up_offsets || !up_idx || !up_val || !b_up || !act) return fail(HFFN_ERROR_ARGUMENT, "up: null pointer");
-    const hipStream_t s = static_cast<hipStream_t>(stream);
     if (mode == HFFN_UP_EDGES) {
         if (int status = check_edges(d_model, n, ld, true)) return status;
-        if (int status = check_store_alignment(up_idx, up_val, value_type)) return status;
+        return check_store_alignment(up_idx, up_val, value_type);
+    }
+    if (mode == HFFN_UP_ROWS) return HFFN_OK;
+    return fail(HFFN_ERROR_ARGUMENT, "unknown up mode %d", mode);
+}
+
+int check_down(int mode, int value_type, const float* act, const int32_t* out_offsets, const int16_t* out_hidden,
+               const void* out_val, const float* b_down, const float* y, uint32_t d_model, uint32_t d_ff, uint32_t n, uint32_t ld) {
+    if (int status = check_shape(d_model, d_ff, n, ld)) return status;
+    if (!valid_value_type(value_type)) return fail(HFFN_ERROR_ARGUMENT, "unknown value type %d", value_type);
+    if (!act || !out_offsets || !out_hidden || !out_val || !b_down || !y) return fail(HFFN_ERROR_ARGUMENT, "down: null pointer");
+    if (mode == HFFN_DOWN_EDGES) {
+        if (int status = check_edges(d_model, n, ld, false)) return status;
+        return check_store_alignment(out_hidden, out_val, value_type);
+    }
+    if (mode == HFFN_DOWN_ROWS) return HFFN_OK;
+    return fail(HFFN_ERROR_ARGUMENT, "unknown down mode %d", mode);
+}
+
+int launch_up(int mode, int value_type, const float* x, const int32_t* up_offsets, const int16_t* up_idx, const void* up_val,
+              const float* b_up, float* act, uint32_t d_model, uint32_t d_ff, uint32_t nnz_up, uint32_t n, uint32_t ld, hipStream_t s) {
+    if (mode == HFFN_UP_EDGES)
         return launched(hffn::launch_up_edges(value_type, x, up_offsets, up_idx, up_val, b_up, act, d_model, d_ff, n, ld, nnz_up, s),
                         "up edges");
+    return launched(hffn::launch_up_rows(value_type, x, up_offsets, up_idx, up_val, b_up, act, d_model, d_ff, n, ld, s), "up rows");
+}
+
+int launch_down(int mode, int value_type, const float* act, const int32_t* out_offsets, const int16_t* out_hidden,
+                const void* out_val, const float* b_down, float* y, uint32_t d_model, uint32_t d_ff, uint32_t nnz_down, uint32_t n,
+                uint32_t ld, hipStream_t s) {
+    if (mode == HFFN_DOWN_EDGES)
+        return launched(hffn::launch_down_edges(value_type, act, out_offsets, out_hidden, out_val, b_down, y, d_model, d_ff, n, ld,
+                                                nnz_down, s),
+                        "down edges");
+    return launched(hffn::launch_down_rows(value_type, act, out_offsets, out_hidden, out_val, b_down, y, d_model, n, ld, s), "down rows");
+}
+
+// Everything of one gather-mode forward but x and the stream.
+struct Plan {
+    int up_mode, down_mode, value_type;
+    const int32_t* up_offsets;
+    const int16_t* up_idx;
+    const void* up_val;
+    const float* b_up;
+    const int32_t* out_offsets;
+    const int16_t* out_hidden;
+    const void* out_val;
+    const float* b_down;
+    float *x_t, *act, *y_t, *y;
+    uint32_t d_model, d_ff, nnz_up, nnz_down, n, ld;
+};
+
+// The checks of hffn_forward with a stand-in for x (checked at each launch instead).
+int check_forward(const Plan& p) {
+    const float* some_x = reinterpret_cast<const float*>(uintptr_t{16});  // non-null, aligned: never dereferenced
+    if (p.up_mode == HFFN_UP_ROWS && !p.x_t) return fail(HFFN_ERROR_ARGUMENT, "forward: null x_t workspace");
+    if (p.down_mode == HFFN_DOWN_ROWS && !p.y_t) return fail(HFFN_ERROR_ARGUMENT, "forward: null y_t workspace");
+    const float* up_in = p.up_mode == HFFN_UP_ROWS ? p.x_t : some_x;
+    if (int status = check_up(p.up_mode, p.value_type, up_in, p.up_offsets, p.up_idx, p.up_val, p.b_up, p.act, p.d_model, p.d_ff,
+                              p.n, p.ld))
+        return status;
+    return check_down(p.down_mode, p.value_type, p.act, p.out_offsets, p.out_hidden, p.out_val, p.b_down,
+                      p.down_mode == HFFN_DOWN_ROWS ? p.y_t : p.y, p.d_model, p.d_ff, p.n, p.ld);
+}
+
+// hffn_forward after its checks.
+int launch_forward(const Plan& p, const float* x, hipStream_t s) {
+    if (p.up_mode == HFFN_UP_ROWS) {
+        if (int status = launched(hffn::launch_transpose(x, p.x_t, p.n, p.d_model, p.d_model, p.ld, s), "input transpose")) return status;
+        x = p.x_t;
     }
-    if (mode == HFFN_UP_ROWS)
-        return launched(hffn::launch_up_rows(value_type, x, up_offsets, up_idx, up_val, b_up, act, d_model, d_ff, n, ld, s), "up rows");
-    return fail(HFFN_ERROR_ARGUMENT, "unknown up mode %d", mode);
+    if (int status = launch_up(p.up_mode, p.value_type, x, p.up_offsets, p.up_idx, p.up_val, p.b_up, p.act, p.d_model, p.d_ff,
+                               p.nnz_up, p.n, p.ld, s))
+        return status;
+    if (p.down_mode == HFFN_DOWN_ROWS) {
+        if (int status = launch_down(p.down_mode, p.value_type, p.act, p.out_offsets, p.out_hidden, p.out_val, p.b_down, p.y_t,
+                                     p.d_model, p.d_ff, p.nnz_down, p.n, p.ld, s))
+            return status;
+        return launched(hffn::launch_transpose(p.y_t, p.y, p.d_model, p.n, p.ld, p.d_model, s), "output transpose");
+    }
+    return launch_down(p.down_mode, p.value_type, p.act, p.out_offsets, p.out_hidden, p.out_val, p.b_down, p.y, p.d_model, p.d_ff,
+                       p.nnz_down, p.n, p.ld, s);
+}
+
+std::mutex g_plans_mutex;
+std::unordered_map<uint64_t, Plan> g_plans;
+uint64_t g_next_plan = 1;
+
+}  // namespace
+
+extern "C" {
+
+int hffn_up(int mode, int value_type, const float* x, const int32_t* up_offsets, const int16_t* up_idx,
+            const void* up_val, const float* b_up, float* act, uint32_t d_model, uint32_t d_ff, uint32_t nnz_up, uint32_t n,
+            uint32_t ld, void* stream) {
+    if (int status = check_up(mode, value_type, x, up_offsets, up_idx, up_val, b_up, act, d_model, d_ff, n, ld)) return status;
+    return launch_up(mode, value_type, x, up_offsets, up_idx, up_val, b_up, act, d_model, d_ff, nnz_up, n, ld,
+                     static_cast<hipStream_t>(stream));
 }
 
 int hffn_down(int mode, int value_type, const float* act, const int32_t* out_offsets, const int16_t* out_hidden,
               const void* out_val, const float* b_down, float* y, uint32_t d_model, uint32_t d_ff, uint32_t nnz_down,
               uint32_t n, uint32_t ld, void* stream) {
-    if (int status = check_shape(d_model, d_ff, n, ld)) return status;
-    if (!valid_value_type(value_type)) return fail(HFFN_ERROR_ARGUMENT, "unknown value type %d", value_type);
-    if (!act || !out_offsets || !out_hidden || !out_val || !b_down || !y) return fail(HFFN_ERROR_ARGUMENT, "down: null pointer");
-    const hipStream_t s = static_cast<hipStream_t>(stream);
-    if (mode == HFFN_DOWN_EDGES) {
-        if (int status = check_edges(d_model, n, ld, false)) return status;
-        if (int status = check_store_alignment(out_hidden, out_val, value_type)) return status;
-        return launched(hffn::launch_down_edges(value_type, act, out_offsets, out_hidden, out_val, b_down, y, d_model, d_ff, n, ld,
-                                                nnz_down, s),
-                        "down edges");
-    }
-    if (mode == HFFN_DOWN_ROWS)
-        return launched(hffn::launch_down_rows(value_type, act, out_offsets, out_hidden, out_val, b_down, y, d_model, n, ld, s), "down rows");
-    return fail(HFFN_ERROR_ARGUMENT, "unknown down mode %d", mode);
+    if (int status = check_down(mode, value_type, act, out_offsets, out_hidden, out_val, b_down, y, d_model, d_ff, n, ld)) return status;
+    return launch_down(mode, value_type, act, out_offsets, out_hidden, out_val, b_down, y, d_model, d_ff, nnz_down, n, ld,
+                       static_cast<hipStream_t>(stream));
 }
 
 int hffn_forward(int up_mode, int down_mode, int value_type, const float* x, const int32_t* up_offsets,
@@ -124,25 +209,43 @@ int hffn_forward(int up_mode, int down_mode, int value_type, const float* x, con
                  const int16_t* out_hidden, const void* out_val, const float* b_down, float* x_t, float* act,
                  float* y_t, float* y, uint32_t d_model, uint32_t d_ff, uint32_t nnz_up, uint32_t nnz_down, uint32_t n,
                  uint32_t ld, void* stream) {
-    if (int status = check_shape(d_model, d_ff, n, ld)) return status;
-    const hipStream_t s = static_cast<hipStream_t>(stream);
-    if (up_mode == HFFN_UP_ROWS) {
-        if (!x || !x_t) return fail(HFFN_ERROR_ARGUMENT, "forward: null input or x_t workspace");
-        if (int status = hffn_transpose(x, x_t, n, d_model, d_model, ld, stream)) return status;
-        if (int status = hffn_up(up_mode, value_type, x_t, up_offsets, up_idx, up_val, b_up, act, d_model, d_ff, nnz_up, n, ld, stream))
-            return status;
-    } else {
-        if (int status = hffn_up(up_mode, value_type, x, up_offsets, up_idx, up_val, b_up, act, d_model, d_ff, nnz_up, n, ld, stream))
-            return status;
+    const Plan plan{up_mode, down_mode, value_type, up_offsets, up_idx, up_val, b_up, out_offsets, out_hidden, out_val, b_down,
+                    x_t, act, y_t, y, d_model, d_ff, nnz_up, nnz_down, n, ld};
+    if (int status = check_forward(plan)) return status;
+    if (!x) return fail(HFFN_ERROR_ARGUMENT, "forward: null input");
+    return launch_forward(plan, x, static_cast<hipStream_t>(stream));
+}
+
+int hffn_plan_forward(int up_mode, int down_mode, int value_type, const int32_t* up_offsets, const int16_t* up_idx,
+                      const void* up_val, const float* b_up, const int32_t* out_offsets, const int16_t* out_hidden,
+                      const void* out_val, const float* b_down, float* x_t, float* act, float* y_t, float* y, uint32_t d_model,
+                      uint32_t d_ff, uint32_t nnz_up, uint32_t nnz_down, uint32_t n, uint32_t ld, uint64_t* plan) {
+    if (!plan) return fail(HFFN_ERROR_ARGUMENT, "plan_forward: null result");
+    const Plan p{up_mode, down_mode, value_type, up_offsets, up_idx, up_val, b_up, out_offsets, out_hidden, out_val, b_down,
+                 x_t, act, y_t, y, d_model, d_ff, nnz_up, nnz_down, n, ld};
+    if (int status = check_forward(p)) return status;
+    const std::lock_guard<std::mutex> lock(g_plans_mutex);
+    *plan = g_next_plan++;
+    g_plans.emplace(*plan, p);
+    return HFFN_OK;
+}
+
+int hffn_plan_launch(uint64_t plan, const float* x, void* stream) {
+    Plan p;
+    {
+        const std::lock_guard<std::mutex> lock(g_plans_mutex);
+        const auto found = g_plans.find(plan);
+        if (found == g_plans.end()) return fail(HFFN_ERROR_ARGUMENT, "plan_launch: unknown plan %llu", static_cast<unsigned long long>(plan));
+        p = found->second;
     }
-    if (down_mode == HFFN_DOWN_ROWS) {
-        if (!y_t) return fail(HFFN_ERROR_ARGUMENT, "forward: null y_t workspace");
-        if (int status = hffn_down(down_mode, value_type, act, out_offsets, out_hidden, out_val, b_down, y_t, d_model, d_ff, nnz_down,
-                                   n, ld, stream))
-            return status;
-        return launched(hffn::launch_transpose(y_t, y, d_model, n, ld, d_model, s), "output transpose");
-    }
-    return hffn_down(down_mode, value_type, act, out_offsets, out_hidden, out_val, b_down, y, d_model, d_ff, nnz_down, n, ld, stream);
+    if (!x) return fail(HFFN_ERROR_ARGUMENT, "plan_launch: null input");
+    return launch_forward(p, x, static_cast<hipStream_t>(stream));
+}
+
+int hffn_plan_release(uint64_t plan) {
+    const std::lock_guard<std::mutex> lock(g_plans_mutex);
+    if (g_plans.erase(plan) == 0) return fail(HFFN_ERROR_ARGUMENT, "plan_release: unknown plan %llu", static_cast<unsigned long long>(plan));
+    return HFFN_OK;
 }
 
 int hffn_output_major_workspace(uint32_t nnz, uint32_t d_model, uint64_t* bytes) {

@@ -127,9 +127,10 @@ def layer_from_export(layer: dict, device: str | torch.device | None = None):
 
 
 def hip_runtime(layers: list[dict], device: str | torch.device = "cuda"):
-    """The HFFN HIP runtime of a model's export layers."""
-    from .runtime import HFFNRuntime
-    return HFFNRuntime([layer_from_export(layer, device) for layer in layers], device)
+    """The HFFN HIP runtime of a model's export layers: ``PreparedRuntime`` (decode calls launched from per-(layer, N)
+    plans), as the reference leaf's ``_runtime`` (``runtime/gpu/nvidia/llm/inference/hffn_pythia_cuda/model.py:18-20``)."""
+    from .prepared_runtime import PreparedRuntime
+    return PreparedRuntime([layer_from_export(layer, device) for layer in layers], device)
 
 
 # --------------------------------------------------------------------------------------------------- the loader

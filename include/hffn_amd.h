@@ -27,7 +27,7 @@
 extern "C" {
 #endif
 
-#define HFFN_ABI_VERSION 2
+#define HFFN_ABI_VERSION 3
 
 #define HFFN_OK 0
 #define HFFN_ERROR_ARGUMENT (-1) /* invalid shape, mode, pointer or workspace */
@@ -81,13 +81,26 @@ int hffn_down(int mode, int value_type, const float* act, const int32_t* out_off
 
 /* The whole layer for x[n, d_model] -> y[n, d_model]: the transposes the modes need, up, down.
  * x_t and y_t may be NULL when the modes do not use them. Replaces HFFNRuntime._launch
- * (runtime/gpu/nvidia/common/kernels/hffn_cuda/runtime.py:134-163) and the two driver launches of
- * PreparedRuntime.forward (runtime/gpu/nvidia/llm/inference/hffn_pythia_cuda/prepared_runtime.py:62-82). */
+ * (runtime/gpu/nvidia/common/kernels/hffn_cuda/runtime.py:134-163). */
 int hffn_forward(int up_mode, int down_mode, int value_type, const float* x, const int32_t* up_offsets,
                  const int16_t* up_idx, const void* up_val, const float* b_up, const int32_t* out_offsets,
                  const int16_t* out_hidden, const void* out_val, const float* b_down, float* x_t, float* act,
                  float* y_t, float* y, uint32_t d_model, uint32_t d_ff, uint32_t nnz_up, uint32_t nnz_down, uint32_t n,
                  uint32_t ld, void* stream);
+
+/* Prepared forward (the decode launch path). hffn_plan_forward checks every argument of hffn_forward but x and
+ * the stream, as hffn_forward does, and keeps them under a new nonzero handle *plan; hffn_plan_launch(plan, x,
+ * stream) then launches that forward for x (launch errors only); hffn_plan_release drops the handle. The pointers
+ * are kept as given: a plan must be released before any of its buffers is freed or reallocated. Handles are
+ * process-wide and the table is locked, so plans may be made and launched from several threads. Replaces the
+ * per-(layer, N) _Descriptor of PreparedRuntime (pre-packed driver argument tables, x patched per call) and its two
+ * driver launches: runtime/gpu/nvidia/llm/inference/hffn_pythia_cuda/prepared_runtime.py:34-82. */
+int hffn_plan_forward(int up_mode, int down_mode, int value_type, const int32_t* up_offsets, const int16_t* up_idx,
+                      const void* up_val, const float* b_up, const int32_t* out_offsets, const int16_t* out_hidden,
+                      const void* out_val, const float* b_down, float* x_t, float* act, float* y_t, float* y, uint32_t d_model,
+                      uint32_t d_ff, uint32_t nnz_up, uint32_t nnz_down, uint32_t n, uint32_t ld, uint64_t* plan);
+int hffn_plan_launch(uint64_t plan, const float* x, void* stream);
+int hffn_plan_release(uint64_t plan);
 
 /* Bytes of device workspace hffn_output_major needs for nnz down slots (host-only query). */
 int hffn_output_major_workspace(uint32_t nnz, uint32_t d_model, uint64_t* bytes);

@@ -137,3 +137,27 @@ def test_bf16_rounding():
     values = torch.randn(10000).numpy().astype("float32")
     rounded = synth.round_bf16(values)
     assert torch.equal(torch.from_numpy(rounded), torch.from_numpy(values).to(torch.bfloat16).float())
+
+
+@pytest.mark.skipif(torch.cuda.is_available(), reason="uses placeholder pointers: never run where a launch could reach a GPU")
+def test_plans_are_checked_once_and_released():
+    """hffn_plan_forward runs the checks of hffn_forward (without x); plans are kept under distinct handles until
+    released; an unknown handle is refused before any launch."""
+    lib = _lib.load()
+    p = ctypes.c_void_p(16)
+    handle = ctypes.c_uint64(0)
+    model = [p] * 8
+    work = [p] * 4
+    _expect_argument_error(lib.hffn_plan_forward(1, 1, 0, *model, *work, 17, 64, 64, 64, 1, 4, ctypes.byref(handle)), "d_model=17")
+    _expect_argument_error(lib.hffn_plan_forward(9, 1, 0, *model, *work, 64, 64, 64, 64, 1, 4, ctypes.byref(handle)), "unknown up mode")
+    _expect_argument_error(lib.hffn_plan_forward(1, 1, 0, *model, *work, 4096, 64, 64, 64, 8, 8, ctypes.byref(handle)), "LDS")
+    _expect_argument_error(lib.hffn_plan_forward(2, 1, 0, *model, None, p, p, p, 64, 64, 64, 64, 1, 4, ctypes.byref(handle)), "x_t")
+    _expect_argument_error(lib.hffn_plan_forward(1, 1, 0, *model, *work, 64, 64, 64, 64, 1, 4, None), "null result")
+    assert lib.hffn_plan_forward(1, 1, 0, *model, *work, 64, 64, 64, 64, 1, 4, ctypes.byref(handle)) == _lib.OK
+    first = handle.value
+    assert lib.hffn_plan_forward(2, 2, 0, *model, *work, 64, 64, 64, 64, 5, 8, ctypes.byref(handle)) == _lib.OK
+    assert first != 0 and handle.value not in (0, first)
+    assert lib.hffn_plan_release(first) == _lib.OK
+    assert lib.hffn_plan_release(handle.value) == _lib.OK
+    _expect_argument_error(lib.hffn_plan_release(first), "unknown plan")
+    _expect_argument_error(lib.hffn_plan_launch(first, p, None), "unknown plan")
