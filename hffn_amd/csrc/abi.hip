@@ -116,11 +116,12 @@ int check_down(int mode, int value_type, const float* act, const int32_t* out_of
 }
 
 int launch_up(int mode, int value_type, const float* x, const int32_t* up_offsets, const int16_t* up_idx, const void* up_val,
-              const float* b_up, float* act, uint32_t d_model, uint32_t d_ff, uint32_t nnz_up, uint32_t n, uint32_t ld, hipStream_t s) {
+              const float* b_up, float* act, uint32_t d_model, uint32_t d_ff, uint32_t nnz_up, uint32_t n, uint32_t ld, hipStream_t s,
+              float* z = nullptr) {
     if (mode == HFFN_UP_EDGES)
-        return launched(hffn::launch_up_edges(value_type, x, up_offsets, up_idx, up_val, b_up, act, d_model, d_ff, n, ld, nnz_up, s),
+        return launched(hffn::launch_up_edges(value_type, x, up_offsets, up_idx, up_val, b_up, act, z, d_model, d_ff, n, ld, nnz_up, s),
                         "up edges");
-    return launched(hffn::launch_up_rows(value_type, x, up_offsets, up_idx, up_val, b_up, act, d_model, d_ff, n, ld, s), "up rows");
+    return launched(hffn::launch_up_rows(value_type, x, up_offsets, up_idx, up_val, b_up, act, z, d_model, d_ff, n, ld, s), "up rows");
 }
 
 int launch_down(int mode, int value_type, const float* act, const int32_t* out_offsets, const int16_t* out_hidden,
@@ -161,14 +162,15 @@ int check_forward(const Plan& p) {
                       p.down_mode == HFFN_DOWN_ROWS ? p.y_t : p.y, p.d_model, p.d_ff, p.n, p.ld);
 }
 
-// hffn_forward after its checks.
-int launch_forward(const Plan& p, const float* x, hipStream_t s) {
-    if (p.up_mode == HFFN_UP_ROWS) {
+// hffn_forward after its checks. With z (the training forward) the pre-activations go to z and x_t is written for
+// every mode (the backward reads x feature-major).
+int launch_forward(const Plan& p, const float* x, hipStream_t s, float* z = nullptr) {
+    if (p.up_mode == HFFN_UP_ROWS || z) {
         if (int status = launched(hffn::launch_transpose(x, p.x_t, p.n, p.d_model, p.d_model, p.ld, s), "input transpose")) return status;
-        x = p.x_t;
     }
+    if (p.up_mode == HFFN_UP_ROWS) x = p.x_t;
     if (int status = launch_up(p.up_mode, p.value_type, x, p.up_offsets, p.up_idx, p.up_val, p.b_up, p.act, p.d_model, p.d_ff,
-                               p.nnz_up, p.n, p.ld, s))
+                               p.nnz_up, p.n, p.ld, s, z))
         return status;
     if (p.down_mode == HFFN_DOWN_ROWS) {
         if (int status = launch_down(p.down_mode, p.value_type, p.act, p.out_offsets, p.out_hidden, p.out_val, p.b_down, p.y_t,
@@ -345,6 +347,78 @@ int hffn_forward_mfma(int value_type, const float* x, const void* up_planes, con
     if (int status = hffn_mfma_up(value_type, x, up_planes, up_binades, b_up, workspace, workspace_bytes, d_model, d_ff, n, stream))
         return status;
     return hffn_mfma_down(value_type, down_planes, down_binades, b_down, y, workspace, workspace_bytes, d_model, d_ff, n, stream);
+}
+
+// ----------------------------------------------------------------------------------------------------- training
+
+int hffn_forward_z(int up_mode, int down_mode, const float* x, const int32_t* up_offsets, const int16_t* up_idx, const float* up_val,
+                   const float* b_up, const int32_t* out_offsets, const int16_t* out_hidden, const float* out_val, const float* b_down,
+                   float* x_t, float* act, float* y_t, float* y, float* z, uint32_t d_model, uint32_t d_ff, uint32_t nnz_up,
+                   uint32_t nnz_down, uint32_t n, uint32_t ld, void* stream) {
+    const Plan plan{up_mode, down_mode, HFFN_VALUE_F32, up_offsets, up_idx, up_val, b_up, out_offsets, out_hidden, out_val, b_down,
+                    x_t, act, y_t, y, d_model, d_ff, nnz_up, nnz_down, n, ld};
+    if (int status = check_forward(plan)) return status;
+    if (!x || !x_t || !z) return fail(HFFN_ERROR_ARGUMENT, "forward_z: null input, x_t or z");
+    return launch_forward(plan, x, static_cast<hipStream_t>(stream), z);
+}
+
+int hffn_grad_sddmm(const float* row, const float* mat, const int32_t* offsets, const int16_t* index, float* g, float* gb,
+                    uint32_t rows, uint32_t n, uint32_t ld, uint32_t stride, void* stream) {
+    if (int status = check_shape(16, rows, n, ld)) return status;
+    if (!row || !mat || !offsets || !index || !g || !gb) return fail(HFFN_ERROR_ARGUMENT, "grad_sddmm: null pointer");
+    if (reinterpret_cast<uintptr_t>(row) % 16 != 0 || reinterpret_cast<uintptr_t>(mat) % 16 != 0)
+        return fail(HFFN_ERROR_ARGUMENT, "grad_sddmm: row and mat must be 16-byte aligned");
+    if (hffn::grad_tiles(n) > 1 && stride == 0) return fail(HFFN_ERROR_ARGUMENT, "grad_sddmm: n=%u needs a partial stride", n);
+    return launched(hffn::launch_grad_sddmm(row, mat, offsets, index, g, gb, rows, n, ld, stride, static_cast<hipStream_t>(stream)),
+                    "grad_sddmm");
+}
+
+int hffn_grad_hidden(const float* gy_t, const float* z, const int32_t* down_offsets, const int16_t* down_idx, const float* down_val,
+                     float* gz, uint32_t d_model, uint32_t d_ff, uint32_t n, uint32_t ld, void* stream) {
+    if (int status = check_shape(d_model, d_ff, n, ld)) return status;
+    if (!gy_t || !z || !down_offsets || !down_idx || !down_val || !gz) return fail(HFFN_ERROR_ARGUMENT, "grad_hidden: null pointer");
+    if (reinterpret_cast<uintptr_t>(gy_t) % 16 != 0) return fail(HFFN_ERROR_ARGUMENT, "grad_hidden: gy_t must be 16-byte aligned");
+    return launched(hffn::launch_grad_hidden_rows(gy_t, down_offsets, down_idx, down_val, z, gz, d_ff, n, ld,
+                                                  static_cast<hipStream_t>(stream)),
+                    "grad_hidden");
+}
+
+int hffn_grad_x(const float* gz, const int32_t* in_offsets, const int16_t* in_hidden, const float* in_val, float* gx_t, float* gx,
+                uint32_t d_model, uint32_t d_ff, uint32_t n, uint32_t ld, void* stream) {
+    if (int status = check_shape(d_model, d_ff, n, ld)) return status;
+    if (!gz || !in_offsets || !in_hidden || !in_val || !gx_t || !gx) return fail(HFFN_ERROR_ARGUMENT, "grad_x: null pointer");
+    if (reinterpret_cast<uintptr_t>(gz) % 16 != 0) return fail(HFFN_ERROR_ARGUMENT, "grad_x: gz must be 16-byte aligned");
+    const hipStream_t s = static_cast<hipStream_t>(stream);
+    if (int status = launched(hffn::launch_down_rows(HFFN_VALUE_F32, gz, in_offsets, in_hidden, in_val, nullptr, gx_t, d_model, n,
+                                                     ld, s),
+                              "grad_x"))
+        return status;
+    return launched(hffn::launch_transpose(gx_t, gx, d_model, n, ld, d_model, s), "grad_x transpose");
+}
+
+int hffn_reduce_tiles(const float* ws, uint32_t stride, uint32_t tiles, uint32_t c1, uint32_t c2, uint32_t c3, float* g_down,
+                      float* gb_down, float* g_up, float* gb_up, void* stream) {
+    if (!ws || !g_down || !gb_down || !g_up || !gb_up) return fail(HFFN_ERROR_ARGUMENT, "reduce_tiles: null pointer");
+    if (tiles == 0 || !(c1 <= c2 && c2 <= c3 && c3 <= stride))
+        return fail(HFFN_ERROR_ARGUMENT, "reduce_tiles: columns %u <= %u <= %u <= %u and tiles=%u >= 1 required", c1, c2, c3, stride, tiles);
+    if (static_cast<uint64_t>(tiles) * stride >= (1ull << 32)) return fail(HFFN_ERROR_ARGUMENT, "reduce_tiles: workspace beyond 32-bit indexing");
+    return launched(hffn::launch_reduce_tiles(ws, stride, tiles, c1, c2, c3, g_down, gb_down, g_up, gb_up, static_cast<hipStream_t>(stream)),
+                    "reduce_tiles");
+}
+
+int hffn_adamw(float* p, const float* g, float* m, float* v, uint32_t count, float lr_decay, float beta1, float one_minus_beta1,
+               float beta2, float one_minus_beta2, float step_size, float bias2_sqrt, float eps, void* stream) {
+    if (count == 0) return HFFN_OK;
+    if (!p || !g || !m || !v) return fail(HFFN_ERROR_ARGUMENT, "adamw: null pointer");
+    return launched(hffn::launch_adamw(p, g, m, v, count, lr_decay, beta1, one_minus_beta1, beta2, one_minus_beta2, step_size, bias2_sqrt,
+                                       eps, static_cast<hipStream_t>(stream)),
+                    "adamw");
+}
+
+int hffn_gather_values(const float* src, const int32_t* pos, float* dst, uint32_t count, void* stream) {
+    if (count == 0) return HFFN_OK;
+    if (!src || !pos || !dst) return fail(HFFN_ERROR_ARGUMENT, "gather_values: null pointer");
+    return launched(hffn::launch_gather_values(src, pos, dst, count, static_cast<hipStream_t>(stream)), "gather_values");
 }
 
 }  // extern "C"

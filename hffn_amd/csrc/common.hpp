@@ -8,18 +8,25 @@ namespace hffn {
 
 constexpr int kWave = 64;
 
+// exp(y) as the hardware base-2 exponential of y log2(e) carried in two floats: the product's rounding error and the
+// tail of log2(e) are put back by a first-order factor, so that it loses nothing against expf to the rounding of a
+// large |y|.
+__device__ __forceinline__ float exp_split(float y) {
+    constexpr float kLog2e = 1.44269502162933349609375f, kLog2eTail = 1.925963033500011e-8f, kLn2 = 0.69314718055994531f;
+    const float h = y * kLog2e;
+    const float l = fmaf(y, kLog2eTail, fmaf(y, kLog2e, -h));  // y log2(e) = h + l to about 2^-48 |h|
+    return __builtin_amdgcn_exp2f(h) * fmaf(l, kLn2, 1.0f);
+}
+
 // Exact GELU (erf form, PyTorch's approximate="none"; `gelu` of
 // runtime/gpu/nvidia/common/kernels/hffn_cuda/kernels.py:87-89), written as z/2 erfc(-z/sqrt 2) so that negative z
 // keep their relative accuracy (no 1 + erf cancellation), with erfc from the Chebyshev fit of Press, Teukolsky,
 // Vetterling and Flannery, Numerical Recipes (2nd ed., section 6.2, "erfcc"; fractional error below 1.2e-7 for
 // every argument): for x >= 0, erfc(x) = t exp(-x^2 + P(t)) with t = 1 / (1 + x / 2), and erfc(-x) = 2 - erfc(x).
 // Branch-free, so that a wave evaluates many independent GELUs back to back. The reciprocal is the hardware one
-// (1 ulp) refined by a Newton step; exp(y) is the hardware base-2 exponential of y log2(e) carried in two floats
-// (the product's rounding error and the tail of log2(e) are put back by a first-order factor), so that it loses
-// nothing against expf to the rounding of a large |y|.
-__device__ __forceinline__ float gelu(float z) {
-    const float x = -z * 0.70710678118654752f;
-    const float a = fabsf(x);
+// (1 ulp) refined by a Newton step; the exponential is exp_split.
+// erfc(a) for a >= 0:
+__device__ __forceinline__ float erfc_nonneg(float a) {
     const float d = fmaf(0.5f, a, 1.0f);
     const float t0 = __builtin_amdgcn_rcpf(d);
     const float t = fmaf(t0, fmaf(-d, t0, 1.0f), t0);
@@ -33,12 +40,24 @@ __device__ __forceinline__ float gelu(float z) {
     p = fmaf(p, t, 0.37409196f);
     p = fmaf(p, t, 1.00002368f);
     p = fmaf(p, t, -1.26551223f);
-    const float y = fmaf(-a, a, p);
-    constexpr float kLog2e = 1.44269502162933349609375f, kLog2eTail = 1.925963033500011e-8f, kLn2 = 0.69314718055994531f;
-    const float h = y * kLog2e;
-    const float l = fmaf(y, kLog2eTail, fmaf(y, kLog2e, -h));  // y log2(e) = h + l to about 2^-48 |h|
-    const float tail = t * (__builtin_amdgcn_exp2f(h) * fmaf(l, kLn2, 1.0f));  // erfc(|x|)
+    return t * exp_split(fmaf(-a, a, p));
+}
+
+__device__ __forceinline__ float gelu(float z) {
+    const float x = -z * 0.70710678118654752f;
+    const float tail = erfc_nonneg(fabsf(x));  // erfc(|x|)
     return 0.5f * z * (x >= 0.0f ? tail : 2.0f - tail);
+}
+
+// d gelu / dz = Phi(z) + z phi(z) (the form of PyTorch's GELU backward, approximate="none"; `gelu_grad` of
+// runtime/gpu/nvidia/ffn/training/kernels_train.py:111-113), Phi(z) = erfc(-z/sqrt 2)/2 as in gelu and
+// phi(z) = exp(-z^2/2)/sqrt(2 pi).
+__device__ __forceinline__ float gelu_grad(float z) {
+    const float x = -z * 0.70710678118654752f;
+    const float tail = erfc_nonneg(fabsf(x));
+    const float cdf = 0.5f * (x >= 0.0f ? tail : 2.0f - tail);
+    const float pdf = 0.39894228040143268f * exp_split((-0.5f * z) * z);
+    return fmaf(z, pdf, cdf);
 }
 
 // Value loads: float32 store, or bfloat16 bits widened exactly to float32.

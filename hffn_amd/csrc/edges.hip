@@ -175,8 +175,9 @@ __device__ __forceinline__ void segment(int32_t begin, int32_t end, uint32_t par
 template <int NT, int P, typename V, int WAVES>
 __global__ __launch_bounds__(WAVES * kWave) void up_edges_kernel(const float* __restrict__ x, const int32_t* __restrict__ off,
                                                                 const int16_t* __restrict__ idx, const V* __restrict__ w,
-                                                                const float* __restrict__ b, float* __restrict__ act, uint32_t d,
-                                                                uint32_t h, uint32_t n, uint32_t ld, int32_t nnz, uint32_t per_block) {
+                                                                const float* __restrict__ b, float* __restrict__ act,
+                                                                float* __restrict__ z, uint32_t d, uint32_t h, uint32_t n,
+                                                                uint32_t ld, int32_t nnz, uint32_t per_block) {
     extern __shared__ float smem[];  // x of NT tokens, [d][NT]; then the segment totals [WAVES][NT]
     float* xs = smem;
     float* totals = smem + static_cast<size_t>(d) * NT;
@@ -215,7 +216,11 @@ __global__ __launch_bounds__(WAVES * kWave) void up_edges_kernel(const float* __
                 for (int t = 0; t < NT; ++t) acc[t] = 0.0f;
             }
             const float total = row_total<NT, P>(acc, lane, part, row_in_pass, totals);
-            if (r < r1 && part == 0 && lane < tokens) act[static_cast<size_t>(r) * ld + c0 + lane] = gelu(b[r] + total);
+            if (r < r1 && part == 0 && lane < tokens) {
+                const float pre = b[r] + total;
+                if (z) z[static_cast<size_t>(r) * ld + c0 + lane] = pre;  // the training forward keeps the pre-activation
+                act[static_cast<size_t>(r) * ld + c0 + lane] = gelu(pre);
+            }
         }
     }
 }
@@ -300,21 +305,21 @@ hipError_t allow_lds(size_t lds) {
 // Every block stages x of its NT tokens (d * NT floats from L2): from 4 tokens on, blocks of 16 waves (a quarter as
 // many blocks) cut that traffic by 4.
 template <int NT, int P, typename V, int WAVES>
-hipError_t up_waves(const float* x, const int32_t* off, const int16_t* idx, const V* w, const float* b, float* act, uint32_t d,
+hipError_t up_waves(const float* x, const int32_t* off, const int16_t* idx, const V* w, const float* b, float* act, float* z, uint32_t d,
                     uint32_t h, uint32_t n, uint32_t ld, uint32_t nnz, hipStream_t stream) {
     const uint32_t per = rows_per_block(h, P, WAVES, WAVES == kWaves ? 1024 : 256);
     const size_t lds = (static_cast<size_t>(d) * NT + WAVES * NT) * sizeof(float);
     if (const hipError_t status = allow_lds<up_edges_kernel<NT, P, V, WAVES>>(lds); status != hipSuccess) return status;
     hipLaunchKernelGGL((up_edges_kernel<NT, P, V, WAVES>), dim3(ceil_div(h, per)), dim3(WAVES * kWave), lds, stream, x, off, idx, w, b,
-                       act, d, h, n, ld, static_cast<int32_t>(nnz), per);
+                       act, z, d, h, n, ld, static_cast<int32_t>(nnz), per);
     return hipGetLastError();
 }
 
 template <int NT, int P, typename V>
-hipError_t up_shape(const float* x, const int32_t* off, const int16_t* idx, const V* w, const float* b, float* act, uint32_t d,
-                    uint32_t h, uint32_t n, uint32_t ld, uint32_t nnz, hipStream_t stream) {
-    if constexpr (NT >= 4) return up_waves<NT, P, V, 16>(x, off, idx, w, b, act, d, h, n, ld, nnz, stream);
-    else return up_waves<NT, P, V, kWaves>(x, off, idx, w, b, act, d, h, n, ld, nnz, stream);
+hipError_t up_shape(const float* x, const int32_t* off, const int16_t* idx, const V* w, const float* b, float* act, float* z,
+                    uint32_t d, uint32_t h, uint32_t n, uint32_t ld, uint32_t nnz, hipStream_t stream) {
+    if constexpr (NT >= 4) return up_waves<NT, P, V, 16>(x, off, idx, w, b, act, z, d, h, n, ld, nnz, stream);
+    else return up_waves<NT, P, V, kWaves>(x, off, idx, w, b, act, z, d, h, n, ld, nnz, stream);
 }
 
 // With act staged in LDS (small n), blocks of 16 waves take 4x the rows of 4-wave blocks, so each block's staging
@@ -341,10 +346,10 @@ hipError_t down_shape(const float* act, const int32_t* off, const int16_t* hid, 
 
 template <int NT, typename V>
 hipError_t up_parts(int parts, const float* x, const int32_t* off, const int16_t* idx, const V* w, const float* b, float* act,
-                    uint32_t d, uint32_t h, uint32_t n, uint32_t ld, uint32_t nnz, hipStream_t stream) {
-    if (parts == 4) return up_shape<NT, 4>(x, off, idx, w, b, act, d, h, n, ld, nnz, stream);
-    if (parts == 2) return up_shape<NT, 2>(x, off, idx, w, b, act, d, h, n, ld, nnz, stream);
-    return up_shape<NT, 1>(x, off, idx, w, b, act, d, h, n, ld, nnz, stream);
+                    float* z, uint32_t d, uint32_t h, uint32_t n, uint32_t ld, uint32_t nnz, hipStream_t stream) {
+    if (parts == 4) return up_shape<NT, 4>(x, off, idx, w, b, act, z, d, h, n, ld, nnz, stream);
+    if (parts == 2) return up_shape<NT, 2>(x, off, idx, w, b, act, z, d, h, n, ld, nnz, stream);
+    return up_shape<NT, 1>(x, off, idx, w, b, act, z, d, h, n, ld, nnz, stream);
 }
 
 template <int NT, typename V>
@@ -356,14 +361,14 @@ hipError_t down_parts(int parts, const float* act, const int32_t* off, const int
 }
 
 template <typename V>
-hipError_t up_typed(const float* x, const int32_t* off, const int16_t* idx, const V* w, const float* b, float* act, uint32_t d,
-                    uint32_t h, uint32_t n, uint32_t ld, uint32_t nnz, hipStream_t stream) {
+hipError_t up_typed(const float* x, const int32_t* off, const int16_t* idx, const V* w, const float* b, float* act, float* z,
+                    uint32_t d, uint32_t h, uint32_t n, uint32_t ld, uint32_t nnz, hipStream_t stream) {
     const int parts = parts_for(nnz, h);
     switch (edges_tokens(n)) {
-        case 1: return up_parts<1>(parts, x, off, idx, w, b, act, d, h, n, ld, nnz, stream);
-        case 2: return up_parts<2>(parts, x, off, idx, w, b, act, d, h, n, ld, nnz, stream);
-        case 4: return up_parts<4>(parts, x, off, idx, w, b, act, d, h, n, ld, nnz, stream);
-        default: return up_parts<8>(parts, x, off, idx, w, b, act, d, h, n, ld, nnz, stream);
+        case 1: return up_parts<1>(parts, x, off, idx, w, b, act, z, d, h, n, ld, nnz, stream);
+        case 2: return up_parts<2>(parts, x, off, idx, w, b, act, z, d, h, n, ld, nnz, stream);
+        case 4: return up_parts<4>(parts, x, off, idx, w, b, act, z, d, h, n, ld, nnz, stream);
+        default: return up_parts<8>(parts, x, off, idx, w, b, act, z, d, h, n, ld, nnz, stream);
     }
 }
 
@@ -382,9 +387,9 @@ hipError_t down_typed(const float* act, const int32_t* off, const int16_t* hid, 
 }  // namespace
 
 hipError_t launch_up_edges(int vt, const float* x, const int32_t* off, const int16_t* idx, const void* w, const float* b,
-                           float* act, uint32_t d, uint32_t h, uint32_t n, uint32_t ld, uint32_t nnz, hipStream_t stream) {
-    if (vt == kBF16) return up_typed(x, off, idx, static_cast<const uint16_t*>(w), b, act, d, h, n, ld, nnz, stream);
-    return up_typed(x, off, idx, static_cast<const float*>(w), b, act, d, h, n, ld, nnz, stream);
+                           float* act, float* z, uint32_t d, uint32_t h, uint32_t n, uint32_t ld, uint32_t nnz, hipStream_t stream) {
+    if (vt == kBF16) return up_typed(x, off, idx, static_cast<const uint16_t*>(w), b, act, z, d, h, n, ld, nnz, stream);
+    return up_typed(x, off, idx, static_cast<const float*>(w), b, act, z, d, h, n, ld, nnz, stream);
 }
 
 hipError_t launch_down_edges(int vt, const float* act, const int32_t* off, const int16_t* hid, const void* v,

@@ -15,11 +15,15 @@ constexpr uint32_t kBlock = 256;
 constexpr uint32_t kWaves = kBlock / kWave;
 
 // ------------------------------------------------------------------------------------------- up, rows
-template <int TPL, typename V>
+// EPI kGelu: act = gelu(b + acc), and z = b + acc where z is not null (the training forward keeps it). EPI kGeluGrad
+// (the backward's gz): act = acc * gelu'(z), z read, b unused.
+enum RowsEpilogue : int { kGelu = 0, kGeluGrad = 1 };
+
+template <int TPL, typename V, int EPI>
 __global__ __launch_bounds__(kBlock) void up_rows_kernel(const float* __restrict__ x_t, const int32_t* __restrict__ off,
                                                         const int16_t* __restrict__ idx, const V* __restrict__ w,
                                                         const float* __restrict__ b, float* __restrict__ act,
-                                                        uint32_t h, uint32_t n, uint32_t ld) {
+                                                        float* __restrict__ z, uint32_t h, uint32_t n, uint32_t ld) {
     const uint32_t r = blockIdx.x * kWaves + uniform(threadIdx.x / kWave);
     if (r >= h) return;
     const uint32_t t0 = (blockIdx.y * kWave + threadIdx.x % kWave) * TPL;
@@ -52,11 +56,22 @@ __global__ __launch_bounds__(kBlock) void up_rows_kernel(const float* __restrict
 #pragma unroll
         for (int j = 0; j < TPL; ++j) acc[j] = fmaf(wv, xv[j], acc[j]);
     }
-    const float bias = b[r];
     float* out = act + static_cast<size_t>(r) * ld + t0;
+    float* zr = z ? z + static_cast<size_t>(r) * ld + t0 : nullptr;
+    if constexpr (EPI == kGelu) {
+        const float bias = b[r];
 #pragma unroll
-    for (int j = 0; j < TPL; ++j)
-        if (t0 + j < n) out[j] = gelu(bias + acc[j]);
+        for (int j = 0; j < TPL; ++j)
+            if (t0 + j < n) {
+                const float pre = bias + acc[j];
+                if (zr) zr[j] = pre;
+                out[j] = gelu(pre);
+            }
+    } else {
+#pragma unroll
+        for (int j = 0; j < TPL; ++j)
+            if (t0 + j < n) out[j] = acc[j] * gelu_grad(zr[j]);
+    }
 }
 
 // ----------------------------------------------------------------------------------------- down, rows
@@ -97,7 +112,7 @@ __global__ __launch_bounds__(kBlock) void down_rows_kernel(const float* __restri
 #pragma unroll
         for (int j = 0; j < TPL; ++j) acc[j] = fmaf(vv, av[j], acc[j]);
     }
-    const float bo = bias[o];
+    const float bo = bias ? bias[o] : 0.0f;  // no bias: the backward's gx
     float* out = y_t + static_cast<size_t>(o) * ld + t0;
 #pragma unroll
     for (int j = 0; j < TPL; ++j)
@@ -123,16 +138,16 @@ __global__ __launch_bounds__(kBlock) void transpose_kernel(const float* __restri
 
 uint32_t ceil_div(uint32_t a, uint32_t b) { return (a + b - 1) / b; }
 
-template <typename V>
+template <typename V, int EPI>
 hipError_t up_rows_typed(const float* x_t, const int32_t* off, const int16_t* idx, const V* w, const float* b, float* act,
-                         uint32_t h, uint32_t n, uint32_t ld, hipStream_t stream) {
+                         float* z, uint32_t h, uint32_t n, uint32_t ld, hipStream_t stream) {
     const dim3 block(kBlock);
     if (n >= 256) {
-        hipLaunchKernelGGL((up_rows_kernel<4, V>), dim3(ceil_div(h, kWaves), ceil_div(n, 4 * kWave)), block, 0, stream, x_t, off, idx, w, b, act, h, n, ld);
+        hipLaunchKernelGGL((up_rows_kernel<4, V, EPI>), dim3(ceil_div(h, kWaves), ceil_div(n, 4 * kWave)), block, 0, stream, x_t, off, idx, w, b, act, z, h, n, ld);
     } else if (n >= 128) {
-        hipLaunchKernelGGL((up_rows_kernel<2, V>), dim3(ceil_div(h, kWaves), ceil_div(n, 2 * kWave)), block, 0, stream, x_t, off, idx, w, b, act, h, n, ld);
+        hipLaunchKernelGGL((up_rows_kernel<2, V, EPI>), dim3(ceil_div(h, kWaves), ceil_div(n, 2 * kWave)), block, 0, stream, x_t, off, idx, w, b, act, z, h, n, ld);
     } else {
-        hipLaunchKernelGGL((up_rows_kernel<1, V>), dim3(ceil_div(h, kWaves), ceil_div(n, kWave)), block, 0, stream, x_t, off, idx, w, b, act, h, n, ld);
+        hipLaunchKernelGGL((up_rows_kernel<1, V, EPI>), dim3(ceil_div(h, kWaves), ceil_div(n, kWave)), block, 0, stream, x_t, off, idx, w, b, act, z, h, n, ld);
     }
     return hipGetLastError();
 }
@@ -161,9 +176,14 @@ hipError_t launch_transpose(const float* in, float* out, uint32_t rows, uint32_t
 }
 
 hipError_t launch_up_rows(int vt, const float* x_t, const int32_t* off, const int16_t* idx, const void* w, const float* b,
-                          float* act, uint32_t, uint32_t h, uint32_t n, uint32_t ld, hipStream_t stream) {
-    if (vt == kBF16) return up_rows_typed(x_t, off, idx, static_cast<const uint16_t*>(w), b, act, h, n, ld, stream);
-    return up_rows_typed(x_t, off, idx, static_cast<const float*>(w), b, act, h, n, ld, stream);
+                          float* act, float* z, uint32_t, uint32_t h, uint32_t n, uint32_t ld, hipStream_t stream) {
+    if (vt == kBF16) return up_rows_typed<uint16_t, kGelu>(x_t, off, idx, static_cast<const uint16_t*>(w), b, act, z, h, n, ld, stream);
+    return up_rows_typed<float, kGelu>(x_t, off, idx, static_cast<const float*>(w), b, act, z, h, n, ld, stream);
+}
+
+hipError_t launch_grad_hidden_rows(const float* gy_t, const int32_t* off, const int16_t* idx, const float* v, const float* z,
+                                   float* gz, uint32_t h, uint32_t n, uint32_t ld, hipStream_t stream) {
+    return up_rows_typed<float, kGeluGrad>(gy_t, off, idx, v, nullptr, gz, const_cast<float*>(z), h, n, ld, stream);
 }
 
 hipError_t launch_down_rows(int vt, const float* act, const int32_t* off, const int16_t* hid, const void* v,

@@ -25,13 +25,17 @@ hipError_t launch_transpose(const float* in, float* out, uint32_t rows, uint32_t
 
 // Up projection + bias + GELU. `edges`: one wave per neuron, lanes over its slots, x token-major
 // [n, d_model]; `rows`: one wave per neuron, lanes over tokens, x feature-major x_t[d_model, ld].
-// Activations hidden-major act[d_ff, ld].
+// Activations hidden-major act[d_ff, ld]; z (when not null) receives the pre-activation b + sum, same layout.
 hipError_t launch_up_edges(int vt, const float* x, const int32_t* off, const int16_t* idx, const void* w,
-                           const float* b, float* act, uint32_t d, uint32_t h, uint32_t n, uint32_t ld, uint32_t nnz,
-                           hipStream_t stream);
+                           const float* b, float* act, float* z, uint32_t d, uint32_t h, uint32_t n, uint32_t ld,
+                           uint32_t nnz, hipStream_t stream);
 hipError_t launch_up_rows(int vt, const float* x_t, const int32_t* off, const int16_t* idx, const void* w,
-                          const float* b, float* act, uint32_t d, uint32_t h, uint32_t n, uint32_t ld,
+                          const float* b, float* act, float* z, uint32_t d, uint32_t h, uint32_t n, uint32_t ld,
                           hipStream_t stream);
+// The rows up kernel with the backward's epilogue: gz[r, t] = (sum over the slots of r of v * gy_t[idx, t]) *
+// gelu'(z[r, t]), hidden-major [h, ld] (fp32 values).
+hipError_t launch_grad_hidden_rows(const float* gy_t, const int32_t* off, const int16_t* idx, const float* v, const float* z,
+                                   float* gz, uint32_t h, uint32_t n, uint32_t ld, hipStream_t stream);
 
 // Down projection over the output-major store. `edges`: one wave per output, lanes over its
 // slots, writes y[n, d_model]; `rows`: one wave per output, lanes over tokens, writes
@@ -42,6 +46,21 @@ hipError_t launch_down_edges(int vt, const float* act, const int32_t* off, const
 hipError_t launch_down_rows(int vt, const float* act, const int32_t* off, const int16_t* hid, const void* v,
                             const float* bias, float* y_t, uint32_t d, uint32_t n, uint32_t ld,
                             hipStream_t stream);
+
+// Training (train.hip). Token tiles of kGradTile tokens; with more than one tile the SDDMM kernels write tile
+// partials (row k of a [tiles, stride] workspace) that launch_reduce_tiles adds in tile order.
+constexpr uint32_t kGradTile = 256;
+inline uint32_t grad_tiles(uint32_t n) { return (n + kGradTile - 1) / kGradTile; }
+// For each owner row o (rows of them) and each slot q of o: g[k*stride + q] = sum over the tokens t of tile k of
+// row[o, t] * mat[idx[q], t]; gb[k*stride + o] = sum over the same tokens of row[o, t]. row and mat are [*, ld].
+hipError_t launch_grad_sddmm(const float* row, const float* mat, const int32_t* off, const int16_t* idx, float* g, float* gb,
+                             uint32_t rows, uint32_t n, uint32_t ld, uint32_t stride, hipStream_t stream);
+hipError_t launch_reduce_tiles(const float* ws, uint32_t stride, uint32_t tiles, uint32_t c1, uint32_t c2, uint32_t c3,
+                               float* g_down, float* gb_down, float* g_up, float* gb_up, hipStream_t stream);
+hipError_t launch_adamw(float* p, const float* g, float* m, float* v, uint32_t count, float lr_decay, float beta1,
+                        float one_minus_beta1, float beta2, float one_minus_beta2, float step_size, float bias2_sqrt, float eps,
+                        hipStream_t stream);
+hipError_t launch_gather_values(const float* src, const int32_t* pos, float* dst, uint32_t count, hipStream_t stream);
 
 // Output-major transpose of the hidden-major down store (stable in slot order).
 uint32_t output_major_chunks(uint32_t nnz);

@@ -194,6 +194,7 @@ class HFFNRuntime:
             self._nnz.append((tensors["up_idx"].numel(), tensors["out_hidden"].numel()))
         self.density = max(layer.up_idx.numel() + layer.out_hidden.numel() for layer in layers) / (2 * self.d_model * self.d_ff)
         self._planes: list[dict] | None = None
+        self._stale: set[int] = set()   # layers whose values changed since their planes were built
         if dense and self._mfma_eligible():
             self._planes = [self._densify(tensors) for tensors in self._tensors]
         self.forced_up: str | None = None
@@ -210,23 +211,33 @@ class HFFNRuntime:
         return all(_rows_strictly_increasing(t["up_offsets"], t["up_idx"]) and
                    _rows_strictly_increasing(t["out_offsets"], t["out_hidden"]) for t in self._tensors)
 
-    def _densify(self, tensors: dict) -> dict:
+    def _densify(self, tensors: dict, planes: dict | None = None) -> dict:
         """fp16 hi/lo planes (and per-row binades) of W_up [d_ff, d_model] and W_down [d_model, d_ff], built on the
-        device from the compact store."""
+        device from the compact store (into ``planes`` when given: a rebuild allocates nothing)."""
         value_type = _value_type(tensors["up_val"], "up_val")
         stream = torch.cuda.current_stream(self.device).cuda_stream
-        planes = {}
+        fresh = planes is None
+        planes = {} if fresh else planes
         for side, rows, k, names in (("up", self.d_ff, self.d_model, ("up_offsets", "up_idx", "up_val")),
                                      ("down", self.d_model, self.d_ff, ("out_offsets", "out_hidden", "out_val"))):
-            size = _lib.query_bytes(self._lib.hffn_dense_planes_bytes, rows, k)
-            plane = torch.empty(size // 2, dtype=torch.float16, device=self.device)
-            binades = torch.empty(rows, dtype=torch.int32, device=self.device)
+            if fresh:
+                size = _lib.query_bytes(self._lib.hffn_dense_planes_bytes, rows, k)
+                plane = torch.empty(size // 2, dtype=torch.float16, device=self.device)
+                binades = torch.empty(rows, dtype=torch.int32, device=self.device)
+            else:
+                plane, binades = planes[side], planes[f"{side}_binades"]
             offsets, index, values = (tensors[name] for name in names)
             _lib.check(self._lib.hffn_densify(value_type, offsets.data_ptr(), index.data_ptr(), values.data_ptr(), rows, k,
                                               plane.data_ptr(), binades.data_ptr(), stream), f"densify {side}")
             planes[side] = plane
             planes[f"{side}_binades"] = binades
         return planes
+
+    def invalidate_planes(self, index: int) -> None:
+        """The compact values of layer ``index`` changed in place (a training update): its densified planes are rebuilt
+        before the MFMA path next reads them."""
+        if self._planes is not None:
+            self._stale.add(index)
 
     @property
     def mfma_available(self) -> bool:
@@ -301,6 +312,9 @@ class HFFNRuntime:
         stream = torch.cuda.current_stream(self.device).cuda_stream
         if up == "mfma":
             x = _aligned(x)  # the MFMA path reads x 16 bytes at a time
+            if index in self._stale:
+                self._densify(self._tensors[index], self._planes[index])
+                self._stale.discard(index)
             planes, tensors = self._planes[index], self._tensors[index]
             _lib.check(self._lib.hffn_forward_mfma(value_type, x.data_ptr(), planes["up"].data_ptr(),
                                                    planes["up_binades"].data_ptr(), tensors["b_up"].data_ptr(),

@@ -27,7 +27,7 @@
 extern "C" {
 #endif
 
-#define HFFN_ABI_VERSION 3
+#define HFFN_ABI_VERSION 4
 
 #define HFFN_OK 0
 #define HFFN_ERROR_ARGUMENT (-1) /* invalid shape, mode, pointer or workspace */
@@ -154,6 +154,54 @@ int hffn_mfma_down(int value_type, const void* down_planes, const int32_t* down_
 int hffn_forward_mfma(int value_type, const float* x, const void* up_planes, const int32_t* up_binades, const float* b_up,
                       const void* down_planes, const int32_t* down_binades, const float* b_down, void* workspace,
                       uint64_t workspace_bytes, float* y, uint32_t d_model, uint32_t d_ff, uint32_t n, void* stream);
+
+/* ------------------------------------------------------------------------------------------------ training (fp32)
+ * Layouts: act, z, gz hidden-major [d_ff, ld]; x_t, gy_t, gx_t feature-major [d_model, ld]; x, y, gx token-major
+ * [n, d_model]. Gradients of the compact arrays in their own orders: g_up as up_val (hidden-major slots), g_down as
+ * out_val (output-major edges). Token tiles of 256: for n > 256 the two sampled products write tile partials that
+ * hffn_reduce_tiles adds in tile order. Every result is written by one lane: same bits run to run. */
+
+/* hffn_forward (gather modes, fp32 values) that also writes the pre-activations z = b_up + W_up x (hidden-major, as
+ * act) and x_t = x transposed for every mode. Replaces the forward of HFFNTrainRuntime.forward with a z buffer
+ * (runtime/gpu/nvidia/ffn/training/train_runtime.py:133-152: the up_<mode>_z kernels of forward_source(store_z=True),
+ * kernels_train.py:263). */
+int hffn_forward_z(int up_mode, int down_mode, const float* x, const int32_t* up_offsets, const int16_t* up_idx, const float* up_val,
+                   const float* b_up, const int32_t* out_offsets, const int16_t* out_hidden, const float* out_val, const float* b_down,
+                   float* x_t, float* act, float* y_t, float* y, float* z, uint32_t d_model, uint32_t d_ff, uint32_t nnz_up,
+                   uint32_t nnz_down, uint32_t n, uint32_t ld, void* stream);
+
+/* Sampled product over an owner-row support: for each owner o < rows, token tile k and slot q of o,
+ * g[k*stride + q] = sum_t row[o, t] mat[index[q], t] and gb[k*stride + o] = sum_t row[o, t] (t over tile k, below n);
+ * row, mat 16-byte aligned [*, ld]; stride is ignored for n <= 256 (the results are the gradients). With
+ * row = gy_t, mat = act over the output-major down edges: g_down, gb_down; with row = gz, mat = x_t over the up
+ * slots: g_up, gb_up. Replaces grad_down and grad_up (runtime/gpu/nvidia/ffn/training/kernels_train.py:115-137,
+ * 162-184). */
+int hffn_grad_sddmm(const float* row, const float* mat, const int32_t* offsets, const int16_t* index, float* g, float* gb,
+                    uint32_t rows, uint32_t n, uint32_t ld, uint32_t stride, void* stream);
+
+/* gz[r, t] = (sum over the hidden-major down slots of r of down_val * gy_t[down_idx, t]) * gelu'(z[r, t]); down_val in
+ * hidden-major slot order. Replaces grad_hidden (kernels_train.py:139-160). */
+int hffn_grad_hidden(const float* gy_t, const float* z, const int32_t* down_offsets, const int16_t* down_idx, const float* down_val,
+                     float* gz, uint32_t d_model, uint32_t d_ff, uint32_t n, uint32_t ld, void* stream);
+
+/* gx[t, i] = sum over the input-major up slots of i of in_val * gz[in_hidden, t] (through gx_t, feature-major).
+ * Replaces grad_x (kernels_train.py:201-231). */
+int hffn_grad_x(const float* gz, const int32_t* in_offsets, const int16_t* in_hidden, const float* in_val, float* gx_t, float* gx,
+                uint32_t d_model, uint32_t d_ff, uint32_t n, uint32_t ld, void* stream);
+
+/* Fixed-order sum of the tile partials ws[tiles, stride] into g_down [0, c1), gb_down [c1, c2), g_up [c2, c3),
+ * gb_up [c3, stride). Replaces reduce_tiles (kernels_train.py:186-199). */
+int hffn_reduce_tiles(const float* ws, uint32_t stride, uint32_t tiles, uint32_t c1, uint32_t c2, uint32_t c3, float* g_down,
+                      float* gb_down, float* g_up, float* gb_up, void* stream);
+
+/* Compact AdamW on one array: p -= lr_decay p; m = beta1 m + (1 - beta1) g; v = beta2 v + (1 - beta2) g^2;
+ * p -= step_size m / (sqrt(v) / bias2_sqrt + eps). Replaces adamw (kernels_train.py:233-247). */
+int hffn_adamw(float* p, const float* g, float* m, float* v, uint32_t count, float lr_decay, float beta1, float one_minus_beta1,
+               float beta2, float one_minus_beta2, float step_size, float bias2_sqrt, float eps, void* stream);
+
+/* dst[j] = src[pos[j]]: the values of a transposed support refreshed from the compact array they index (the
+ * reference reads them through the positions inside its kernels, kernels_train.py:142-150, 204-215). */
+int hffn_gather_values(const float* src, const int32_t* pos, float* dst, uint32_t count, void* stream);
 
 #ifdef __cplusplus
 }
