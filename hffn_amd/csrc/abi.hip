@@ -369,26 +369,41 @@ int hffn_grad_sddmm(const float* row, const float* mat, const int32_t* offsets, 
     if (reinterpret_cast<uintptr_t>(row) % 16 != 0 || reinterpret_cast<uintptr_t>(mat) % 16 != 0)
         return fail(HFFN_ERROR_ARGUMENT, "grad_sddmm: row and mat must be 16-byte aligned");
     if (hffn::grad_tiles(n) > 1 && stride == 0) return fail(HFFN_ERROR_ARGUMENT, "grad_sddmm: n=%u needs a partial stride", n);
-    return launched(hffn::launch_grad_sddmm(row, mat, offsets, index, g, gb, rows, n, ld, stride, static_cast<hipStream_t>(stream)),
-                    "grad_sddmm");
+    const hipStream_t s = static_cast<hipStream_t>(stream);
+    if (n <= hffn::kEdgesMaxTokens) {
+        if (ld % hffn::edges_tokens(n) != 0) return fail(HFFN_ERROR_ARGUMENT, "grad_sddmm: ld=%u must be a multiple of %u", ld, hffn::edges_tokens(n));
+        return launched(hffn::launch_grad_sddmm_edges(row, mat, offsets, index, g, gb, rows, n, ld, s), "grad_sddmm (edges)");
+    }
+    return launched(hffn::launch_grad_sddmm(row, mat, offsets, index, g, gb, rows, n, ld, stride, s), "grad_sddmm");
 }
 
-int hffn_grad_hidden(const float* gy_t, const float* z, const int32_t* down_offsets, const int16_t* down_idx, const float* down_val,
-                     float* gz, uint32_t d_model, uint32_t d_ff, uint32_t n, uint32_t ld, void* stream) {
+int hffn_grad_hidden(const float* gy, const float* gy_t, const float* z, const int32_t* down_offsets, const int16_t* down_idx,
+                     const float* down_val, float* gz, uint32_t d_model, uint32_t d_ff, uint32_t nnz_down, uint32_t n, uint32_t ld,
+                     void* stream) {
     if (int status = check_shape(d_model, d_ff, n, ld)) return status;
-    if (!gy_t || !z || !down_offsets || !down_idx || !down_val || !gz) return fail(HFFN_ERROR_ARGUMENT, "grad_hidden: null pointer");
+    if (!gy || !gy_t || !z || !down_offsets || !down_idx || !down_val || !gz) return fail(HFFN_ERROR_ARGUMENT, "grad_hidden: null pointer");
     if (reinterpret_cast<uintptr_t>(gy_t) % 16 != 0) return fail(HFFN_ERROR_ARGUMENT, "grad_hidden: gy_t must be 16-byte aligned");
-    return launched(hffn::launch_grad_hidden_rows(gy_t, down_offsets, down_idx, down_val, z, gz, d_ff, n, ld,
-                                                  static_cast<hipStream_t>(stream)),
-                    "grad_hidden");
+    const hipStream_t s = static_cast<hipStream_t>(stream);
+    if (n <= hffn::kEdgesMaxTokens && hffn_edges_supported(d_model, n) && check_edges(d_model, n, ld, true) == HFFN_OK) {
+        if (int status = check_store_alignment(down_idx, down_val, HFFN_VALUE_F32)) return status;
+        return launched(hffn::launch_grad_hidden_edges(gy, down_offsets, down_idx, down_val, z, gz, d_model, d_ff, n, ld, nnz_down, s),
+                        "grad_hidden (edges)");
+    }
+    return launched(hffn::launch_grad_hidden_rows(gy_t, down_offsets, down_idx, down_val, z, gz, d_ff, n, ld, s), "grad_hidden");
 }
 
 int hffn_grad_x(const float* gz, const int32_t* in_offsets, const int16_t* in_hidden, const float* in_val, float* gx_t, float* gx,
-                uint32_t d_model, uint32_t d_ff, uint32_t n, uint32_t ld, void* stream) {
+                uint32_t d_model, uint32_t d_ff, uint32_t nnz_up, uint32_t n, uint32_t ld, void* stream) {
     if (int status = check_shape(d_model, d_ff, n, ld)) return status;
     if (!gz || !in_offsets || !in_hidden || !in_val || !gx_t || !gx) return fail(HFFN_ERROR_ARGUMENT, "grad_x: null pointer");
     if (reinterpret_cast<uintptr_t>(gz) % 16 != 0) return fail(HFFN_ERROR_ARGUMENT, "grad_x: gz must be 16-byte aligned");
     const hipStream_t s = static_cast<hipStream_t>(stream);
+    if (n <= hffn::kEdgesMaxTokens && check_edges(d_model, n, ld, false) == HFFN_OK) {
+        if (int status = check_store_alignment(in_hidden, in_val, HFFN_VALUE_F32)) return status;
+        return launched(hffn::launch_down_edges(HFFN_VALUE_F32, gz, in_offsets, in_hidden, in_val, nullptr, gx, d_model, d_ff, n, ld,
+                                                nnz_up, s),
+                        "grad_x (edges)");
+    }
     if (int status = launched(hffn::launch_down_rows(HFFN_VALUE_F32, gz, in_offsets, in_hidden, in_val, nullptr, gx_t, d_model, n,
                                                      ld, s),
                               "grad_x"))

@@ -172,7 +172,7 @@ __device__ __forceinline__ void segment(int32_t begin, int32_t end, uint32_t par
 }
 
 // ------------------------------------------------------------------------------------------------- up
-template <int NT, int P, typename V, int WAVES>
+template <int NT, int P, typename V, int WAVES, bool GRAD = false>
 __global__ __launch_bounds__(WAVES * kWave) void up_edges_kernel(const float* __restrict__ x, const int32_t* __restrict__ off,
                                                                 const int16_t* __restrict__ idx, const V* __restrict__ w,
                                                                 const float* __restrict__ b, float* __restrict__ act,
@@ -217,9 +217,14 @@ __global__ __launch_bounds__(WAVES * kWave) void up_edges_kernel(const float* __
             }
             const float total = row_total<NT, P>(acc, lane, part, row_in_pass, totals);
             if (r < r1 && part == 0 && lane < tokens) {
-                const float pre = b[r] + total;
-                if (z) z[static_cast<size_t>(r) * ld + c0 + lane] = pre;  // the training forward keeps the pre-activation
-                act[static_cast<size_t>(r) * ld + c0 + lane] = gelu(pre);
+                const size_t at = static_cast<size_t>(r) * ld + c0 + lane;
+                if constexpr (GRAD) {  // the backward's gz: z holds the forward's pre-activations
+                    act[at] = total * gelu_grad(z[at]);
+                } else {
+                    const float pre = b[r] + total;
+                    if (z) z[at] = pre;  // the training forward keeps the pre-activation
+                    act[at] = gelu(pre);
+                }
             }
         }
     }
@@ -270,7 +275,7 @@ __global__ __launch_bounds__(WAVES * kWave) void down_edges_kernel(const float* 
                 for (int t = 0; t < NT; ++t) acc[t] = 0.0f;
             }
             const float total = row_total<NT, P>(acc, lane, part, row_in_pass, totals);
-            if (o < o1 && part == 0 && lane < tokens) y[static_cast<size_t>(c0 + lane) * d + o] = total + bias[o];
+            if (o < o1 && part == 0 && lane < tokens) y[static_cast<size_t>(c0 + lane) * d + o] = bias ? total + bias[o] : total;
         }
     }
 }
@@ -304,22 +309,22 @@ hipError_t allow_lds(size_t lds) {
 
 // Every block stages x of its NT tokens (d * NT floats from L2): from 4 tokens on, blocks of 16 waves (a quarter as
 // many blocks) cut that traffic by 4.
-template <int NT, int P, typename V, int WAVES>
+template <int NT, int P, typename V, int WAVES, bool GRAD>
 hipError_t up_waves(const float* x, const int32_t* off, const int16_t* idx, const V* w, const float* b, float* act, float* z, uint32_t d,
                     uint32_t h, uint32_t n, uint32_t ld, uint32_t nnz, hipStream_t stream) {
     const uint32_t per = rows_per_block(h, P, WAVES, WAVES == kWaves ? 1024 : 256);
     const size_t lds = (static_cast<size_t>(d) * NT + WAVES * NT) * sizeof(float);
-    if (const hipError_t status = allow_lds<up_edges_kernel<NT, P, V, WAVES>>(lds); status != hipSuccess) return status;
-    hipLaunchKernelGGL((up_edges_kernel<NT, P, V, WAVES>), dim3(ceil_div(h, per)), dim3(WAVES * kWave), lds, stream, x, off, idx, w, b,
+    if (const hipError_t status = allow_lds<up_edges_kernel<NT, P, V, WAVES, GRAD>>(lds); status != hipSuccess) return status;
+    hipLaunchKernelGGL((up_edges_kernel<NT, P, V, WAVES, GRAD>), dim3(ceil_div(h, per)), dim3(WAVES * kWave), lds, stream, x, off, idx, w, b,
                        act, z, d, h, n, ld, static_cast<int32_t>(nnz), per);
     return hipGetLastError();
 }
 
-template <int NT, int P, typename V>
+template <int NT, int P, typename V, bool GRAD>
 hipError_t up_shape(const float* x, const int32_t* off, const int16_t* idx, const V* w, const float* b, float* act, float* z,
                     uint32_t d, uint32_t h, uint32_t n, uint32_t ld, uint32_t nnz, hipStream_t stream) {
-    if constexpr (NT >= 4) return up_waves<NT, P, V, 16>(x, off, idx, w, b, act, z, d, h, n, ld, nnz, stream);
-    else return up_waves<NT, P, V, kWaves>(x, off, idx, w, b, act, z, d, h, n, ld, nnz, stream);
+    if constexpr (NT >= 4) return up_waves<NT, P, V, 16, GRAD>(x, off, idx, w, b, act, z, d, h, n, ld, nnz, stream);
+    else return up_waves<NT, P, V, kWaves, GRAD>(x, off, idx, w, b, act, z, d, h, n, ld, nnz, stream);
 }
 
 // With act staged in LDS (small n), blocks of 16 waves take 4x the rows of 4-wave blocks, so each block's staging
@@ -344,12 +349,12 @@ hipError_t down_shape(const float* act, const int32_t* off, const int16_t* hid, 
     return hipGetLastError();
 }
 
-template <int NT, typename V>
+template <int NT, typename V, bool GRAD>
 hipError_t up_parts(int parts, const float* x, const int32_t* off, const int16_t* idx, const V* w, const float* b, float* act,
                     float* z, uint32_t d, uint32_t h, uint32_t n, uint32_t ld, uint32_t nnz, hipStream_t stream) {
-    if (parts == 4) return up_shape<NT, 4>(x, off, idx, w, b, act, z, d, h, n, ld, nnz, stream);
-    if (parts == 2) return up_shape<NT, 2>(x, off, idx, w, b, act, z, d, h, n, ld, nnz, stream);
-    return up_shape<NT, 1>(x, off, idx, w, b, act, z, d, h, n, ld, nnz, stream);
+    if (parts == 4) return up_shape<NT, 4, V, GRAD>(x, off, idx, w, b, act, z, d, h, n, ld, nnz, stream);
+    if (parts == 2) return up_shape<NT, 2, V, GRAD>(x, off, idx, w, b, act, z, d, h, n, ld, nnz, stream);
+    return up_shape<NT, 1, V, GRAD>(x, off, idx, w, b, act, z, d, h, n, ld, nnz, stream);
 }
 
 template <int NT, typename V>
@@ -360,15 +365,15 @@ hipError_t down_parts(int parts, const float* act, const int32_t* off, const int
     return down_shape<NT, 1>(act, off, hid, v, bias, y, d, h, n, ld, nnz, stream);
 }
 
-template <typename V>
+template <typename V, bool GRAD = false>
 hipError_t up_typed(const float* x, const int32_t* off, const int16_t* idx, const V* w, const float* b, float* act, float* z,
                     uint32_t d, uint32_t h, uint32_t n, uint32_t ld, uint32_t nnz, hipStream_t stream) {
     const int parts = parts_for(nnz, h);
     switch (edges_tokens(n)) {
-        case 1: return up_parts<1>(parts, x, off, idx, w, b, act, z, d, h, n, ld, nnz, stream);
-        case 2: return up_parts<2>(parts, x, off, idx, w, b, act, z, d, h, n, ld, nnz, stream);
-        case 4: return up_parts<4>(parts, x, off, idx, w, b, act, z, d, h, n, ld, nnz, stream);
-        default: return up_parts<8>(parts, x, off, idx, w, b, act, z, d, h, n, ld, nnz, stream);
+        case 1: return up_parts<1, V, GRAD>(parts, x, off, idx, w, b, act, z, d, h, n, ld, nnz, stream);
+        case 2: return up_parts<2, V, GRAD>(parts, x, off, idx, w, b, act, z, d, h, n, ld, nnz, stream);
+        case 4: return up_parts<4, V, GRAD>(parts, x, off, idx, w, b, act, z, d, h, n, ld, nnz, stream);
+        default: return up_parts<8, V, GRAD>(parts, x, off, idx, w, b, act, z, d, h, n, ld, nnz, stream);
     }
 }
 
@@ -390,6 +395,11 @@ hipError_t launch_up_edges(int vt, const float* x, const int32_t* off, const int
                            float* act, float* z, uint32_t d, uint32_t h, uint32_t n, uint32_t ld, uint32_t nnz, hipStream_t stream) {
     if (vt == kBF16) return up_typed(x, off, idx, static_cast<const uint16_t*>(w), b, act, z, d, h, n, ld, nnz, stream);
     return up_typed(x, off, idx, static_cast<const float*>(w), b, act, z, d, h, n, ld, nnz, stream);
+}
+
+hipError_t launch_grad_hidden_edges(const float* gy, const int32_t* off, const int16_t* idx, const float* v, const float* z,
+                                    float* gz, uint32_t d, uint32_t h, uint32_t n, uint32_t ld, uint32_t nnz, hipStream_t stream) {
+    return up_typed<float, true>(gy, off, idx, v, nullptr, gz, const_cast<float*>(z), d, h, n, ld, nnz, stream);
 }
 
 hipError_t launch_down_edges(int vt, const float* act, const int32_t* off, const int16_t* hid, const void* v,

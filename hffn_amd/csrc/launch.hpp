@@ -34,12 +34,15 @@ hipError_t launch_up_rows(int vt, const float* x_t, const int32_t* off, const in
                           hipStream_t stream);
 // The rows up kernel with the backward's epilogue: gz[r, t] = (sum over the slots of r of v * gy_t[idx, t]) *
 // gelu'(z[r, t]), hidden-major [h, ld] (fp32 values).
+// The same with the edges up kernel (small n; gy token-major [n, d_model], its stage must fit the LDS as for the up).
+hipError_t launch_grad_hidden_edges(const float* gy, const int32_t* off, const int16_t* idx, const float* v, const float* z,
+                                    float* gz, uint32_t d, uint32_t h, uint32_t n, uint32_t ld, uint32_t nnz, hipStream_t stream);
 hipError_t launch_grad_hidden_rows(const float* gy_t, const int32_t* off, const int16_t* idx, const float* v, const float* z,
                                    float* gz, uint32_t h, uint32_t n, uint32_t ld, hipStream_t stream);
 
 // Down projection over the output-major store. `edges`: one wave per output, lanes over its
 // slots, writes y[n, d_model]; `rows`: one wave per output, lanes over tokens, writes
-// y_t[d_model, ld] (the caller transposes).
+// y_t[d_model, ld] (the caller transposes). A null bias adds nothing (the backward's gx).
 hipError_t launch_down_edges(int vt, const float* act, const int32_t* off, const int16_t* hid, const void* v,
                              const float* bias, float* y, uint32_t d, uint32_t h, uint32_t n, uint32_t ld, uint32_t nnz,
                              hipStream_t stream);
@@ -53,6 +56,9 @@ constexpr uint32_t kGradTile = 256;
 inline uint32_t grad_tiles(uint32_t n) { return (n + kGradTile - 1) / kGradTile; }
 // For each owner row o (rows of them) and each slot q of o: g[k*stride + q] = sum over the tokens t of tile k of
 // row[o, t] * mat[idx[q], t]; gb[k*stride + o] = sum over the same tokens of row[o, t]. row and mat are [*, ld].
+// n <= kEdgesMaxTokens: lanes over the slots of an owner row, the n tokens of the row in registers (one tile).
+hipError_t launch_grad_sddmm_edges(const float* row, const float* mat, const int32_t* off, const int16_t* idx, float* g, float* gb,
+                                   uint32_t rows, uint32_t n, uint32_t ld, hipStream_t stream);
 hipError_t launch_grad_sddmm(const float* row, const float* mat, const int32_t* off, const int16_t* idx, float* g, float* gb,
                              uint32_t rows, uint32_t n, uint32_t ld, uint32_t stride, hipStream_t stream);
 hipError_t launch_reduce_tiles(const float* ws, uint32_t stride, uint32_t tiles, uint32_t c1, uint32_t c2, uint32_t c3,

@@ -1,9 +1,10 @@
 // Training kernels of the HFFN layer on CDNA4 (wave64): the two sampled products of the backward (the gradients of
-// the compact weights), the fixed-order sum of their token-tile partials, the compact AdamW and a value gather.
-// The other two backward quantities are gathers with the forward's shapes: gz is the rows up kernel over the
-// hidden-major down support with a gelu' epilogue (gather.hip), gx the rows down kernel over the input-major up
-// support. Semantics follow runtime/gpu/nvidia/ffn/training/kernels_train.py:101-258; every result is written by
-// exactly one lane, with no atomics, so the bits repeat run to run.
+// the compact weights; lanes over tokens in 256-token tiles, or lanes over slots up to 8 tokens), the fixed-order sum
+// of their token-tile partials, the compact AdamW and a value gather. The other two backward quantities are gathers
+// with the forward's shapes: gz is the up kernel (edges up to 8 tokens, else rows) over the hidden-major down support
+// with a gelu' epilogue, gx the down kernel (edges or rows) over the input-major up support with no bias. Semantics
+// follow runtime/gpu/nvidia/ffn/training/kernels_train.py:101-258; every result is written by exactly one lane, with
+// no atomics, so the bits repeat run to run.
 #include "common.hpp"
 #include "launch.hpp"
 
@@ -72,6 +73,33 @@ __global__ __launch_bounds__(kBlock) void grad_sddmm_kernel(const float* __restr
     }
 }
 
+// Sampled product for n <= 8 tokens (one pass): lanes over the slots of owner o (slot q = begin + lane + 64 k), the n
+// values of row o in registers (the same for every lane); each lane forms its slot's sum over the tokens in ascending
+// order and writes it, so no cross-lane reduction is needed. Lane 0 writes gb.
+template <int NT>
+__global__ __launch_bounds__(kBlock) void grad_sddmm_edges_kernel(const float* __restrict__ row, const float* __restrict__ mat,
+                                                                 const int32_t* __restrict__ off, const int16_t* __restrict__ idx,
+                                                                 float* __restrict__ g, float* __restrict__ gb, uint32_t rows,
+                                                                 uint32_t n, uint32_t ld) {
+    const uint32_t o = blockIdx.x * kWaves + uniform(threadIdx.x / kWave), lane = threadIdx.x % kWave;
+    if (o >= rows) return;
+    float own[NT];
+    load_vec<NT>(row + static_cast<size_t>(o) * ld, own);
+    float sum = 0.0f;
+#pragma unroll
+    for (uint32_t t = 0; t < NT; ++t) sum = t < n ? sum + own[t] : sum;
+    if (lane == 0) gb[o] = sum;
+    const int32_t end = off[o + 1];
+    for (int32_t q = off[o] + static_cast<int32_t>(lane); q < end; q += kWave) {
+        float m[NT];
+        load_vec<NT>(mat + static_cast<size_t>(static_cast<uint16_t>(idx[q])) * ld, m);
+        float s = 0.0f;
+#pragma unroll
+        for (uint32_t t = 0; t < NT; ++t) s = t < n ? fmaf(own[t], m[t], s) : s;
+        g[q] = s;
+    }
+}
+
 // ws [tiles, stride]: columns [0, c1) g_down, [c1, c2) gb_down, [c2, c3) g_up, [c3, stride) gb_up. One thread per
 // column: ((ws[0][j] + ws[1][j]) + ws[2][j]) + ... in ascending tile order (kernels_train.py:186-199).
 __global__ __launch_bounds__(kBlock) void reduce_tiles_kernel(const float* __restrict__ ws, uint32_t stride, uint32_t tiles,
@@ -118,6 +146,18 @@ hipError_t launch_grad_sddmm(const float* row, const float* mat, const int32_t* 
                              uint32_t rows, uint32_t n, uint32_t ld, uint32_t stride, hipStream_t stream) {
     hipLaunchKernelGGL(grad_sddmm_kernel, dim3(ceil_div(rows, kWaves), grad_tiles(n)), dim3(kBlock), 0, stream, row, mat, off, idx,
                        g, gb, rows, n, ld, stride);
+    return hipGetLastError();
+}
+
+hipError_t launch_grad_sddmm_edges(const float* row, const float* mat, const int32_t* off, const int16_t* idx, float* g, float* gb,
+                                   uint32_t rows, uint32_t n, uint32_t ld, hipStream_t stream) {
+    const dim3 grid(ceil_div(rows, kWaves)), block(kBlock);
+    switch (edges_tokens(n)) {
+        case 1: hipLaunchKernelGGL(grad_sddmm_edges_kernel<1>, grid, block, 0, stream, row, mat, off, idx, g, gb, rows, n, ld); break;
+        case 2: hipLaunchKernelGGL(grad_sddmm_edges_kernel<2>, grid, block, 0, stream, row, mat, off, idx, g, gb, rows, n, ld); break;
+        case 4: hipLaunchKernelGGL(grad_sddmm_edges_kernel<4>, grid, block, 0, stream, row, mat, off, idx, g, gb, rows, n, ld); break;
+        default: hipLaunchKernelGGL(grad_sddmm_edges_kernel<8>, grid, block, 0, stream, row, mat, off, idx, g, gb, rows, n, ld); break;
+    }
     return hipGetLastError();
 }
 

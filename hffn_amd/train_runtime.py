@@ -208,9 +208,9 @@ class HFFNTrainRuntime:
             g_down, gb_down, g_up, gb_up = ws, ws + 4 * c1, ws + 4 * c2, ws + 4 * c3
         _lib.check(lib.hffn_grad_sddmm(self._gy_t.data_ptr(), act, params["out_offsets"].data_ptr(), params["out_hidden"].data_ptr(),
                                        g_down, gb_down, d, n, ld, stride, stream), "grad_down")
-        _lib.check(lib.hffn_grad_hidden(self._gy_t.data_ptr(), z_ptr, supports["hid_offsets"].data_ptr(),
+        _lib.check(lib.hffn_grad_hidden(gy.data_ptr(), self._gy_t.data_ptr(), z_ptr, supports["hid_offsets"].data_ptr(),
                                         supports["hid_output"].data_ptr(), values["hid_val"].data_ptr(), self._gz.data_ptr(),
-                                        d, h, n, ld, stream), "grad_hidden")
+                                        d, h, values["hid_val"].numel(), n, ld, stream), "grad_hidden")
         _lib.check(lib.hffn_grad_sddmm(self._gz.data_ptr(), x_t, params["up_offsets"].data_ptr(), params["up_idx"].data_ptr(),
                                        g_up, gb_up, h, n, ld, stride, stream), "grad_up")
         if tiles > 1:
@@ -219,7 +219,8 @@ class HFFNTrainRuntime:
                                              grads["b_down"].data_ptr(), grads["up_val"].data_ptr(), grads["b_up"].data_ptr(),
                                              stream), "reduce_tiles")
         _lib.check(lib.hffn_grad_x(self._gz.data_ptr(), supports["in_offsets"].data_ptr(), supports["in_hidden"].data_ptr(),
-                                   values["in_val"].data_ptr(), self._gx_t.data_ptr(), self._gx.data_ptr(), d, h, n, ld, stream),
+                                   values["in_val"].data_ptr(), self._gx_t.data_ptr(), self._gx.data_ptr(), d, h,
+                                   values["in_val"].numel(), n, ld, stream),
                    "grad_x")
         return self._gx[:n]
 

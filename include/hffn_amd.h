@@ -27,7 +27,7 @@
 extern "C" {
 #endif
 
-#define HFFN_ABI_VERSION 4
+#define HFFN_ABI_VERSION 5
 
 #define HFFN_OK 0
 #define HFFN_ERROR_ARGUMENT (-1) /* invalid shape, mode, pointer or workspace */
@@ -179,15 +179,17 @@ int hffn_forward_z(int up_mode, int down_mode, const float* x, const int32_t* up
 int hffn_grad_sddmm(const float* row, const float* mat, const int32_t* offsets, const int16_t* index, float* g, float* gb,
                     uint32_t rows, uint32_t n, uint32_t ld, uint32_t stride, void* stream);
 
-/* gz[r, t] = (sum over the hidden-major down slots of r of down_val * gy_t[down_idx, t]) * gelu'(z[r, t]); down_val in
- * hidden-major slot order. Replaces grad_hidden (kernels_train.py:139-160). */
-int hffn_grad_hidden(const float* gy_t, const float* z, const int32_t* down_offsets, const int16_t* down_idx, const float* down_val,
-                     float* gz, uint32_t d_model, uint32_t d_ff, uint32_t n, uint32_t ld, void* stream);
+/* gz[r, t] = (sum over the hidden-major down slots of r of down_val * gy[t, down_idx]) * gelu'(z[r, t]); down_val in
+ * hidden-major slot order; gy token-major (read up to 8 tokens) and gy_t feature-major (read above). Replaces
+ * grad_hidden (kernels_train.py:139-160). */
+int hffn_grad_hidden(const float* gy, const float* gy_t, const float* z, const int32_t* down_offsets, const int16_t* down_idx,
+                     const float* down_val, float* gz, uint32_t d_model, uint32_t d_ff, uint32_t nnz_down, uint32_t n, uint32_t ld,
+                     void* stream);
 
-/* gx[t, i] = sum over the input-major up slots of i of in_val * gz[in_hidden, t] (through gx_t, feature-major).
- * Replaces grad_x (kernels_train.py:201-231). */
+/* gx[t, i] = sum over the input-major up slots of i of in_val * gz[in_hidden, t] (above 8 tokens through gx_t,
+ * feature-major). Replaces grad_x (kernels_train.py:201-231). */
 int hffn_grad_x(const float* gz, const int32_t* in_offsets, const int16_t* in_hidden, const float* in_val, float* gx_t, float* gx,
-                uint32_t d_model, uint32_t d_ff, uint32_t n, uint32_t ld, void* stream);
+                uint32_t d_model, uint32_t d_ff, uint32_t nnz_up, uint32_t n, uint32_t ld, void* stream);
 
 /* Fixed-order sum of the tile partials ws[tiles, stride] into g_down [0, c1), gb_down [c1, c2), g_up [c2, c3),
  * gb_up [c3, stride). Replaces reduce_tiles (kernels_train.py:186-199). */
