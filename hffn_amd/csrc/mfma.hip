@@ -137,7 +137,9 @@ __global__ __launch_bounds__(kThreads) void densify_kernel(const int32_t* __rest
 }
 
 // ------------------------------------------------------------------------------------------------ GEMM
-enum class Epi { Up, Down };
+// Up: the up GEMM with the GELU epilogue writing activation planes. Down: the down GEMM writing y or split partials.
+// UpSplit: the up GEMM over a k split, writing fp32 partial sums (no bias, no GELU) for act_planes_kernel.
+enum class Epi { Up, Down, UpSplit };
 
 struct Tile {
     uint32_t m, n, split;
@@ -503,17 +505,17 @@ __device__ __forceinline__ void block_barrier() {
     asm volatile("" ::: "memory");
 }
 
-template <Epi EPI, bool LO_B, int SPLITS>
+template <Epi EPI, bool LO_B>
 __global__ __launch_bounds__(kThreads) void gemm_dma_kernel(
     const _Float16* __restrict__ a_planes,  // [K / 32][8][rows_pad][8]
     const int32_t* __restrict__ a_exp,      // Up: [rows_pad]; Down: [rows_pad, K / kActBlock]
     const _Float16* __restrict__ b_planes,  // [K / 32][8][Ncol][8]
     const int32_t* __restrict__ b_exp,      // [Ncol]
     const float* __restrict__ bias,         // [Ncol]
-    float* __restrict__ out,                // Down: y [M, Ncol] (SPLITS == 1) or partials [SPLITS, M, Ncol]
+    float* __restrict__ out,                // Down: y [M, Ncol] (splits == 1) or partials [splits, M, Ncol]; UpSplit: partials
     _Float16* __restrict__ out_planes,      // Up: activation planes [Ncol / 32][8][rows_pad][8]
     int32_t* __restrict__ out_exp,          // Up: [rows_pad, Ncol / BN] activation block binades
-    uint32_t M, uint32_t rows_pad, uint32_t Ncol, uint32_t K) {
+    uint32_t M, uint32_t rows_pad, uint32_t Ncol, uint32_t K, uint32_t splits) {
     constexpr int MI = 4, NI = 2, BM = kDmaBM, BN = kDmaBN, S = kDmaStages;
     static_assert(BM == kThreads, "one thread per block row for the binade tables");
     constexpr uint32_t kStage = kRuns * (BM + BN) * 8;  // halves per stage
@@ -527,12 +529,12 @@ __global__ __launch_bounds__(kThreads) void gemm_dma_kernel(
     const uint32_t tid = threadIdx.x, lane = tid % kWave, wave = uniform(tid / kWave);
     const uint32_t wm = wave / 2, wn = wave % 2;
     const uint32_t tiles_m = rows_pad / BM, tiles_n = Ncol / BN;
-    const Tile tile = tile_of(blockIdx.x, tiles_m, tiles_n, SPLITS);
+    const Tile tile = tile_of(blockIdx.x, tiles_m, tiles_n, splits);
     const uint32_t m0 = tile.m * BM, n0 = tile.n * BN;
     const uint32_t ktiles = K / kBK;
-    const uint32_t k_begin = tile.split * ktiles / SPLITS, k_end = (tile.split + 1) * ktiles / SPLITS;
+    const uint32_t k_begin = tile.split * ktiles / splits, k_end = (tile.split + 1) * ktiles / splits;
     const uint32_t a_kblocks = K / kActBlock, kb0 = k_begin / kKtPerActBlock;
-    if constexpr (EPI == Epi::Up) {
+    if constexpr (EPI != Epi::Down) {
         e_row[0][tid] = a_exp[m0 + tid];
     } else {
         // the row's binades of this split (whole activation blocks), eight loads in flight at a time
@@ -741,8 +743,8 @@ __global__ __launch_bounds__(kThreads) void gemm_dma_kernel(
             *reinterpret_cast<half8*>(out_planes + plane_at(rows_pad, m0 + tid, n0 + chunk * 8, 1)) = l;
         }
     } else {
-        // y (one split) or this split's partial, powers of two undone: through an fp32 [BM][BN] tile in LDS, so that
-        // every thread writes 16 bytes (a wave: two rows of BN columns)
+        // y (Down, one split) or this split's partial, powers of two undone: through an fp32 [BM][BN] tile in LDS, so
+        // that every thread writes 16 bytes (a wave: two rows of BN columns)
         constexpr uint32_t kLd = BN + 4;
         static_assert(BM * kLd * sizeof(float) <= sizeof(smem), "the epilogue tile fits the staging LDS");
         float* tile_v = reinterpret_cast<float*>(smem);
@@ -756,16 +758,18 @@ __global__ __launch_bounds__(kThreads) void gemm_dma_kernel(
 #pragma unroll
                 for (int r = 0; r < 16; ++r) {
                     const uint32_t m = acc_row<BM>(wm, i, r, lane);
-                    tile_v[m * kLd + c] = ldexpf(acc[i][j][r], e_tab[kb_last][m] + ce);
+                    const int ea = EPI == Epi::Down ? static_cast<int>(e_tab[kb_last][m]) : e_row[0][m];
+                    tile_v[m * kLd + c] = ldexpf(acc[i][j][r], ea + ce);
                 }
         }
         __syncthreads();
-        float* target = out + (SPLITS > 1 ? static_cast<size_t>(tile.split) * M * Ncol : 0);
+        float* target = out + (splits > 1 ? static_cast<size_t>(tile.split) * M * Ncol : 0);
+        const bool add_bias = EPI == Epi::Down && splits == 1;
         for (uint32_t q = tid; q < BM * (BN / 4); q += kThreads) {
             const uint32_t m = q / (BN / 4), c = (q % (BN / 4)) * 4;
             if (m0 + m >= M) break;  // rows ascend with q
             float4 v = *reinterpret_cast<const float4*>(tile_v + m * kLd + c);
-            if constexpr (SPLITS == 1) {
+            if (add_bias) {
                 const float4 b = *reinterpret_cast<const float4*>(bias + n0 + c);
                 v.x += b.x; v.y += b.y; v.z += b.z; v.w += b.w;
             }
@@ -789,6 +793,50 @@ __global__ __launch_bounds__(kThreads) void reduce_splits_kernel(const float* __
     const float4 b = *reinterpret_cast<const float4*>(bias + (i * 4) % Ncol);
     t.x += b.x; t.y += b.y; t.z += b.z; t.w += b.w;
     reinterpret_cast<float4*>(y)[i] = t;
+}
+
+// Activation planes from the up GEMM's k-split partial sums (Epi::UpSplit): v = gelu(sum over the splits, in split
+// order, of partials[s, m, n] + b_up[n]); rows m >= M hold gelu(b_up[n]), as the zero rows of x give in the fused
+// epilogue. Then, per token and 128-neuron block, the binade of the largest |v| and the hi/lo planes, as
+// gemm_dma_kernel<Up> writes them. A wave takes 4 rows of one 128-neuron block: 16 lanes per row, 8 consecutive
+// neurons per lane (one 16-byte chunk per part); the block's maximum is a 16-lane xor butterfly.
+constexpr uint32_t kActRowsPerBlock = kThreads / 16;
+__global__ __launch_bounds__(kThreads) void act_planes_kernel(const float* __restrict__ partials, uint32_t splits,
+                                                             const float* __restrict__ b_up, _Float16* __restrict__ planes,
+                                                             int32_t* __restrict__ exps, uint32_t M, uint32_t rows_pad, uint32_t H) {
+    const uint32_t m = blockIdx.x * kActRowsPerBlock + threadIdx.x / 16, sub = threadIdx.x % 16;
+    const uint32_t nb = blockIdx.y, n = nb * kActBlock + sub * 8;
+    const float4 b0 = *reinterpret_cast<const float4*>(b_up + n), b1 = *reinterpret_cast<const float4*>(b_up + n + 4);
+    float v[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+    if (m < M) {
+        for (uint32_t sp = 0; sp < splits; ++sp) {
+            const float* p = partials + (static_cast<size_t>(sp) * M + m) * H + n;
+            const float4 u = *reinterpret_cast<const float4*>(p), w = *reinterpret_cast<const float4*>(p + 4);
+            v[0] += u.x; v[1] += u.y; v[2] += u.z; v[3] += u.w; v[4] += w.x; v[5] += w.y; v[6] += w.z; v[7] += w.w;
+        }
+    }
+    const float b[8] = {b0.x, b0.y, b0.z, b0.w, b1.x, b1.y, b1.z, b1.w};
+    uint32_t largest = 0;
+#pragma unroll
+    for (int q = 0; q < 8; ++q) {
+        v[q] = gelu(v[q] + b[q]);
+        largest = max(largest, abs_bits(v[q]));
+    }
+#pragma unroll
+    for (int off = 8; off >= 1; off >>= 1) largest = max(largest, static_cast<uint32_t>(__shfl_xor(static_cast<int>(largest), off, kWave)));
+    const int e = binade_of_bits(largest);
+    if (sub == 0) exps[static_cast<size_t>(m) * (H / kActBlock) + nb] = e;
+    const float scale = ldexpf(1.0f, -e);
+    half8 hi, lo;
+#pragma unroll
+    for (int q = 0; q < 8; ++q) {
+        _Float16 hh, ll;
+        split(v[q] * scale, hh, ll);
+        hi[q] = hh;
+        lo[q] = ll;
+    }
+    *reinterpret_cast<half8*>(planes + plane_at(rows_pad, m, n, 0)) = hi;
+    *reinterpret_cast<half8*>(planes + plane_at(rows_pad, m, n, 1)) = lo;
 }
 
 uint32_t ceil_div(uint32_t a, uint32_t b) { return (a + b - 1) / b; }
@@ -858,21 +906,36 @@ constexpr uint32_t kDmaMinBlocks = 128;
 
 uint32_t dma_tiles(uint32_t m, uint32_t ncol) { return rows_padded(m) / kDmaBM * (ncol / kDmaBN); }
 
+// Splits of the streamed down GEMM: doubled (up to kDmaMaxSplits) until the tiles times the splits reach ~192 blocks
+// or a split's activation binades fit LDS; each split a whole number of activation blocks. 0: not streamed.
+constexpr uint32_t kDmaMaxSplits = 32;
 uint32_t dma_down_splits(uint32_t m, uint32_t ncol, uint32_t k) {
     const uint32_t tiles = dma_tiles(m, ncol);
-    uint32_t splits = tiles >= 192 ? 1 : tiles >= 96 ? 2 : 4;
-    while (splits < 4 && k / kActBlock / splits > kDmaMaxActBlocks) splits *= 2;  // the split's binades must fit LDS
+    uint32_t splits = 1;
+    while (splits < kDmaMaxSplits && tiles * splits < 192) splits *= 2;
+    while (splits < kDmaMaxSplits && k / kActBlock / splits > kDmaMaxActBlocks) splits *= 2;  // the split's binades must fit LDS
     while (splits > 1 && k % (kActBlock * splits) != 0) splits /= 2;
-    if (k / kActBlock / splits > kDmaMaxActBlocks) return 0;  // 0: not streamed
+    if (k / kActBlock / splits > kDmaMaxActBlocks) return 0;
     return tiles * splits >= kDmaMinBlocks ? splits : 0;
 }
 
-template <Epi EPI, bool LO_B, int SPLITS>
+// Splits of the streamed up GEMM: 1 when its tiles alone fill the chip, else doubled (up to 8, each split at least
+// one k-tile) until ~192 blocks; the partial sums then go through act_planes_kernel. 0: not streamed.
+constexpr uint32_t kDmaMaxUpSplits = 8;
+uint32_t dma_up_splits(uint32_t m, uint32_t ncol, uint32_t k) {
+    const uint32_t tiles = dma_tiles(m, ncol);
+    if (tiles >= kDmaMinBlocks) return 1;
+    uint32_t splits = 1;
+    while (splits < kDmaMaxUpSplits && tiles * splits < 192 && k % (kBK * splits * 2) == 0) splits *= 2;
+    return tiles * splits >= kDmaMinBlocks ? splits : 0;
+}
+
+template <Epi EPI, bool LO_B>
 hipError_t launch_dma(const _Float16* a_planes, const int32_t* a_exp, const _Float16* b_planes, const int32_t* b_exp,
                       const float* bias, float* out, _Float16* out_planes, int32_t* out_exp, uint32_t M, uint32_t Ncol, uint32_t K,
-                      hipStream_t stream) {
-    hipLaunchKernelGGL((gemm_dma_kernel<EPI, LO_B, SPLITS>), dim3(dma_tiles(M, Ncol) * SPLITS), dim3(kThreads), 0, stream, a_planes,
-                       a_exp, b_planes, b_exp, bias, out, out_planes, out_exp, M, rows_padded(M), Ncol, K);
+                      uint32_t splits, hipStream_t stream) {
+    hipLaunchKernelGGL((gemm_dma_kernel<EPI, LO_B>), dim3(dma_tiles(M, Ncol) * splits), dim3(kThreads), 0, stream, a_planes, a_exp,
+                       b_planes, b_exp, bias, out, out_planes, out_exp, M, rows_padded(M), Ncol, K, splits);
     return hipGetLastError();
 }
 
@@ -880,10 +943,9 @@ template <bool LO_B>
 hipError_t dma_down(uint32_t splits, const _Float16* a_planes, const int32_t* a_exp, const _Float16* b_planes, const int32_t* b_exp,
                     const float* bias, float* y, float* partials, uint32_t M, uint32_t Ncol, uint32_t K, hipStream_t stream) {
     if (splits == 1)
-        return launch_dma<Epi::Down, LO_B, 1>(a_planes, a_exp, b_planes, b_exp, bias, y, nullptr, nullptr, M, Ncol, K, stream);
+        return launch_dma<Epi::Down, LO_B>(a_planes, a_exp, b_planes, b_exp, bias, y, nullptr, nullptr, M, Ncol, K, 1, stream);
     const hipError_t status =
-        splits == 2 ? launch_dma<Epi::Down, LO_B, 2>(a_planes, a_exp, b_planes, b_exp, bias, partials, nullptr, nullptr, M, Ncol, K, stream)
-                    : launch_dma<Epi::Down, LO_B, 4>(a_planes, a_exp, b_planes, b_exp, bias, partials, nullptr, nullptr, M, Ncol, K, stream);
+        launch_dma<Epi::Down, LO_B>(a_planes, a_exp, b_planes, b_exp, bias, partials, nullptr, nullptr, M, Ncol, K, splits, stream);
     if (status != hipSuccess) return status;
     const size_t quads = static_cast<size_t>(M) * Ncol / 4;
     hipLaunchKernelGGL(reduce_splits_kernel, dim3(static_cast<uint32_t>((quads + kThreads - 1) / kThreads)), dim3(kThreads), 0, stream,
@@ -900,6 +962,19 @@ struct Workspace {
     size_t counters, x_binades, act_binades, x_planes, act_planes, partials, bytes;
 };
 
+// Floats of split partial sums any call of up to m tokens may need (the register-staged down GEMM's kMaxSplits, or
+// the streamed GEMMs' splits for every padded row count up to m's): a workspace sized for m serves every smaller n.
+size_t partial_floats(uint32_t m, uint32_t d, uint32_t h) {
+    size_t most = static_cast<size_t>(kMaxSplits) * m * d;
+    for (uint32_t rows = kRowPad; rows <= rows_padded(m); rows += kRowPad) {
+        const size_t tokens = min(m, rows);
+        most = max(most, static_cast<size_t>(dma_down_splits(rows, d, h)) * tokens * d);
+        const uint32_t up = dma_up_splits(rows, h, d);
+        if (up > 1) most = max(most, static_cast<size_t>(up) * tokens * h);
+    }
+    return most;
+}
+
 Workspace workspace_layout(uint32_t m, uint32_t d, uint32_t h) {
     const size_t rows = rows_padded(m);
     Workspace w{};
@@ -911,7 +986,7 @@ Workspace workspace_layout(uint32_t m, uint32_t d, uint32_t h) {
     w.x_planes = (words_end + 255) / 256 * 256;  // bytes from here on
     w.act_planes = w.x_planes + rows * d * 4;
     w.partials = w.act_planes + rows * h * 4;
-    w.bytes = w.partials + static_cast<size_t>(kMaxSplits) * m * d * 4;
+    w.bytes = w.partials + partial_floats(m, d, h) * 4;
     return w;
 }
 
@@ -945,12 +1020,24 @@ hipError_t launch_mfma_up(int vt, const float* x, const void* planes, const int3
                        x_planes, words + w.x_binades);  // one wave per padded row
     if (hipError_t status = hipGetLastError(); status != hipSuccess) return status;
     const auto* p = static_cast<const _Float16*>(planes);
+    if (const uint32_t splits = dma_up_splits(n, h, d); splits > 1) {
+        float* partials = reinterpret_cast<float*>(bytes + w.partials);
+        const hipError_t status =
+            vt == kBF16 ? launch_dma<Epi::UpSplit, false>(x_planes, words + w.x_binades, p, w_exp, nullptr, partials, nullptr, nullptr, n,
+                                                          h, d, splits, stream)
+                        : launch_dma<Epi::UpSplit, true>(x_planes, words + w.x_binades, p, w_exp, nullptr, partials, nullptr, nullptr, n,
+                                                         h, d, splits, stream);
+        if (status != hipSuccess) return status;
+        hipLaunchKernelGGL(act_planes_kernel, dim3(rows_padded(n) / kActRowsPerBlock, h / kActBlock), dim3(kThreads), 0, stream, partials,
+                           splits, b_up, act_planes, words + w.act_binades, n, rows_padded(n), h);
+        return hipGetLastError();
+    }
     if (dma_tiles(n, h) >= kDmaMinBlocks) {
         if (vt == kBF16)
-            return launch_dma<Epi::Up, false, 1>(x_planes, words + w.x_binades, p, w_exp, b_up, nullptr, act_planes, words + w.act_binades,
-                                                 n, h, d, stream);
-        return launch_dma<Epi::Up, true, 1>(x_planes, words + w.x_binades, p, w_exp, b_up, nullptr, act_planes, words + w.act_binades, n,
-                                            h, d, stream);
+            return launch_dma<Epi::Up, false>(x_planes, words + w.x_binades, p, w_exp, b_up, nullptr, act_planes, words + w.act_binades,
+                                              n, h, d, 1, stream);
+        return launch_dma<Epi::Up, true>(x_planes, words + w.x_binades, p, w_exp, b_up, nullptr, act_planes, words + w.act_binades, n,
+                                         h, d, 1, stream);
     }
     const Shape shape = up_shape(n, h);
     if (vt == kBF16)

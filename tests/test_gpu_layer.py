@@ -156,13 +156,22 @@ def test_densified_planes_reconstruct_the_weights(name, test_layers, device):
 @pytest.mark.parametrize("up,down", [("edges", "edges"), ("rows", "rows"), ("rows", "edges"), ("edges", "rows"),
                                      ("mfma", "mfma")])
 def test_token_result_does_not_depend_on_the_batch(up, down, test_layers, device):
+    """The gather kernels sum each token in a fixed order whatever the batch: bit-identical. The MFMA path splits K
+    into more parts when fewer tokens leave blocks idle, so a token's sums are grouped differently: equal to 1e-6 of
+    the output's scale, and bit-identical between calls of the same N."""
     compact, case, layer = test_layers["homog_512_2048"]
     runtime = HFFNRuntime([layer], device)
     runtime.force(up, down)
     x = torch.from_numpy(synth.make_input(case, 300)).to(device)
     whole = runtime.forward(0, x).clone()
     for start, size in ((0, 1), (7, 5), (64, 129), (299, 1)):
-        assert torch.equal(runtime.forward(0, x[start:start + size].contiguous()), whole[start:start + size])
+        part = runtime.forward(0, x[start:start + size].contiguous()).clone()
+        if up == "mfma":
+            scale = float(whole.abs().max())
+            assert float((part - whole[start:start + size]).abs().max()) <= 1e-6 * scale
+            assert torch.equal(runtime.forward(0, x[start:start + size].contiguous()), part)
+        else:
+            assert torch.equal(part, whole[start:start + size])
 
 
 def test_mfma_workspace_reused_at_shrinking_token_counts(test_layers, device):
