@@ -312,6 +312,11 @@ int hffn_mfma_workspace(uint32_t n, uint32_t d_model, uint32_t d_ff, uint64_t* b
     return HFFN_OK;
 }
 
+int hffn_mfma_streamed(uint32_t n, uint32_t d_model, uint32_t d_ff) {
+    if (int status = check_mfma(HFFN_VALUE_F32, d_model, d_ff, n)) return status;
+    return hffn::mfma_streamed(n, d_model, d_ff) ? 1 : 0;
+}
+
 namespace {
 int check_workspace(uint64_t bytes, uint32_t d_model, uint32_t d_ff, uint32_t n, const char* what) {
     const uint64_t needed = hffn::mfma_workspace_bytes(n, d_model, d_ff);

@@ -171,6 +171,24 @@ __device__ __forceinline__ void segment(int32_t begin, int32_t end, uint32_t par
     }
 }
 
+// A wave's first chunk of one row segment, requested ahead of its use.
+template <typename V>
+struct Slots {
+    Segment<V, kGroups> seg;
+    int32_t pb = 0, pe = 0;  // empty unless requested
+};
+
+// Requests the first chunk of part `part` of row r (nothing when r >= rows).
+template <int P, typename V>
+__device__ __forceinline__ void request_row(Slots<V>& s, const int32_t* __restrict__ off, const int16_t* __restrict__ idx,
+                                            const V* __restrict__ val, uint32_t r, uint32_t rows, uint32_t part, int32_t nnz,
+                                            uint32_t lane) {
+    if (r < rows) {
+        segment<P>(off[r], off[r + 1], part, s.pb, s.pe);
+        load_segment(s.seg, idx, val, s.pb, s.pe, nnz, lane, 0);
+    }
+}
+
 // ------------------------------------------------------------------------------------------------- up
 template <int NT, int P, typename V, int WAVES, bool GRAD = false>
 __global__ __launch_bounds__(WAVES * kWave) void up_edges_kernel(const float* __restrict__ x, const int32_t* __restrict__ off,
@@ -189,12 +207,8 @@ __global__ __launch_bounds__(WAVES * kWave) void up_edges_kernel(const float* __
     for (uint32_t c0 = 0; c0 < n; c0 += NT) {
         const uint32_t tokens = min(n - c0, static_cast<uint32_t>(NT));
         // the first row's slots are requested before the block stages x and waits for it
-        int32_t pb = 0, pe = 0;
-        Segment<V, kGroups> first;
-        if (r0 + row_in_pass < r1) {
-            segment<P>(off[r0 + row_in_pass], off[r0 + row_in_pass + 1], part, pb, pe);
-            load_segment(first, idx, w, pb, pe, nnz, lane, 0);
-        }
+        Slots<V> cur;
+        request_row<P>(cur, off, idx, w, r0 + row_in_pass, r1, part, nnz, lane);
         if (c0) __syncthreads();
         for (uint32_t i = threadIdx.x; i < d * NT; i += WAVES * kWave) {
             const uint32_t feature = i / NT, t = i % NT;
@@ -204,13 +218,12 @@ __global__ __launch_bounds__(WAVES * kWave) void up_edges_kernel(const float* __
         const StagedInput input{xs};
         for (uint32_t base = r0; base < r1; base += kRowsPerPass) {  // uniform trip count across the block
             const uint32_t r = base + row_in_pass;
+            // the wave's next row is requested before this row's sums, so its slots stream meanwhile
+            Slots<V> next;
+            request_row<P>(next, off, idx, w, r + kRowsPerPass, r1, part, nnz, lane);
             float acc[NT];
             if (r < r1) {
-                if (base != r0) {
-                    segment<P>(off[r], off[r + 1], part, pb, pe);
-                    load_segment(first, idx, w, pb, pe, nnz, lane, 0);
-                }
-                row_partials<NT>(first, idx, w, pb, pe, nnz, input, lane, acc);
+                row_partials<NT>(cur.seg, idx, w, cur.pb, cur.pe, nnz, input, lane, acc);
             } else {
 #pragma unroll
                 for (int t = 0; t < NT; ++t) acc[t] = 0.0f;
@@ -226,6 +239,7 @@ __global__ __launch_bounds__(WAVES * kWave) void up_edges_kernel(const float* __
                     act[at] = gelu(pre);
                 }
             }
+            cur = next;
         }
     }
 }
@@ -246,12 +260,8 @@ __global__ __launch_bounds__(WAVES * kWave) void down_edges_kernel(const float* 
     const uint32_t o1 = min(d, o0 + per_block);
     for (uint32_t c0 = 0; c0 < n; c0 += NT) {
         const uint32_t tokens = min(n - c0, static_cast<uint32_t>(NT));
-        int32_t pb = 0, pe = 0;
-        Segment<V, kGroups> first;
-        if (o0 + row_in_pass < o1) {
-            segment<P>(off[o0 + row_in_pass], off[o0 + row_in_pass + 1], part, pb, pe);
-            load_segment(first, hid, v, pb, pe, nnz, lane, 0);
-        }
+        Slots<V> cur;
+        request_row<P>(cur, off, hid, v, o0 + row_in_pass, o1, part, nnz, lane);
         if constexpr (STAGE) {
             if (c0) __syncthreads();
             for (uint32_t i = threadIdx.x; i < h * NT; i += WAVES * kWave) {
@@ -262,20 +272,19 @@ __global__ __launch_bounds__(WAVES * kWave) void down_edges_kernel(const float* 
         }
         for (uint32_t base = o0; base < o1; base += kRowsPerPass) {
             const uint32_t o = base + row_in_pass;
+            Slots<V> next;
+            request_row<P>(next, off, hid, v, o + kRowsPerPass, o1, part, nnz, lane);
             float acc[NT];
             if (o < o1) {
-                if (base != o0) {
-                    segment<P>(off[o], off[o + 1], part, pb, pe);
-                    load_segment(first, hid, v, pb, pe, nnz, lane, 0);
-                }
-                if constexpr (STAGE) row_partials<NT>(first, hid, v, pb, pe, nnz, StagedInput{as}, lane, acc);
-                else row_partials<NT>(first, hid, v, pb, pe, nnz, GlobalInput{act + c0, ld}, lane, acc);
+                if constexpr (STAGE) row_partials<NT>(cur.seg, hid, v, cur.pb, cur.pe, nnz, StagedInput{as}, lane, acc);
+                else row_partials<NT>(cur.seg, hid, v, cur.pb, cur.pe, nnz, GlobalInput{act + c0, ld}, lane, acc);
             } else {
 #pragma unroll
                 for (int t = 0; t < NT; ++t) acc[t] = 0.0f;
             }
             const float total = row_total<NT, P>(acc, lane, part, row_in_pass, totals);
             if (o < o1 && part == 0 && lane < tokens) y[static_cast<size_t>(c0 + lane) * d + o] = bias ? total + bias[o] : total;
+            cur = next;
         }
     }
 }

@@ -80,6 +80,7 @@ hipError_t launch_output_major(int vt, const int32_t* down_offsets, const int16_
 // leaves the activations in the workspace, where the down launcher reads them.
 size_t dense_plane_halves(uint32_t rows, uint32_t k);
 bool mfma_shape_supported(uint32_t d, uint32_t h);
+bool mfma_streamed(uint32_t n, uint32_t d, uint32_t h);  // both projections on the streamed (LDS DMA) GEMM
 size_t mfma_workspace_bytes(uint32_t n, uint32_t d, uint32_t h);
 hipError_t launch_densify(int vt, const int32_t* off, const int16_t* idx, const void* val, uint32_t rows, uint32_t k,
                           void* planes, int32_t* exps, hipStream_t stream);

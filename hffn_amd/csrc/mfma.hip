@@ -505,7 +505,11 @@ __device__ __forceinline__ void block_barrier() {
     asm volatile("" ::: "memory");
 }
 
-template <Epi EPI, bool LO_B>
+// LIVE < BM (one row tile of up to LIVE tokens): only the first LIVE rows of A are transferred and multiplied; the
+// waves of the second row half (all padding) only transfer and meet at the barriers. The live rows get the same
+// products in the same order as with LIVE = BM, and the padding rows' accumulators stay zero, as zero A rows leave
+// them, so the results are bitwise those of the full tile.
+template <Epi EPI, bool LO_B, int LIVE>
 __global__ __launch_bounds__(kThreads) void gemm_dma_kernel(
     const _Float16* __restrict__ a_planes,  // [K / 32][8][rows_pad][8]
     const int32_t* __restrict__ a_exp,      // Up: [rows_pad]; Down: [rows_pad, K / kActBlock]
@@ -518,9 +522,12 @@ __global__ __launch_bounds__(kThreads) void gemm_dma_kernel(
     uint32_t M, uint32_t rows_pad, uint32_t Ncol, uint32_t K, uint32_t splits) {
     constexpr int MI = 4, NI = 2, BM = kDmaBM, BN = kDmaBN, S = kDmaStages;
     static_assert(BM == kThreads, "one thread per block row for the binade tables");
+    static_assert(LIVE == BM || LIVE == 128 || LIVE == 64, "live rows: the whole tile, its first half or first quarter");
     constexpr uint32_t kStage = kRuns * (BM + BN) * 8;  // halves per stage
-    constexpr int kLoadsA = BM * kRuns / kWave / 4, kLoadsB = BN * kRuns / kWave / 4;  // DMA instructions per wave
+    constexpr int kRowRuns = LIVE / 64;                  // 64-row runs of A transferred per (part, chunk)
+    constexpr int kLoadsA = kRowRuns * kRuns / 4, kLoadsB = BN * kRuns / kWave / 4;  // DMA instructions per wave
     constexpr int kLoads = kLoadsA + kLoadsB;
+    constexpr int MIL = LIVE >= BM / 2 ? MI : LIVE / 32;  // multiplied 32-row tiles of a live wave
 
     __shared__ __attribute__((aligned(16))) _Float16 smem[S * kStage];
     __shared__ int32_t e_row[1][BM];  // Up: x binades
@@ -528,6 +535,7 @@ __global__ __launch_bounds__(kThreads) void gemm_dma_kernel(
 
     const uint32_t tid = threadIdx.x, lane = tid % kWave, wave = uniform(tid / kWave);
     const uint32_t wm = wave / 2, wn = wave % 2;
+    const bool live = LIVE > BM / 2 || wm == 0;  // wave-uniform: this wave's rows hold tokens
     const uint32_t tiles_m = rows_pad / BM, tiles_n = Ncol / BN;
     const Tile tile = tile_of(blockIdx.x, tiles_m, tiles_n, splits);
     const uint32_t m0 = tile.m * BM, n0 = tile.n * BN;
@@ -555,7 +563,7 @@ __global__ __launch_bounds__(kThreads) void gemm_dma_kernel(
     // kLoadsA), then of B
     const auto issue_piece = [&](uint32_t kt, uint32_t slot, int q) {
         if (q < kLoadsA) {
-            const uint32_t at = wave * kLoadsA + q, run = at / (BM / 64), rb = at % (BM / 64);
+            const uint32_t at = wave * kLoadsA + q, run = at / kRowRuns, rb = at % kRowRuns;
             dma16(a_planes + ((static_cast<size_t>(kt) * kRuns + run) * rows_pad + m0 + rb * 64) * 8, lane,
                   smem + slot * kStage + (run * BM + rb * 64) * 8);
         } else {
@@ -582,11 +590,12 @@ __global__ __launch_bounds__(kThreads) void gemm_dma_kernel(
         half8 ah[MI], al[MI], bh[NI], bl[NI];
     };
     const auto load = [&](Frags& f, uint32_t slot, int kk) {
+        if (!live) return;
         const _Float16* s_a = smem + slot * kStage;
         const _Float16* s_b = s_a + kRuns * BM * 8;
         const uint32_t chunk = kk * 2 + lane / 32;
 #pragma unroll
-        for (int i = 0; i < MI; ++i) {
+        for (int i = 0; i < MIL; ++i) {
             const uint32_t r = wm * (BM / 2) + i * 32 + lane % 32;
             f.ah[i] = *reinterpret_cast<const half8*>(s_a + (chunk * BM + r) * 8);
             f.al[i] = *reinterpret_cast<const half8*>(s_a + ((4 + chunk) * BM + r) * 8);
@@ -599,8 +608,9 @@ __global__ __launch_bounds__(kThreads) void gemm_dma_kernel(
         }
     };
     const auto multiply = [&](const Frags& f) {
+        if (!live) return;
 #pragma unroll
-        for (int i = 0; i < MI; ++i)
+        for (int i = 0; i < MIL; ++i)
 #pragma unroll
             for (int j = 0; j < NI; ++j) {
                 acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(f.ah[i], f.bh[j], acc[i][j], 0, 0, 0);
@@ -614,6 +624,12 @@ __global__ __launch_bounds__(kThreads) void gemm_dma_kernel(
     constexpr int kProducts = LO_B ? 3 : 2, kMfmas = MI * NI * kProducts;
     static_assert(kMfmas >= kLoads, "at most one transfer per MFMA");
     const auto multiply_issuing = [&](const Frags& f, uint32_t kt, uint32_t slot, bool transfer) {
+        if constexpr (LIVE < BM) {  // few MFMAs: the stage's transfers go out first, in one burst
+            if (transfer) issue(kt, slot);
+            __builtin_amdgcn_sched_barrier(0);
+            multiply(f);
+            return;
+        }
 #pragma unroll
         for (int p = 0; p < kProducts; ++p)  // product-major: consecutive MFMAs accumulate into different tiles
 #pragma unroll
@@ -647,10 +663,10 @@ __global__ __launch_bounds__(kThreads) void gemm_dma_kernel(
     // registers 4g .. 4g + 3 hold 4 consecutive rows, so one 4-byte read per block and group
     const auto rescale = [&](uint32_t kt) {
         if constexpr (EPI == Epi::Down) {
-            if (kt % kKtPerActBlock == 0 && kt != k_begin) {
+            if (kt % kKtPerActBlock == 0 && kt != k_begin && live) {
                 const uint32_t kb = kt / kKtPerActBlock - kb0;
 #pragma unroll
-                for (int i = 0; i < MI; ++i)
+                for (int i = 0; i < MIL; ++i)
 #pragma unroll
                     for (int g = 0; g < 4; ++g) {
                         const uint32_t m = acc_row<BM>(wm, i, 4 * g, lane);
@@ -786,9 +802,16 @@ __global__ __launch_bounds__(kThreads) void reduce_splits_kernel(const float* __
     if (i >= quads) return;
     const float4* p = reinterpret_cast<const float4*>(partials);
     float4 t = p[i];
-    for (uint32_t s = 1; s < splits; ++s) {
-        const float4 u = p[s * quads + i];
-        t.x += u.x; t.y += u.y; t.z += u.z; t.w += u.w;
+    for (uint32_t s0 = 1; s0 < splits; s0 += 8) {  // 8 loads in flight, added in split order
+        float4 u[8];
+#pragma unroll
+        for (uint32_t q = 0; q < 8; ++q)
+            if (s0 + q < splits) u[q] = p[(s0 + q) * quads + i];
+#pragma unroll
+        for (uint32_t q = 0; q < 8; ++q)
+            if (s0 + q < splits) {
+                t.x += u[q].x; t.y += u[q].y; t.z += u[q].z; t.w += u[q].w;
+            }
     }
     const float4 b = *reinterpret_cast<const float4*>(bias + (i * 4) % Ncol);
     t.x += b.x; t.y += b.y; t.z += b.z; t.w += b.w;
@@ -809,10 +832,21 @@ __global__ __launch_bounds__(kThreads) void act_planes_kernel(const float* __res
     const float4 b0 = *reinterpret_cast<const float4*>(b_up + n), b1 = *reinterpret_cast<const float4*>(b_up + n + 4);
     float v[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
     if (m < M) {
-        for (uint32_t sp = 0; sp < splits; ++sp) {
-            const float* p = partials + (static_cast<size_t>(sp) * M + m) * H + n;
-            const float4 u = *reinterpret_cast<const float4*>(p), w = *reinterpret_cast<const float4*>(p + 4);
-            v[0] += u.x; v[1] += u.y; v[2] += u.z; v[3] += u.w; v[4] += w.x; v[5] += w.y; v[6] += w.z; v[7] += w.w;
+        for (uint32_t s0 = 0; s0 < splits; s0 += 4) {  // 8 loads in flight, added in split order
+            float4 u[4], w[4];
+#pragma unroll
+            for (uint32_t q = 0; q < 4; ++q)
+                if (s0 + q < splits) {
+                    const float* p = partials + (static_cast<size_t>(s0 + q) * M + m) * H + n;
+                    u[q] = *reinterpret_cast<const float4*>(p);
+                    w[q] = *reinterpret_cast<const float4*>(p + 4);
+                }
+#pragma unroll
+            for (uint32_t q = 0; q < 4; ++q)
+                if (s0 + q < splits) {
+                    v[0] += u[q].x; v[1] += u[q].y; v[2] += u[q].z; v[3] += u[q].w;
+                    v[4] += w[q].x; v[5] += w[q].y; v[6] += w[q].z; v[7] += w[q].w;
+                }
         }
     }
     const float b[8] = {b0.x, b0.y, b0.z, b0.w, b1.x, b1.y, b1.z, b1.w};
@@ -898,11 +932,11 @@ hipError_t gemm(Shape shape, const _Float16* a_planes, const int32_t* a_exp, con
     return hipErrorInvalidValue;
 }
 
-// The streamed kernel takes a GEMM when its 256 x 128 tiles (times the k splits of a down projection) give at least
-// 128 blocks; a down projection splits K in 2 or 4 to reach about 256 blocks, or to bring a split's activation
-// binades within kDmaMaxActBlocks (each split a whole number of activation blocks); its partials are added by
-// reduce_splits_kernel.
+// The streamed kernel takes a GEMM when its 256 x 128 tiles times its k splits give at least kDmaMinBlocks blocks
+// (an up projection) or kDmaMinDownBlocks (a down projection, whose split count is bounded by the activation blocks
+// of narrow layers); the split partials are added by reduce_splits_kernel (down) or act_planes_kernel (up).
 constexpr uint32_t kDmaMinBlocks = 128;
+constexpr uint32_t kDmaMinDownBlocks = 64;
 
 uint32_t dma_tiles(uint32_t m, uint32_t ncol) { return rows_padded(m) / kDmaBM * (ncol / kDmaBN); }
 
@@ -916,7 +950,7 @@ uint32_t dma_down_splits(uint32_t m, uint32_t ncol, uint32_t k) {
     while (splits < kDmaMaxSplits && k / kActBlock / splits > kDmaMaxActBlocks) splits *= 2;  // the split's binades must fit LDS
     while (splits > 1 && k % (kActBlock * splits) != 0) splits /= 2;
     if (k / kActBlock / splits > kDmaMaxActBlocks) return 0;
-    return tiles * splits >= kDmaMinBlocks ? splits : 0;
+    return tiles * splits >= kDmaMinDownBlocks ? splits : 0;
 }
 
 // Splits of the streamed up GEMM: 1 when its tiles alone fill the chip, else doubled (up to 8, each split at least
@@ -930,12 +964,22 @@ uint32_t dma_up_splits(uint32_t m, uint32_t ncol, uint32_t k) {
     return tiles * splits >= kDmaMinBlocks ? splits : 0;
 }
 
+// One row tile of at most 64 or 128 tokens takes the kernel that transfers and multiplies only those rows.
 template <Epi EPI, bool LO_B>
 hipError_t launch_dma(const _Float16* a_planes, const int32_t* a_exp, const _Float16* b_planes, const int32_t* b_exp,
                       const float* bias, float* out, _Float16* out_planes, int32_t* out_exp, uint32_t M, uint32_t Ncol, uint32_t K,
                       uint32_t splits, hipStream_t stream) {
-    hipLaunchKernelGGL((gemm_dma_kernel<EPI, LO_B>), dim3(dma_tiles(M, Ncol) * splits), dim3(kThreads), 0, stream, a_planes, a_exp,
-                       b_planes, b_exp, bias, out, out_planes, out_exp, M, rows_padded(M), Ncol, K, splits);
+    const dim3 grid(dma_tiles(M, Ncol) * splits), block(kThreads);
+    const uint32_t rows_pad = rows_padded(M);
+    if (M <= 64)
+        hipLaunchKernelGGL((gemm_dma_kernel<EPI, LO_B, 64>), grid, block, 0, stream, a_planes, a_exp, b_planes, b_exp, bias, out,
+                           out_planes, out_exp, M, rows_pad, Ncol, K, splits);
+    else if (M <= 128)
+        hipLaunchKernelGGL((gemm_dma_kernel<EPI, LO_B, 128>), grid, block, 0, stream, a_planes, a_exp, b_planes, b_exp, bias, out,
+                           out_planes, out_exp, M, rows_pad, Ncol, K, splits);
+    else
+        hipLaunchKernelGGL((gemm_dma_kernel<EPI, LO_B, kDmaBM>), grid, block, 0, stream, a_planes, a_exp, b_planes, b_exp, bias, out,
+                           out_planes, out_exp, M, rows_pad, Ncol, K, splits);
     return hipGetLastError();
 }
 
@@ -995,6 +1039,8 @@ Workspace workspace_layout(uint32_t m, uint32_t d, uint32_t h) {
 size_t dense_plane_halves(uint32_t rows, uint32_t k) { return static_cast<size_t>(rows) * k * 2; }
 
 bool mfma_shape_supported(uint32_t d, uint32_t h) { return d % 256 == 0 && h % 256 == 0; }
+
+bool mfma_streamed(uint32_t n, uint32_t d, uint32_t h) { return dma_up_splits(n, h, d) != 0 && dma_down_splits(n, d, h) != 0; }
 
 size_t mfma_workspace_bytes(uint32_t n, uint32_t d, uint32_t h) { return workspace_layout(n, d, h).bytes; }
 

@@ -31,8 +31,14 @@ from . import _lib
 UP_MODES = ("edges", "rows", "mfma")
 DOWN_MODES = ("edges", "rows", "mfma")
 EDGES_MAX_TOKENS = 32     # the policy's last N for the lane-per-slot shapes
-MFMA_MIN_TOKENS = 33      # the policy's first N for the tile-densified MFMA path
-MFMA_MIN_DENSITY = 0.05   # ... and the lowest support density it takes
+EDGES_PASS_TOKENS = 8     # tokens one pass of the lane-per-slot kernels takes
+MFMA_MIN_DENSITY = 0.05   # the lowest support density the tile-densified MFMA path takes
+# The policy's time estimates (µs per call), fitted to forced-pair timings of HFFNRuntime.forward on MI355X (layer
+# copies rotated so that every call reads HBM; the 70M/20 %, 410M/10 % and 50 % and 1.4B/20 % bf16 layers, N = 1-256):
+# one lane-per-slot pass costs EDGES_PASS_US + EDGES_SLOT_US per stored slot of both sides; the MFMA path costs
+# MFMA_BASE_US + MFMA_ENTRY_US per densified weight of both sides + MFMA_TOKEN_US per token up to 64.
+EDGES_PASS_US, EDGES_SLOT_US = 5.4, 2.93e-6
+MFMA_BASE_US, MFMA_ENTRY_US, MFMA_TOKEN_US = 22.0, 1.0e-6, 0.2
 MAX_TOKENS = 1 << 18      # runtime/gpu/nvidia/common/kernels/hffn_cuda/runtime.py:26
 
 _VALUE_TYPES = {torch.float32: _lib.VALUE_F32, torch.bfloat16: _lib.VALUE_BF16}
@@ -52,6 +58,24 @@ def down_mode(n: int, d_ff: int | None = None) -> str:
 
 def edges_supported(d_model: int, n: int) -> bool:
     return bool(_lib.load().hffn_edges_supported(d_model, n))
+
+
+def mfma_preferred(n: int, d_model: int, d_ff: int, slots: int) -> bool:
+    """Whether the MFMA path's estimated time beats the lane-per-slot passes' for N tokens (``slots``: stored slots of
+    both sides); above ``EDGES_MAX_TOKENS`` tokens it always does."""
+    if n > EDGES_MAX_TOKENS:
+        return True
+    edges = -(-n // EDGES_PASS_TOKENS) * (EDGES_PASS_US + EDGES_SLOT_US * slots)
+    mfma = MFMA_BASE_US + MFMA_ENTRY_US * 2 * d_model * d_ff + MFMA_TOKEN_US * min(n, 64)
+    return mfma < edges
+
+
+def mfma_streamed(n: int, d_model: int, d_ff: int) -> bool:
+    """Whether both MFMA projections of N tokens run on the streamed GEMM (``hffn_mfma_streamed``)."""
+    status = _lib.load().hffn_mfma_streamed(n, d_model, d_ff)
+    if status < 0:
+        _lib.check(status, "mfma_streamed")
+    return status == 1
 
 
 def leading_dim(n: int) -> int:
@@ -192,7 +216,8 @@ class HFFNRuntime:
                                *(tensors[name].data_ptr() for name in ("up_offsets", "up_idx", "up_val", "b_up",
                                                                        "out_offsets", "out_hidden", "out_val", "b_down"))))
             self._nnz.append((tensors["up_idx"].numel(), tensors["out_hidden"].numel()))
-        self.density = max(layer.up_idx.numel() + layer.out_hidden.numel() for layer in layers) / (2 * self.d_model * self.d_ff)
+        self._slots = max(layer.up_idx.numel() + layer.out_hidden.numel() for layer in layers)
+        self.density = self._slots / (2 * self.d_model * self.d_ff)
         self._planes: list[dict] | None = None
         self._stale: set[int] = set()   # layers whose values changed since their planes were built
         if dense and self._mfma_eligible():
@@ -282,7 +307,8 @@ class HFFNRuntime:
     def modes(self, n: int) -> tuple[str, str]:
         """The (up, down) shapes a call of N tokens takes (forced ones first)."""
         if self.forced_up is None and self.forced_down is None and self._planes is not None \
-                and n >= MFMA_MIN_TOKENS and self.density >= MFMA_MIN_DENSITY:
+                and self.density >= MFMA_MIN_DENSITY and mfma_preferred(n, self.d_model, self.d_ff, self._slots) \
+                and mfma_streamed(n, self.d_model, self.d_ff):
             return "mfma", "mfma"
         up = self.forced_up or up_mode(n, self.d_model)
         if up == "edges" and not edges_supported(self.d_model, n):

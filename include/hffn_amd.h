@@ -27,7 +27,7 @@
 extern "C" {
 #endif
 
-#define HFFN_ABI_VERSION 5
+#define HFFN_ABI_VERSION 6
 
 #define HFFN_OK 0
 #define HFFN_ERROR_ARGUMENT (-1) /* invalid shape, mode, pointer or workspace */
@@ -123,6 +123,12 @@ int hffn_output_major(int value_type, const int32_t* down_offsets, const int16_t
 
 /* 1 if the MFMA path takes this shape (d_model and d_ff multiples of 256), else 0 (host-only query). */
 int hffn_mfma_supported(uint32_t d_model, uint32_t d_ff);
+
+/* 1 if both projections of n tokens run on the streamed GEMM (256 x 128 tiles whose k-tiles are transferred straight
+ * into LDS, enough blocks with the k split to fill the chip), 0 if one of them falls back to the register-staged GEMM
+ * (narrow layers at small n); negative on an unsupported shape. Host-only query. No counterpart in the reference,
+ * whose policy (runtime.py:29-39) has no densified path; the runtime's policy takes the MFMA path only when this is 1. */
+int hffn_mfma_streamed(uint32_t n, uint32_t d_model, uint32_t d_ff);
 
 /* Bytes of the planes of a dense [rows, k] matrix (host-only query). */
 int hffn_dense_planes_bytes(uint32_t rows, uint32_t k, uint64_t* bytes);

@@ -13,8 +13,9 @@ pytestmark = pytest.mark.gpu
 SHAPES = {
     # Gather kernels only (d_model 64 has no MFMA tiling): prefill 2x16 and decode 2 tokens per call.
     "tiny": dict(num_hidden_layers=2, hidden_size=64, num_attention_heads=4, intermediate_size=256, vocab_size=500),
-    # MFMA prefill (2x64 tokens per call) and edges decode, 4 blocks of the Pythia layout at width 256.
-    "narrow": dict(num_hidden_layers=4, hidden_size=256, num_attention_heads=4, intermediate_size=1024, vocab_size=2000),
+    # MFMA prefill (2x64 tokens per call, on the streamed GEMM) and edges decode, 4 blocks of the Pythia layout at the
+    # 70M widths.
+    "narrow": dict(num_hidden_layers=4, hidden_size=512, num_attention_heads=8, intermediate_size=2048, vocab_size=2000),
 }
 
 

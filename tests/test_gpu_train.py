@@ -213,6 +213,7 @@ def test_inference_after_training_reads_the_updated_values(device):
     planes_before = runtime._planes[0]["up"].clone()
     for k in range(3):
         train.step(0, x, make_gy(case, n, k).to(device))
+    runtime.force("mfma", "mfma")  # a 256-wide layer takes the register-staged GEMM, which the policy leaves out
     y_mfma = runtime.forward(0, x).clone()
     assert runtime.calls["mfma", "mfma"] == 1
     assert not torch.equal(runtime._planes[0]["up"], planes_before)

@@ -91,6 +91,28 @@ def test_policy():
     assert [runtime.leading_dim(n) for n in (1, 2, 3, 4, 5, 8, 9, 2048, 2049)] == [4, 4, 4, 4, 8, 8, 16, 2048, 2056]
 
 
+def test_mfma_policy_crossovers():
+    """The estimated crossovers land where the forced-pair timings put them: the 410M/50 % layer takes the MFMA path
+    from its second lane-per-slot pass (9 tokens), the 1.4B/20 % layer from its third (17), the narrow 70M/20 % layer
+    only above 32 tokens, where it always does."""
+    def first(d, h, slots):
+        return next(n for n in range(1, 40) if runtime.mfma_preferred(n, d, h, slots))
+    assert first(1024, 4096, 2 * 4096 * 512) == 9
+    assert first(2048, 8192, 2 * 8192 * 410) == 17
+    assert first(512, 2048, 2 * 2048 * 102) == 33
+    assert runtime.mfma_preferred(33, 512, 2048, 1) and not runtime.mfma_preferred(32, 512, 2048, 1)
+
+
+def test_mfma_streamed_query():
+    """Both projections stream for the model shapes at every token count; a 256 x 1024 layer's up projection has too
+    few 128-column tiles below 512 tokens and falls back to the register-staged GEMM."""
+    for d, h in ((512, 2048), (1024, 4096), (2048, 8192), (2560, 10240)):
+        assert all(runtime.mfma_streamed(n, d, h) for n in (1, 64, 65, 128, 129, 256, 257, 2048, 4096))
+    assert not runtime.mfma_streamed(1, 256, 1024) and runtime.mfma_streamed(2048, 256, 1024)
+    with pytest.raises(ValueError, match="multiples of 256"):
+        runtime.mfma_streamed(1, 320, 1024)
+
+
 def test_runtime_refuses_other_devices():
     with pytest.raises(ValueError, match="cuda:0"):
         runtime.HFFNRuntime([], "cuda:1")
