@@ -34,12 +34,12 @@ EDGES_MAX_TOKENS = 32     # the policy's last N for the lane-per-slot shapes
 EDGES_PASS_TOKENS = 8     # tokens one pass of the lane-per-slot kernels takes
 MFMA_MIN_DENSITY = 0.05   # the lowest support density the tile-densified MFMA path takes
 # The policy's time estimates (µs per call), fitted to forced-pair timings of HFFNRuntime.forward on MI355X (layer
-# copies rotated so that every call reads HBM; the 70M/20 %, 410M/10 % and 50 % and 1.4B/20 % bf16 layers, N = 1-256):
-# one lane-per-slot pass costs EDGES_PASS_US + EDGES_SLOT_US per stored slot of both sides; the MFMA path costs
+# copies rotated so that every call reads HBM; the 70M/20 %, 410M/10 % and 50 % and 1.4B/20 % bf16 layers, N = 1-256).
+# Lane-per-slot kernels: EDGES_CALL_US per call, plus per pass of up to 8 tokens (EDGES_PASS_US + EDGES_SLOT_US per
+# stored slot of both sides) weighted by (1 + NT / 8) / 2 for a pass of NT = 1, 2, 4 or 8 tokens. MFMA path:
 # MFMA_BASE_US + MFMA_ENTRY_US per densified weight of both sides + MFMA_TOKEN_US per token up to 64.
-EDGES_PASS_US, EDGES_SLOT_US = 5.4, 2.93e-6
-MFMA_BASE_US, MFMA_ENTRY_US, MFMA_TOKEN_US = 22.0, 1.0e-6, 0.2
-MAX_TOKENS = 1 << 18      # runtime/gpu/nvidia/common/kernels/hffn_cuda/runtime.py:26
+EDGES_CALL_US, EDGES_PASS_US, EDGES_SLOT_US = 6.0, 4.0, 3.5e-6
+MFMA_BASE_US, MFMA_ENTRY_US, MFMA_TOKEN_US = 22.0, 0.93e-6, 0.1
 
 _VALUE_TYPES = {torch.float32: _lib.VALUE_F32, torch.bfloat16: _lib.VALUE_BF16}
 
@@ -61,11 +61,16 @@ def edges_supported(d_model: int, n: int) -> bool:
 
 
 def mfma_preferred(n: int, d_model: int, d_ff: int, slots: int) -> bool:
-    """Whether the MFMA path's estimated time beats the lane-per-slot passes' for N tokens (``slots``: stored slots of
+    """Whether the MFMA path's estimated time beats the lane-per-slot kernels' for N tokens (``slots``: stored slots of
     both sides); above ``EDGES_MAX_TOKENS`` tokens it always does."""
     if n > EDGES_MAX_TOKENS:
         return True
-    edges = -(-n // EDGES_PASS_TOKENS) * (EDGES_PASS_US + EDGES_SLOT_US * slots)
+    full = EDGES_PASS_US + EDGES_SLOT_US * slots
+    passes, rest = divmod(n, EDGES_PASS_TOKENS)
+    edges = EDGES_CALL_US + passes * full
+    if rest:
+        nt = 1 << (rest - 1).bit_length()  # the pass's token width: 1, 2, 4 or 8
+        edges += (1 + nt / EDGES_PASS_TOKENS) / 2 * full
     mfma = MFMA_BASE_US + MFMA_ENTRY_US * 2 * d_model * d_ff + MFMA_TOKEN_US * min(n, 64)
     return mfma < edges
 
@@ -222,6 +227,7 @@ class HFFNRuntime:
         self._stale: set[int] = set()   # layers whose values changed since their planes were built
         if dense and self._mfma_eligible():
             self._planes = [self._densify(tensors) for tensors in self._tensors]
+        self._policy: dict[int, tuple[str, str]] = {}  # N -> the policy's (up, down)
         self.forced_up: str | None = None
         self.forced_down: str | None = None
         self.calls: Counter = Counter()
@@ -305,7 +311,16 @@ class HFFNRuntime:
         return 4 * (self._x_t.numel() + self._act.numel() + self._y_t.numel() + self._y.numel() + self._mfma_work.numel())
 
     def modes(self, n: int) -> tuple[str, str]:
-        """The (up, down) shapes a call of N tokens takes (forced ones first)."""
+        """The (up, down) shapes a call of N tokens takes (forced ones first). The policy's choice depends on N and the
+        layers only, so it is worked out once per N (the library queries behind it are ctypes calls)."""
+        chosen = self._policy.get(n) if self.forced_up is None and self.forced_down is None else None
+        if chosen is None:
+            chosen = self._modes(n)
+            if self.forced_up is None and self.forced_down is None:
+                self._policy[n] = chosen
+        return chosen
+
+    def _modes(self, n: int) -> tuple[str, str]:
         if self.forced_up is None and self.forced_down is None and self._planes is not None \
                 and self.density >= MFMA_MIN_DENSITY and mfma_preferred(n, self.d_model, self.d_ff, self._slots) \
                 and mfma_streamed(n, self.d_model, self.d_ff):

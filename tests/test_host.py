@@ -93,13 +93,13 @@ def test_policy():
 
 def test_mfma_policy_crossovers():
     """The estimated crossovers land where the forced-pair timings put them: the 410M/50 % layer takes the MFMA path
-    from its second lane-per-slot pass (9 tokens), the 1.4B/20 % layer from its third (17), the narrow 70M/20 % layer
-    only above 32 tokens, where it always does."""
+    from 9 tokens (a second lane-per-slot pass), the 1.4B/20 % layer from 13, the narrow 70M/20 % layer from 29;
+    above 32 tokens always."""
     def first(d, h, slots):
         return next(n for n in range(1, 40) if runtime.mfma_preferred(n, d, h, slots))
     assert first(1024, 4096, 2 * 4096 * 512) == 9
-    assert first(2048, 8192, 2 * 8192 * 410) == 17
-    assert first(512, 2048, 2 * 2048 * 102) == 33
+    assert first(2048, 8192, 2 * 8192 * 410) == 13
+    assert first(512, 2048, 2 * 2048 * 102) == 29
     assert runtime.mfma_preferred(33, 512, 2048, 1) and not runtime.mfma_preferred(32, 512, 2048, 1)
 
 
