@@ -40,6 +40,7 @@ MFMA_MIN_DENSITY = 0.05   # the lowest support density the tile-densified MFMA p
 # MFMA_BASE_US + MFMA_ENTRY_US per densified weight of both sides + MFMA_TOKEN_US per token up to 64.
 EDGES_CALL_US, EDGES_PASS_US, EDGES_SLOT_US = 6.0, 4.0, 3.5e-6
 MFMA_BASE_US, MFMA_ENTRY_US, MFMA_TOKEN_US = 22.0, 0.93e-6, 0.1
+MAX_TOKENS = 1 << 18      # runtime/gpu/nvidia/common/kernels/hffn_cuda/runtime.py:26
 
 _VALUE_TYPES = {torch.float32: _lib.VALUE_F32, torch.bfloat16: _lib.VALUE_BF16}
 
