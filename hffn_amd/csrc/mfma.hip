@@ -62,41 +62,73 @@ __device__ __forceinline__ size_t plane_at(uint32_t rows, uint32_t row, uint32_t
 }
 
 // ------------------------------------------------------------------------------------------ input planes
-// X [M, K] fp32 -> planes of X [rows_pad, K] and e[row] = binade of max |x[row, :]| (rows past M: zeros, e = 0).
-// One wave per row: the row's largest |x|, then each lane splits 8 consecutive k per step (a 16-byte chunk per part;
-// the 4 rows of a block fill 64 contiguous bytes of each chunk run).
-constexpr uint32_t kSplitRows = kThreads / kWave;
+// X [M, K] fp32 -> planes of X [rows_pad, K] and e[row] = binade of max |x[row, :]| (rows M .. 8 * gridDim.x: zeros,
+// e = 0; K a multiple of 256). A block takes 8 rows; its wave w takes k in [w K/4, (w + 1) K/4) in steps of 64,
+// up to 4 steps (a chunk) at a time: in a step, lane l holds 8 consecutive k (piece l / 8) of row l % 8, so that the
+// 8 lanes of a row read 256 contiguous bytes of it and the 8 lanes of a piece write the 8 rows' 16 bytes of one
+// 128-byte run of the planes. First the row maxima (lanes, then the 4 waves through LDS), then the split; a wave
+// whose range is one chunk keeps its values in registers, longer ranges are read again (from L2).
+constexpr uint32_t kSplitBlockRows = 8;
+constexpr uint32_t kSplitChunk = 256;  // k per chunk: 4 steps of 64
 __global__ __launch_bounds__(kThreads) void split_rows_kernel(const float* __restrict__ x, uint32_t M, uint32_t rows_pad,
                                                              uint32_t K, _Float16* __restrict__ planes, int32_t* __restrict__ e) {
-    const uint32_t lane = threadIdx.x % kWave, row = blockIdx.x * kSplitRows + threadIdx.x / kWave;
-    const float* p = x + static_cast<size_t>(row) * K;
+    constexpr uint32_t kWaves = kThreads / kWave;
+    __shared__ uint32_t part[kWaves][kSplitBlockRows];
+    const uint32_t lane = threadIdx.x % kWave, wave = uniform(threadIdx.x / kWave);
+    const uint32_t r = lane % kSplitBlockRows, piece = lane / kSplitBlockRows;
+    const uint32_t row = blockIdx.x * kSplitBlockRows + r;
+    const uint32_t span = K / kWaves, k_begin = wave * span, k_end = k_begin + span;
+    const float* src = x + static_cast<size_t>(row) * K;
+    const bool real = row < M;
+    float v[4][8];
+    const auto load_chunk = [&](uint32_t k0) {
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            float4 a = make_float4(0.f, 0.f, 0.f, 0.f), b = a;
+            if (real && k0 + 64 * i < k_end) {
+                const float* q = src + k0 + 64 * i + 8 * piece;
+                a = *reinterpret_cast<const float4*>(q);
+                b = *reinterpret_cast<const float4*>(q + 4);
+            }
+            v[i][0] = a.x; v[i][1] = a.y; v[i][2] = a.z; v[i][3] = a.w;
+            v[i][4] = b.x; v[i][5] = b.y; v[i][6] = b.z; v[i][7] = b.w;
+        }
+    };
     uint32_t m = 0;
-    if (row < M)
-        for (uint32_t c = lane * 4; c < K; c += kWave * 4) {
-            const float4 u = *reinterpret_cast<const float4*>(p + c);
-            m = max(max(m, max(abs_bits(u.x), abs_bits(u.y))), max(abs_bits(u.z), abs_bits(u.w)));
-        }
+    for (uint32_t k0 = k_begin; k0 < k_end; k0 += kSplitChunk) {
+        load_chunk(k0);
 #pragma unroll
-    for (int s = 32; s >= 1; s >>= 1) m = max(m, static_cast<uint32_t>(__shfl_xor(static_cast<int>(m), s, kWave)));
-    const int be = binade_of_bits(m);
-    if (lane == 0) e[row] = be;
+        for (int i = 0; i < 4; ++i)
+#pragma unroll
+            for (int q = 0; q < 8; ++q) m = max(m, abs_bits(v[i][q]));
+    }
+#pragma unroll
+    for (int s = kSplitBlockRows; s < kWave; s <<= 1) m = max(m, static_cast<uint32_t>(__shfl_xor(static_cast<int>(m), s, kWave)));
+    if (piece == 0) part[wave][r] = m;
+    __syncthreads();
+    uint32_t mx = part[0][r];
+#pragma unroll
+    for (uint32_t w = 1; w < kWaves; ++w) mx = max(mx, part[w][r]);
+    const int be = binade_of_bits(mx);
+    if (wave == 0 && piece == 0) e[row] = be;
     const float scale = ldexpf(1.0f, -be);
-    for (uint32_t q = lane; q < K / 8; q += kWave) {
-        float v[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
-        if (row < M) {
-            const float4 u = *reinterpret_cast<const float4*>(p + q * 8), w = *reinterpret_cast<const float4*>(p + q * 8 + 4);
-            v[0] = u.x; v[1] = u.y; v[2] = u.z; v[3] = u.w; v[4] = w.x; v[5] = w.y; v[6] = w.z; v[7] = w.w;
-        }
-        half8 h, l;
+    for (uint32_t k0 = k_begin; k0 < k_end; k0 += kSplitChunk) {
+        if (span > kSplitChunk) load_chunk(k0);  // one chunk: still in registers
 #pragma unroll
-        for (int i = 0; i < 8; ++i) {
-            _Float16 hh, ll;
-            split(v[i] * scale, hh, ll);
-            h[i] = hh;
-            l[i] = ll;
+        for (int i = 0; i < 4; ++i) {
+            if (k0 + 64 * i >= k_end) break;
+            half8 h, l;
+#pragma unroll
+            for (int q = 0; q < 8; ++q) {
+                _Float16 hh, ll;
+                split(v[i][q] * scale, hh, ll);
+                h[q] = hh;
+                l[q] = ll;
+            }
+            const uint32_t k = k0 + 64 * i + 8 * piece;
+            *reinterpret_cast<half8*>(planes + plane_at(rows_pad, row, k, 0)) = h;
+            *reinterpret_cast<half8*>(planes + plane_at(rows_pad, row, k, 1)) = l;
         }
-        *reinterpret_cast<half8*>(planes + plane_at(rows_pad, row, q * 8, 0)) = h;
-        *reinterpret_cast<half8*>(planes + plane_at(rows_pad, row, q * 8, 1)) = l;
     }
 }
 
@@ -883,6 +915,11 @@ constexpr int kMaxSplits = 4;
 
 uint32_t rows_padded(uint32_t m) { return ceil_div(m, kRowPad) * kRowPad; }
 
+// Rows of the token and activation planes that a call of m tokens reads: one row tile of at most 64 or 128 tokens
+// runs the live-row GEMMs (gemm_dma_kernel<..., 64 or 128>), which read only its first 64 or 128 rows; otherwise every
+// padded row. The split and activation-plane passes write these rows only.
+uint32_t rows_live(uint32_t m) { return m <= 64 ? 64 : m <= 128 ? 128 : rows_padded(m); }
+
 // Up: 128 x 128 blocks (the column tile is the activation block). Down: 64 x 128 blocks without a k split; K is
 // split only when a down projection has fewer than 64 blocks (the fixup's device-scope fences write back the L2).
 Shape up_shape(uint32_t, uint32_t) { return {2, 2, 1}; }
@@ -970,11 +1007,11 @@ hipError_t launch_dma(const _Float16* a_planes, const int32_t* a_exp, const _Flo
                       const float* bias, float* out, _Float16* out_planes, int32_t* out_exp, uint32_t M, uint32_t Ncol, uint32_t K,
                       uint32_t splits, hipStream_t stream) {
     const dim3 grid(dma_tiles(M, Ncol) * splits), block(kThreads);
-    const uint32_t rows_pad = rows_padded(M);
-    if (M <= 64)
+    const uint32_t rows_pad = rows_padded(M), live = rows_live(M);
+    if (live == 64)
         hipLaunchKernelGGL((gemm_dma_kernel<EPI, LO_B, 64>), grid, block, 0, stream, a_planes, a_exp, b_planes, b_exp, bias, out,
                            out_planes, out_exp, M, rows_pad, Ncol, K, splits);
-    else if (M <= 128)
+    else if (live == 128)
         hipLaunchKernelGGL((gemm_dma_kernel<EPI, LO_B, 128>), grid, block, 0, stream, a_planes, a_exp, b_planes, b_exp, bias, out,
                            out_planes, out_exp, M, rows_pad, Ncol, K, splits);
     else
@@ -1062,8 +1099,8 @@ hipError_t launch_mfma_up(int vt, const float* x, const void* planes, const int3
     char* bytes = static_cast<char*>(workspace);
     auto* x_planes = reinterpret_cast<_Float16*>(bytes + w.x_planes);
     auto* act_planes = reinterpret_cast<_Float16*>(bytes + w.act_planes);
-    hipLaunchKernelGGL(split_rows_kernel, dim3(rows_padded(n) / kSplitRows), dim3(kThreads), 0, stream, x, n, rows_padded(n), d,
-                       x_planes, words + w.x_binades);  // one wave per padded row
+    hipLaunchKernelGGL(split_rows_kernel, dim3(rows_live(n) / kSplitBlockRows), dim3(kThreads), 0, stream, x, n, rows_padded(n), d,
+                       x_planes, words + w.x_binades);  // 8 rows per block
     if (hipError_t status = hipGetLastError(); status != hipSuccess) return status;
     const auto* p = static_cast<const _Float16*>(planes);
     if (const uint32_t splits = dma_up_splits(n, h, d); splits > 1) {
@@ -1074,7 +1111,7 @@ hipError_t launch_mfma_up(int vt, const float* x, const void* planes, const int3
                         : launch_dma<Epi::UpSplit, true>(x_planes, words + w.x_binades, p, w_exp, nullptr, partials, nullptr, nullptr, n,
                                                          h, d, splits, stream);
         if (status != hipSuccess) return status;
-        hipLaunchKernelGGL(act_planes_kernel, dim3(rows_padded(n) / kActRowsPerBlock, h / kActBlock), dim3(kThreads), 0, stream, partials,
+        hipLaunchKernelGGL(act_planes_kernel, dim3(rows_live(n) / kActRowsPerBlock, h / kActBlock), dim3(kThreads), 0, stream, partials,
                            splits, b_up, act_planes, words + w.act_binades, n, rows_padded(n), h);
         return hipGetLastError();
     }
