@@ -16,9 +16,15 @@
 // A block's tile of B rows is 8 runs of B * 16 contiguous bytes, and LDS keeps the same order, so the MFMA operand
 // reads (32 lanes on 32 consecutive rows of one chunk) and the staging writes touch consecutive 16-byte blocks: no
 // LDS bank conflicts, no padding. Token planes have a row count padded to kRowPad (rows past N are zeros in X and
-// hold gelu(b_up) in A; their outputs are never stored).
+// hold gelu(b_up) in A; their outputs are never stored); a call of at most 64 or 128 tokens writes and reads only
+// the first 64 or 128 rows (rows_live).
 //
-// GEMM blocks: 4 waves in 2 x 2, each wave a (32 MI) x (32 NI) tile of 32x32 MFMA accumulators; the k loop stages
+// Two GEMM kernels: the streamed one (gemm_dma_kernel: 256 x 128 tiles whose k-tiles go from global memory straight
+// into LDS, K split 2-32 ways when the tiles alone leave CUs idle, partials added by separate passes) takes every
+// shape whose tiles and splits give enough blocks; the register-staged one below (gemm_planes_kernel) remains for
+// narrower layers at small N.
+//
+// Register-staged GEMM blocks: 4 waves in 2 x 2, each wave a (32 MI) x (32 NI) tile of 32x32 MFMA accumulators; the k loop stages
 // 32-wide k-tiles of both planes through double-buffered LDS with plain 16-byte copies (one barrier per k-tile, the
 // next tile's global loads in flight during the current tile's MFMAs). The grid is one-dimensional and remapped so
 // that each of the 8 XCDs works on one compact group of output tiles (its L2 then holds the A rows and B columns
@@ -1037,7 +1043,8 @@ hipError_t dma_down(uint32_t splits, const _Float16* a_planes, const int32_t* a_
 // Workspace layout (int32 words unless stated; rows = M padded to kRowPad): split counters [down tiles of the
 // largest token count, 64 x 64 tiles] | x binades [rows] | activation block binades [rows, d_ff / kActBlock] |
 // (256-byte aligned, bytes) x planes [rows * d_model * 2 halves] | activation planes [rows * d_ff * 2 halves] |
-// float partials [4, M, d_model]. The counters come first and are sized for every M and tile shape, so a call at
+// float partials (partial_floats: the largest [splits, M, d_model] or [splits, M, d_ff] of any N up to M). The counters
+// come first and are sized for every M and tile shape, so a call at
 // any M finds them where the previous call, at any other M, left them (at zero).
 struct Workspace {
     size_t counters, x_binades, act_binades, x_planes, act_planes, partials, bytes;
