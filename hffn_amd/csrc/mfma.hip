@@ -55,6 +55,16 @@ __device__ __forceinline__ int binade_of_bits(uint32_t bits) {
     return bits == 0 ? 0 : static_cast<int>((bits >> 23) & 0xff) - 127;
 }
 
+// Power of two of an activation block (a token's kActBlock neurons): the binade of its largest |v| rounded up to a
+// multiple of kActBinadeStep. The block's largest value scaled still lies below 2, and the planes' resolution (2^-24
+// after scaling, fp16's smallest subnormal) stays within 2^-21 of it; neighbouring blocks of a token then mostly
+// share their power of two, and the down GEMM has nothing to rescale between them.
+constexpr int kActBinadeStep = 4;
+__device__ __forceinline__ int act_binade(uint32_t bits) {
+    const int e = binade_of_bits(bits);
+    return e >= 0 ? (e + kActBinadeStep - 1) / kActBinadeStep * kActBinadeStep : -(-e / kActBinadeStep * kActBinadeStep);
+}
+
 __device__ __forceinline__ uint32_t abs_bits(float v) { return __float_as_uint(v) & 0x7fffffffu; }
 
 __device__ __forceinline__ void split(float v, _Float16& hi, _Float16& lo) {
@@ -393,7 +403,7 @@ __global__ __launch_bounds__(kThreads) void gemm_planes_kernel(
         }
         __syncthreads();
         if (tid < BM) {
-            const int e = binade_of_bits(max(row_max[0][tid], row_max[1][tid]));
+            const int e = act_binade(max(row_max[0][tid], row_max[1][tid]));
             row_e[1][tid] = e;
             out_exp[static_cast<size_t>(m0 + tid) * tiles_n + tile.n] = e;
         }
@@ -516,6 +526,7 @@ __global__ __launch_bounds__(kThreads) void gemm_planes_kernel(
 constexpr int kDmaStages = 3;
 constexpr int kDmaBM = 256, kDmaBN = 128;
 constexpr uint32_t kDmaMaxActBlocks = 40;  // activation blocks of one down split held in LDS (int8 binades)
+static_assert(kDmaMaxActBlocks <= 64, "one bit per activation block of a split in two 32-bit masks");
 
 // s_waitcnt vmcnt(N) lgkmcnt(0): at most N vector-memory loads of this wave still in flight, its LDS accesses done.
 template <int N>
@@ -570,6 +581,7 @@ __global__ __launch_bounds__(kThreads) void gemm_dma_kernel(
     __shared__ __attribute__((aligned(16))) _Float16 smem[S * kStage];
     __shared__ int32_t e_row[1][BM];  // Up: x binades
     __shared__ __attribute__((aligned(4))) int8_t e_tab[EPI == Epi::Down ? kDmaMaxActBlocks : 1][EPI == Epi::Down ? BM : 1];  // Down: [block][row]
+    __shared__ uint32_t change_masks[EPI == Epi::Down ? kThreads / kWave : 1][2];
 
     const uint32_t tid = threadIdx.x, lane = tid % kWave, wave = uniform(tid / kWave);
     const uint32_t wm = wave / 2, wn = wave % 2;
@@ -594,8 +606,30 @@ __global__ __launch_bounds__(kThreads) void gemm_dma_kernel(
             for (uint32_t q = 0; q < 8; ++q)
                 if (b0 + q < blocks) e_tab[b0 + q][tid] = static_cast<int8_t>(v[q]);
         }
+        // bit b of `changes`: this row's power of two differs between activation blocks b - 1 and b of the split;
+        // ORed over the wave, then over the block through LDS
+        uint32_t changes[2] = {0, 0};
+        for (uint32_t b = 1; b < blocks; ++b)
+            if (e_tab[b][tid] != e_tab[b - 1][tid]) changes[b / 32] |= 1u << (b % 32);
+#pragma unroll
+        for (int h = 0; h < 2; ++h) {
+#pragma unroll
+            for (int off = 32; off >= 1; off >>= 1)
+                changes[h] |= static_cast<uint32_t>(__shfl_xor(static_cast<int>(changes[h]), off, kWave));
+            if (lane == 0) change_masks[wave][h] = changes[h];
+        }
     }
     __syncthreads();
+    uint32_t changed[2] = {0, 0};  // Down: activation blocks at whose start some row of the tile changes its power of two
+    if constexpr (EPI == Epi::Down) {
+#pragma unroll
+        for (int h = 0; h < 2; ++h) {
+            uint32_t c = 0;
+#pragma unroll
+            for (int w = 0; w < kThreads / kWave; ++w) c |= change_masks[w][h];
+            changed[h] = uniform(c);
+        }
+    }
 
     // piece q of stage kt into ring slot `slot`: wave w copies runs of 64 rows (1 KB each) of A (pieces below
     // kLoadsA), then of B
@@ -701,8 +735,8 @@ __global__ __launch_bounds__(kThreads) void gemm_dma_kernel(
     // registers 4g .. 4g + 3 hold 4 consecutive rows, so one 4-byte read per block and group
     const auto rescale = [&](uint32_t kt) {
         if constexpr (EPI == Epi::Down) {
-            if (kt % kKtPerActBlock == 0 && kt != k_begin && live) {
-                const uint32_t kb = kt / kKtPerActBlock - kb0;
+            const uint32_t kb = kt / kKtPerActBlock - kb0;
+            if (kt % kKtPerActBlock == 0 && kt != k_begin && live && ((changed[kb / 32] >> (kb % 32)) & 1)) {
 #pragma unroll
                 for (int i = 0; i < MIL; ++i)
 #pragma unroll
@@ -777,7 +811,7 @@ __global__ __launch_bounds__(kThreads) void gemm_dma_kernel(
             const float4 v = *reinterpret_cast<const float4*>(row_v + c);
             largest = max(largest, max(max(abs_bits(v.x), abs_bits(v.y)), max(abs_bits(v.z), abs_bits(v.w))));
         }
-        const int e = binade_of_bits(largest);
+        const int e = act_binade(largest);
         out_exp[static_cast<size_t>(m0 + tid) * tiles_n + tile.n] = e;
         const float scale = ldexpf(1.0f, -e);
 #pragma unroll 4
@@ -896,7 +930,7 @@ __global__ __launch_bounds__(kThreads) void act_planes_kernel(const float* __res
     }
 #pragma unroll
     for (int off = 8; off >= 1; off >>= 1) largest = max(largest, static_cast<uint32_t>(__shfl_xor(static_cast<int>(largest), off, kWave)));
-    const int e = binade_of_bits(largest);
+    const int e = act_binade(largest);
     if (sub == 0) exps[static_cast<size_t>(m) * (H / kActBlock) + nb] = e;
     const float scale = ldexpf(1.0f, -e);
     half8 hi, lo;
