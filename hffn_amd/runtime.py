@@ -10,10 +10,11 @@ Kernel shapes (the build's own policy, ``up_mode``/``down_mode``):
 
 * ``edges`` - lanes over a row's slots, tokens in registers, input staged in LDS; decode-sized N (N <= 32).
 * ``rows``  - lanes over tokens (1, 2 or 4 per lane), slots walked in order; larger N on layers without the MFMA path.
-* ``mfma``  - tile-densified split-fp16 MFMA GEMMs (up and down together); N >= 33 on layers that qualify.
+* ``mfma``  - tile-densified split-fp16 MFMA GEMMs (up and down together) on layers that qualify, from the N where
+  its estimated time beats the ``edges`` passes' (``mfma_preferred``; always above 32 tokens).
 
-On the Pythia-410M layer at 50 % (12 rotating copies, MI355X), per call: N = 1: edges 17.7 us, mfma 91.6, rows 187;
-N = 32: edges 104, mfma 107; N = 64: mfma 111, rows 187, edges 194; N = 2048: mfma 179 us.
+On the Pythia-410M layer at 50 % (12 rotating copies, MI355X), per call: N = 1: edges 20.4 us, mfma 30.4, rows 189;
+N = 16: mfma 35.5, edges 41.7; N = 64: mfma 42.8, rows 190, edges 144; N = 2048: mfma 140 us.
 
 Model arrays stay on the device. Work buffers are dense, shared by all layers, sized for the largest N seen and
 reused. Kernels are queued on PyTorch's current stream of the device, so they run in call order with the PyTorch
@@ -196,8 +197,8 @@ class HFFNRuntime:
     """``HFFNRuntime`` of ``runtime/gpu/nvidia/common/kernels/hffn_cuda/runtime.py:76-163`` on the HIP library."""
 
     def __init__(self, layers: list[HFFNLayer], device: str | torch.device = "cuda", dense: bool = True) -> None:
-        """``dense``: also build the densified planes of the MFMA path when the layers qualify (shape a multiple of
-        64, distinct sorted indices per row); without them every call takes the gather kernels."""
+        """``dense``: also build the densified planes of the MFMA path when the layers qualify (``d_model`` and
+        ``d_ff`` multiples of 256, distinct sorted indices per row); without them every call takes the gather kernels."""
         self.device = _device(device)
         self.layers = layers
         self.d_model, self.d_ff = layers[0].d_model, layers[0].d_ff
