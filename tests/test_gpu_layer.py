@@ -235,6 +235,20 @@ def test_410m_store_bitwise(w410m):
     _bitwise_store(layer, compact)
 
 
+def test_live_row_gemms_equal_the_full_tile(w410m, device):
+    """One row tile of at most 64 or 128 tokens runs GEMMs that transfer and multiply only those rows. Up to 256 tokens
+    the row tiles, hence the k splits, are the same, so the first 64 (100) tokens of a 200-token call (full tile) and
+    a call on those tokens alone (live rows) are the same products in the same order: bitwise equal."""
+    compact, workload, layer = w410m
+    runtime = HFFNRuntime([layer], device)
+    runtime.force("mfma", "mfma")
+    x = torch.from_numpy(synth.make_input(workload, 200)).to(device)
+    full = runtime.forward(0, x).clone()
+    for n in (1, 17, 64, 65, 100, 128):
+        part = runtime.forward(0, x[:n].contiguous())
+        assert torch.equal(part, full[:n]), n
+
+
 @pytest.mark.parametrize("n", [1, 4, 8, 16, 32, 2048])
 def test_410m_relative_error(n, w410m, device):
     """Pythia-410M shape, 50 % density, fp32: max |y - y64| / max(1, |y64|) <= 1e-5 for every kernel pair."""
