@@ -10,7 +10,7 @@ import ctypes
 from pathlib import Path
 
 LIBRARY = Path(__file__).resolve().with_name("libhffn_amd.so")
-ABI_VERSION = 6
+ABI_VERSION = 7
 
 OK = 0
 VALUE_F32, VALUE_BF16 = 0, 1
@@ -48,6 +48,7 @@ SIGNATURES = {
     "hffn_mfma_up": [_I, _P, _P, _P, _P, _P, _U64, _U32, _U32, _U32, _P],
     "hffn_mfma_down": [_I, _P, _P, _P, _P, _P, _U64, _U32, _U32, _U32, _P],
     "hffn_forward_mfma": [_I] + [_P] * 8 + [_U64, _P] + [_U32] * 3 + [_P],
+    "hffn_forward_gemv": [_I] + [_P] * 9 + [_U32] * 3 + [_P],
 }
 
 

@@ -354,6 +354,27 @@ int hffn_forward_mfma(int value_type, const float* x, const void* up_planes, con
     return hffn_mfma_down(value_type, down_planes, down_binades, b_down, y, workspace, workspace_bytes, d_model, d_ff, n, stream);
 }
 
+namespace {
+int check_gemv(int value_type, uint32_t d_model, uint32_t d_ff, uint32_t n) {
+    if (int status = check_mfma(value_type, d_model, d_ff, n)) return status;
+    if (n > hffn::kGemvMaxTokens) return fail(HFFN_ERROR_ARGUMENT, "gemv path: n=%u above %u tokens", n, hffn::kGemvMaxTokens);
+    return HFFN_OK;
+}
+}  // namespace
+
+int hffn_forward_gemv(int value_type, const float* x, const void* up_planes, const int32_t* up_binades, const float* b_up,
+                      const void* down_planes, const int32_t* down_binades, const float* b_down, float* act, float* y,
+                      uint32_t d_model, uint32_t d_ff, uint32_t n, void* stream) {
+    if (int status = check_gemv(value_type, d_model, d_ff, n)) return status;
+    if (!x || !up_planes || !up_binades || !b_up || !down_planes || !down_binades || !b_down || !act || !y)
+        return fail(HFFN_ERROR_ARGUMENT, "forward_gemv: null pointer");
+    if (reinterpret_cast<uintptr_t>(x) % 16 != 0 || reinterpret_cast<uintptr_t>(act) % 16 != 0)
+        return fail(HFFN_ERROR_ARGUMENT, "forward_gemv: x and act must be 16-byte aligned");
+    return launched(hffn::launch_gemv_forward(value_type, x, up_planes, up_binades, b_up, down_planes, down_binades, b_down, act, y,
+                                              d_model, d_ff, n, static_cast<hipStream_t>(stream)),
+                    "forward (gemv)");
+}
+
 // ----------------------------------------------------------------------------------------------------- training
 
 int hffn_forward_z(int up_mode, int down_mode, const float* x, const int32_t* up_offsets, const int16_t* up_idx, const float* up_val,

@@ -1,0 +1,158 @@
+// Decode-sized projections over the densified planes (gfx950, wave64): both projections of the layer for 1-32 tokens
+// on v_mfma_f32_16x16x32_f16, one kernel per projection and no workspace. A decode call is bound by reading the
+// weights once; the MFMA units deliver the operands, so the cost per token stays small (an fp32 FMA GEMV spends its
+// time feeding every lane the inputs of every token).
+//
+// Planes as the MFMA path keeps them (mfma.hip): planes[(((kt*2 + p)*4 + c)*rows + r)*8 + k % 8], kt = k / 32,
+// c = (k % 32) / 8, p = 0 hi / 1 lo, one power of two per row. A block takes 16 rows (neurons) over the whole K; its
+// W waves (8, or 16 when the row tiles alone leave CUs idle) split K in W spans of whole 32-k tiles. Per tile, lane
+// (r, c) = (lane % 16, lane / 16) holds row r's chunk c of both planes as the B operand (the 16 lanes of a chunk read
+// 256 contiguous bytes), and the 8 inputs of token r at the same k as the A operand, scaled by the token's power of
+// two over the tile and split into fp16 hi and lo: D[token, row] = x_hi w_hi + x_hi w_lo + x_lo w_hi (x_hi w_hi +
+// x_lo w_hi for bf16 weights, exact in the hi plane), accumulated in fp32 with the token's power of two undone
+// exactly. The waves' sums are added in wave order, then the row's power of two is undone; every output is written by
+// one thread, the sums do not depend on the other tokens of the call, and the bits repeat run to run.
+//
+// Up: act[t, r] = gelu(b_up[r] + sum_k W_up[r, k] x[t, k]) (token-major act); down: y[t, o] = b_down[o] +
+// sum_r W_down[o, r] act[t, r].
+#include "common.hpp"
+#include "launch.hpp"
+
+namespace hffn {
+namespace {
+
+typedef _Float16 half8 __attribute__((ext_vector_type(8)));
+typedef float floatx4 __attribute__((ext_vector_type(4)));
+
+constexpr uint32_t kGemvRows = 16;   // rows per block: one MFMA column tile
+constexpr uint32_t kGemvTile = 16;   // tokens per MFMA row tile
+constexpr uint32_t kGemvK = 32;      // k per MFMA, one plane k-tile
+constexpr uint32_t kGemvMinBlocks = 256;  // below this many row tiles a block takes 16 waves instead of 8
+
+// floor(log2(m)) of a non-negative float given by its bits; 0 for zero.
+__device__ __forceinline__ int gemv_binade(uint32_t bits) { return bits == 0 ? 0 : static_cast<int>((bits >> 23) & 0xff) - 127; }
+
+template <int W, int TT, bool LO_B, bool UP>
+__global__ __launch_bounds__(W* kWave) void gemv_mfma_kernel(const float* __restrict__ in,        // [n, K]
+                                                                 const _Float16* __restrict__ planes,  // [K/32][8][rows][8]
+                                                                 const int32_t* __restrict__ exps,     // [rows]
+                                                                 const float* __restrict__ bias,       // [rows]
+                                                                 float* __restrict__ out,              // [n, rows]
+                                                                 uint32_t rows, uint32_t K, uint32_t n) {
+    constexpr uint32_t kTokens = TT * kGemvTile;
+    constexpr uint32_t kThreads = W * kWave;
+    constexpr uint32_t kChunk = W >= 16 ? 8 / (2 * TT) : 8;  // k-tiles whose loads are issued together (VGPR budget)
+    __shared__ float sums[W][kTokens][kGemvRows];
+    const uint32_t lane = threadIdx.x % kWave, wave = uniform(threadIdx.x / kWave);
+    const uint32_t r = lane % 16, c = lane / 16;
+    const uint32_t row = blockIdx.x * kGemvRows + r;  // < rows: the grid covers rows exactly (rows % 16 == 0)
+    const uint32_t tiles = K / kGemvK / W, kt0 = wave * tiles;  // K % (32 W) == 0
+    const size_t run = static_cast<size_t>(rows) * 8;  // halves between consecutive runs
+    const _Float16* wbase = planes + static_cast<size_t>(c) * run + static_cast<size_t>(row) * 8;
+    floatx4 acc[TT];
+#pragma unroll
+    for (int tt = 0; tt < TT; ++tt) acc[tt] = floatx4{0.0f, 0.0f, 0.0f, 0.0f};
+    for (uint32_t j0 = 0; j0 < tiles; j0 += kChunk) {
+        const uint32_t count = min(tiles - j0, kChunk);
+        half8 wh[kChunk], wl[kChunk];
+        float v[kChunk][TT][8];
+#pragma unroll
+        for (uint32_t j = 0; j < kChunk; ++j) {
+            if (j >= count) break;
+            const _Float16* p = wbase + static_cast<size_t>(kt0 + j0 + j) * 8 * run;
+            wh[j] = *reinterpret_cast<const half8*>(p);
+            if constexpr (LO_B) wl[j] = *reinterpret_cast<const half8*>(p + 4 * run);
+        }
+#pragma unroll
+        for (uint32_t j = 0; j < kChunk; ++j) {
+            if (j >= count) break;
+            const uint32_t k = (kt0 + j0 + j) * kGemvK + c * 8;
+#pragma unroll
+            for (int tt = 0; tt < TT; ++tt) {
+                const uint32_t t = tt * kGemvTile + r;
+                if (t < n) load_vec<8>(in + static_cast<size_t>(t) * K + k, v[j][tt]);
+                else {
+#pragma unroll
+                    for (int i = 0; i < 8; ++i) v[j][tt][i] = 0.0f;
+                }
+            }
+        }
+#pragma unroll
+        for (uint32_t j = 0; j < kChunk; ++j) {
+            if (j >= count) break;
+#pragma unroll
+            for (int tt = 0; tt < TT; ++tt) {
+                // the token's power of two over this 32-k tile: its 32 inputs sit in lanes r, r + 16, r + 32, r + 48
+                uint32_t m = 0;
+#pragma unroll
+                for (int i = 0; i < 8; ++i) m = max(m, __float_as_uint(v[j][tt][i]) & 0x7fffffffu);
+                m = max(m, static_cast<uint32_t>(__shfl_xor(static_cast<int>(m), 16, kWave)));
+                m = max(m, static_cast<uint32_t>(__shfl_xor(static_cast<int>(m), 32, kWave)));
+                const int e = gemv_binade(m);
+                const float scale = ldexpf(1.0f, -e);
+                half8 xh, xl;
+#pragma unroll
+                for (int i = 0; i < 8; ++i) {
+                    const float s = v[j][tt][i] * scale;
+                    const _Float16 h = static_cast<_Float16>(s);
+                    xh[i] = h;
+                    xl[i] = static_cast<_Float16>(s - static_cast<float>(h));
+                }
+                floatx4 d = __builtin_amdgcn_mfma_f32_16x16x32_f16(xh, wh[j], floatx4{0.0f, 0.0f, 0.0f, 0.0f}, 0, 0, 0);
+                if constexpr (LO_B) d = __builtin_amdgcn_mfma_f32_16x16x32_f16(xh, wl[j], d, 0, 0, 0);
+                d = __builtin_amdgcn_mfma_f32_16x16x32_f16(xl, wh[j], d, 0, 0, 0);
+                // D register i holds token 4c + i: undo that token's power of two (held by lane 4c + i) exactly
+#pragma unroll
+                for (int i = 0; i < 4; ++i) acc[tt][i] += ldexpf(d[i], __shfl(e, static_cast<int>(4 * c + i), kWave));
+            }
+        }
+    }
+    // D register i of token tile tt: token tt*16 + 4c + i, row r
+#pragma unroll
+    for (int tt = 0; tt < TT; ++tt)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) sums[wave][tt * kGemvTile + 4 * c + i][r] = acc[tt][i];
+    __syncthreads();
+    for (uint32_t o = threadIdx.x; o < kTokens * kGemvRows; o += kThreads) {
+        const uint32_t t = o / kGemvRows, rr = o % kGemvRows, out_row = blockIdx.x * kGemvRows + rr;
+        if (t >= n) break;
+        float s = sums[0][t][rr];
+#pragma unroll
+        for (uint32_t w = 1; w < W; ++w) s += sums[w][t][rr];
+        const float z = ldexpf(s, exps[out_row]) + bias[out_row];
+        out[static_cast<size_t>(t) * rows + out_row] = UP ? gelu(z) : z;
+    }
+}
+
+template <int W, bool LO_B, bool UP>
+void gemv_launch(const float* in, const _Float16* planes, const int32_t* exps, const float* bias, float* out, uint32_t rows, uint32_t K,
+                 uint32_t n, hipStream_t stream) {
+    const dim3 grid(rows / kGemvRows), block(W * kWave);
+    if (n <= kGemvTile) hipLaunchKernelGGL((gemv_mfma_kernel<W, 1, LO_B, UP>), grid, block, 0, stream, in, planes, exps, bias, out, rows, K, n);
+    else hipLaunchKernelGGL((gemv_mfma_kernel<W, 2, LO_B, UP>), grid, block, 0, stream, in, planes, exps, bias, out, rows, K, n);
+}
+
+// 8 waves per block; 16 (more loads in flight per CU) when the row tiles alone leave CUs idle and K has a 32-k tile
+// for each of them.
+template <bool LO_B, bool UP>
+hipError_t gemv_side(const float* in, const void* planes, const int32_t* exps, const float* bias, float* out, uint32_t rows,
+                     uint32_t K, uint32_t n, hipStream_t stream) {
+    const auto* p = static_cast<const _Float16*>(planes);
+    if (rows / kGemvRows < kGemvMinBlocks && K % (16 * kGemvK) == 0) gemv_launch<16, LO_B, UP>(in, p, exps, bias, out, rows, K, n, stream);
+    else gemv_launch<8, LO_B, UP>(in, p, exps, bias, out, rows, K, n, stream);
+    return hipGetLastError();
+}
+
+}  // namespace
+
+hipError_t launch_gemv_forward(int vt, const float* x, const void* up_planes, const int32_t* up_exps, const float* b_up,
+                               const void* down_planes, const int32_t* down_exps, const float* b_down, float* act, float* y,
+                               uint32_t d, uint32_t h, uint32_t n, hipStream_t stream) {
+    const hipError_t status = vt == kBF16 ? gemv_side<false, true>(x, up_planes, up_exps, b_up, act, h, d, n, stream)
+                                          : gemv_side<true, true>(x, up_planes, up_exps, b_up, act, h, d, n, stream);
+    if (status != hipSuccess) return status;
+    return vt == kBF16 ? gemv_side<false, false>(act, down_planes, down_exps, b_down, y, d, h, n, stream)
+                       : gemv_side<true, false>(act, down_planes, down_exps, b_down, y, d, h, n, stream);
+}
+
+}  // namespace hffn

@@ -89,4 +89,11 @@ hipError_t launch_mfma_up(int vt, const float* x, const void* planes, const int3
 hipError_t launch_mfma_down(int vt, const void* planes, const int32_t* v_exp, const float* b_down, float* y, void* workspace,
                             uint32_t n, uint32_t d, uint32_t h, hipStream_t stream);
 
+// Decode-sized projections over the same planes (gemv.hip): act token-major [n, h] (16-byte aligned), y token-major
+// [n, d]; no workspace.
+constexpr uint32_t kGemvMaxTokens = 32;
+hipError_t launch_gemv_forward(int vt, const float* x, const void* up_planes, const int32_t* up_exps, const float* b_up,
+                               const void* down_planes, const int32_t* down_exps, const float* b_down, float* act, float* y,
+                               uint32_t d, uint32_t h, uint32_t n, hipStream_t stream);
+
 }  // namespace hffn

@@ -4,7 +4,8 @@
 For one input, the runtime runs with its policy and with each forced (up, down) kernel pair. Criteria: two
 consecutive calls on the same input give the same bits; ``max |y - y64|`` and ``max |y - y64| / max(1, |y64|)`` are
 reported for the caller to compare with its tolerance. The pairs are the policy, the four gather pairs (edges or
-rows up, edges or rows down) and, when the runtime holds densified planes, the MFMA path.
+rows up, edges or rows down) and, when the runtime holds densified planes, the MFMA path and (up to 32 tokens) the
+decode GEMVs.
 """
 from __future__ import annotations
 
@@ -12,10 +13,10 @@ from dataclasses import dataclass
 
 import torch
 
-from .runtime import HFFNRuntime
+from .runtime import GEMV_MAX_TOKENS, HFFNRuntime
 
 GATHER = ("edges", "rows")
-PAIRS = [(None, None)] + [(up, down) for up in GATHER for down in GATHER] + [("mfma", "mfma")]
+PAIRS = [(None, None)] + [(up, down) for up in GATHER for down in GATHER] + [("mfma", "mfma"), ("gemv", "gemv")]
 
 
 @dataclass
@@ -32,7 +33,9 @@ def check(runtime: HFFNRuntime, index: int, x: torch.Tensor, expected: torch.Ten
     result = Parity(0.0, 0.0, True, {})
     try:
         for up, down in pairs:
-            if up == "mfma" and not runtime.mfma_available:
+            if up in ("mfma", "gemv") and not runtime.mfma_available:
+                continue
+            if up == "gemv" and x.shape[0] > GEMV_MAX_TOKENS:
                 continue
             runtime.force(up, down)
             y = runtime.forward(index, x).clone()

@@ -5,8 +5,8 @@ A gather-mode call (every decode step, and small prefills: the ``edges`` and ``r
 N tokens launches from a *plan* that the library builds once per (index, N): every argument of the forward but
 ``x`` and the stream is checked and stored on the library side (``hffn_plan_forward``), so a call is one ctypes call
 with three arguments (``hffn_plan_launch``) instead of the full argument list and its checks. The kernels, modes,
-work buffers, results and the ``calls`` counter are those of ``HFFNRuntime``; MFMA-path calls (large N) run the
-control's ``forward``.
+work buffers, results and the ``calls`` counter are those of ``HFFNRuntime``; calls on the planes paths (``mfma``,
+``gemv``: one ABI call each already) run the control's ``forward``.
 
 Baked device pointers: the eight arrays of the layer (never reassigned, kept alive by the runtime) and the work
 buffers; ``_reserve`` (which reallocates the buffers) and ``force`` release every plan, as the reference drops its

@@ -10,11 +10,15 @@ Kernel shapes (the build's own policy, ``up_mode``/``down_mode``):
 
 * ``edges`` - lanes over a row's slots, tokens in registers, input staged in LDS; decode-sized N (N <= 32).
 * ``rows``  - lanes over tokens (1, 2 or 4 per lane), slots walked in order; larger N on layers without the MFMA path.
-* ``mfma``  - tile-densified split-fp16 MFMA GEMMs (up and down together) on layers that qualify, from the N where
-  its estimated time beats the ``edges`` passes' (``mfma_preferred``; always above 32 tokens).
+* ``mfma``  - tile-densified split-fp16 MFMA GEMMs (up and down together) on layers that qualify (``d_model`` and
+  ``d_ff`` multiples of 256, density at least ``MFMA_MIN_DENSITY``); always above 32 tokens.
+* ``gemv``  - decode GEMVs over the same planes (up and down together, 1-32 tokens): one kernel per projection on
+  16x16x32 MFMAs, the planes read once as whole lines.
 
-On the Pythia-410M layer at 50 % (12 rotating copies, MI355X), per call: N = 1: edges 20.4 us, mfma 30.4, rows 189;
-N = 16: mfma 35.5, edges 41.7; N = 64: mfma 42.8, rows 190, edges 144; N = 2048: mfma 140 us.
+Up to 32 tokens the policy takes whichever of ``edges``, ``gemv`` and ``mfma`` has the least estimated time
+(``planes_mode``). On the Pythia-410M layer at 50 % (12 rotating copies, MI355X), per call: N = 1: edges 13.7 us,
+gemv 17.5, mfma 28.5; N = 8: gemv 19.7, edges 23.8, mfma 29.8; N = 16: gemv 23.5, mfma 31.2, edges 41.5; N = 32:
+mfma 33.1, gemv 33.1; N = 2048: mfma 140 us.
 
 Model arrays stay on the device. Work buffers are dense, shared by all layers, sized for the largest N seen and
 reused. Kernels are queued on PyTorch's current stream of the device, so they run in call order with the PyTorch
@@ -29,8 +33,10 @@ import torch
 
 from . import _lib
 
-UP_MODES = ("edges", "rows", "mfma")
-DOWN_MODES = ("edges", "rows", "mfma")
+UP_MODES = ("edges", "rows", "mfma", "gemv")
+DOWN_MODES = ("edges", "rows", "mfma", "gemv")
+PAIR_MODES = ("mfma", "gemv")  # the planes paths: up and down run together
+GEMV_MAX_TOKENS = 32      # the planes GEMVs' largest call
 EDGES_MAX_TOKENS = 32     # the policy's last N for the lane-per-slot shapes
 EDGES_PASS_TOKENS = 8     # tokens one pass of the lane-per-slot kernels takes
 MFMA_MIN_DENSITY = 0.05   # the lowest support density the tile-densified MFMA path takes
@@ -41,6 +47,10 @@ MFMA_MIN_DENSITY = 0.05   # the lowest support density the tile-densified MFMA p
 # MFMA_BASE_US + MFMA_ENTRY_US per densified weight of both sides + MFMA_TOKEN_US per token up to 64.
 EDGES_CALL_US, EDGES_PASS_US, EDGES_SLOT_US = 6.0, 4.0, 3.5e-6
 MFMA_BASE_US, MFMA_ENTRY_US, MFMA_TOKEN_US = 22.0, 0.93e-6, 0.1
+# Decode GEMVs (N <= 32): GEMV_BASE_US + per MB of planes (both sides) GEMV_MB_US, plus GEMV_TOKEN_MB_US per token up to
+# 16 and GEMV_TILE2_MB_US per token beyond (the second 16-token MFMA tile); fitted to the 70M/20 %, 410M/50 %,
+# 1.4B/20 % bf16 and 2.8B/80 % bf16 layers, N = 1-32.
+GEMV_BASE_US, GEMV_MB_US, GEMV_TOKEN_MB_US, GEMV_TILE2_MB_US = 9.0, 0.324, 0.012, 0.02
 MAX_TOKENS = 1 << 18      # runtime/gpu/nvidia/common/kernels/hffn_cuda/runtime.py:26
 
 _VALUE_TYPES = {torch.float32: _lib.VALUE_F32, torch.bfloat16: _lib.VALUE_BF16}
@@ -62,19 +72,46 @@ def edges_supported(d_model: int, n: int) -> bool:
     return bool(_lib.load().hffn_edges_supported(d_model, n))
 
 
-def mfma_preferred(n: int, d_model: int, d_ff: int, slots: int) -> bool:
-    """Whether the MFMA path's estimated time beats the lane-per-slot kernels' for N tokens (``slots``: stored slots of
-    both sides); above ``EDGES_MAX_TOKENS`` tokens it always does."""
-    if n > EDGES_MAX_TOKENS:
-        return True
+def edges_us(n: int, slots: int) -> float:
+    """Estimated µs of a call on the lane-per-slot kernels (``slots``: stored slots of both sides)."""
     full = EDGES_PASS_US + EDGES_SLOT_US * slots
     passes, rest = divmod(n, EDGES_PASS_TOKENS)
     edges = EDGES_CALL_US + passes * full
     if rest:
         nt = 1 << (rest - 1).bit_length()  # the pass's token width: 1, 2, 4 or 8
         edges += (1 + nt / EDGES_PASS_TOKENS) / 2 * full
-    mfma = MFMA_BASE_US + MFMA_ENTRY_US * 2 * d_model * d_ff + MFMA_TOKEN_US * min(n, 64)
-    return mfma < edges
+    return edges
+
+
+def mfma_us(n: int, d_model: int, d_ff: int) -> float:
+    """Estimated µs of a call on the MFMA GEMMs."""
+    return MFMA_BASE_US + MFMA_ENTRY_US * 2 * d_model * d_ff + MFMA_TOKEN_US * min(n, 64)
+
+
+def gemv_us(n: int, d_model: int, d_ff: int, plane_bytes: int) -> float:
+    """Estimated µs of a call on the decode GEMVs (``plane_bytes``: bytes per densified weight, 4 for fp32 weights
+    and 2 for bf16)."""
+    mb = 2 * d_model * d_ff * plane_bytes / 1e6
+    return GEMV_BASE_US + mb * (GEMV_MB_US + GEMV_TOKEN_MB_US * (min(n, 16) - 1) + GEMV_TILE2_MB_US * max(n - 16, 0))
+
+
+def mfma_preferred(n: int, d_model: int, d_ff: int, slots: int) -> bool:
+    """Whether the MFMA path's estimated time beats the lane-per-slot kernels' for N tokens (``slots``: stored slots of
+    both sides); above ``EDGES_MAX_TOKENS`` tokens it always does."""
+    return n > EDGES_MAX_TOKENS or mfma_us(n, d_model, d_ff) < edges_us(n, slots)
+
+
+def planes_mode(n: int, d_model: int, d_ff: int, slots: int, plane_bytes: int, streamed: bool) -> str | None:
+    """The planes path (``gemv`` or ``mfma``) of least estimated time for N tokens when it beats the lane-per-slot
+    kernels, else None. Above ``EDGES_MAX_TOKENS`` tokens the MFMA path is taken whenever its GEMMs are streamed
+    (``streamed``), as in ``mfma_preferred``."""
+    options = {}
+    if n <= EDGES_MAX_TOKENS:
+        options[None] = edges_us(n, slots)
+        options["gemv"] = gemv_us(n, d_model, d_ff, plane_bytes)
+    if streamed:
+        options["mfma"] = mfma_us(n, d_model, d_ff) if n <= EDGES_MAX_TOKENS else 0.0
+    return min(options, key=options.get) if options else None
 
 
 def mfma_streamed(n: int, d_model: int, d_ff: int) -> bool:
@@ -283,16 +320,17 @@ class HFFNRuntime:
         return sum(t.numel() * t.element_size() for planes in self._planes for t in planes.values())
 
     def force(self, up: str | None, down: str | None) -> None:
-        """Diagnostic: fix the up and/or the down kernel regardless of N (None: the policy). The MFMA path runs up and
-        down together (its activations stay in its own workspace as fp16 planes): ``mfma`` is forced as a pair."""
+        """Diagnostic: fix the up and/or the down kernel regardless of N (None: the policy). The planes paths run up and
+        down together: ``mfma`` and ``gemv`` are forced as pairs (``gemv`` serves 1-32 tokens)."""
         if up not in (None, *UP_MODES) or down not in (None, *DOWN_MODES):
             raise ValueError("unknown kernel mode")
         if up == "edges" and not edges_supported(self.d_model, 1):
             raise ValueError("the edges up shape cannot stage this d_model")
-        if (up == "mfma") != (down == "mfma"):
-            raise ValueError("the mfma path runs up and down together: force ('mfma', 'mfma')")
-        if up == "mfma" and self._planes is None:
-            raise ValueError("the mfma path is not available for these layers")
+        for pair in PAIR_MODES:
+            if (up == pair) != (down == pair):
+                raise ValueError(f"the {pair} path runs up and down together: force ('{pair}', '{pair}')")
+        if up in PAIR_MODES and self._planes is None:
+            raise ValueError(f"the {up} path is not available for these layers")
         self.forced_up, self.forced_down = up, down
 
     def _reserve(self, n: int) -> None:
@@ -324,9 +362,12 @@ class HFFNRuntime:
 
     def _modes(self, n: int) -> tuple[str, str]:
         if self.forced_up is None and self.forced_down is None and self._planes is not None \
-                and self.density >= MFMA_MIN_DENSITY and mfma_preferred(n, self.d_model, self.d_ff, self._slots) \
-                and mfma_streamed(n, self.d_model, self.d_ff):
-            return "mfma", "mfma"
+                and self.density >= MFMA_MIN_DENSITY:
+            plane_bytes = 2 if self._args[0][0] == _lib.VALUE_BF16 else 4
+            mode = planes_mode(n, self.d_model, self.d_ff, self._slots, plane_bytes,
+                               mfma_streamed(n, self.d_model, self.d_ff))
+            if mode is not None:
+                return mode, mode
         up = self.forced_up or up_mode(n, self.d_model)
         if up == "edges" and not edges_supported(self.d_model, n):
             up = "rows"
@@ -353,12 +394,19 @@ class HFFNRuntime:
         value_type, *model = self._args[index]
         x_t, act, y_t, y = self._work
         stream = torch.cuda.current_stream(self.device).cuda_stream
-        if up == "mfma":
-            x = _aligned(x)  # the MFMA path reads x 16 bytes at a time
+        if up in PAIR_MODES:
+            x = _aligned(x)  # the planes paths read x 16 bytes at a time
             if index in self._stale:
                 self._densify(self._tensors[index], self._planes[index])
                 self._stale.discard(index)
             planes, tensors = self._planes[index], self._tensors[index]
+            if up == "gemv":
+                _lib.check(self._lib.hffn_forward_gemv(value_type, x.data_ptr(), planes["up"].data_ptr(),
+                                                       planes["up_binades"].data_ptr(), tensors["b_up"].data_ptr(),
+                                                       planes["down"].data_ptr(), planes["down_binades"].data_ptr(),
+                                                       tensors["b_down"].data_ptr(), act, y, self.d_model, self.d_ff, n,
+                                                       stream), "forward (gemv, gemv)")
+                return
             _lib.check(self._lib.hffn_forward_mfma(value_type, x.data_ptr(), planes["up"].data_ptr(),
                                                    planes["up_binades"].data_ptr(), tensors["b_up"].data_ptr(),
                                                    planes["down"].data_ptr(), planes["down_binades"].data_ptr(),

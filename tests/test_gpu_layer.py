@@ -16,7 +16,7 @@ import torch
 
 from hffn_amd import parity, synth
 from hffn_amd.ffn import hip_layer
-from hffn_amd.runtime import MAX_TOKENS, HFFNLayer, HFFNRuntime
+from hffn_amd.runtime import GEMV_MAX_TOKENS, MAX_TOKENS, HFFNLayer, HFFNRuntime
 from oracle import reference, transpose
 
 pytestmark = pytest.mark.gpu
@@ -112,7 +112,8 @@ def test_forced_pairs_match_the_oracle(name, test_layers, device):
         result = parity.check(runtime, 0, torch.from_numpy(x_np).to(device), expected)
         assert result.repeatable, f"{name} N{n}: bits differ on repeat"
         assert result.error <= ATOL, f"{name} N{n}: {result.pairs}"
-    assert sum(runtime.calls.values()) == 2 * len(BATCHES) * len(parity.PAIRS)
+    gemv_skipped = sum(n > GEMV_MAX_TOKENS for n in BATCHES)  # the decode GEMVs take at most 32 tokens
+    assert sum(runtime.calls.values()) == 2 * (len(BATCHES) * len(parity.PAIRS) - gemv_skipped)
 
 
 def test_shared_buffers_between_calls(test_layers, device):
@@ -172,6 +173,30 @@ def test_token_result_does_not_depend_on_the_batch(up, down, test_layers, device
             assert torch.equal(runtime.forward(0, x[start:start + size].contiguous()), part)
         else:
             assert torch.equal(part, whole[start:start + size])
+
+
+@pytest.mark.parametrize("name", ["homog_512_2048", "irreg_512_2048"])
+def test_gemv_token_result_does_not_depend_on_the_batch(name, test_layers, device):
+    """The decode GEMVs scale each token by its own power of two per 32-k tile and sum its products in a fixed order,
+    whatever the other tokens (one or two 16-token MFMA tiles): a token's result is bit-identical alone and in any
+    batch of up to 32 tokens."""
+    compact, case, layer = test_layers[name]
+    runtime = HFFNRuntime([layer], device)
+    runtime.force("gemv", "gemv")
+    x = torch.from_numpy(synth.make_input(case, 32)).to(device)
+    whole = runtime.forward(0, x).clone()
+    for start, size in ((0, 1), (7, 5), (3, 16), (16, 16), (5, 17), (31, 1)):
+        assert torch.equal(runtime.forward(0, x[start:start + size].contiguous()), whole[start:start + size]), (start, size)
+    expected = reference.forward(compact, x.cpu().numpy())
+    assert _relative(whole, expected) <= 1e-5
+
+
+def test_gemv_refuses_more_than_32_tokens(test_layers, device):
+    compact, case, layer = test_layers["homog_512_2048"]
+    runtime = HFFNRuntime([layer], device)
+    runtime.force("gemv", "gemv")
+    with pytest.raises(ValueError, match="above 32"):
+        runtime.forward(0, torch.from_numpy(synth.make_input(case, 33)).to(device))
 
 
 def test_mfma_workspace_reused_at_shrinking_token_counts(test_layers, device):

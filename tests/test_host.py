@@ -66,6 +66,10 @@ def test_abi_refuses_bad_shapes_before_launching():
     _expect_argument_error(lib.hffn_forward_mfma(0, p, p, p, p, p, p, p, p, small, p, 1024, 4096, 2048, None), "workspace")
     _expect_argument_error(lib.hffn_mfma_up(0, p, p, p, p, p, 1 << 40, 1024, 4000, 2048, None), "multiples")
     _expect_argument_error(lib.hffn_mfma_up(0, ctypes.c_void_p(20), p, p, p, p, 1 << 40, 1024, 4096, 2048, None), "aligned")
+    _expect_argument_error(lib.hffn_forward_gemv(0, p, p, p, p, p, p, p, p, p, 1024, 4096, 33, None), "above 32")
+    _expect_argument_error(lib.hffn_forward_gemv(0, p, p, p, p, p, p, p, p, p, 1024, 4000, 8, None), "multiples")
+    _expect_argument_error(lib.hffn_forward_gemv(0, ctypes.c_void_p(20), p, p, p, p, p, p, p, p, 1024, 4096, 8, None), "aligned")
+    _expect_argument_error(lib.hffn_forward_gemv(0, p, p, p, p, p, p, p, None, p, 1024, 4096, 8, None), "null")
     needed = ctypes.c_uint64(0)
     assert lib.hffn_output_major_workspace(2_097_152, 1024, ctypes.byref(needed)) == _lib.OK
     assert needed.value == 1024 * 1024 * 4
@@ -101,6 +105,20 @@ def test_mfma_policy_crossovers():
     assert first(2048, 8192, 2 * 8192 * 410) == 13
     assert first(512, 2048, 2 * 2048 * 102) == 29
     assert runtime.mfma_preferred(33, 512, 2048, 1) and not runtime.mfma_preferred(32, 512, 2048, 1)
+
+
+def test_planes_policy():
+    """Three-way estimate up to 32 tokens: on the Pythia-410M layer at 50 % the lane-per-slot kernels at one token,
+    the decode GEMVs at 8 and 16, the MFMA path above 32 (when its GEMMs are streamed); on a dense bf16 layer the
+    GEMVs from one token."""
+    slots = 2 * 4096 * 512
+    assert runtime.planes_mode(1, 1024, 4096, slots, 4, True) is None
+    assert runtime.planes_mode(8, 1024, 4096, slots, 4, True) == "gemv"
+    assert runtime.planes_mode(16, 1024, 4096, slots, 4, True) == "gemv"
+    assert runtime.planes_mode(33, 1024, 4096, slots, 4, True) == "mfma"
+    assert runtime.planes_mode(33, 1024, 4096, slots, 4, False) is None
+    assert runtime.planes_mode(1, 2560, 10240, 2 * 10240 * 2048, 2, True) == "gemv"
+    assert runtime.gemv_us(16, 1024, 4096, 2) < runtime.gemv_us(16, 1024, 4096, 4)
 
 
 def test_mfma_streamed_query():
