@@ -48,7 +48,8 @@ SIGNATURES = {
     "hffn_mfma_up": [_I, _P, _P, _P, _P, _P, _U64, _U32, _U32, _U32, _P],
     "hffn_mfma_down": [_I, _P, _P, _P, _P, _P, _U64, _U32, _U32, _U32, _P],
     "hffn_forward_mfma": [_I] + [_P] * 8 + [_U64, _P] + [_U32] * 3 + [_P],
-    "hffn_forward_gemv": [_I] + [_P] * 9 + [_U32] * 3 + [_P],
+    "hffn_gemv_workspace": [_U32, _U32, _P],
+    "hffn_forward_gemv": [_I] + [_P] * 9 + [_U64, _P] + [_U32] * 3 + [_P],
 }
 
 

@@ -362,16 +362,27 @@ int check_gemv(int value_type, uint32_t d_model, uint32_t d_ff, uint32_t n) {
 }
 }  // namespace
 
+int hffn_gemv_workspace(uint32_t d_model, uint32_t d_ff, uint64_t* bytes) {
+    if (!bytes) return fail(HFFN_ERROR_ARGUMENT, "gemv_workspace: null result");
+    if (int status = check_gemv(HFFN_VALUE_F32, d_model, d_ff, 1)) return status;
+    *bytes = hffn::gemv_workspace_bytes(d_model, d_ff);
+    return HFFN_OK;
+}
+
 int hffn_forward_gemv(int value_type, const float* x, const void* up_planes, const int32_t* up_binades, const float* b_up,
-                      const void* down_planes, const int32_t* down_binades, const float* b_down, float* act, float* y,
-                      uint32_t d_model, uint32_t d_ff, uint32_t n, void* stream) {
+                      const void* down_planes, const int32_t* down_binades, const float* b_down, float* act, void* workspace,
+                      uint64_t workspace_bytes, float* y, uint32_t d_model, uint32_t d_ff, uint32_t n, void* stream) {
     if (int status = check_gemv(value_type, d_model, d_ff, n)) return status;
-    if (!x || !up_planes || !up_binades || !b_up || !down_planes || !down_binades || !b_down || !act || !y)
+    if (!x || !up_planes || !up_binades || !b_up || !down_planes || !down_binades || !b_down || !act || !workspace || !y)
         return fail(HFFN_ERROR_ARGUMENT, "forward_gemv: null pointer");
     if (reinterpret_cast<uintptr_t>(x) % 16 != 0 || reinterpret_cast<uintptr_t>(act) % 16 != 0)
         return fail(HFFN_ERROR_ARGUMENT, "forward_gemv: x and act must be 16-byte aligned");
-    return launched(hffn::launch_gemv_forward(value_type, x, up_planes, up_binades, b_up, down_planes, down_binades, b_down, act, y,
-                                              d_model, d_ff, n, static_cast<hipStream_t>(stream)),
+    const uint64_t needed = hffn::gemv_workspace_bytes(d_model, d_ff);
+    if (workspace_bytes < needed)
+        return fail(HFFN_ERROR_ARGUMENT, "forward_gemv: workspace of %llu bytes, %llu needed",
+                    static_cast<unsigned long long>(workspace_bytes), static_cast<unsigned long long>(needed));
+    return launched(hffn::launch_gemv_forward(value_type, x, up_planes, up_binades, b_up, down_planes, down_binades, b_down, act,
+                                              static_cast<float*>(workspace), y, d_model, d_ff, n, static_cast<hipStream_t>(stream)),
                     "forward (gemv)");
 }
 

@@ -15,6 +15,8 @@
 //
 // Up: act[t, r] = gelu(b_up[r] + sum_k W_up[r, k] x[t, k]) (token-major act); down: y[t, o] = b_down[o] +
 // sum_r W_down[o, r] act[t, r].
+#include <algorithm>
+
 #include "common.hpp"
 #include "launch.hpp"
 
@@ -38,6 +40,7 @@ __global__ __launch_bounds__(W* kWave) void gemv_mfma_kernel(const float* __rest
                                                                  const int32_t* __restrict__ exps,     // [rows]
                                                                  const float* __restrict__ bias,       // [rows]
                                                                  float* __restrict__ out,              // [n, rows]
+                                                                 float* __restrict__ partials,  // [splits, n, rows] when split
                                                                  uint32_t rows, uint32_t K, uint32_t n) {
     constexpr uint32_t kTokens = TT * kGemvTile;
     constexpr uint32_t kThreads = W * kWave;
@@ -46,7 +49,8 @@ __global__ __launch_bounds__(W* kWave) void gemv_mfma_kernel(const float* __rest
     const uint32_t lane = threadIdx.x % kWave, wave = uniform(threadIdx.x / kWave);
     const uint32_t r = lane % 16, c = lane / 16;
     const uint32_t row = blockIdx.x * kGemvRows + r;  // < rows: the grid covers rows exactly (rows % 16 == 0)
-    const uint32_t tiles = K / kGemvK / W, kt0 = wave * tiles;  // K % (32 W) == 0
+    const uint32_t splits = gridDim.y;  // k splits of the row tile (blockIdx.y); K % (32 W splits) == 0
+    const uint32_t tiles = K / kGemvK / W / splits, kt0 = (blockIdx.y * W + wave) * tiles;
     const size_t run = static_cast<size_t>(rows) * 8;  // halves between consecutive runs
     const _Float16* wbase = planes + static_cast<size_t>(c) * run + static_cast<size_t>(row) * 8;
     floatx4 acc[TT];
@@ -119,40 +123,88 @@ __global__ __launch_bounds__(W* kWave) void gemv_mfma_kernel(const float* __rest
         float s = sums[0][t][rr];
 #pragma unroll
         for (uint32_t w = 1; w < W; ++w) s += sums[w][t][rr];
-        const float z = ldexpf(s, exps[out_row]) + bias[out_row];
-        out[static_cast<size_t>(t) * rows + out_row] = UP ? gelu(z) : z;
+        if (splits > 1) {
+            partials[(static_cast<size_t>(blockIdx.y) * n + t) * rows + out_row] = s;
+        } else {
+            const float z = ldexpf(s, exps[out_row]) + bias[out_row];
+            out[static_cast<size_t>(t) * rows + out_row] = UP ? gelu(z) : z;
+        }
     }
 }
 
-template <int W, bool LO_B, bool UP>
-void gemv_launch(const float* in, const _Float16* planes, const int32_t* exps, const float* bias, float* out, uint32_t rows, uint32_t K,
-                 uint32_t n, hipStream_t stream) {
-    const dim3 grid(rows / kGemvRows), block(W * kWave);
-    if (n <= kGemvTile) hipLaunchKernelGGL((gemv_mfma_kernel<W, 1, LO_B, UP>), grid, block, 0, stream, in, planes, exps, bias, out, rows, K, n);
-    else hipLaunchKernelGGL((gemv_mfma_kernel<W, 2, LO_B, UP>), grid, block, 0, stream, in, planes, exps, bias, out, rows, K, n);
+// out[t, r] = epilogue(sum of the k splits' partials in split order); one thread per output.
+template <bool UP>
+__global__ __launch_bounds__(256) void gemv_reduce_kernel(const float* __restrict__ partials, uint32_t splits,
+                                                          const int32_t* __restrict__ exps, const float* __restrict__ bias,
+                                                          float* __restrict__ out, uint32_t rows, uint32_t n) {
+    const uint32_t o = blockIdx.x * 256 + threadIdx.x;
+    if (o >= n * rows) return;
+    const uint32_t row = o % rows;
+    const size_t stride = static_cast<size_t>(n) * rows;
+    float s = partials[o];
+    for (uint32_t k = 1; k < splits; ++k) s += partials[k * stride + o];
+    const float z = ldexpf(s, exps[row]) + bias[row];
+    out[o] = UP ? gelu(z) : z;
 }
 
-// 8 waves per block; 16 (more loads in flight per CU) when the row tiles alone leave CUs idle and K has a 32-k tile
-// for each of them.
+// k splits of a projection whose row tiles alone leave CUs idle: the most (up to 8) that still fit one round of
+// kGemvMinBlocks blocks of 8 waves, each wave keeping at least one 32-k tile; none for a side of less than
+// kGemvSplitBytes of planes, where the second kernel costs more than the split gains.
+constexpr size_t kGemvSplitBytes = size_t(8) << 20;
+uint32_t gemv_splits(uint32_t rows, uint32_t K, uint32_t weight_bytes) {
+    constexpr uint32_t kMaxSplits = 8;
+    if (static_cast<size_t>(rows) * K * weight_bytes < kGemvSplitBytes) return 1;
+    uint32_t splits = 1;
+    while (splits < kMaxSplits && rows / kGemvRows * splits * 2 <= kGemvMinBlocks && K % (2 * splits * 8 * kGemvK) == 0) splits *= 2;
+    return splits;
+}
+
+template <int W, bool LO_B, bool UP>
+void gemv_launch(const float* in, const _Float16* planes, const int32_t* exps, const float* bias, float* out, float* partials,
+                 uint32_t splits, uint32_t rows, uint32_t K, uint32_t n, hipStream_t stream) {
+    const dim3 grid(rows / kGemvRows, splits), block(W * kWave);
+    if (n <= kGemvTile)
+        hipLaunchKernelGGL((gemv_mfma_kernel<W, 1, LO_B, UP>), grid, block, 0, stream, in, planes, exps, bias, out, partials, rows, K, n);
+    else
+        hipLaunchKernelGGL((gemv_mfma_kernel<W, 2, LO_B, UP>), grid, block, 0, stream, in, planes, exps, bias, out, partials, rows, K, n);
+}
+
+// 8 waves per block, with k splits (added by gemv_reduce_kernel) where gemv_splits finds them worth a second kernel;
+// else 16 waves per block when the row tiles alone leave CUs idle.
 template <bool LO_B, bool UP>
-hipError_t gemv_side(const float* in, const void* planes, const int32_t* exps, const float* bias, float* out, uint32_t rows,
-                     uint32_t K, uint32_t n, hipStream_t stream) {
+hipError_t gemv_side(const float* in, const void* planes, const int32_t* exps, const float* bias, float* out, float* partials,
+                     uint32_t rows, uint32_t K, uint32_t n, hipStream_t stream) {
     const auto* p = static_cast<const _Float16*>(planes);
-    if (rows / kGemvRows < kGemvMinBlocks && K % (16 * kGemvK) == 0) gemv_launch<16, LO_B, UP>(in, p, exps, bias, out, rows, K, n, stream);
-    else gemv_launch<8, LO_B, UP>(in, p, exps, bias, out, rows, K, n, stream);
+    const uint32_t splits = gemv_splits(rows, K, LO_B ? 4 : 2);
+    if (splits > 1) {
+        gemv_launch<8, LO_B, UP>(in, p, exps, bias, out, partials, splits, rows, K, n, stream);
+        if (hipError_t status = hipGetLastError(); status != hipSuccess) return status;
+        hipLaunchKernelGGL(gemv_reduce_kernel<UP>, dim3((n * rows + 255) / 256), dim3(256), 0, stream, partials, splits, exps, bias, out,
+                           rows, n);
+    } else if (rows / kGemvRows < kGemvMinBlocks && K % (16 * kGemvK) == 0) {
+        gemv_launch<16, LO_B, UP>(in, p, exps, bias, out, partials, 1, rows, K, n, stream);
+    } else {
+        gemv_launch<8, LO_B, UP>(in, p, exps, bias, out, partials, 1, rows, K, n, stream);
+    }
     return hipGetLastError();
 }
 
 }  // namespace
 
+size_t gemv_workspace_bytes(uint32_t d, uint32_t h) {
+    const size_t up = gemv_splits(h, d, 4), down = gemv_splits(d, h, 4);  // fp32 weights split at least as often
+    const size_t floats = std::max(up > 1 ? up * kGemvMaxTokens * h : 0, down > 1 ? down * kGemvMaxTokens * d : 0);
+    return std::max<size_t>(floats * sizeof(float), 256);
+}
+
 hipError_t launch_gemv_forward(int vt, const float* x, const void* up_planes, const int32_t* up_exps, const float* b_up,
-                               const void* down_planes, const int32_t* down_exps, const float* b_down, float* act, float* y,
-                               uint32_t d, uint32_t h, uint32_t n, hipStream_t stream) {
-    const hipError_t status = vt == kBF16 ? gemv_side<false, true>(x, up_planes, up_exps, b_up, act, h, d, n, stream)
-                                          : gemv_side<true, true>(x, up_planes, up_exps, b_up, act, h, d, n, stream);
+                               const void* down_planes, const int32_t* down_exps, const float* b_down, float* act, float* work,
+                               float* y, uint32_t d, uint32_t h, uint32_t n, hipStream_t stream) {
+    const hipError_t status = vt == kBF16 ? gemv_side<false, true>(x, up_planes, up_exps, b_up, act, work, h, d, n, stream)
+                                          : gemv_side<true, true>(x, up_planes, up_exps, b_up, act, work, h, d, n, stream);
     if (status != hipSuccess) return status;
-    return vt == kBF16 ? gemv_side<false, false>(act, down_planes, down_exps, b_down, y, d, h, n, stream)
-                       : gemv_side<true, false>(act, down_planes, down_exps, b_down, y, d, h, n, stream);
+    return vt == kBF16 ? gemv_side<false, false>(act, down_planes, down_exps, b_down, y, work, d, h, n, stream)
+                       : gemv_side<true, false>(act, down_planes, down_exps, b_down, y, work, d, h, n, stream);
 }
 
 }  // namespace hffn

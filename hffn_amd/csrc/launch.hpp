@@ -90,10 +90,11 @@ hipError_t launch_mfma_down(int vt, const void* planes, const int32_t* v_exp, co
                             uint32_t n, uint32_t d, uint32_t h, hipStream_t stream);
 
 // Decode-sized projections over the same planes (gemv.hip): act token-major [n, h] (16-byte aligned), y token-major
-// [n, d]; no workspace.
+// [n, d]; `work` (gemv_workspace_bytes) holds the k-split partial sums.
 constexpr uint32_t kGemvMaxTokens = 32;
+size_t gemv_workspace_bytes(uint32_t d, uint32_t h);
 hipError_t launch_gemv_forward(int vt, const float* x, const void* up_planes, const int32_t* up_exps, const float* b_up,
-                               const void* down_planes, const int32_t* down_exps, const float* b_down, float* act, float* y,
-                               uint32_t d, uint32_t h, uint32_t n, hipStream_t stream);
+                               const void* down_planes, const int32_t* down_exps, const float* b_down, float* act, float* work,
+                               float* y, uint32_t d, uint32_t h, uint32_t n, hipStream_t stream);
 
 }  // namespace hffn

@@ -41,16 +41,17 @@ EDGES_MAX_TOKENS = 32     # the policy's last N for the lane-per-slot shapes
 EDGES_PASS_TOKENS = 8     # tokens one pass of the lane-per-slot kernels takes
 MFMA_MIN_DENSITY = 0.05   # the lowest support density the tile-densified MFMA path takes
 # The policy's time estimates (µs per call), fitted to forced-pair timings of HFFNRuntime.forward on MI355X (layer
-# copies rotated so that every call reads HBM; the 70M/20 %, 410M/10 % and 50 % and 1.4B/20 % bf16 layers, N = 1-256).
-# Lane-per-slot kernels: EDGES_CALL_US per call, plus per pass of up to 8 tokens (EDGES_PASS_US + EDGES_SLOT_US per
-# stored slot of both sides) weighted by (1 + NT / 8) / 2 for a pass of NT = 1, 2, 4 or 8 tokens. MFMA path:
-# MFMA_BASE_US + MFMA_ENTRY_US per densified weight of both sides + MFMA_TOKEN_US per token up to 64.
+# copies rotated so that every call reads HBM; the 70M/20 %, 410M/10 % and 50 %, 1.4B/20 % bf16 and 2.8B/80 % bf16
+# layers, N = 1-256). Lane-per-slot kernels: EDGES_CALL_US per call, plus per pass of up to 8 tokens
+# (EDGES_PASS_US + EDGES_SLOT_US per stored slot of both sides) weighted by EDGES_PASS_WEIGHT of the pass's token
+# width. MFMA path: MFMA_BASE_US + MFMA_ENTRY_US per densified weight of both sides + MFMA_TOKEN_US per token up to
+# 64. Decode GEMVs (N <= 32): GEMV_BASE_US + per densified weight of both sides GEMV_ENTRY_US, plus GEMV_TOKEN_US
+# per weight and token beyond the first up to 16, and beyond 16 (the second 16-token MFMA tile) GEMV_TILE2_US per
+# weight and token plus GEMV_TILE2_TOKEN_US per token.
 EDGES_CALL_US, EDGES_PASS_US, EDGES_SLOT_US = 6.0, 4.0, 3.5e-6
+EDGES_PASS_WEIGHT = {1: 0.42, 2: 0.49, 4: 0.52, 8: 1.0}
 MFMA_BASE_US, MFMA_ENTRY_US, MFMA_TOKEN_US = 22.0, 0.93e-6, 0.1
-# Decode GEMVs (N <= 32): GEMV_BASE_US + per MB of planes (both sides) GEMV_MB_US, plus GEMV_TOKEN_MB_US per token up to
-# 16 and GEMV_TILE2_MB_US per token beyond (the second 16-token MFMA tile); fitted to the 70M/20 %, 410M/50 %,
-# 1.4B/20 % bf16 and 2.8B/80 % bf16 layers, N = 1-32.
-GEMV_BASE_US, GEMV_MB_US, GEMV_TOKEN_MB_US, GEMV_TILE2_MB_US = 9.0, 0.324, 0.012, 0.02
+GEMV_BASE_US, GEMV_ENTRY_US, GEMV_TOKEN_US, GEMV_TILE2_US, GEMV_TILE2_TOKEN_US = 10.9, 0.638e-6, 0.019e-6, 0.04e-6, 0.2
 MAX_TOKENS = 1 << 18      # runtime/gpu/nvidia/common/kernels/hffn_cuda/runtime.py:26
 
 _VALUE_TYPES = {torch.float32: _lib.VALUE_F32, torch.bfloat16: _lib.VALUE_BF16}
@@ -78,8 +79,7 @@ def edges_us(n: int, slots: int) -> float:
     passes, rest = divmod(n, EDGES_PASS_TOKENS)
     edges = EDGES_CALL_US + passes * full
     if rest:
-        nt = 1 << (rest - 1).bit_length()  # the pass's token width: 1, 2, 4 or 8
-        edges += (1 + nt / EDGES_PASS_TOKENS) / 2 * full
+        edges += EDGES_PASS_WEIGHT[1 << (rest - 1).bit_length()] * full  # the pass's token width: 1, 2, 4 or 8
     return edges
 
 
@@ -88,11 +88,11 @@ def mfma_us(n: int, d_model: int, d_ff: int) -> float:
     return MFMA_BASE_US + MFMA_ENTRY_US * 2 * d_model * d_ff + MFMA_TOKEN_US * min(n, 64)
 
 
-def gemv_us(n: int, d_model: int, d_ff: int, plane_bytes: int) -> float:
-    """Estimated µs of a call on the decode GEMVs (``plane_bytes``: bytes per densified weight, 4 for fp32 weights
-    and 2 for bf16)."""
-    mb = 2 * d_model * d_ff * plane_bytes / 1e6
-    return GEMV_BASE_US + mb * (GEMV_MB_US + GEMV_TOKEN_MB_US * (min(n, 16) - 1) + GEMV_TILE2_MB_US * max(n - 16, 0))
+def gemv_us(n: int, d_model: int, d_ff: int) -> float:
+    """Estimated µs of a call on the decode GEMVs (N <= 32)."""
+    entries = 2 * d_model * d_ff
+    return (GEMV_BASE_US + entries * (GEMV_ENTRY_US + GEMV_TOKEN_US * (min(n, 16) - 1))
+            + max(n - 16, 0) * (GEMV_TILE2_US * entries + GEMV_TILE2_TOKEN_US))
 
 
 def mfma_preferred(n: int, d_model: int, d_ff: int, slots: int) -> bool:
@@ -101,14 +101,14 @@ def mfma_preferred(n: int, d_model: int, d_ff: int, slots: int) -> bool:
     return n > EDGES_MAX_TOKENS or mfma_us(n, d_model, d_ff) < edges_us(n, slots)
 
 
-def planes_mode(n: int, d_model: int, d_ff: int, slots: int, plane_bytes: int, streamed: bool) -> str | None:
+def planes_mode(n: int, d_model: int, d_ff: int, slots: int, streamed: bool) -> str | None:
     """The planes path (``gemv`` or ``mfma``) of least estimated time for N tokens when it beats the lane-per-slot
     kernels, else None. Above ``EDGES_MAX_TOKENS`` tokens the MFMA path is taken whenever its GEMMs are streamed
     (``streamed``), as in ``mfma_preferred``."""
     options = {}
     if n <= EDGES_MAX_TOKENS:
         options[None] = edges_us(n, slots)
-        options["gemv"] = gemv_us(n, d_model, d_ff, plane_bytes)
+        options["gemv"] = gemv_us(n, d_model, d_ff)
     if streamed:
         options["mfma"] = mfma_us(n, d_model, d_ff) if n <= EDGES_MAX_TOKENS else 0.0
     return min(options, key=options.get) if options else None
@@ -264,8 +264,11 @@ class HFFNRuntime:
         self.density = self._slots / (2 * self.d_model * self.d_ff)
         self._planes: list[dict] | None = None
         self._stale: set[int] = set()   # layers whose values changed since their planes were built
+        self._gemv_work = torch.empty(1, device=self.device)
         if dense and self._mfma_eligible():
             self._planes = [self._densify(tensors) for tensors in self._tensors]
+            words = (_lib.query_bytes(self._lib.hffn_gemv_workspace, self.d_model, self.d_ff) + 3) // 4
+            self._gemv_work = torch.empty(words, device=self.device)  # the decode GEMVs' k-split partial sums
         self._policy: dict[int, tuple[str, str]] = {}  # N -> the policy's (up, down)
         self.forced_up: str | None = None
         self.forced_down: str | None = None
@@ -348,7 +351,8 @@ class HFFNRuntime:
         self._work = (self._x_t.data_ptr(), self._act.data_ptr(), self._y_t.data_ptr(), self._y.data_ptr())
 
     def workspace_bytes(self) -> int:
-        return 4 * (self._x_t.numel() + self._act.numel() + self._y_t.numel() + self._y.numel() + self._mfma_work.numel())
+        return 4 * (self._x_t.numel() + self._act.numel() + self._y_t.numel() + self._y.numel() + self._mfma_work.numel() +
+                    self._gemv_work.numel())
 
     def modes(self, n: int) -> tuple[str, str]:
         """The (up, down) shapes a call of N tokens takes (forced ones first). The policy's choice depends on N and the
@@ -363,9 +367,7 @@ class HFFNRuntime:
     def _modes(self, n: int) -> tuple[str, str]:
         if self.forced_up is None and self.forced_down is None and self._planes is not None \
                 and self.density >= MFMA_MIN_DENSITY:
-            plane_bytes = 2 if self._args[0][0] == _lib.VALUE_BF16 else 4
-            mode = planes_mode(n, self.d_model, self.d_ff, self._slots, plane_bytes,
-                               mfma_streamed(n, self.d_model, self.d_ff))
+            mode = planes_mode(n, self.d_model, self.d_ff, self._slots, mfma_streamed(n, self.d_model, self.d_ff))
             if mode is not None:
                 return mode, mode
         up = self.forced_up or up_mode(n, self.d_model)
@@ -404,8 +406,9 @@ class HFFNRuntime:
                 _lib.check(self._lib.hffn_forward_gemv(value_type, x.data_ptr(), planes["up"].data_ptr(),
                                                        planes["up_binades"].data_ptr(), tensors["b_up"].data_ptr(),
                                                        planes["down"].data_ptr(), planes["down_binades"].data_ptr(),
-                                                       tensors["b_down"].data_ptr(), act, y, self.d_model, self.d_ff, n,
-                                                       stream), "forward (gemv, gemv)")
+                                                       tensors["b_down"].data_ptr(), act, self._gemv_work.data_ptr(),
+                                                       4 * self._gemv_work.numel(), y, self.d_model, self.d_ff, n, stream),
+                           "forward (gemv, gemv)")
                 return
             _lib.check(self._lib.hffn_forward_mfma(value_type, x.data_ptr(), planes["up"].data_ptr(),
                                                    planes["up_binades"].data_ptr(), tensors["b_up"].data_ptr(),

@@ -163,15 +163,20 @@ int hffn_forward_mfma(int value_type, const float* x, const void* up_planes, con
 
 /* ---- Decode path on the planes (1-32 tokens). No reference counterpart: the reference decodes on its gather kernels
  * (runtime/gpu/nvidia/common/kernels/hffn_cuda/kernels.py). One kernel per projection reads the planes once as
- * whole lines and multiplies on v_mfma_f32_16x16x32_f16 (tokens padded to 16 or 32); no workspace. */
+ * whole lines and multiplies on v_mfma_f32_16x16x32_f16 (tokens padded to 16 or 32). */
+
+/* Bytes of the device workspace of hffn_forward_gemv (host-only query; the same for every n): the k-split partial sums
+ * of a projection whose 16-row tiles alone leave CUs idle (added by a second, small kernel). No initial contents are
+ * needed. Calls that share a workspace must be ordered (one stream). */
+int hffn_gemv_workspace(uint32_t d_model, uint32_t d_ff, uint64_t* bytes);
 
 /* act[t, r] = gelu(b_up[r] + sum_i W_up[r, i] x[t, i]) into act (token-major [n, d_ff], 16-byte aligned, like x),
  * then y[t, o] = b_down[o] + sum_r W_down[o, r] act[t, r] (token-major [n, d_model]); 1 <= n <= 32. The inputs are
- * split into fp16 hi/lo with one power of two per token and k span, the products summed as on the MFMA path. Every
- * output is a fixed-order sum, independent of the other tokens of the call. */
+ * split into fp16 hi/lo with one power of two per token and 32-k tile, the products summed as on the MFMA path.
+ * Every output is a fixed-order sum, independent of the other tokens of the call. */
 int hffn_forward_gemv(int value_type, const float* x, const void* up_planes, const int32_t* up_binades, const float* b_up,
-                      const void* down_planes, const int32_t* down_binades, const float* b_down, float* act, float* y,
-                      uint32_t d_model, uint32_t d_ff, uint32_t n, void* stream);
+                      const void* down_planes, const int32_t* down_binades, const float* b_down, float* act, void* workspace,
+                      uint64_t workspace_bytes, float* y, uint32_t d_model, uint32_t d_ff, uint32_t n, void* stream);
 
 /* ------------------------------------------------------------------------------------------------ training (fp32)
  * Layouts: act, z, gz hidden-major [d_ff, ld]; x_t, gy_t, gx_t feature-major [d_model, ld]; x, y, gx token-major

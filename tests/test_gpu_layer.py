@@ -274,6 +274,18 @@ def test_live_row_gemms_equal_the_full_tile(w410m, device):
         assert torch.equal(part, full[:n]), n
 
 
+def test_410m_gemv_split_token_independence(w410m, device):
+    """The 410M down projection runs the decode GEMV with its K split over 4 blocks and a second kernel adding the
+    splits in order: still a fixed order per token, so a token alone and in a 32-token batch give the same bits."""
+    compact, workload, layer = w410m
+    runtime = HFFNRuntime([layer], device)
+    runtime.force("gemv", "gemv")
+    x = torch.from_numpy(synth.make_input(workload, 32)).to(device)
+    whole = runtime.forward(0, x).clone()
+    for start, size in ((0, 1), (9, 7), (16, 16), (31, 1)):
+        assert torch.equal(runtime.forward(0, x[start:start + size].contiguous()), whole[start:start + size]), (start, size)
+
+
 @pytest.mark.parametrize("n", [1, 4, 8, 16, 32, 2048])
 def test_410m_relative_error(n, w410m, device):
     """Pythia-410M shape, 50 % density, fp32: max |y - y64| / max(1, |y64|) <= 1e-5 for every kernel pair."""

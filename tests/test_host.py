@@ -66,10 +66,14 @@ def test_abi_refuses_bad_shapes_before_launching():
     _expect_argument_error(lib.hffn_forward_mfma(0, p, p, p, p, p, p, p, p, small, p, 1024, 4096, 2048, None), "workspace")
     _expect_argument_error(lib.hffn_mfma_up(0, p, p, p, p, p, 1 << 40, 1024, 4000, 2048, None), "multiples")
     _expect_argument_error(lib.hffn_mfma_up(0, ctypes.c_void_p(20), p, p, p, p, 1 << 40, 1024, 4096, 2048, None), "aligned")
-    _expect_argument_error(lib.hffn_forward_gemv(0, p, p, p, p, p, p, p, p, p, 1024, 4096, 33, None), "above 32")
-    _expect_argument_error(lib.hffn_forward_gemv(0, p, p, p, p, p, p, p, p, p, 1024, 4000, 8, None), "multiples")
-    _expect_argument_error(lib.hffn_forward_gemv(0, ctypes.c_void_p(20), p, p, p, p, p, p, p, p, 1024, 4096, 8, None), "aligned")
-    _expect_argument_error(lib.hffn_forward_gemv(0, p, p, p, p, p, p, p, None, p, 1024, 4096, 8, None), "null")
+    gemv_needed = ctypes.c_uint64(0)
+    assert lib.hffn_gemv_workspace(1024, 4096, ctypes.byref(gemv_needed)) == _lib.OK
+    big = gemv_needed.value
+    _expect_argument_error(lib.hffn_forward_gemv(0, p, p, p, p, p, p, p, p, p, big, p, 1024, 4096, 33, None), "above 32")
+    _expect_argument_error(lib.hffn_forward_gemv(0, p, p, p, p, p, p, p, p, p, big, p, 1024, 4000, 8, None), "multiples")
+    _expect_argument_error(lib.hffn_forward_gemv(0, ctypes.c_void_p(20), p, p, p, p, p, p, p, p, big, p, 1024, 4096, 8, None), "aligned")
+    _expect_argument_error(lib.hffn_forward_gemv(0, p, p, p, p, p, p, p, None, p, big, p, 1024, 4096, 8, None), "null")
+    _expect_argument_error(lib.hffn_forward_gemv(0, p, p, p, p, p, p, p, p, p, big - 1, p, 1024, 4096, 8, None), "workspace")
     needed = ctypes.c_uint64(0)
     assert lib.hffn_output_major_workspace(2_097_152, 1024, ctypes.byref(needed)) == _lib.OK
     assert needed.value == 1024 * 1024 * 4
@@ -108,17 +112,22 @@ def test_mfma_policy_crossovers():
 
 
 def test_planes_policy():
-    """Three-way estimate up to 32 tokens: on the Pythia-410M layer at 50 % the lane-per-slot kernels at one token,
-    the decode GEMVs at 8 and 16, the MFMA path above 32 (when its GEMMs are streamed); on a dense bf16 layer the
-    GEMVs from one token."""
+    """Three-way estimate up to 32 tokens: on the Pythia-410M layer at 50 % the lane-per-slot kernels at 1-4 tokens,
+    the decode GEMVs from 8 to 32, the MFMA path above 32 (when its GEMMs are streamed); on the dense 2.8B-shape
+    layer the GEMVs up to 16 tokens and the MFMA path at 32; on the 1.4B layer at 20 % the gather kernels at 1-4
+    tokens and the GEMVs at 16."""
     slots = 2 * 4096 * 512
-    assert runtime.planes_mode(1, 1024, 4096, slots, 4, True) is None
-    assert runtime.planes_mode(8, 1024, 4096, slots, 4, True) == "gemv"
-    assert runtime.planes_mode(16, 1024, 4096, slots, 4, True) == "gemv"
-    assert runtime.planes_mode(33, 1024, 4096, slots, 4, True) == "mfma"
-    assert runtime.planes_mode(33, 1024, 4096, slots, 4, False) is None
-    assert runtime.planes_mode(1, 2560, 10240, 2 * 10240 * 2048, 2, True) == "gemv"
-    assert runtime.gemv_us(16, 1024, 4096, 2) < runtime.gemv_us(16, 1024, 4096, 4)
+    assert runtime.planes_mode(1, 1024, 4096, slots, True) is None
+    assert runtime.planes_mode(2, 1024, 4096, slots, True) is None and runtime.planes_mode(4, 1024, 4096, slots, True) is None
+    assert all(runtime.planes_mode(n, 1024, 4096, slots, True) == "gemv" for n in (8, 16, 24, 32))
+    assert runtime.planes_mode(33, 1024, 4096, slots, True) == "mfma"
+    assert runtime.planes_mode(33, 1024, 4096, slots, False) is None
+    dense = 2 * 10240 * 2048
+    assert all(runtime.planes_mode(n, 2560, 10240, dense, True) == "gemv" for n in (1, 4, 16))
+    assert runtime.planes_mode(32, 2560, 10240, dense, True) == "mfma"
+    sparse = 2 * 8192 * 410
+    assert all(runtime.planes_mode(n, 2048, 8192, sparse, True) is None for n in (1, 4))
+    assert runtime.planes_mode(16, 2048, 8192, sparse, True) == "gemv"
 
 
 def test_mfma_streamed_query():
