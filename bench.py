@@ -80,6 +80,8 @@ def layer_costs(compact, n: int) -> dict:
         "up": {"bytes": up_store + 4 * n * d + 4 * n * h, "flops": 2 * nnz_up * n},
         "down": {"bytes": down_store + 4 * n * h + 4 * n * d, "flops": 2 * nnz_down * n},
         "transpose_out": {"bytes": 8 * n * d, "flops": 0},
+        # the decode GEMVs run both projections in one ABI call (timed as one); priced on the same algorithmic bytes
+        "gemv": {"bytes": up_store + down_store + 8 * n * d + 8 * n * h, "flops": 2 * (nnz_up + nnz_down) * n},
         "model_bytes": up_store + down_store,
         "step_bytes": up_store + down_store + 8 * n * d,
         "step_flops": 2 * (nnz_up + nnz_down) * n,
@@ -120,6 +122,23 @@ def time_kernels(runtime, x: torch.Tensor, steps: int, copies: int) -> dict:
             for i, name in enumerate(names):
                 totals[name] += events[i].elapsed_time(events[i + 1]) * 1e-3
         return {name: total / steps for name, total in totals.items()}
+    if up == "gemv":
+        total = 0.0
+        work, work_bytes = runtime._gemv_work.data_ptr(), 4 * runtime._gemv_work.numel()
+        for step in range(steps):
+            index = step % copies
+            value_type = runtime._args[index][0]
+            planes, tensors = runtime._planes[index], runtime._tensors[index]
+            events = [torch.cuda.Event(enable_timing=True) for _ in range(2)]
+            events[0].record()
+            _lib.check(lib.hffn_forward_gemv(value_type, x.data_ptr(), planes["up"].data_ptr(), planes["up_binades"].data_ptr(),
+                                             tensors["b_up"].data_ptr(), planes["down"].data_ptr(), planes["down_binades"].data_ptr(),
+                                             tensors["b_down"].data_ptr(), act, work, work_bytes, y, runtime.d_model, runtime.d_ff,
+                                             n, stream), "gemv")
+            events[1].record()
+            torch.cuda.synchronize()
+            total += events[0].elapsed_time(events[1]) * 1e-3
+        return {"gemv": total / steps}
     names = (["transpose_in"] if up == "rows" else []) + ["up", "down"] + (["transpose_out"] if down == "rows" else [])
     totals = {name: 0.0 for name in names}
     for step in range(steps):
@@ -214,7 +233,7 @@ def main() -> int:
     up, down = runtime.modes(n)
 
     kernels = time_kernels(runtime, x, max(20, min(args.steps, 200)), copies)
-    dominant = max((k for k in kernels if k in ("up", "down")), key=kernels.get)
+    dominant = max((k for k in kernels if k in ("up", "down", "gemv")), key=kernels.get)
     cost = costs[dominant]
     compute_bound = cost["flops"] / cost["bytes"] > RIDGE
     if compute_bound:
@@ -224,7 +243,7 @@ def main() -> int:
         roofline = {"bound": "hbm", "achieved": round(cost["bytes"] / kernels[dominant] / 1e9, 1), "peak": HBM_PEAK / 1e9,
                     "unit": "GB/s"}
     roofline["frac"] = round(roofline["achieved"] / roofline["peak"], 4)
-    roofline["kernel"] = f"{dominant} ({up if dominant == 'up' else down})"
+    roofline["kernel"] = "up+down (gemv)" if dominant == "gemv" else f"{dominant} ({up if dominant == 'up' else down})"
     roofline["traffic"] = measured_traffic(workload.name, n, roofline["kernel"])
     if up == "mfma":
         # what the MFMA units execute: the dense products of the planes, 3 (fp32 values) or 2 (bf16) fp16 MFMAs each
