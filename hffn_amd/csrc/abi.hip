@@ -182,8 +182,25 @@ int launch_forward(const Plan& p, const float* x, hipStream_t s, float* z = null
                        p.nnz_down, p.n, p.ld, s);
 }
 
-std::mutex g_plans_mutex;
+// Everything of one decode-GEMV forward (hffn_forward_gemv) but x and the stream.
+struct GemvPlan {
+    int value_type;
+    const void* up_planes;
+    const int32_t* up_binades;
+    const float* b_up;
+    const void* down_planes;
+    const int32_t* down_binades;
+    const float* b_down;
+    float* act;
+    void* workspace;
+    uint64_t workspace_bytes;
+    float* y;
+    uint32_t d_model, d_ff, n;
+};
+
+std::mutex g_plans_mutex;  // guards both tables and the handle counter (handles are unique across them)
 std::unordered_map<uint64_t, Plan> g_plans;
+std::unordered_map<uint64_t, GemvPlan> g_gemv_plans;
 uint64_t g_next_plan = 1;
 
 }  // namespace
@@ -234,19 +251,30 @@ int hffn_plan_forward(int up_mode, int down_mode, int value_type, const int32_t*
 
 int hffn_plan_launch(uint64_t plan, const float* x, void* stream) {
     Plan p;
+    GemvPlan g;
+    bool gemv = false;
     {
         const std::lock_guard<std::mutex> lock(g_plans_mutex);
-        const auto found = g_plans.find(plan);
-        if (found == g_plans.end()) return fail(HFFN_ERROR_ARGUMENT, "plan_launch: unknown plan %llu", static_cast<unsigned long long>(plan));
-        p = found->second;
+        if (const auto found = g_plans.find(plan); found != g_plans.end()) {
+            p = found->second;
+        } else if (const auto found_gemv = g_gemv_plans.find(plan); found_gemv != g_gemv_plans.end()) {
+            g = found_gemv->second;
+            gemv = true;
+        } else {
+            return fail(HFFN_ERROR_ARGUMENT, "plan_launch: unknown plan %llu", static_cast<unsigned long long>(plan));
+        }
     }
     if (!x) return fail(HFFN_ERROR_ARGUMENT, "plan_launch: null input");
+    if (gemv)  // the planned arguments passed their checks; x's alignment is checked here
+        return hffn_forward_gemv(g.value_type, x, g.up_planes, g.up_binades, g.b_up, g.down_planes, g.down_binades, g.b_down, g.act,
+                                 g.workspace, g.workspace_bytes, g.y, g.d_model, g.d_ff, g.n, stream);
     return launch_forward(p, x, static_cast<hipStream_t>(stream));
 }
 
 int hffn_plan_release(uint64_t plan) {
     const std::lock_guard<std::mutex> lock(g_plans_mutex);
-    if (g_plans.erase(plan) == 0) return fail(HFFN_ERROR_ARGUMENT, "plan_release: unknown plan %llu", static_cast<unsigned long long>(plan));
+    if (g_plans.erase(plan) == 0 && g_gemv_plans.erase(plan) == 0)
+        return fail(HFFN_ERROR_ARGUMENT, "plan_release: unknown plan %llu", static_cast<unsigned long long>(plan));
     return HFFN_OK;
 }
 
@@ -369,9 +397,10 @@ int hffn_gemv_workspace(uint32_t d_model, uint32_t d_ff, uint64_t* bytes) {
     return HFFN_OK;
 }
 
-int hffn_forward_gemv(int value_type, const float* x, const void* up_planes, const int32_t* up_binades, const float* b_up,
-                      const void* down_planes, const int32_t* down_binades, const float* b_down, float* act, void* workspace,
-                      uint64_t workspace_bytes, float* y, uint32_t d_model, uint32_t d_ff, uint32_t n, void* stream) {
+namespace {
+int check_gemv_call(int value_type, const float* x, const void* up_planes, const int32_t* up_binades, const float* b_up,
+                    const void* down_planes, const int32_t* down_binades, const float* b_down, float* act, void* workspace,
+                    uint64_t workspace_bytes, float* y, uint32_t d_model, uint32_t d_ff, uint32_t n) {
     if (int status = check_gemv(value_type, d_model, d_ff, n)) return status;
     if (!x || !up_planes || !up_binades || !b_up || !down_planes || !down_binades || !b_down || !act || !workspace || !y)
         return fail(HFFN_ERROR_ARGUMENT, "forward_gemv: null pointer");
@@ -381,9 +410,35 @@ int hffn_forward_gemv(int value_type, const float* x, const void* up_planes, con
     if (workspace_bytes < needed)
         return fail(HFFN_ERROR_ARGUMENT, "forward_gemv: workspace of %llu bytes, %llu needed",
                     static_cast<unsigned long long>(workspace_bytes), static_cast<unsigned long long>(needed));
+    return HFFN_OK;
+}
+}  // namespace
+
+int hffn_forward_gemv(int value_type, const float* x, const void* up_planes, const int32_t* up_binades, const float* b_up,
+                      const void* down_planes, const int32_t* down_binades, const float* b_down, float* act, void* workspace,
+                      uint64_t workspace_bytes, float* y, uint32_t d_model, uint32_t d_ff, uint32_t n, void* stream) {
+    if (int status = check_gemv_call(value_type, x, up_planes, up_binades, b_up, down_planes, down_binades, b_down, act, workspace,
+                                     workspace_bytes, y, d_model, d_ff, n))
+        return status;
     return launched(hffn::launch_gemv_forward(value_type, x, up_planes, up_binades, b_up, down_planes, down_binades, b_down, act,
                                               static_cast<float*>(workspace), y, d_model, d_ff, n, static_cast<hipStream_t>(stream)),
                     "forward (gemv)");
+}
+
+int hffn_plan_gemv(int value_type, const void* up_planes, const int32_t* up_binades, const float* b_up, const void* down_planes,
+                   const int32_t* down_binades, const float* b_down, float* act, void* workspace, uint64_t workspace_bytes, float* y,
+                   uint32_t d_model, uint32_t d_ff, uint32_t n, uint64_t* plan) {
+    if (!plan) return fail(HFFN_ERROR_ARGUMENT, "plan_gemv: null result");
+    const float* some_x = reinterpret_cast<const float*>(uintptr_t{16});  // non-null, aligned: never dereferenced
+    if (int status = check_gemv_call(value_type, some_x, up_planes, up_binades, b_up, down_planes, down_binades, b_down, act, workspace,
+                                     workspace_bytes, y, d_model, d_ff, n))
+        return status;
+    const GemvPlan g{value_type, up_planes, up_binades, b_up, down_planes, down_binades, b_down, act, workspace, workspace_bytes,
+                     y, d_model, d_ff, n};
+    const std::lock_guard<std::mutex> lock(g_plans_mutex);
+    *plan = g_next_plan++;
+    g_gemv_plans.emplace(*plan, g);
+    return HFFN_OK;
 }
 
 // ----------------------------------------------------------------------------------------------------- training

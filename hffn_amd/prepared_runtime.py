@@ -1,15 +1,15 @@
 """``PreparedRuntime``: the decode launch path, as ``hffn_pythia_cuda.prepared_runtime``
 (``runtime/gpu/nvidia/llm/inference/hffn_pythia_cuda/prepared_runtime.py:34-82``).
 
-A gather-mode call (every decode step, and small prefills: the ``edges`` and ``rows`` kernels) of layer ``index`` on
-N tokens launches from a *plan* that the library builds once per (index, N): every argument of the forward but
-``x`` and the stream is checked and stored on the library side (``hffn_plan_forward``), so a call is one ctypes call
-with three arguments (``hffn_plan_launch``) instead of the full argument list and its checks. The kernels, modes,
-work buffers, results and the ``calls`` counter are those of ``HFFNRuntime``; calls on the planes paths (``mfma``,
-``gemv``: one ABI call each already) run the control's ``forward``.
+A decode-sized call of layer ``index`` on N tokens (the gather kernels ``edges`` and ``rows``, or the decode GEMVs
+``gemv``) launches from a *plan* that the library builds once per (index, N): every argument of the forward but ``x``
+and the stream is checked and stored on the library side (``hffn_plan_forward``, ``hffn_plan_gemv``), so a call is
+one ctypes call with three arguments (``hffn_plan_launch``) instead of the full argument list and its checks. The
+kernels, modes, work buffers, results and the ``calls`` counter are those of ``HFFNRuntime``; MFMA-path calls (large
+N) run the control's ``forward``.
 
-Baked device pointers: the eight arrays of the layer (never reassigned, kept alive by the runtime) and the work
-buffers; ``_reserve`` (which reallocates the buffers) and ``force`` release every plan, as the reference drops its
+Baked device pointers: the eight arrays of the layer (never reassigned, kept alive by the runtime), its planes
+(rebuilt in place after a training update, before the next planned launch as before any other) and the work buffers; ``_reserve`` (which reallocates the buffers) and ``force`` release every plan, as the reference drops its
 descriptors. ``x`` is never baked. Unlike the reference's descriptors (default stream only), a plan launches on the
 device's current stream of each call.
 """
@@ -20,7 +20,7 @@ import ctypes
 import torch
 
 from . import _lib
-from .runtime import MAX_TOKENS, HFFNRuntime, leading_dim
+from .runtime import MAX_TOKENS, HFFNRuntime, _aligned, leading_dim
 
 _GATHER = ("edges", "rows")
 
@@ -54,13 +54,22 @@ class PreparedRuntime(HFFNRuntime):
             pass
 
     def _plan(self, index: int, n: int):
-        """(handle, up, down) for a gather-mode call, or False for a call that takes the control's path."""
+        """(handle, up, down) for a gather-mode or decode-GEMV call, or False for a call that takes the control's path."""
         up, down = self.modes(n)
-        if up not in _GATHER or down not in _GATHER:
-            return False
         value_type, *model = self._args[index]
         x_t, act, y_t, y = self._work
         handle = ctypes.c_uint64(0)
+        if up == "gemv":
+            planes, tensors = self._planes[index], self._tensors[index]
+            _lib.check(self._lib.hffn_plan_gemv(value_type, planes["up"].data_ptr(), planes["up_binades"].data_ptr(),
+                                                tensors["b_up"].data_ptr(), planes["down"].data_ptr(),
+                                                planes["down_binades"].data_ptr(), tensors["b_down"].data_ptr(), act,
+                                                self._gemv_work.data_ptr(), 4 * self._gemv_work.numel(), y, self.d_model,
+                                                self.d_ff, n, ctypes.byref(handle)),
+                       "plan (gemv, gemv)")
+            return handle.value, up, down
+        if up not in _GATHER or down not in _GATHER:
+            return False
         _lib.check(self._lib.hffn_plan_forward(_lib.UP_MODES[up], _lib.DOWN_MODES[down], value_type, *model, x_t, act, y_t, y,
                                                self.d_model, self.d_ff, *self._nnz[index], n, leading_dim(n),
                                                ctypes.byref(handle)),
@@ -82,6 +91,11 @@ class PreparedRuntime(HFFNRuntime):
         if entry is False:
             return super().forward(index, x)
         handle, up, down = entry
+        if up == "gemv":
+            x = _aligned(x)  # the GEMVs read x 16 bytes at a time
+            if index in self._stale:  # a training update changed the values: rebuild the planes in place first
+                self._densify(self._tensors[index], self._planes[index])
+                self._stale.discard(index)
         stream = self._stream_of(self.device.index) if self._stream_of else torch.cuda.current_stream(self.device).cuda_stream
         _lib.check(self._lib.hffn_plan_launch(handle, x.data_ptr(), stream), f"forward ({up}, {down})")
         self.calls[up, down] += 1

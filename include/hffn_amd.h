@@ -27,7 +27,7 @@
 extern "C" {
 #endif
 
-#define HFFN_ABI_VERSION 7
+#define HFFN_ABI_VERSION 8
 
 #define HFFN_OK 0
 #define HFFN_ERROR_ARGUMENT (-1) /* invalid shape, mode, pointer or workspace */
@@ -177,6 +177,14 @@ int hffn_gemv_workspace(uint32_t d_model, uint32_t d_ff, uint64_t* bytes);
 int hffn_forward_gemv(int value_type, const float* x, const void* up_planes, const int32_t* up_binades, const float* b_up,
                       const void* down_planes, const int32_t* down_binades, const float* b_down, float* act, void* workspace,
                       uint64_t workspace_bytes, float* y, uint32_t d_model, uint32_t d_ff, uint32_t n, void* stream);
+
+/* Prepared decode-GEMV forward: checks every argument of hffn_forward_gemv but x and the stream and keeps them under a
+ * new nonzero handle, launched by hffn_plan_launch (which then checks x's alignment) and dropped by hffn_plan_release,
+ * like hffn_plan_forward's. No reference counterpart beyond the prepared descriptors that plan_forward mirrors
+ * (prepared_runtime.py:34-82): this is the same launch path for the decode GEMVs. */
+int hffn_plan_gemv(int value_type, const void* up_planes, const int32_t* up_binades, const float* b_up, const void* down_planes,
+                   const int32_t* down_binades, const float* b_down, float* act, void* workspace, uint64_t workspace_bytes, float* y,
+                   uint32_t d_model, uint32_t d_ff, uint32_t n, uint64_t* plan);
 
 /* ------------------------------------------------------------------------------------------------ training (fp32)
  * Layouts: act, z, gz hidden-major [d_ff, ld]; x_t, gy_t, gx_t feature-major [d_model, ld]; x, y, gx token-major

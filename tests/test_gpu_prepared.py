@@ -1,5 +1,5 @@
 """The decode launch path (``PreparedRuntime``, plans of the C ABI) on the GPU: bit-identical to ``HFFNRuntime`` on
-every gather pair and token count it serves, the same ``calls`` bookkeeping, plans released when the work buffers move
+every gather pair, the decode GEMVs and every token count it serves, the same ``calls`` bookkeeping, plans released when the work buffers move
 or a mode is forced, and the float64 oracle on the reference test layers (2e-5 absolute, as
 runtime/gpu/nvidia/ffn/inference/checks/parity.py:26-61)."""
 from __future__ import annotations
@@ -44,13 +44,14 @@ def test_prepared_matches_control_bitwise(name, runtimes):
         assert float((got.double().cpu() - torch.from_numpy(oracle_y)).abs().max()) <= ATOL, (name, n)
 
 
-@pytest.mark.parametrize("pair", [("edges", "edges"), ("edges", "rows"), ("rows", "edges"), ("rows", "rows")])
+@pytest.mark.parametrize("pair", [("edges", "edges"), ("edges", "rows"), ("rows", "edges"), ("rows", "rows"),
+                                  ("gemv", "gemv")])
 def test_prepared_forced_pairs(pair, runtimes, device):
     compact, case, control, prepared = runtimes["irreg_512_2048"]
     try:
         control.force(*pair)
         prepared.force(*pair)
-        for n in (1, 4, 7, 64):
+        for n in ((1, 4, 7, 24) if pair[0] == "gemv" else (1, 4, 7, 64)):
             x = torch.from_numpy(synth.make_input(case, n)).to(device)
             assert torch.equal(prepared.forward(0, x), control.forward(0, x)), (pair, n)
             assert prepared._plans[(0, n)][1:] == pair
@@ -94,3 +95,23 @@ def test_prepared_refuses_what_the_control_refuses(device):
     with pytest.raises(IndexError):
         prepared.forward(3, torch.zeros(1, case.d_model, device=device))
     assert np.isfinite(prepared.forward(0, torch.ones(1, case.d_model, device=device)).cpu().numpy()).all()
+
+
+def test_gemv_plans_see_updated_values(device):
+    """A GEMV plan bakes the layer's plane pointers; after a training-style update of the compact values (in place,
+    then invalidate_planes) the planned launch rebuilds the planes first and matches the control bit for bit."""
+    case = synth.CASES["homog_512_2048"]
+    compact = synth.make_layer(case)
+    control, prepared = HFFNRuntime([hip_layer(compact)], device), PreparedRuntime([hip_layer(compact)], device)
+    control.force("gemv", "gemv")
+    prepared.force("gemv", "gemv")
+    x = torch.from_numpy(synth.make_input(case, 16)).to(device)
+    before = control.forward(0, x).clone()
+    assert torch.equal(prepared.forward(0, x), before)
+    assert (0, 16) in prepared._plans
+    for runtime in (control, prepared):
+        runtime._tensors[0]["up_val"].mul_(0.5)
+        runtime.invalidate_planes(0)
+    after = prepared.forward(0, x).clone()  # launched from the plan made before the update
+    assert torch.equal(after, control.forward(0, x))
+    assert not torch.equal(after, before)

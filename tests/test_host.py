@@ -74,6 +74,11 @@ def test_abi_refuses_bad_shapes_before_launching():
     _expect_argument_error(lib.hffn_forward_gemv(0, ctypes.c_void_p(20), p, p, p, p, p, p, p, p, big, p, 1024, 4096, 8, None), "aligned")
     _expect_argument_error(lib.hffn_forward_gemv(0, p, p, p, p, p, p, p, None, p, big, p, 1024, 4096, 8, None), "null")
     _expect_argument_error(lib.hffn_forward_gemv(0, p, p, p, p, p, p, p, p, p, big - 1, p, 1024, 4096, 8, None), "workspace")
+    handle = ctypes.c_uint64(0)
+    _expect_argument_error(lib.hffn_plan_gemv(0, p, p, p, p, p, p, p, p, big, p, 1024, 4096, 33, ctypes.byref(handle)), "above 32")
+    _expect_argument_error(lib.hffn_plan_gemv(0, p, p, p, p, p, p, ctypes.c_void_p(20), p, big, p, 1024, 4096, 8,
+                                              ctypes.byref(handle)), "aligned")
+    _expect_argument_error(lib.hffn_plan_gemv(0, p, p, p, p, p, p, p, p, big, p, 1024, 4096, 8, None), "null result")
     needed = ctypes.c_uint64(0)
     assert lib.hffn_output_major_workspace(2_097_152, 1024, ctypes.byref(needed)) == _lib.OK
     assert needed.value == 1024 * 1024 * 4
@@ -210,3 +215,11 @@ def test_plans_are_checked_once_and_released():
     assert lib.hffn_plan_release(handle.value) == _lib.OK
     _expect_argument_error(lib.hffn_plan_release(first), "unknown plan")
     _expect_argument_error(lib.hffn_plan_launch(first, p, None), "unknown plan")
+    # a decode-GEMV plan: same table and handles; its launch still checks x's alignment before launching
+    gemv_bytes = ctypes.c_uint64(0)
+    assert lib.hffn_gemv_workspace(1024, 4096, ctypes.byref(gemv_bytes)) == _lib.OK
+    assert lib.hffn_plan_gemv(0, p, p, p, p, p, p, p, p, gemv_bytes.value, p, 1024, 4096, 8, ctypes.byref(handle)) == _lib.OK
+    assert handle.value not in (0, first)
+    _expect_argument_error(lib.hffn_plan_launch(handle.value, ctypes.c_void_p(20), None), "aligned")
+    assert lib.hffn_plan_release(handle.value) == _lib.OK
+    _expect_argument_error(lib.hffn_plan_release(handle.value), "unknown plan")
