@@ -1,17 +1,20 @@
 // Decode-sized projections over the densified planes (gfx950, wave64): both projections of the layer for 1-32 tokens
-// on v_mfma_f32_16x16x32_f16, one kernel per projection and no workspace. A decode call is bound by reading the
-// weights once; the MFMA units deliver the operands, so the cost per token stays small (an fp32 FMA GEMV spends its
-// time feeding every lane the inputs of every token).
+// on v_mfma_f32_16x16x32_f16, one kernel per projection (and, for a large side whose row tiles alone leave CUs idle,
+// a small second kernel adding its k splits). A decode call is bound by reading the weights once; the MFMA units
+// deliver the operands, so the cost per token stays small (an fp32 FMA GEMV spends its time feeding every lane the
+// inputs of every token).
 //
 // Planes as the MFMA path keeps them (mfma.hip): planes[(((kt*2 + p)*4 + c)*rows + r)*8 + k % 8], kt = k / 32,
-// c = (k % 32) / 8, p = 0 hi / 1 lo, one power of two per row. A block takes 16 rows (neurons) over the whole K; its
-// W waves (8, or 16 when the row tiles alone leave CUs idle) split K in W spans of whole 32-k tiles. Per tile, lane
-// (r, c) = (lane % 16, lane / 16) holds row r's chunk c of both planes as the B operand (the 16 lanes of a chunk read
-// 256 contiguous bytes), and the 8 inputs of token r at the same k as the A operand, scaled by the token's power of
-// two over the tile and split into fp16 hi and lo: D[token, row] = x_hi w_hi + x_hi w_lo + x_lo w_hi (x_hi w_hi +
-// x_lo w_hi for bf16 weights, exact in the hi plane), accumulated in fp32 with the token's power of two undone
-// exactly. The waves' sums are added in wave order, then the row's power of two is undone; every output is written by
-// one thread, the sums do not depend on the other tokens of the call, and the bits repeat run to run.
+// c = (k % 32) / 8, p = 0 hi / 1 lo, one power of two per row. A block takes 16 rows (neurons) over the whole K or
+// one of 2-8 k splits (blockIdx.y); its W waves (8, or 16 when the row tiles alone leave CUs idle and K is not split)
+// split that range in W spans of whole 32-k tiles. Per tile, lane (r, c) = (lane % 16, lane / 16) holds row r's
+// chunk c of both planes as the B operand (the 16 lanes of a chunk read 256 contiguous bytes), and the 8 inputs of
+// token r at the same k as the A operand, scaled by the token's power of two over the tile and split into fp16 hi and
+// lo: D[token, row] = x_hi w_hi + x_hi w_lo + x_lo w_hi (x_hi w_hi + x_lo w_hi for bf16 weights, exact in the hi
+// plane), accumulated in fp32 with the token's power of two undone exactly. The waves' sums are added in wave order
+// (then the splits' partials in split order by gemv_reduce_kernel), then the row's power of two is undone; every
+// output is written by one thread, the sums do not depend on the other tokens of the call, and the bits repeat run to
+// run.
 //
 // Up: act[t, r] = gelu(b_up[r] + sum_k W_up[r, k] x[t, k]) (token-major act); down: y[t, o] = b_down[o] +
 // sum_r W_down[o, r] act[t, r].
@@ -29,7 +32,7 @@ typedef float floatx4 __attribute__((ext_vector_type(4)));
 constexpr uint32_t kGemvRows = 16;   // rows per block: one MFMA column tile
 constexpr uint32_t kGemvTile = 16;   // tokens per MFMA row tile
 constexpr uint32_t kGemvK = 32;      // k per MFMA, one plane k-tile
-constexpr uint32_t kGemvMinBlocks = 256;  // below this many row tiles a block takes 16 waves instead of 8
+constexpr uint32_t kGemvMinBlocks = 256;  // blocks of one round (one per CU); fewer row tiles call for splits or 16 waves
 
 // floor(log2(m)) of a non-negative float given by its bits; 0 for zero.
 __device__ __forceinline__ int gemv_binade(uint32_t bits) { return bits == 0 ? 0 : static_cast<int>((bits >> 23) & 0xff) - 127; }
