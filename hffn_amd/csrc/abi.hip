@@ -454,6 +454,34 @@ int hffn_forward_z(int up_mode, int down_mode, const float* x, const int32_t* up
     return launch_forward(plan, x, static_cast<hipStream_t>(stream), z);
 }
 
+int hffn_grad_dense_workspace(uint32_t rows, uint32_t cols, uint32_t n, uint64_t* bytes) {
+    if (!bytes) return fail(HFFN_ERROR_ARGUMENT, "grad_dense_workspace: null result");
+    if (int status = check_shape(16, rows, n, (n + 3) / 4 * 4)) return status;
+    if (cols == 0 || cols > HFFN_MAX_WIDTH) return fail(HFFN_ERROR_ARGUMENT, "grad_dense: cols=%u", cols);
+    const size_t needed = hffn::grad_dense_workspace_bytes(rows, cols, n);
+    if (needed == 0)
+        return fail(HFFN_ERROR_ARGUMENT, "grad_dense: rows=%u cols=%u n=%u do not run on the streamed GEMM (multiples of 256, enough tiles)",
+                    rows, cols, n);
+    *bytes = needed;
+    return HFFN_OK;
+}
+
+int hffn_grad_dense(const float* row, const float* mat, const int32_t* offsets, const int16_t* index, float* g, float* gb,
+                    uint32_t rows, uint32_t cols, uint32_t n, uint32_t ld, void* workspace, uint64_t workspace_bytes, void* stream) {
+    uint64_t needed = 0;
+    if (int status = hffn_grad_dense_workspace(rows, cols, n, &needed)) return status;
+    if (ld < n || ld % 4 != 0) return fail(HFFN_ERROR_ARGUMENT, "grad_dense: ld=%u must be a multiple of 4 and at least n=%u", ld, n);
+    if (!row || !mat || !offsets || !index || !g || !gb || !workspace) return fail(HFFN_ERROR_ARGUMENT, "grad_dense: null pointer");
+    if (reinterpret_cast<uintptr_t>(row) % 16 != 0 || reinterpret_cast<uintptr_t>(mat) % 16 != 0 ||
+        reinterpret_cast<uintptr_t>(workspace) % 256 != 0)
+        return fail(HFFN_ERROR_ARGUMENT, "grad_dense: row and mat must be 16-byte aligned, the workspace 256-byte aligned");
+    if (workspace_bytes < needed)
+        return fail(HFFN_ERROR_ARGUMENT, "grad_dense: workspace of %llu bytes, %llu needed", static_cast<unsigned long long>(workspace_bytes),
+                    static_cast<unsigned long long>(needed));
+    return launched(hffn::launch_grad_dense(row, mat, offsets, index, g, gb, rows, cols, n, ld, workspace, static_cast<hipStream_t>(stream)),
+                    "grad_dense");
+}
+
 int hffn_grad_sddmm(const float* row, const float* mat, const int32_t* offsets, const int16_t* index, float* g, float* gb,
                     uint32_t rows, uint32_t n, uint32_t ld, uint32_t stride, void* stream) {
     if (int status = check_shape(16, rows, n, ld)) return status;

@@ -89,6 +89,13 @@ hipError_t launch_mfma_up(int vt, const float* x, const void* planes, const int3
 hipError_t launch_mfma_down(int vt, const void* planes, const int32_t* v_exp, const float* b_down, float* y, void* workspace,
                             uint32_t n, uint32_t d, uint32_t h, hipStream_t stream);
 
+// Sampled products of the training backward on the streamed GEMM (mfma.hip): the dense G = A B^T over the tokens,
+// then the support's entries and the bias gradient (A [rows, ld], B [cols, ld] row-major, n real columns).
+// grad_dense_workspace_bytes is 0 for shapes the streamed GEMM does not take.
+size_t grad_dense_workspace_bytes(uint32_t rows, uint32_t cols, uint32_t n);
+hipError_t launch_grad_dense(const float* row, const float* mat, const int32_t* off, const int16_t* idx, float* g, float* gb,
+                             uint32_t rows, uint32_t cols, uint32_t n, uint32_t ld, void* workspace, hipStream_t stream);
+
 // Decode-sized projections over the same planes (gemv.hip): act token-major [n, h] (16-byte aligned), y token-major
 // [n, d]; `work` (gemv_workspace_bytes) holds the k-split partial sums.
 constexpr uint32_t kGemvMaxTokens = 32;

@@ -78,8 +78,8 @@ __device__ __forceinline__ size_t plane_at(uint32_t rows, uint32_t row, uint32_t
 }
 
 // ------------------------------------------------------------------------------------------ input planes
-// X [M, K] fp32 -> planes of X [rows_pad, K] and e[row] = binade of max |x[row, :]| (rows M .. 8 * gridDim.x: zeros,
-// e = 0; K a multiple of 256). A block takes 8 rows; its wave w takes k in [w K/4, (w + 1) K/4) in steps of 64,
+// X [M, K] fp32 (row stride ld; entries at k >= k_real read as zeros) -> planes of X [rows_pad, K] and e[row] =
+// binade of max |x[row, :]| (rows M .. 8 * gridDim.x: zeros, e = 0; K a multiple of 256). A block takes 8 rows; its wave w takes k in [w K/4, (w + 1) K/4) in steps of 64,
 // up to 4 steps (a chunk) at a time: in a step, lane l holds 8 consecutive k (piece l / 8) of row l % 8, so that the
 // 8 lanes of a row read 256 contiguous bytes of it and the 8 lanes of a piece write the 8 rows' 16 bytes of one
 // 128-byte run of the planes. First the row maxima (lanes, then the 4 waves through LDS), then the split; a wave
@@ -87,24 +87,37 @@ __device__ __forceinline__ size_t plane_at(uint32_t rows, uint32_t row, uint32_t
 constexpr uint32_t kSplitBlockRows = 8;
 constexpr uint32_t kSplitChunk = 256;  // k per chunk: 4 steps of 64
 __global__ __launch_bounds__(kThreads) void split_rows_kernel(const float* __restrict__ x, uint32_t M, uint32_t rows_pad,
-                                                             uint32_t K, _Float16* __restrict__ planes, int32_t* __restrict__ e) {
+                                                             uint32_t K, uint32_t ld, uint32_t k_real, _Float16* __restrict__ planes,
+                                                             int32_t* __restrict__ e) {
     constexpr uint32_t kWaves = kThreads / kWave;
     __shared__ uint32_t part[kWaves][kSplitBlockRows];
     const uint32_t lane = threadIdx.x % kWave, wave = uniform(threadIdx.x / kWave);
     const uint32_t r = lane % kSplitBlockRows, piece = lane / kSplitBlockRows;
     const uint32_t row = blockIdx.x * kSplitBlockRows + r;
     const uint32_t span = K / kWaves, k_begin = wave * span, k_end = k_begin + span;
-    const float* src = x + static_cast<size_t>(row) * K;
+    const float* src = x + static_cast<size_t>(row) * ld;
     const bool real = row < M;
     float v[4][8];
     const auto load_chunk = [&](uint32_t k0) {
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
             float4 a = make_float4(0.f, 0.f, 0.f, 0.f), b = a;
-            if (real && k0 + 64 * i < k_end) {
-                const float* q = src + k0 + 64 * i + 8 * piece;
-                a = *reinterpret_cast<const float4*>(q);
-                b = *reinterpret_cast<const float4*>(q + 4);
+            const uint32_t k = k0 + 64 * i + 8 * piece;
+            if (real && k0 + 64 * i < k_end && k < k_real) {
+                const float* q = src + k;
+                if (k + 8 <= k_real) {
+                    a = *reinterpret_cast<const float4*>(q);
+                    b = *reinterpret_cast<const float4*>(q + 4);
+                } else {  // a piece across the end of the real columns: only those are read (the row may end there)
+                    const uint32_t valid = k_real - k;
+                    a.x = q[0];
+                    if (valid > 1) a.y = q[1];
+                    if (valid > 2) a.z = q[2];
+                    if (valid > 3) a.w = q[3];
+                    if (valid > 4) b.x = q[4];
+                    if (valid > 5) b.y = q[5];
+                    if (valid > 6) b.z = q[6];
+                }
             }
             v[i][0] = a.x; v[i][1] = a.y; v[i][2] = a.z; v[i][3] = a.w;
             v[i][4] = b.x; v[i][5] = b.y; v[i][6] = b.z; v[i][7] = b.w;
@@ -1041,6 +1054,32 @@ uint32_t dma_up_splits(uint32_t m, uint32_t ncol, uint32_t k) {
     return tiles * splits >= kDmaMinBlocks ? splits : 0;
 }
 
+// Sampled products of the training backward from a dense product: G[rows, cols] = A[rows, n] B[cols, n]^T by the
+// streamed GEMM (Epi::UpSplit partials [splits, rows, cols], powers of two undone), then one wave per owner row o:
+// g[q] = sum over the splits (in split order) of G[o, idx[q]] for the row's slots q, and gb[o] = sum_t A[o, t]
+// (lanes over the tokens, then the fixed xor butterfly).
+__global__ __launch_bounds__(kThreads) void gather_dense_kernel(const float* __restrict__ partials, uint32_t splits,
+                                                               const float* __restrict__ a, uint32_t ld, uint32_t n,
+                                                               const int32_t* __restrict__ off, const int16_t* __restrict__ idx,
+                                                               float* __restrict__ g, float* __restrict__ gb, uint32_t rows,
+                                                               uint32_t cols) {
+    const uint32_t o = blockIdx.x * (kThreads / kWave) + uniform(threadIdx.x / kWave), lane = threadIdx.x % kWave;
+    if (o >= rows) return;
+    float s = 0.0f;
+    for (uint32_t t = lane; t < n; t += kWave) s += a[static_cast<size_t>(o) * ld + t];
+    s = wave_sum(s);
+    if (lane == 0) gb[o] = s;
+    const size_t plane = static_cast<size_t>(rows) * cols;
+    const float* row = partials + static_cast<size_t>(o) * cols;
+    const int32_t end = off[o + 1];
+    for (int32_t q = off[o] + static_cast<int32_t>(lane); q < end; q += kWave) {
+        const uint32_t c = static_cast<uint16_t>(idx[q]);
+        float v = row[c];
+        for (uint32_t sp = 1; sp < splits; ++sp) v += row[sp * plane + c];
+        g[q] = v;
+    }
+}
+
 // One row tile of at most 64 or 128 tokens takes the kernel that transfers and multiplies only those rows.
 template <Epi EPI, bool LO_B>
 hipError_t launch_dma(const _Float16* a_planes, const int32_t* a_exp, const _Float16* b_planes, const int32_t* b_exp,
@@ -1120,6 +1159,57 @@ bool mfma_shape_supported(uint32_t d, uint32_t h) { return d % 256 == 0 && h % 2
 
 bool mfma_streamed(uint32_t n, uint32_t d, uint32_t h) { return dma_up_splits(n, h, d) != 0 && dma_down_splits(n, d, h) != 0; }
 
+// Workspace of the dense sampled product (bytes, 256-aligned parts): the planes of A [rows, k_pad] and B [cols,
+// k_pad] (tokens padded to a multiple of 256, split_rows' k granularity), their row binades and the GEMM's partials.
+namespace {
+struct GradDenseLayout {
+    size_t a_planes, b_planes, a_exp, b_exp, partials, bytes;
+    uint32_t k_pad, splits;
+};
+size_t align256(size_t v) { return (v + 255) / 256 * 256; }
+GradDenseLayout grad_dense_layout(uint32_t rows, uint32_t cols, uint32_t n) {
+    GradDenseLayout l{};
+    l.k_pad = ceil_div(n, 256) * 256;
+    l.splits = dma_up_splits(rows, cols, l.k_pad);
+    l.a_planes = 0;
+    l.b_planes = align256(l.a_planes + dense_plane_halves(rows, l.k_pad) * 2);
+    l.a_exp = align256(l.b_planes + dense_plane_halves(cols, l.k_pad) * 2);
+    l.b_exp = align256(l.a_exp + static_cast<size_t>(rows) * 4);
+    l.partials = align256(l.b_exp + static_cast<size_t>(cols) * 4);
+    l.bytes = l.partials + static_cast<size_t>(l.splits) * rows * cols * 4;
+    return l;
+}
+}  // namespace
+
+size_t grad_dense_workspace_bytes(uint32_t rows, uint32_t cols, uint32_t n) {
+    if (rows % kRowPad != 0 || cols % kDmaBN != 0) return 0;
+    const GradDenseLayout l = grad_dense_layout(rows, cols, n);
+    return l.splits == 0 ? 0 : l.bytes;
+}
+
+hipError_t launch_grad_dense(const float* row, const float* mat, const int32_t* off, const int16_t* idx, float* g, float* gb,
+                             uint32_t rows, uint32_t cols, uint32_t n, uint32_t ld, void* workspace, hipStream_t stream) {
+    const GradDenseLayout l = grad_dense_layout(rows, cols, n);
+    char* w = static_cast<char*>(workspace);
+    auto* a_planes = reinterpret_cast<_Float16*>(w + l.a_planes);
+    auto* b_planes = reinterpret_cast<_Float16*>(w + l.b_planes);
+    auto* a_exp = reinterpret_cast<int32_t*>(w + l.a_exp);
+    auto* b_exp = reinterpret_cast<int32_t*>(w + l.b_exp);
+    auto* partials = reinterpret_cast<float*>(w + l.partials);
+    hipLaunchKernelGGL(split_rows_kernel, dim3(rows / kSplitBlockRows), dim3(kThreads), 0, stream, row, rows, rows, l.k_pad, ld, n,
+                       a_planes, a_exp);
+    hipLaunchKernelGGL(split_rows_kernel, dim3(cols / kSplitBlockRows), dim3(kThreads), 0, stream, mat, cols, cols, l.k_pad, ld, n,
+                       b_planes, b_exp);
+    if (hipError_t status = hipGetLastError(); status != hipSuccess) return status;
+    if (hipError_t status = launch_dma<Epi::UpSplit, true>(a_planes, a_exp, b_planes, b_exp, nullptr, partials, nullptr, nullptr, rows,
+                                                           cols, l.k_pad, l.splits, stream);
+        status != hipSuccess)
+        return status;
+    hipLaunchKernelGGL(gather_dense_kernel, dim3(ceil_div(rows, kThreads / kWave)), dim3(kThreads), 0, stream, partials, l.splits, row,
+                       ld, n, off, idx, g, gb, rows, cols);
+    return hipGetLastError();
+}
+
 size_t mfma_workspace_bytes(uint32_t n, uint32_t d, uint32_t h) { return workspace_layout(n, d, h).bytes; }
 
 hipError_t launch_densify(int vt, const int32_t* off, const int16_t* idx, const void* val, uint32_t rows, uint32_t k,
@@ -1140,8 +1230,8 @@ hipError_t launch_mfma_up(int vt, const float* x, const void* planes, const int3
     char* bytes = static_cast<char*>(workspace);
     auto* x_planes = reinterpret_cast<_Float16*>(bytes + w.x_planes);
     auto* act_planes = reinterpret_cast<_Float16*>(bytes + w.act_planes);
-    hipLaunchKernelGGL(split_rows_kernel, dim3(rows_live(n) / kSplitBlockRows), dim3(kThreads), 0, stream, x, n, rows_padded(n), d,
-                       x_planes, words + w.x_binades);  // 8 rows per block
+    hipLaunchKernelGGL(split_rows_kernel, dim3(rows_live(n) / kSplitBlockRows), dim3(kThreads), 0, stream, x, n, rows_padded(n), d, d,
+                       d, x_planes, words + w.x_binades);  // 8 rows per block
     if (hipError_t status = hipGetLastError(); status != hipSuccess) return status;
     const auto* p = static_cast<const _Float16*>(planes);
     if (const uint32_t splits = dma_up_splits(n, h, d); splits > 1) {

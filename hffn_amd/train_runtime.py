@@ -33,12 +33,14 @@ from collections import Counter
 import torch
 
 from . import _lib
-from .runtime import MAX_TOKENS, HFFNRuntime, down_mode, edges_supported, leading_dim, up_mode
+from .runtime import MAX_TOKENS, MFMA_MIN_DENSITY, HFFNRuntime, down_mode, edges_supported, leading_dim, up_mode
 
 PARAMETERS = ("up_val", "b_up", "out_val", "b_down")
 SUPPORTS = ("in_offsets", "in_pos", "in_hidden", "hid_offsets", "hid_pos", "hid_output")
 GRAD_TILE = 256              # tokens per tile of the sampled products
 PARTIAL_MAX_TOKENS = 2048    # default largest N: the tile partials are sized at construction, never in a step
+GRAD_DENSE_MIN_TOKENS = 64   # from this N the sampled products run as dense MFMA products (when the shapes allow)
+GRAD_MODES = ("gather", "dense")
 
 
 def grad_tiles(n: int) -> int:
@@ -94,11 +96,14 @@ class HFFNTrainRuntime:
         self.steps = [0] * len(runtime.layers)   # AdamW step count per layer (part of the optimiser state)
         self.calls: Counter = Counter()          # (up, down) of the forwards with a z buffer
         self._partial_tiles, self._partials = 1, None
+        self._dense_bytes, self._dense_work = 0, None
+        self.forced_grad: str | None = None      # diagnostic: fix the sampled products' formulation
         self._saved: tuple | None = None
         self._tokens = 0
         self.growths = 0
         self.reserve(1)
         self._reserve_partials(max_tokens)
+        self._reserve_dense(max_tokens)
         self.growths = 0     # buffer growths after construction: a timed window must leave it unchanged
 
     # -- buffers ---------------------------------------------------------------------------------------------------
@@ -120,6 +125,41 @@ class HFFNTrainRuntime:
             self._gx = torch.empty(n, self.d_model, device=device)
             self._saved = None
         self._reserve_partials(n)
+        self._reserve_dense(n)
+
+    def _dense_need(self, n: int) -> int:
+        """Workspace bytes of the dense sampled products at N (the larger of the two shapes), 0 where the streamed GEMM
+        does not take them."""
+        need = 0
+        for rows, cols in ((self.d_model, self.d_ff), (self.d_ff, self.d_model)):
+            result = _lib.ctypes.c_uint64(0)
+            if self._lib.hffn_grad_dense_workspace(rows, cols, n, _lib.ctypes.byref(result)) != _lib.OK:
+                return 0
+            need = max(need, result.value)
+        return need
+
+    def _reserve_dense(self, n: int) -> None:
+        if self.grad_mode(n) != "dense":
+            return
+        need = self._dense_need(n)
+        if need > self._dense_bytes:
+            self._dense_bytes = need
+            self.growths += 1
+            self._dense_work = torch.empty(need, dtype=torch.uint8, device=self.runtime.device)
+
+    def grad_mode(self, n: int) -> str:
+        """How the two sampled products run at N: ``dense`` (split-fp16 MFMA products over the tokens, then the
+        support's entries) from ``GRAD_DENSE_MIN_TOKENS`` on layers of at least ``MFMA_MIN_DENSITY`` whose shapes the
+        streamed GEMM takes; else ``gather`` (``hffn_grad_sddmm``). ``forced_grad`` overrides it."""
+        if self.forced_grad is not None:
+            if self.forced_grad not in GRAD_MODES:
+                raise ValueError("unknown sampled-product mode")
+            if self.forced_grad == "dense" and self._dense_need(n) == 0:
+                raise ValueError("the dense sampled products do not take this shape")
+            return self.forced_grad
+        if n >= GRAD_DENSE_MIN_TOKENS and self.runtime.density >= MFMA_MIN_DENSITY and self._dense_need(n) > 0:
+            return "dense"
+        return "gather"
 
     def _reserve_partials(self, n: int) -> None:
         tiles = grad_tiles(n)
@@ -198,21 +238,33 @@ class HFFNTrainRuntime:
                                           values["hid_val"].numel(), stream), "down values, hidden-major")
         _lib.check(lib.hffn_gather_values(params["up_val"].data_ptr(), supports["in_pos"].data_ptr(), values["in_val"].data_ptr(),
                                           values["in_val"].numel(), stream), "up values, input-major")
-        tiles = grad_tiles(n)
-        if tiles == 1:   # the tile partial is the gradient
+        dense = self.grad_mode(n) == "dense"
+        if dense:
+            self._reserve_dense(n)  # a forced mode may need it first
+        tiles = 1 if dense else grad_tiles(n)
+        if tiles == 1:   # the tile partial is the gradient (and the dense products write the gradients themselves)
             stride = 0
             g_down, gb_down, g_up, gb_up = (grads[name].data_ptr() for name in ("out_val", "b_down", "up_val", "b_up"))
         else:
             c1, c2, c3, stride = self._columns[index]
             ws = self._partials.data_ptr()
             g_down, gb_down, g_up, gb_up = ws, ws + 4 * c1, ws + 4 * c2, ws + 4 * c3
-        _lib.check(lib.hffn_grad_sddmm(self._gy_t.data_ptr(), act, params["out_offsets"].data_ptr(), params["out_hidden"].data_ptr(),
-                                       g_down, gb_down, d, n, ld, stride, stream), "grad_down")
+        if dense:
+            work, work_bytes = self._dense_work.data_ptr(), self._dense_work.numel()
+            _lib.check(lib.hffn_grad_dense(self._gy_t.data_ptr(), act, params["out_offsets"].data_ptr(), params["out_hidden"].data_ptr(),
+                                           g_down, gb_down, d, h, n, ld, work, work_bytes, stream), "grad_down (dense)")
+        else:
+            _lib.check(lib.hffn_grad_sddmm(self._gy_t.data_ptr(), act, params["out_offsets"].data_ptr(), params["out_hidden"].data_ptr(),
+                                           g_down, gb_down, d, n, ld, stride, stream), "grad_down")
         _lib.check(lib.hffn_grad_hidden(gy.data_ptr(), self._gy_t.data_ptr(), z_ptr, supports["hid_offsets"].data_ptr(),
                                         supports["hid_output"].data_ptr(), values["hid_val"].data_ptr(), self._gz.data_ptr(),
                                         d, h, values["hid_val"].numel(), n, ld, stream), "grad_hidden")
-        _lib.check(lib.hffn_grad_sddmm(self._gz.data_ptr(), x_t, params["up_offsets"].data_ptr(), params["up_idx"].data_ptr(),
-                                       g_up, gb_up, h, n, ld, stride, stream), "grad_up")
+        if dense:
+            _lib.check(lib.hffn_grad_dense(self._gz.data_ptr(), x_t, params["up_offsets"].data_ptr(), params["up_idx"].data_ptr(),
+                                           g_up, gb_up, h, d, n, ld, work, work_bytes, stream), "grad_up (dense)")
+        else:
+            _lib.check(lib.hffn_grad_sddmm(self._gz.data_ptr(), x_t, params["up_offsets"].data_ptr(), params["up_idx"].data_ptr(),
+                                           g_up, gb_up, h, n, ld, stride, stream), "grad_up")
         if tiles > 1:
             c1, c2, c3, stride = self._columns[index]
             _lib.check(lib.hffn_reduce_tiles(self._partials.data_ptr(), stride, tiles, c1, c2, c3, grads["out_val"].data_ptr(),

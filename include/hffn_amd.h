@@ -27,7 +27,7 @@
 extern "C" {
 #endif
 
-#define HFFN_ABI_VERSION 8
+#define HFFN_ABI_VERSION 9
 
 #define HFFN_OK 0
 #define HFFN_ERROR_ARGUMENT (-1) /* invalid shape, mode, pointer or workspace */
@@ -200,6 +200,17 @@ int hffn_forward_z(int up_mode, int down_mode, const float* x, const int32_t* up
                    const float* b_up, const int32_t* out_offsets, const int16_t* out_hidden, const float* out_val, const float* b_down,
                    float* x_t, float* act, float* y_t, float* y, float* z, uint32_t d_model, uint32_t d_ff, uint32_t nnz_up,
                    uint32_t nnz_down, uint32_t n, uint32_t ld, void* stream);
+
+/* The two sampled products of hffn_grad_sddmm (same g, gb and slot orders; no tile partials) from a dense product
+ * on the streamed MFMA GEMM: G[rows, cols] = row[rows, :n] mat[cols, :n]^T with both operands split into fp16 hi/lo
+ * (one power of two per row; hi*hi + hi*lo + lo*hi in fp32), then g[q] = G[o, index[q]] for the slots of each owner
+ * row o, and gb[o] = sum_t row[o, t]. row and mat row-major with stride ld (16-byte aligned); rows a multiple of 256,
+ * cols of 128. hffn_grad_dense_workspace refuses shapes the streamed GEMM does not take (too few tiles). No reference
+ * counterpart (the reference's sampled products are gathers, kernels_train.py:115-184); for high density and many
+ * tokens, where a gather reads nnz * n * 4 bytes of activations per product. */
+int hffn_grad_dense_workspace(uint32_t rows, uint32_t cols, uint32_t n, uint64_t* bytes);
+int hffn_grad_dense(const float* row, const float* mat, const int32_t* offsets, const int16_t* index, float* g, float* gb,
+                    uint32_t rows, uint32_t cols, uint32_t n, uint32_t ld, void* workspace, uint64_t workspace_bytes, void* stream);
 
 /* Sampled product over an owner-row support: for each owner o < rows, token tile k and slot q of o,
  * g[k*stride + q] = sum_t row[o, t] mat[index[q], t] and gb[k*stride + o] = sum_t row[o, t] (t over tile k, below n);

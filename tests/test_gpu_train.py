@@ -11,6 +11,9 @@ runtime/gpu/nvidia/ffn/training/check.py:1-12:
 then: no buffer growth in a step after ``reserve``, the ordering check of ``backward``, and the MFMA path of the
 inference runtime reading the updated values.
 N covers one tile (1, 33, 100, 128), a one-token last tile (257), partial last tiles (300, 2100) and exact tiles (512).
+The sampled products run as gathers (``gather``) or as dense split-fp16 MFMA products sampled at the support
+(``dense``, the policy's choice from 64 tokens on the 512 x 2048 layers); cases force either where the policy would
+not take it, so both meet every gate.
 """
 from __future__ import annotations
 
@@ -32,7 +35,9 @@ HYPER = dict(lr=1e-3, betas=(0.9, 0.999), eps=1e-8, weight_decay=1e-2)
 GROUPS = ("y", "gb_down", "g_down", "gz", "g_up", "gb_up", "gx")
 GATE2_FACTOR, GATE2_FLOOR = 10.0, 1e-7
 GATE3_CONDITIONING, GATE3_RELATIVE = 100.0, 1e-5
-CASES = [("homog_256_1024", n) for n in (1, 33, 100, 128, 257, 300, 512, 2100)] + [("irreg_512_2048", n) for n in (4, 300)]
+CASES = ([("homog_256_1024", n, None) for n in (1, 33, 100, 128, 257, 300, 512, 2100)]
+         + [("irreg_512_2048", 4, None), ("irreg_512_2048", 300, None), ("irreg_512_2048", 300, "gather"),
+            ("irreg_512_2048", 33, "dense"), ("homog_512_2048", 64, None), ("homog_512_2048", 2100, None)])
 
 
 def make_gy(case, n: int, salt: int) -> torch.Tensor:
@@ -117,14 +122,17 @@ def _update_errors(pre: dict, post: dict, groups: dict, masks: dict, step: int) 
     return worst
 
 
-@pytest.mark.parametrize("name,n", CASES)
-def test_training_gates(name, n, device):
+@pytest.mark.parametrize("name,n,grad", CASES)
+def test_training_gates(name, n, grad, device):
     case = synth.CASES[name]
     layer = synth.make_layer(case)
     x = torch.from_numpy(synth.make_input(case, n)).to(device)
     gy = make_gy(case, n, 0).to(device)
     baseline = HFFNRuntime([hip_layer(layer)], device)
     train = HFFNTrainRuntime(HFFNRuntime([hip_layer(layer)], device), **HYPER, max_tokens=max(n, 2048))
+    train.forced_grad = grad
+    if name.endswith("512_2048") and grad is None:
+        assert train.grad_mode(n) == ("dense" if n >= 64 else "gather")
     train.reserve(n)
     # gate 1: the inference call is untouched; the forward with z has the bits of the same gather forward
     for pair in ((None, None), ("edges", "edges"), ("rows", "rows"), ("edges", "rows"), ("rows", "edges")):
