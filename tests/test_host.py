@@ -74,6 +74,15 @@ def test_abi_refuses_bad_shapes_before_launching():
     _expect_argument_error(lib.hffn_forward_gemv(0, ctypes.c_void_p(20), p, p, p, p, p, p, p, p, big, p, 1024, 4096, 8, None), "aligned")
     _expect_argument_error(lib.hffn_forward_gemv(0, p, p, p, p, p, p, p, None, p, big, p, 1024, 4096, 8, None), "null")
     _expect_argument_error(lib.hffn_forward_gemv(0, p, p, p, p, p, p, p, p, p, big - 1, p, 1024, 4096, 8, None), "workspace")
+    dense = ctypes.c_uint64(0)
+    _expect_argument_error(lib.hffn_grad_dense_workspace(256, 1024, 64, ctypes.byref(dense)), "streamed GEMM")
+    assert lib.hffn_grad_dense_workspace(1024, 4096, 64, ctypes.byref(dense)) == _lib.OK and dense.value > 0
+    work = ctypes.c_void_p(256)
+    _expect_argument_error(lib.hffn_grad_dense(p, p, p, p, p, p, 1024, 4096, 64, 62, work, dense.value, None), "ld=62")
+    _expect_argument_error(lib.hffn_grad_dense(ctypes.c_void_p(20), p, p, p, p, p, 1024, 4096, 64, 64, work, dense.value, None),
+                           "aligned")
+    _expect_argument_error(lib.hffn_grad_dense(p, p, None, p, p, p, 1024, 4096, 64, 64, work, dense.value, None), "null")
+    _expect_argument_error(lib.hffn_grad_dense(p, p, p, p, p, p, 1024, 4096, 64, 64, work, dense.value - 1, None), "workspace")
     handle = ctypes.c_uint64(0)
     _expect_argument_error(lib.hffn_plan_gemv(0, p, p, p, p, p, p, p, p, big, p, 1024, 4096, 33, ctypes.byref(handle)), "above 32")
     _expect_argument_error(lib.hffn_plan_gemv(0, p, p, p, p, p, p, ctypes.c_void_p(20), p, big, p, 1024, 4096, 8,
