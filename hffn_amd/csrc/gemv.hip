@@ -1,4 +1,4 @@
-// Decode-sized projections over the densified planes (gfx950, wave64): both projections of the layer for 1-32 tokens
+// Decode-sized projections over the densified planes (gfx950, wave64): both projections of the layer for 1-64 tokens
 // on v_mfma_f32_16x16x32_f16, one kernel per projection (and, for a large side whose row tiles alone leave CUs idle,
 // a small second kernel adding its k splits). A decode call is bound by reading the weights once; the MFMA units
 // deliver the operands, so the cost per token stays small (an fp32 FMA GEMV spends its time feeding every lane the
@@ -47,7 +47,8 @@ __global__ __launch_bounds__(W* kWave) void gemv_mfma_kernel(const float* __rest
                                                                  uint32_t rows, uint32_t K, uint32_t n) {
     constexpr uint32_t kTokens = TT * kGemvTile;
     constexpr uint32_t kThreads = W * kWave;
-    constexpr uint32_t kChunk = W >= 16 ? 8 / (2 * TT) : 8;  // k-tiles whose loads are issued together (VGPR budget)
+    // k-tiles whose loads are issued together, within the VGPR budget (128 per lane with 16 waves, 256 with 8)
+    constexpr uint32_t kChunk = W >= 16 ? (TT >= 4 ? 1 : 4 / TT) : (TT >= 4 ? 4 : 8);
     __shared__ float sums[W][kTokens][kGemvRows];
     const uint32_t lane = threadIdx.x % kWave, wave = uniform(threadIdx.x / kWave);
     const uint32_t r = lane % 16, c = lane / 16;
@@ -168,8 +169,10 @@ void gemv_launch(const float* in, const _Float16* planes, const int32_t* exps, c
     const dim3 grid(rows / kGemvRows, splits), block(W * kWave);
     if (n <= kGemvTile)
         hipLaunchKernelGGL((gemv_mfma_kernel<W, 1, LO_B, UP>), grid, block, 0, stream, in, planes, exps, bias, out, partials, rows, K, n);
-    else
+    else if (n <= 2 * kGemvTile)
         hipLaunchKernelGGL((gemv_mfma_kernel<W, 2, LO_B, UP>), grid, block, 0, stream, in, planes, exps, bias, out, partials, rows, K, n);
+    else
+        hipLaunchKernelGGL((gemv_mfma_kernel<W, 4, LO_B, UP>), grid, block, 0, stream, in, planes, exps, bias, out, partials, rows, K, n);
 }
 
 // 8 waves per block, with k splits (added by gemv_reduce_kernel) where gemv_splits finds them worth a second kernel;

@@ -98,7 +98,7 @@ hipError_t launch_grad_dense(const float* row, const float* mat, const int32_t* 
 
 // Decode-sized projections over the same planes (gemv.hip): act token-major [n, h] (16-byte aligned), y token-major
 // [n, d]; `work` (gemv_workspace_bytes) holds the k-split partial sums.
-constexpr uint32_t kGemvMaxTokens = 32;
+constexpr uint32_t kGemvMaxTokens = 64;
 size_t gemv_workspace_bytes(uint32_t d, uint32_t h);
 hipError_t launch_gemv_forward(int vt, const float* x, const void* up_planes, const int32_t* up_exps, const float* b_up,
                                const void* down_planes, const int32_t* down_exps, const float* b_down, float* act, float* work,

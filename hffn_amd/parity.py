@@ -4,7 +4,7 @@
 For one input, the runtime runs with its policy and with each forced (up, down) kernel pair. Criteria: two
 consecutive calls on the same input give the same bits; ``max |y - y64|`` and ``max |y - y64| / max(1, |y64|)`` are
 reported for the caller to compare with its tolerance. The pairs are the policy, the four gather pairs (edges or
-rows up, edges or rows down) and, when the runtime holds densified planes, the MFMA path and (up to 32 tokens) the
+rows up, edges or rows down) and, when the runtime holds densified planes, the MFMA path and (up to 64 tokens) the
 decode GEMVs.
 """
 from __future__ import annotations

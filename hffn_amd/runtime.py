@@ -11,11 +11,11 @@ Kernel shapes (the build's own policy, ``up_mode``/``down_mode``):
 * ``edges`` - lanes over a row's slots, tokens in registers, input staged in LDS; decode-sized N (N <= 32).
 * ``rows``  - lanes over tokens (1, 2 or 4 per lane), slots walked in order; larger N on layers without the MFMA path.
 * ``mfma``  - tile-densified split-fp16 MFMA GEMMs (up and down together) on layers that qualify (``d_model`` and
-  ``d_ff`` multiples of 256, density at least ``MFMA_MIN_DENSITY``); always above 32 tokens.
-* ``gemv``  - decode GEMVs over the same planes (up and down together, 1-32 tokens): one kernel per projection on
+  ``d_ff`` multiples of 256, density at least ``MFMA_MIN_DENSITY``); always above 64 tokens.
+* ``gemv``  - decode GEMVs over the same planes (up and down together, 1-64 tokens): one kernel per projection on
   16x16x32 MFMAs, the planes read once as whole lines.
 
-Up to 32 tokens the policy takes whichever of ``edges``, ``gemv`` and ``mfma`` has the least estimated time
+Up to 64 tokens the policy takes whichever of ``edges`` (up to 32), ``gemv`` and ``mfma`` has the least estimated time
 (``planes_mode``). On the Pythia-410M layer at 50 % (12 rotating copies, MI355X), per call: N = 1: edges 13.7 us,
 gemv 17.5, mfma 28.5; N = 8: gemv 19.7, edges 23.8, mfma 29.8; N = 16: gemv 23.5, mfma 31.2, edges 41.5; N = 32:
 mfma 33.1, gemv 33.1; N = 2048: mfma 140 us.
@@ -36,7 +36,7 @@ from . import _lib
 UP_MODES = ("edges", "rows", "mfma", "gemv")
 DOWN_MODES = ("edges", "rows", "mfma", "gemv")
 PAIR_MODES = ("mfma", "gemv")  # the planes paths: up and down run together
-GEMV_MAX_TOKENS = 32      # the planes GEMVs' largest call
+GEMV_MAX_TOKENS = 64      # the planes GEMVs' largest call
 EDGES_MAX_TOKENS = 32     # the policy's last N for the lane-per-slot shapes
 EDGES_PASS_TOKENS = 8     # tokens one pass of the lane-per-slot kernels takes
 MFMA_MIN_DENSITY = 0.05   # the lowest support density the tile-densified MFMA path takes
@@ -45,8 +45,8 @@ MFMA_MIN_DENSITY = 0.05   # the lowest support density the tile-densified MFMA p
 # layers, N = 1-256). Lane-per-slot kernels: EDGES_CALL_US per call, plus per pass of up to 8 tokens
 # (EDGES_PASS_US + EDGES_SLOT_US per stored slot of both sides) weighted by EDGES_PASS_WEIGHT of the pass's token
 # width. MFMA path: MFMA_BASE_US + MFMA_ENTRY_US per densified weight of both sides + MFMA_TOKEN_US per token up to
-# 64. Decode GEMVs (N <= 32): GEMV_BASE_US + per densified weight of both sides GEMV_ENTRY_US, plus GEMV_TOKEN_US
-# per weight and token beyond the first up to 16, and beyond 16 (the second 16-token MFMA tile) GEMV_TILE2_US per
+# 64. Decode GEMVs (N <= 64): GEMV_BASE_US + per densified weight of both sides GEMV_ENTRY_US, plus GEMV_TOKEN_US
+# per weight and token beyond the first up to 16, and beyond 16 (the second and later 16-token MFMA tiles) GEMV_TILE2_US per
 # weight and token plus GEMV_TILE2_TOKEN_US per token.
 EDGES_CALL_US, EDGES_PASS_US, EDGES_SLOT_US = 6.0, 4.0, 3.5e-6
 EDGES_PASS_WEIGHT = {1: 0.42, 2: 0.49, 4: 0.52, 8: 1.0}
@@ -89,7 +89,7 @@ def mfma_us(n: int, d_model: int, d_ff: int) -> float:
 
 
 def gemv_us(n: int, d_model: int, d_ff: int) -> float:
-    """Estimated µs of a call on the decode GEMVs (N <= 32)."""
+    """Estimated µs of a call on the decode GEMVs (N <= 64)."""
     entries = 2 * d_model * d_ff
     return (GEMV_BASE_US + entries * (GEMV_ENTRY_US + GEMV_TOKEN_US * (min(n, 16) - 1))
             + max(n - 16, 0) * (GEMV_TILE2_US * entries + GEMV_TILE2_TOKEN_US))
@@ -103,14 +103,15 @@ def mfma_preferred(n: int, d_model: int, d_ff: int, slots: int) -> bool:
 
 def planes_mode(n: int, d_model: int, d_ff: int, slots: int, streamed: bool) -> str | None:
     """The planes path (``gemv`` or ``mfma``) of least estimated time for N tokens when it beats the lane-per-slot
-    kernels, else None. Above ``EDGES_MAX_TOKENS`` tokens the MFMA path is taken whenever its GEMMs are streamed
-    (``streamed``), as in ``mfma_preferred``."""
+    kernels (up to ``EDGES_MAX_TOKENS``), else None. Above ``GEMV_MAX_TOKENS`` tokens the MFMA path is taken whenever
+    its GEMMs are streamed (``streamed``)."""
     options = {}
     if n <= EDGES_MAX_TOKENS:
         options[None] = edges_us(n, slots)
+    if n <= GEMV_MAX_TOKENS:
         options["gemv"] = gemv_us(n, d_model, d_ff)
     if streamed:
-        options["mfma"] = mfma_us(n, d_model, d_ff) if n <= EDGES_MAX_TOKENS else 0.0
+        options["mfma"] = mfma_us(n, d_model, d_ff) if n <= GEMV_MAX_TOKENS else 0.0
     return min(options, key=options.get) if options else None
 
 
@@ -324,7 +325,7 @@ class HFFNRuntime:
 
     def force(self, up: str | None, down: str | None) -> None:
         """Diagnostic: fix the up and/or the down kernel regardless of N (None: the policy). The planes paths run up and
-        down together: ``mfma`` and ``gemv`` are forced as pairs (``gemv`` serves 1-32 tokens)."""
+        down together: ``mfma`` and ``gemv`` are forced as pairs (``gemv`` serves 1-64 tokens)."""
         if up not in (None, *UP_MODES) or down not in (None, *DOWN_MODES):
             raise ValueError("unknown kernel mode")
         if up == "edges" and not edges_supported(self.d_model, 1):

@@ -161,9 +161,9 @@ int hffn_forward_mfma(int value_type, const float* x, const void* up_planes, con
                       const void* down_planes, const int32_t* down_binades, const float* b_down, void* workspace,
                       uint64_t workspace_bytes, float* y, uint32_t d_model, uint32_t d_ff, uint32_t n, void* stream);
 
-/* ---- Decode path on the planes (1-32 tokens). No reference counterpart: the reference decodes on its gather kernels
+/* ---- Decode path on the planes (1-64 tokens). No reference counterpart: the reference decodes on its gather kernels
  * (runtime/gpu/nvidia/common/kernels/hffn_cuda/kernels.py). One kernel per projection reads the planes once as
- * whole lines and multiplies on v_mfma_f32_16x16x32_f16 (tokens padded to 16 or 32). */
+ * whole lines and multiplies on v_mfma_f32_16x16x32_f16 (tokens padded to 16, 32 or 64). */
 
 /* Bytes of the device workspace of hffn_forward_gemv (host-only query; the same for every n): the k-split partial sums
  * of a projection whose 16-row tiles alone leave CUs idle (added by a second, small kernel). No initial contents are
@@ -171,7 +171,7 @@ int hffn_forward_mfma(int value_type, const float* x, const void* up_planes, con
 int hffn_gemv_workspace(uint32_t d_model, uint32_t d_ff, uint64_t* bytes);
 
 /* act[t, r] = gelu(b_up[r] + sum_i W_up[r, i] x[t, i]) into act (token-major [n, d_ff], 16-byte aligned, like x),
- * then y[t, o] = b_down[o] + sum_r W_down[o, r] act[t, r] (token-major [n, d_model]); 1 <= n <= 32. The inputs are
+ * then y[t, o] = b_down[o] + sum_r W_down[o, r] act[t, r] (token-major [n, d_model]); 1 <= n <= 64. The inputs are
  * split into fp16 hi/lo with one power of two per token and 32-k tile, the products summed as on the MFMA path.
  * Every output is a fixed-order sum, independent of the other tokens of the call. */
 int hffn_forward_gemv(int value_type, const float* x, const void* up_planes, const int32_t* up_binades, const float* b_up,

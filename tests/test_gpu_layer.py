@@ -112,7 +112,7 @@ def test_forced_pairs_match_the_oracle(name, test_layers, device):
         result = parity.check(runtime, 0, torch.from_numpy(x_np).to(device), expected)
         assert result.repeatable, f"{name} N{n}: bits differ on repeat"
         assert result.error <= ATOL, f"{name} N{n}: {result.pairs}"
-    gemv_skipped = sum(n > GEMV_MAX_TOKENS for n in BATCHES)  # the decode GEMVs take at most 32 tokens
+    gemv_skipped = sum(n > GEMV_MAX_TOKENS for n in BATCHES)  # the decode GEMVs take at most 64 tokens
     assert sum(runtime.calls.values()) == 2 * (len(BATCHES) * len(parity.PAIRS) - gemv_skipped)
 
 
@@ -178,25 +178,25 @@ def test_token_result_does_not_depend_on_the_batch(up, down, test_layers, device
 @pytest.mark.parametrize("name", ["homog_512_2048", "irreg_512_2048"])
 def test_gemv_token_result_does_not_depend_on_the_batch(name, test_layers, device):
     """The decode GEMVs scale each token by its own power of two per 32-k tile and sum its products in a fixed order,
-    whatever the other tokens (one or two 16-token MFMA tiles): a token's result is bit-identical alone and in any
-    batch of up to 32 tokens."""
+    whatever the other tokens (one, two or four 16-token MFMA tiles): a token's result is bit-identical alone and in
+    any batch of up to 64 tokens."""
     compact, case, layer = test_layers[name]
     runtime = HFFNRuntime([layer], device)
     runtime.force("gemv", "gemv")
-    x = torch.from_numpy(synth.make_input(case, 32)).to(device)
+    x = torch.from_numpy(synth.make_input(case, 64)).to(device)
     whole = runtime.forward(0, x).clone()
-    for start, size in ((0, 1), (7, 5), (3, 16), (16, 16), (5, 17), (31, 1)):
+    for start, size in ((0, 1), (7, 5), (3, 16), (16, 16), (5, 17), (31, 1), (20, 33), (0, 48), (63, 1)):
         assert torch.equal(runtime.forward(0, x[start:start + size].contiguous()), whole[start:start + size]), (start, size)
     expected = reference.forward(compact, x.cpu().numpy())
     assert _relative(whole, expected) <= 1e-5
 
 
-def test_gemv_refuses_more_than_32_tokens(test_layers, device):
+def test_gemv_refuses_more_than_64_tokens(test_layers, device):
     compact, case, layer = test_layers["homog_512_2048"]
     runtime = HFFNRuntime([layer], device)
     runtime.force("gemv", "gemv")
-    with pytest.raises(ValueError, match="above 32"):
-        runtime.forward(0, torch.from_numpy(synth.make_input(case, 33)).to(device))
+    with pytest.raises(ValueError, match="above 64"):
+        runtime.forward(0, torch.from_numpy(synth.make_input(case, 65)).to(device))
 
 
 def test_mfma_workspace_reused_at_shrinking_token_counts(test_layers, device):

@@ -69,7 +69,7 @@ def test_abi_refuses_bad_shapes_before_launching():
     gemv_needed = ctypes.c_uint64(0)
     assert lib.hffn_gemv_workspace(1024, 4096, ctypes.byref(gemv_needed)) == _lib.OK
     big = gemv_needed.value
-    _expect_argument_error(lib.hffn_forward_gemv(0, p, p, p, p, p, p, p, p, p, big, p, 1024, 4096, 33, None), "above 32")
+    _expect_argument_error(lib.hffn_forward_gemv(0, p, p, p, p, p, p, p, p, p, big, p, 1024, 4096, 65, None), "above 64")
     _expect_argument_error(lib.hffn_forward_gemv(0, p, p, p, p, p, p, p, p, p, big, p, 1024, 4000, 8, None), "multiples")
     _expect_argument_error(lib.hffn_forward_gemv(0, ctypes.c_void_p(20), p, p, p, p, p, p, p, p, big, p, 1024, 4096, 8, None), "aligned")
     _expect_argument_error(lib.hffn_forward_gemv(0, p, p, p, p, p, p, p, None, p, big, p, 1024, 4096, 8, None), "null")
@@ -84,7 +84,7 @@ def test_abi_refuses_bad_shapes_before_launching():
     _expect_argument_error(lib.hffn_grad_dense(p, p, None, p, p, p, 1024, 4096, 64, 64, work, dense.value, None), "null")
     _expect_argument_error(lib.hffn_grad_dense(p, p, p, p, p, p, 1024, 4096, 64, 64, work, dense.value - 1, None), "workspace")
     handle = ctypes.c_uint64(0)
-    _expect_argument_error(lib.hffn_plan_gemv(0, p, p, p, p, p, p, p, p, big, p, 1024, 4096, 33, ctypes.byref(handle)), "above 32")
+    _expect_argument_error(lib.hffn_plan_gemv(0, p, p, p, p, p, p, p, p, big, p, 1024, 4096, 65, ctypes.byref(handle)), "above 64")
     _expect_argument_error(lib.hffn_plan_gemv(0, p, p, p, p, p, p, ctypes.c_void_p(20), p, big, p, 1024, 4096, 8,
                                               ctypes.byref(handle)), "aligned")
     _expect_argument_error(lib.hffn_plan_gemv(0, p, p, p, p, p, p, p, p, big, p, 1024, 4096, 8, None), "null result")
@@ -126,16 +126,18 @@ def test_mfma_policy_crossovers():
 
 
 def test_planes_policy():
-    """Three-way estimate up to 32 tokens: on the Pythia-410M layer at 50 % the lane-per-slot kernels at 1-4 tokens,
-    the decode GEMVs from 8 to 32, the MFMA path above 32 (when its GEMMs are streamed); on the dense 2.8B-shape
+    """Estimates up to 64 tokens: on the Pythia-410M layer at 50 % the lane-per-slot kernels at 1-4 tokens, the decode
+    GEMVs from 8 to 40, the MFMA path at 64 and always above (when its GEMMs are streamed); on the dense 2.8B-shape
     layer the GEMVs up to 16 tokens and the MFMA path at 32; on the 1.4B layer at 20 % the gather kernels at 1-4
     tokens and the GEMVs at 16."""
     slots = 2 * 4096 * 512
     assert runtime.planes_mode(1, 1024, 4096, slots, True) is None
     assert runtime.planes_mode(2, 1024, 4096, slots, True) is None and runtime.planes_mode(4, 1024, 4096, slots, True) is None
-    assert all(runtime.planes_mode(n, 1024, 4096, slots, True) == "gemv" for n in (8, 16, 24, 32))
-    assert runtime.planes_mode(33, 1024, 4096, slots, True) == "mfma"
-    assert runtime.planes_mode(33, 1024, 4096, slots, False) is None
+    assert all(runtime.planes_mode(n, 1024, 4096, slots, True) == "gemv" for n in (8, 16, 24, 32, 33, 40))
+    assert runtime.planes_mode(64, 1024, 4096, slots, True) == "mfma"
+    assert runtime.planes_mode(65, 1024, 4096, slots, True) == "mfma"
+    assert runtime.planes_mode(65, 1024, 4096, slots, False) is None
+    assert runtime.planes_mode(48, 512, 2048, 2 * 2048 * 102, True) == "gemv"
     dense = 2 * 10240 * 2048
     assert all(runtime.planes_mode(n, 2560, 10240, dense, True) == "gemv" for n in (1, 4, 16))
     assert runtime.planes_mode(32, 2560, 10240, dense, True) == "mfma"
