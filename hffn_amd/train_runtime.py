@@ -13,11 +13,14 @@ and updates them in place. Added here, allocated at construction or by ``reserve
 * dense, shared by the layers: ``z``, ``gz`` ``[d_ff, ld]``, ``gy_t``, ``gx_t`` ``[d_model, ld]``, ``gx`` ``[N, d_model]``
   (``ld = leading_dim(N)``, the runtime's stride);
 * the tile partials of the two sampled products, ``[tiles, S]`` with ``S = nnz_down + d_model + nnz_up + d_ff``
-  columns, sized at construction for ``max_tokens`` and grown only by ``reserve``.
+  columns, sized at construction for ``max_tokens`` and grown only by ``reserve``;
+* for the dense sampled products (from ``GRAD_DENSE_MIN_TOKENS`` tokens): the planes of both operands over the tokens
+  and the GEMM's partials (``hffn_grad_dense_workspace``), sized like the tile partials.
 
 No dense ``W_up``, ``W_down``, gradient or moment exists. The kernels: the forward is the runtime's gather forward with
 ``z`` stored (``hffn_forward_z``); ``g_down``/``gb_down`` and ``g_up``/``gb_up`` are sampled products
-(``hffn_grad_sddmm``) over token tiles of 256, summed in tile order (``hffn_reduce_tiles``) above 256 tokens; ``gz`` is
+(``hffn_grad_sddmm``) over token tiles of 256, summed in tile order (``hffn_reduce_tiles``) above 256 tokens, or from
+64 tokens dense split-fp16 MFMA products gathered at the support (``hffn_grad_dense``, ``grad_mode``); ``gz`` is
 the rows up kernel over the hidden-major down support with a gelu' epilogue (``hffn_grad_hidden``); ``gx`` the rows
 down kernel over the input-major up support (``hffn_grad_x``); AdamW elementwise (``hffn_adamw``). fp32 values only.
 
@@ -325,7 +328,8 @@ class HFFNTrainRuntime:
 
     def nbytes(self, index: int) -> dict[str, int]:
         """Bytes of layer ``index``: values, gradients, moments, indices (runtime and transposed supports, with the values
-        in the transposed orders); dense workspace; the tile partials (shared, allocated size)."""
+        in the transposed orders); dense workspace (with the dense sampled products' planes and partials); the tile
+        partials (shared, allocated size)."""
         def size(tensors) -> int:
             return sum(t.numel() * t.element_size() for t in tensors)
         params = self.runtime._tensors[index]
@@ -334,5 +338,6 @@ class HFFNTrainRuntime:
                 "moments": size(t for pair in self._moments[index].values() for t in pair),
                 "indices": size(params[name] for name in ("up_offsets", "up_idx", "out_offsets", "out_hidden"))
                 + size(self._supports[index].values()) + size(self._transposed_values[index].values()),
-                "workspace": self.runtime.workspace_bytes() + size((self._z, self._gz, self._gy_t, self._gx_t, self._gx)),
+                "workspace": self.runtime.workspace_bytes() + size((self._z, self._gz, self._gy_t, self._gx_t, self._gx))
+                + self._dense_bytes,
                 "partials": size((self._partials,)) if self._partials is not None else 0}
