@@ -6,8 +6,8 @@
 //
 // Planes as the MFMA path keeps them (mfma.hip): planes[(((kt*2 + p)*4 + c)*rows + r)*8 + k % 8], kt = k / 32,
 // c = (k % 32) / 8, p = 0 hi / 1 lo, one power of two per row. A block takes 16 rows (neurons) over the whole K or
-// one of 2-8 k splits (blockIdx.y); its W waves (8; 16 when the row tiles alone leave CUs idle and K is not split; 4
-// when the row tiles outnumber the CUs)
+// one of 2-8 k splits (blockIdx.y); its W waves (16 when K is not split and the row tiles do not outnumber the CUs;
+// 4 when they do; 8 with k splits or a short K)
 // split that range in W spans of whole 32-k tiles. Per tile, lane (r, c) = (lane % 16, lane / 16) holds row r's
 // chunk c of both planes as the B operand (the 16 lanes of a chunk read 256 contiguous bytes), and the 8 inputs of
 // token r at the same k as the A operand, scaled by the token's power of two over the tile and split into fp16 hi and
@@ -177,8 +177,8 @@ void gemv_launch(const float* in, const _Float16* planes, const int32_t* exps, c
 }
 
 // 8 waves per block, with k splits (added by gemv_reduce_kernel) where gemv_splits finds them worth a second kernel;
-// else 16 waves per block when the row tiles alone leave CUs idle; 4 waves when there are more row tiles than one
-// block per CU (2-3 blocks of 4 waves then share a CU, so every block is resident from the start).
+// else 16 waves per block while the row tiles do not outnumber the CUs (more load streams per CU); 4 waves when
+// they do (2-3 blocks of 4 waves then share a CU, so every block is resident from the start).
 template <bool LO_B, bool UP>
 hipError_t gemv_side(const float* in, const void* planes, const int32_t* exps, const float* bias, float* out, float* partials,
                      uint32_t rows, uint32_t K, uint32_t n, hipStream_t stream) {
@@ -189,7 +189,7 @@ hipError_t gemv_side(const float* in, const void* planes, const int32_t* exps, c
         if (hipError_t status = hipGetLastError(); status != hipSuccess) return status;
         hipLaunchKernelGGL(gemv_reduce_kernel<UP>, dim3((n * rows + 255) / 256), dim3(256), 0, stream, partials, splits, exps, bias, out,
                            rows, n);
-    } else if (rows / kGemvRows < kGemvMinBlocks && K % (16 * kGemvK) == 0) {
+    } else if (rows / kGemvRows <= kGemvMinBlocks && K % (16 * kGemvK) == 0) {
         gemv_launch<16, LO_B, UP>(in, p, exps, bias, out, partials, 1, rows, K, n, stream);
     } else if (rows / kGemvRows > kGemvMinBlocks) {
         gemv_launch<4, LO_B, UP>(in, p, exps, bias, out, partials, 1, rows, K, n, stream);
