@@ -6,8 +6,8 @@
 //
 // Planes as the MFMA path keeps them (mfma.hip): planes[(((kt*2 + p)*4 + c)*rows + r)*8 + k % 8], kt = k / 32,
 // c = (k % 32) / 8, p = 0 hi / 1 lo, one power of two per row. A block takes 16 rows (neurons) over the whole K or
-// one of 2-8 k splits (blockIdx.y); its W waves (16 when K is not split and the row tiles do not outnumber the CUs;
-// 4 when they do; 8 with k splits or a short K)
+// one of 2-8 k splits (blockIdx.y); its W waves (16 when the row tiles, times the splits, do not outnumber the CUs
+// and K has a 32-k tile for each; 4 when the row tiles outnumber the CUs; else 8)
 // split that range in W spans of whole 32-k tiles. Per tile, lane (r, c) = (lane % 16, lane / 16) holds row r's
 // chunk c of both planes as the B operand (the 16 lanes of a chunk read 256 contiguous bytes), and the 8 inputs of
 // token r at the same k as the A operand, scaled by the token's power of two over the tile and split into fp16 hi and
@@ -176,16 +176,17 @@ void gemv_launch(const float* in, const _Float16* planes, const int32_t* exps, c
         hipLaunchKernelGGL((gemv_mfma_kernel<W, 4, LO_B, UP>), grid, block, 0, stream, in, planes, exps, bias, out, partials, rows, K, n);
 }
 
-// 8 waves per block, with k splits (added by gemv_reduce_kernel) where gemv_splits finds them worth a second kernel;
-// else 16 waves per block while the row tiles do not outnumber the CUs (more load streams per CU); 4 waves when
-// they do (2-3 blocks of 4 waves then share a CU, so every block is resident from the start).
+// k splits (added by gemv_reduce_kernel) where gemv_splits finds them worth a second kernel; 16 waves per block
+// while the blocks do not outnumber the CUs (more load streams per CU) and K allows, 4 waves when the row tiles do
+// outnumber them (2-3 blocks of 4 waves then share a CU, so every block is resident from the start), else 8.
 template <bool LO_B, bool UP>
 hipError_t gemv_side(const float* in, const void* planes, const int32_t* exps, const float* bias, float* out, float* partials,
                      uint32_t rows, uint32_t K, uint32_t n, hipStream_t stream) {
     const auto* p = static_cast<const _Float16*>(planes);
     const uint32_t splits = gemv_splits(rows, K, LO_B ? 4 : 2);
     if (splits > 1) {
-        gemv_launch<8, LO_B, UP>(in, p, exps, bias, out, partials, splits, rows, K, n, stream);
+        if (K % (16 * kGemvK * splits) == 0) gemv_launch<16, LO_B, UP>(in, p, exps, bias, out, partials, splits, rows, K, n, stream);
+        else gemv_launch<8, LO_B, UP>(in, p, exps, bias, out, partials, splits, rows, K, n, stream);
         if (hipError_t status = hipGetLastError(); status != hipSuccess) return status;
         hipLaunchKernelGGL(gemv_reduce_kernel<UP>, dim3((n * rows + 255) / 256), dim3(256), 0, stream, partials, splits, exps, bias, out,
                            rows, n);

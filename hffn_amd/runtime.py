@@ -51,7 +51,7 @@ MFMA_MIN_DENSITY = 0.05   # the lowest support density the tile-densified MFMA p
 EDGES_CALL_US, EDGES_PASS_US, EDGES_SLOT_US = 6.0, 4.0, 3.5e-6
 EDGES_PASS_WEIGHT = {1: 0.42, 2: 0.49, 4: 0.52, 8: 1.0}
 MFMA_BASE_US, MFMA_ENTRY_US, MFMA_TOKEN_US = 22.0, 0.93e-6, 0.1
-GEMV_BASE_US, GEMV_ENTRY_US, GEMV_TOKEN_US, GEMV_TILE2_US, GEMV_TILE2_TOKEN_US = 11.9, 0.482e-6, 0.019e-6, 0.04e-6, 0.2
+GEMV_BASE_US, GEMV_ENTRY_US, GEMV_TOKEN_US, GEMV_TILE2_US, GEMV_TILE2_TOKEN_US = 11.9, 0.482e-6, 0.019e-6, 0.038e-6, 0.084
 MAX_TOKENS = 1 << 18      # runtime/gpu/nvidia/common/kernels/hffn_cuda/runtime.py:26
 
 _VALUE_TYPES = {torch.float32: _lib.VALUE_F32, torch.bfloat16: _lib.VALUE_BF16}
