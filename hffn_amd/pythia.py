@@ -1,25 +1,30 @@
-"""Pythia (GPT-NeoX) with its FFNs executed dense or by the HFFN HIP runtime: the two-arm loader, its hook, the
-compact export format, and a writer of random-init Pythia-shaped checkpoints with synthetic exports.
+"""Pythia (GPT-NeoX) whose FFNs run dense or on the HFFN HIP runtime: the compact export format, the two-arm
+loader and its hook, and writers of random-init Pythia-shaped checkpoints with synthetic exports.
 
-Drop-in for the reference's shared Pythia level and its NVIDIA leaf:
+Interfaces kept from the reference (paths relative to its root):
 
-* ``load_pythia(model_dir, export_dir, ffn, device="cuda", make_runtime=None)`` — both
-  ``runtime/gpu/nvidia/llm/inference/hffn_pythia_cuda/model.py:23-28`` (leaf: the HIP runtime is built by default)
-  and ``runtime/common/pythia/hffn_pythia/model.py:82-111`` (shared: ``make_runtime(layers)`` given);
-* ``HFFNMLP(runtime, index)`` — ``model.py:27-37``: replaces ``block.mlp``; its output is a view of the runtime's
-  output buffer, consumed by the block's residual sum before the next FFN call;
-* ``layer_from_export(layer)`` — ``hffn_pythia_cuda/model.py:11-15``;
-* ``read_layer``/``read_layers``/``hidden_of_slot`` — ``runtime/common/pythia/hffn_pythia/export.py:13-57``, the
-  ``hffn_training_compact_g4_v2`` format, with its validation; ``write_layer`` writes the same format.
+* the export format ``hffn_training_compact_g4_v2`` (``runtime/common/pythia/hffn_pythia/export.py:13-57``): one
+  ``torch.save`` dict per layer, hidden-major ``up_*``/``down_*`` arrays, biases, and the four-group hidden
+  partition; ``read_layer(path, groups=False)`` returns its arrays and raises ``ValueError`` on a malformed file;
+* ``load_pythia(model_dir, export_dir, ffn, device, make_runtime)`` - both the NVIDIA leaf's loader
+  (``runtime/gpu/nvidia/llm/inference/hffn_pythia_cuda/model.py:23-28``, which builds the GPU runtime) and the shared
+  one (``runtime/common/pythia/hffn_pythia/model.py:82-111``, which takes ``make_runtime``); the HFFN arm exposes
+  ``model.hffn_runtime``;
+* ``HFFNMLP(runtime, index)`` (``model.py:27-37``) in place of ``block.mlp``; ``layer_from_export`` (leaf
+  ``model.py:11-15``); ``share_non_ffn(model, source)`` (``model.py:114-124``).
 
-Both arms build the same GPT-NeoX model, load the same non-FFN tensors from ``model_dir/model.safetensors`` and read
-the FFNs from the same export: the dense arm sets ``GPTNeoXMLP`` weights on the fixed support (zeros elsewhere), the
-HFFN arm never allocates a dense FFN and hands the activations to the runtime. Embeddings, attention (PyTorch SDPA),
-LayerNorm, KV cache and head stay PyTorch.
+How this module builds the arms:
+
+* every model is built from its ``config.json``; the HFFN arm is built with a zero-width MLP (``intermediate_size``
+  set to 0 while the modules are created, so the two projections hold no weight) and each block's MLP is then
+  replaced by ``HFFNMLP``: no dense FFN tensor is ever created for that arm;
+* the non-FFN tensors come from ``model.safetensors`` through ``load_state_dict(strict=False)``; the only keys allowed
+  to differ are the FFN's own and the attention buffers that older checkpoints carry and the model rebuilds itself;
+* the dense arm's two projections are the export's hidden-major stores read as CSR matrices (``up``: rows are
+  neurons over the input features; ``down``: rows are neurons over the outputs, transposed), densified by torch.
 """
 from __future__ import annotations
 
-from contextlib import contextmanager
 from pathlib import Path
 
 import numpy as np
@@ -27,47 +32,62 @@ import torch
 from torch import nn
 
 FORMAT = "hffn_training_compact_g4_v2"
-_TYPES = {
+# The arrays of one export and their dtypes (export.py:13-17): hidden-major offsets over d_ff + 1 entries, int16
+# feature indices, float32 values and biases.
+ARRAYS = {
     "up_row_offsets": torch.int32, "up_idx": torch.int16, "up_val": torch.float32, "b_up": torch.float32,
     "down_row_offsets": torch.int32, "down_idx": torch.int16, "down_val": torch.float32, "b_down": torch.float32,
 }
-# Buffers of older GPT-NeoX checkpoints that the model classes rebuild themselves.
-_LEGACY = (".attention.bias", ".attention.masked_bias", ".attention.rotary_emb.inv_freq")
+GROUPS = "group_hidden_offsets"  # int32[5]: the four hidden groups of the CPU runtimes, from 0 to d_ff
+# Attention buffers that checkpoints of older transformers releases hold and current GPT-NeoX modules recompute.
+REBUILT_BUFFERS = ("attention.bias", "attention.masked_bias", "attention.rotary_emb.inv_freq")
 
 
 # ------------------------------------------------------------------------------------------------- export format
 
+def _is_partition(bounds: torch.Tensor, total: int) -> bool:
+    """Whether ``bounds`` runs from 0 to ``total`` without ever decreasing."""
+    return bounds.numel() >= 1 and int(bounds[0]) == 0 and int(bounds[-1]) == total and not bool((bounds[1:] < bounds[:-1]).any())
+
+
 def read_layer(path: str | Path, *, groups: bool = False) -> dict:
-    """The validated arrays of one export file, as contiguous CPU tensors (``export.py:20-48``). With ``groups``,
-    also ``group_hidden_offsets`` (int32[5], 0 .. d_ff, monotonic)."""
+    """One export file as a dict of contiguous CPU tensors plus ``d_model`` and ``d_ff``; with ``groups`` also
+    ``group_hidden_offsets``. A file that is not a valid ``hffn_training_compact_g4_v2`` layer raises ``ValueError``
+    naming the first problem found."""
     path = Path(path)
-    raw = torch.load(path, map_location="cpu", weights_only=True)
-    if raw.get("format") != FORMAT:
-        raise ValueError(f"{path}: expected a {FORMAT} export")
-    layer: dict = {"d_model": int(raw["d_model"]), "d_ff": int(raw["d_ff"])}
-    for name, dtype in _TYPES.items():
-        if raw[name].dtype != dtype:
-            raise ValueError(f"{path}: {name} must be {dtype}")
-        layer[name] = raw[name].contiguous()
-    h, f = layer["d_model"], layer["d_ff"]
-    if layer["b_up"].numel() != f or layer["b_down"].numel() != h:
-        raise ValueError(f"{path}: bias dimensions do not match d_model/d_ff")
+    blob = torch.load(path, map_location="cpu", weights_only=True)
+    if not isinstance(blob, dict) or blob.get("format") != FORMAT:
+        raise ValueError(f"{path}: not a {FORMAT} layer file")
+    d_model, d_ff = int(blob["d_model"]), int(blob["d_ff"])
+    layer: dict = {"d_model": d_model, "d_ff": d_ff}
+    wanted = dict(ARRAYS, **({GROUPS: torch.int32} if groups else {}))
+    for name, dtype in wanted.items():
+        array = blob.get(name)
+        if not isinstance(array, torch.Tensor) or array.dtype != dtype or array.dim() != 1:
+            raise ValueError(f"{path}: {name} is missing or not a 1-D {dtype} array")
+        layer[name] = array.contiguous()
+    problems = []
+    if layer["b_up"].numel() != d_ff:
+        problems.append(f"b_up has {layer['b_up'].numel()} entries for d_ff {d_ff}")
+    if layer["b_down"].numel() != d_model:
+        problems.append(f"b_down has {layer['b_down'].numel()} entries for d_model {d_model}")
     for side in ("up", "down"):
         offsets, index, values = layer[f"{side}_row_offsets"], layer[f"{side}_idx"], layer[f"{side}_val"]
-        if offsets.numel() != f + 1 or int(offsets[0]) != 0 or int(offsets[-1]) != values.numel() or index.numel() != values.numel():
-            raise ValueError(f"{path}: invalid {side} hidden-major storage")
-        if bool((offsets.diff() < 0).any()) or (index.numel() and (int(index.min()) < 0 or int(index.max()) >= h)):
-            raise ValueError(f"{path}: invalid {side} offsets or feature index")
-    if groups:
-        partition = raw["group_hidden_offsets"]
-        if partition.dtype != torch.int32 or tuple(partition.shape) != (5,) or int(partition[0]) != 0 \
-                or int(partition[-1]) != f or bool((partition.diff() < 0).any()):
-            raise ValueError(f"{path}: invalid group_hidden_offsets")
-        layer["group_hidden_offsets"] = partition.contiguous()
+        if index.numel() != values.numel():
+            problems.append(f"{side}: {index.numel()} indices for {values.numel()} values")
+        elif offsets.numel() != d_ff + 1 or not _is_partition(offsets, values.numel()):
+            problems.append(f"{side}: the row offsets do not split the {values.numel()} slots over {d_ff} neurons")
+        elif index.numel() and not (0 <= int(index.min()) and int(index.max()) < d_model):
+            problems.append(f"{side}: feature index outside [0, {d_model})")
+    if groups and (layer[GROUPS].numel() != 5 or not _is_partition(layer[GROUPS], d_ff)):
+        problems.append(f"{GROUPS} is not a partition of the {d_ff} neurons into four groups")
+    if problems:
+        raise ValueError(f"{path}: " + "; ".join(problems))
     return layer
 
 
 def layer_path(export_dir: str | Path, index: int) -> Path:
+    """Where layer ``index`` of an export lives: ``<export_dir>/layer<index>/<FORMAT>.pt``."""
     return Path(export_dir) / f"layer{index}" / f"{FORMAT}.pt"
 
 
@@ -76,50 +96,63 @@ def read_layers(export_dir: str | Path, count: int) -> list[dict]:
 
 
 def write_layer(path: str | Path, layer: dict) -> None:
-    """Write one export file in the ``hffn_training_compact_g4_v2`` format (readable by ``read_layer``)."""
+    """Save one layer dict (the keys ``read_layer`` returns) in the export format."""
     path = Path(path)
     path.parent.mkdir(parents=True, exist_ok=True)
-    f = int(layer["d_ff"])
-    raw = {"format": FORMAT, "d_model": int(layer["d_model"]), "d_ff": f,
-           "group_hidden_offsets": layer.get("group_hidden_offsets",
-                                             torch.tensor([(g * f) // 4 for g in range(5)], dtype=torch.int32))}
-    for name, dtype in _TYPES.items():
-        raw[name] = layer[name].to(dtype).contiguous()
-    torch.save(raw, path)
+    d_ff = int(layer["d_ff"])
+    blob = {"format": FORMAT, "d_model": int(layer["d_model"]), "d_ff": d_ff}
+    blob.update({name: torch.as_tensor(layer[name]).to(dtype).contiguous() for name, dtype in ARRAYS.items()})
+    quarters = torch.tensor([d_ff * g // 4 for g in range(5)], dtype=torch.int32)
+    blob[GROUPS] = torch.as_tensor(layer.get(GROUPS, quarters)).to(torch.int32).contiguous()
+    torch.save(blob, path)
 
 
 def hidden_of_slot(layer: dict, side: str) -> torch.Tensor:
-    """Hidden neuron owning each compact slot of one side (int64[nnz])."""
-    return torch.repeat_interleave(torch.arange(layer["d_ff"]), layer[f"{side}_row_offsets"].diff().long())
+    """Owner neuron of every slot of one side, int64[nnz] (neuron r repeated for each of its slots)."""
+    counts = (layer[f"{side}_row_offsets"][1:] - layer[f"{side}_row_offsets"][:-1]).long()
+    return torch.arange(layer["d_ff"]).repeat_interleave(counts)
 
 
 def export_of_compact(compact) -> dict:
-    """The export dict of a compact hidden-major layer (``hffn_amd.synth.CompactLayer``)."""
-    t = torch.from_numpy
-    return {"d_model": compact.d_model, "d_ff": compact.d_ff, "up_row_offsets": t(compact.up_offsets),
-            "up_idx": t(compact.up_idx), "up_val": t(compact.up_val), "b_up": t(compact.b_up),
-            "down_row_offsets": t(compact.down_offsets), "down_idx": t(compact.down_idx),
-            "down_val": t(compact.down_val), "b_down": t(compact.b_down),
-            "group_hidden_offsets": t(compact.groups)}
+    """The layer dict of a compact hidden-major layer (``hffn_amd.synth.CompactLayer``)."""
+    pairs = (("up_row_offsets", "up_offsets"), ("up_idx", "up_idx"), ("up_val", "up_val"), ("b_up", "b_up"),
+             ("down_row_offsets", "down_offsets"), ("down_idx", "down_idx"), ("down_val", "down_val"),
+             ("b_down", "b_down"), (GROUPS, "groups"))
+    layer = {key: torch.from_numpy(np.ascontiguousarray(getattr(compact, field))) for key, field in pairs}
+    layer.update(d_model=compact.d_model, d_ff=compact.d_ff)
+    return layer
+
+
+def dense_projections(layer: dict) -> tuple[torch.Tensor, torch.Tensor]:
+    """float32 ``W_up [d_ff, d_model]`` and ``W_down [d_model, d_ff]``, zero outside the support: each side's
+    hidden-major store read as a CSR matrix with one row per neuron."""
+    shape = (layer["d_ff"], layer["d_model"])
+
+    def csr(side: str) -> torch.Tensor:
+        return torch.sparse_csr_tensor(layer[f"{side}_row_offsets"].long(), layer[f"{side}_idx"].long(),
+                                       layer[f"{side}_val"].float(), size=shape).to_dense()
+
+    return csr("up"), csr("down").T.contiguous()
 
 
 # ----------------------------------------------------------------------------------------------------- the hook
 
 class HFFNMLP(nn.Module):
-    """Replacement of ``block.mlp``. Its output is a view of the runtime's output buffer, which the block consumes
-    (residual sum) before the next FFN call overwrites it."""
+    """``block.mlp`` of the HFFN arm: the block's FFN input, flattened to tokens, through layer ``index`` of the
+    runtime. The result is a view of the runtime's output buffer; the block adds it into its residual before the next
+    FFN call overwrites it."""
 
     def __init__(self, runtime, index: int) -> None:
         super().__init__()
         self.runtime, self.index = runtime, index
 
     def forward(self, hidden_states: torch.Tensor) -> torch.Tensor:
-        shape = hidden_states.shape
-        return self.runtime.forward(self.index, hidden_states.reshape(-1, shape[-1])).view(shape)
+        width = hidden_states.shape[-1]
+        return self.runtime.forward(self.index, hidden_states.reshape(-1, width)).view(hidden_states.shape)
 
 
 def layer_from_export(layer: dict, device: str | torch.device | None = None):
-    """The ``HFFNLayer`` of one export layer (``read_layer``); the output-major store is built on the device."""
+    """``HFFNLayer`` of one layer dict; its output-major down store is built on the device."""
     from .runtime import HFFNLayer
     return HFFNLayer.from_hidden_major(layer["d_model"], layer["d_ff"], layer["b_up"], layer["up_row_offsets"],
                                        layer["up_idx"], layer["up_val"], layer["b_down"], layer["down_row_offsets"],
@@ -127,89 +160,100 @@ def layer_from_export(layer: dict, device: str | torch.device | None = None):
 
 
 def hip_runtime(layers: list[dict], device: str | torch.device = "cuda"):
-    """The HFFN HIP runtime of a model's export layers: ``PreparedRuntime`` (decode calls launched from per-(layer, N)
-    plans), as the reference leaf's ``_runtime`` (``runtime/gpu/nvidia/llm/inference/hffn_pythia_cuda/model.py:18-20``)."""
+    """The leaf's runtime of an export (the reference leaf's ``_runtime``, ``hffn_pythia_cuda/model.py:18-20``): a
+    ``PreparedRuntime``, whose decode calls launch from per-(layer, N) plans."""
     from .prepared_runtime import PreparedRuntime
     return PreparedRuntime([layer_from_export(layer, device) for layer in layers], device)
 
 
 # --------------------------------------------------------------------------------------------------- the loader
 
-@torch.no_grad()
-def _set_dense_mlp(mlp: nn.Module, layer: dict) -> None:
-    up, down = mlp.dense_h_to_4h, mlp.dense_4h_to_h
-    if tuple(up.weight.shape) != (layer["d_ff"], layer["d_model"]):
-        raise ValueError("export and model dimensions differ")
-    up.weight.zero_()
-    up.weight[hidden_of_slot(layer, "up"), layer["up_idx"].long()] = layer["up_val"].to(up.weight.dtype)
-    up.bias.copy_(layer["b_up"])
-    down.weight.zero_()
-    down.weight[layer["down_idx"].long(), hidden_of_slot(layer, "down")] = layer["down_val"].to(down.weight.dtype)
-    down.bias.copy_(layer["b_down"])
-
-
-@torch.no_grad()
-def _load_non_ffn(model: nn.Module, checkpoint: Path) -> None:
-    from safetensors import safe_open
-    targets = {name: tensor for name, tensor in model.state_dict().items() if ".mlp." not in name}
-    with safe_open(str(checkpoint), framework="pt", device="cpu") as source:
-        names = [name for name in source.keys() if ".mlp." not in name and (name in targets or not name.endswith(_LEGACY))]
-        if set(names) != set(targets):
-            raise ValueError(f"checkpoint and model tensors differ: {sorted(set(names) ^ set(targets))}")
-        for name in names:
-            targets[name].copy_(source.get_tensor(name))
-
-
-class _NoFFN(nn.Module):
-    """Parameterless stand-in for ``GPTNeoXMLP`` while the HFFN arm is built: no dense FFN is allocated (nor
-    initialised); ``HFFNMLP`` takes its place before the model is used."""
-
-    def __init__(self, config):
-        super().__init__()
-
-
-@contextmanager
-def without_dense_ffn():
-    from transformers.models.gpt_neox import modeling_gpt_neox
-    original = modeling_gpt_neox.GPTNeoXMLP
-    modeling_gpt_neox.GPTNeoXMLP = _NoFFN
+def _build(config, ffn_width: int | None = None) -> nn.Module:
+    """A float32 causal LM of ``config``; with ``ffn_width`` the MLPs are created that wide (0: no FFN weights) and
+    the config keeps its own width afterwards."""
+    from transformers import AutoModelForCausalLM
+    if ffn_width is None:
+        return AutoModelForCausalLM.from_config(config, dtype=torch.float32)
+    width = config.intermediate_size
+    config.intermediate_size = ffn_width
     try:
-        yield
+        model = AutoModelForCausalLM.from_config(config, dtype=torch.float32)
     finally:
-        modeling_gpt_neox.GPTNeoXMLP = original
+        config.intermediate_size = width
+    model.config.intermediate_size = width
+    return model
+
+
+def _is_ffn(name: str) -> bool:
+    return ".mlp." in name
+
+
+def _load_attention_and_embeddings(model: nn.Module, checkpoint: Path) -> None:
+    """Every non-FFN tensor of the model from ``checkpoint`` (safetensors). FFN keys are ignored on both sides; the
+    checkpoint may also hold buffers the model rebuilds (``REBUILT_BUFFERS``); anything else that does not match is a
+    ``ValueError``."""
+    from safetensors.torch import load_file
+    state = {name: tensor for name, tensor in load_file(str(checkpoint)).items() if not _is_ffn(name)}
+    missing, unexpected = model.load_state_dict(state, strict=False)
+    missing = [name for name in missing if not _is_ffn(name)]
+    unexpected = [name for name in unexpected if not name.endswith(REBUILT_BUFFERS)]
+    if missing or unexpected:
+        raise ValueError(f"{checkpoint} does not fit the model: missing {sorted(missing)}, extra {sorted(unexpected)}")
 
 
 def load_pythia(model_dir: str | Path, export_dir: str | Path, ffn: str, device: str | torch.device = "cuda",
                 make_runtime=None) -> nn.Module:
-    """Pythia in eval mode (float32, on ``device``) with its FFNs from ``export_dir``, executed dense or by HFFN.
-
-    ``make_runtime(layers)`` builds the HFFN runtime from the export layers (default: the HIP runtime on ``device``);
-    it is called for the HFFN arm only, so the dense arm needs no GPU kernel. The HFFN arm exposes its runtime as
-    ``model.hffn_runtime`` (None in the dense arm)."""
-    from transformers import AutoConfig, AutoModelForCausalLM
+    """A Pythia model in eval mode (float32, on ``device``, no gradients) whose FFNs come from ``export_dir``:
+    ``ffn="dense"`` runs them as the model's own ``GPTNeoXMLP`` on the densified support, ``ffn="hffn"`` through
+    ``HFFNMLP`` and the runtime ``make_runtime(layers)`` builds from the layer dicts (default: ``hip_runtime`` on
+    ``device``), which is exposed as ``model.hffn_runtime`` (None for the dense arm)."""
+    from transformers import AutoConfig
     if ffn not in ("dense", "hffn"):
-        raise ValueError("ffn must be 'dense' or 'hffn'")
+        raise ValueError(f"ffn is 'dense' or 'hffn', not {ffn!r}")
+    model_dir = Path(model_dir)
     config = AutoConfig.from_pretrained(str(model_dir))
-    if ffn == "hffn":
-        with without_dense_ffn():
-            model = AutoModelForCausalLM.from_config(config, dtype=torch.float32)
-        assert not any(".mlp." in name for name, _ in model.named_parameters())
-    else:
-        model = AutoModelForCausalLM.from_config(config, dtype=torch.float32)
-    _load_non_ffn(model, Path(model_dir) / "model.safetensors")
+    model = _build(config, ffn_width=0 if ffn == "hffn" else None)
+    _load_attention_and_embeddings(model, model_dir / "model.safetensors")
     blocks = model.gpt_neox.layers
     layers = read_layers(export_dir, len(blocks))
     runtime = None
     if ffn == "dense":
-        for block, layer in zip(blocks, layers):
-            _set_dense_mlp(block.mlp, layer)
+        with torch.no_grad():
+            for block, layer in zip(blocks, layers):
+                up, down = block.mlp.dense_h_to_4h, block.mlp.dense_4h_to_h
+                if tuple(up.weight.shape) != (layer["d_ff"], layer["d_model"]):
+                    raise ValueError(f"export layer of {layer['d_model']} x {layer['d_ff']} does not fit an MLP of "
+                                     f"{tuple(up.weight.shape[::-1])}")
+                w_up, w_down = dense_projections(layer)
+                up.weight.copy_(w_up)
+                up.bias.copy_(layer["b_up"])
+                down.weight.copy_(w_down)
+                down.bias.copy_(layer["b_down"])
     else:
-        runtime = (make_runtime or (lambda ls: hip_runtime(ls, device)))(layers)
+        runtime = make_runtime(layers) if make_runtime is not None else hip_runtime(layers, device)
         for index, block in enumerate(blocks):
             block.mlp = HFFNMLP(runtime, index)
+        if any(_is_ffn(name) for name, _ in model.named_parameters()):
+            raise RuntimeError("the HFFN arm still holds FFN parameters")
     model = model.to(device).eval().requires_grad_(False)
     model.hffn_runtime = runtime
     return model
+
+
+@torch.no_grad()
+def share_non_ffn(model: nn.Module, source: nn.Module) -> None:
+    """Point every non-FFN parameter of ``model`` at the tensor ``source`` holds under the same name (both arms loaded
+    from one checkpoint), so that two arms in one process read one copy of those weights and differ by their FFNs
+    only."""
+    for name, parameter in source.named_parameters():
+        if _is_ffn(name):
+            continue
+        owner_name, _, attribute = name.rpartition(".")
+        owner = model.get_submodule(owner_name)
+        current = getattr(owner, attribute)
+        if current.shape != parameter.shape:
+            raise ValueError(f"{name}: {tuple(current.shape)} in the model, {tuple(parameter.shape)} in the source")
+        setattr(owner, attribute, parameter)
 
 
 # ------------------------------------------------------------------------------ random-init Pythia-shaped models
@@ -233,19 +277,17 @@ def pythia_config(**overrides):
 
 
 def write_random_checkpoint(model_dir: str | Path, seed: int = 104, **config_overrides):
-    """Write a random-init Pythia-shaped checkpoint: ``config.json`` + ``model.safetensors`` of the non-FFN tensors,
-    initialised by the model class from ``torch.manual_seed(seed)``. Returns the config."""
+    """Write ``config.json`` and a ``model.safetensors`` of the non-FFN tensors of a model initialised by its classes
+    after ``torch.manual_seed(seed)``. Returns the config."""
     from safetensors.torch import save_file
-    from transformers import AutoModelForCausalLM
     config = pythia_config(**config_overrides)
     model_dir = Path(model_dir)
     model_dir.mkdir(parents=True, exist_ok=True)
     config.save_pretrained(str(model_dir))
     torch.manual_seed(seed)
-    with without_dense_ffn():
-        model = AutoModelForCausalLM.from_config(config, dtype=torch.float32)
-    state = {name: tensor.contiguous() for name, tensor in model.state_dict().items() if ".mlp." not in name}
-    save_file(state, str(model_dir / "model.safetensors"))
+    model = _build(config, ffn_width=0)
+    save_file({name: tensor.contiguous() for name, tensor in model.state_dict().items() if not _is_ffn(name)},
+              str(model_dir / "model.safetensors"))
     return config
 
 
@@ -267,19 +309,6 @@ def write_random_pythia(model_dir: str | Path, export_dir: str | Path, density: 
     (``write_random_exports``)."""
     config = write_random_checkpoint(model_dir, seed, **config_overrides)
     write_random_exports(export_dir, config, density, seed)
-
-
-@torch.no_grad()
-def share_non_ffn(model: nn.Module, source: nn.Module) -> None:
-    """Make ``model`` read the non-FFN parameters of ``source`` (both loaded from the same checkpoint) instead of its
-    own copy, so that two arms in one process differ by their FFNs only (``runtime/common/pythia/hffn_pythia/
-    model.py:114-124``)."""
-    owned = dict(source.named_parameters())
-    for prefix, module in model.named_modules():
-        for key, parameter in list(module._parameters.items()):
-            name = f"{prefix}.{key}" if prefix else key
-            if parameter is not None and ".mlp." not in name:
-                module._parameters[key] = owned[name]
 
 
 def synthetic_prompts(batch: int, length: int, vocab: int, seed: int = 1041) -> torch.Tensor:

@@ -350,3 +350,46 @@ def _cached(name: str):
     if name not in _CACHE:
         _CACHE[name] = synth.make_workload_layer(name)
     return _CACHE[name]
+
+
+@pytest.fixture(scope="module")
+def w2p8b(device):
+    workload = synth.WORKLOADS["pythia2p8b_d80_zipf_bf16"]
+    compact = _cached(workload.name)
+    return compact, workload, HFFNRuntime([hip_layer(compact)], device), reference.dense_weights(compact)
+
+
+@pytest.mark.parametrize("n", [1, 16, 26, 64])
+def test_2p8b_zipf_forced_pairs(n, w2p8b, device):
+    """Pythia-2.8B shape, uneven fan-in (support sizes clip(N(2048, 300), 256, 2560)) with Zipf-biased indices, bf16:
+    the policy and every forced pair (edges, rows and their mixes, the decode GEMVs, the MFMA path) against the float64
+    oracle on the same (bf16-exact) weights. The stated bf16 bound is 2e-2; the fp32 accumulation of ~2048-term rows
+    is held to 5e-5."""
+    compact, workload, runtime, weights = w2p8b
+    x_np = synth.make_input(workload, n)
+    expected = torch.from_numpy(reference.forward_dense(compact, x_np, weights)).to(device)
+    result = parity.check(runtime, 0, torch.from_numpy(x_np).to(device), expected)
+    assert result.repeatable
+    assert result.relative <= 5e-5, result.pairs
+    assert {("edges", "edges"), ("rows", "rows"), ("gemv", "gemv"), ("mfma", "mfma")} <= set(result.pairs)
+
+
+@pytest.mark.parametrize("name,tokens", [("pythia410m_d50", (33, 40, 48, 64)), ("pythia1p4b_d20_bf16", (24, 32, 64))])
+def test_gemv_wide_calls(name, tokens, device):
+    """The decode GEMVs at 17-64 tokens on the workload layers: two and four 16-token MFMA tiles, the 16-wave k-split
+    kernel and its ordered reduction (410M down side), the 4-wave blocks with several token tiles (1.4B up side).
+    Each call within 1e-5 relative of the float64 oracle, and every token's result bit-identical alone and inside the
+    batch."""
+    workload = synth.WORKLOADS[name]
+    compact = _cached(name)
+    runtime = HFFNRuntime([hip_layer(compact)], device)
+    runtime.force("gemv", "gemv")
+    weights = reference.dense_weights(compact)
+    for n in tokens:
+        x_np = synth.make_input(workload, n)
+        x = torch.from_numpy(x_np).to(device)
+        whole = runtime.forward(0, x).clone()
+        assert _relative(whole, reference.forward_dense(compact, x_np, weights)) <= 1e-5, n
+        for start, size in ((0, 1), (n - 1, 1), (n // 2, n - n // 2), (3, 16)):
+            part = runtime.forward(0, x[start:start + size].contiguous())
+            assert torch.equal(part, whole[start:start + size]), (n, start, size)
