@@ -10,7 +10,7 @@ import ctypes
 from pathlib import Path
 
 LIBRARY = Path(__file__).resolve().with_name("libhffn_amd.so")
-ABI_VERSION = 9
+ABI_VERSION = 10
 
 OK = 0
 VALUE_F32, VALUE_BF16 = 0, 1
@@ -53,6 +53,7 @@ SIGNATURES = {
     "hffn_gemv_workspace": [_U32, _U32, _P],
     "hffn_forward_gemv": [_I] + [_P] * 9 + [_U64, _P] + [_U32] * 3 + [_P],
     "hffn_plan_gemv": [_I] + [_P] * 8 + [_U64, _P] + [_U32] * 3 + [_P],
+    "hffn_forward_gemv_static": [_I] + [_P] * 9 + [_U32] * 3 + [_P],
 }
 
 

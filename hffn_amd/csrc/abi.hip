@@ -425,6 +425,25 @@ int hffn_forward_gemv(int value_type, const float* x, const void* up_planes, con
                     "forward (gemv)");
 }
 
+int hffn_forward_gemv_static(int value_type, const float* x, const void* up_planes, const int32_t* up_binades, const float* b_up,
+                             const void* down_planes, const int32_t* down_binades, const float* b_down, float* act, float* y,
+                             uint32_t d_model, uint32_t d_ff, uint32_t n, void* stream) {
+    const uint64_t limit = hffn::gemv_scratch_bytes();
+    if (int status = check_gemv(value_type, d_model, d_ff, n)) return status;
+    const uint64_t needed = hffn::gemv_workspace_bytes(d_model, d_ff);
+    if (needed > limit)
+        return fail(HFFN_ERROR_ARGUMENT, "forward_gemv_static: d_model=%u d_ff=%u need %llu bytes of partials, beyond the %llu-byte static scratch",
+                    d_model, d_ff, static_cast<unsigned long long>(needed), static_cast<unsigned long long>(limit));
+    float* scratch = nullptr;
+    if (int status = launched(hffn::gemv_scratch_address(&scratch), "forward_gemv_static: scratch address")) return status;
+    if (int status = check_gemv_call(value_type, x, up_planes, up_binades, b_up, down_planes, down_binades, b_down, act, scratch,
+                                     limit, y, d_model, d_ff, n))
+        return status;
+    return launched(hffn::launch_gemv_forward(value_type, x, up_planes, up_binades, b_up, down_planes, down_binades, b_down, act,
+                                              scratch, y, d_model, d_ff, n, static_cast<hipStream_t>(stream)),
+                    "forward (gemv, static scratch)");
+}
+
 int hffn_plan_gemv(int value_type, const void* up_planes, const int32_t* up_binades, const float* b_up, const void* down_planes,
                    const int32_t* down_binades, const float* b_down, float* act, void* workspace, uint64_t workspace_bytes, float* y,
                    uint32_t d_model, uint32_t d_ff, uint32_t n, uint64_t* plan) {

@@ -20,7 +20,9 @@
 // Up: act[t, r] = gelu(b_up[r] + sum_k W_up[r, k] x[t, k]) (token-major act); down: y[t, o] = b_down[o] +
 // sum_r W_down[o, r] act[t, r].
 #include <algorithm>
+#include <mutex>
 
+#include "../../include/hffn_amd.h"
 #include "common.hpp"
 #include "launch.hpp"
 
@@ -200,7 +202,34 @@ hipError_t gemv_side(const float* in, const void* planes, const int32_t* exps, c
     return hipGetLastError();
 }
 
+// The k-split partials of the allocation-free entry point: one array per GPU, alive until the process ends. Splits
+// are taken only while rows / 16 * splits <= kGemvMinBlocks, so a split side holds at most 16 * kGemvMinBlocks rows'
+// worth of partials for kGemvMaxTokens tokens: 64 * 4096 floats (1 MiB) for every shape.
+constexpr size_t kScratchFloats = size_t(kGemvMaxTokens) * kGemvRows * kGemvMinBlocks;
+static __device__ __align__(256) float scratch[kScratchFloats];
+static_assert(sizeof(scratch) == HFFN_GEMV_STATIC_SCRATCH_BYTES, "the header states the scratch size");
+
+constexpr int kMaxDevices = 64;
+std::mutex g_scratch_mutex;
+float* g_scratch[kMaxDevices] = {};  // device address of `scratch` on each GPU, looked up once per GPU
+
 }  // namespace
+
+size_t gemv_scratch_bytes() { return kScratchFloats * sizeof(float); }
+
+hipError_t gemv_scratch_address(float** address) {
+    int device = 0;
+    if (const hipError_t status = hipGetDevice(&device); status != hipSuccess) return status;
+    if (device < 0 || device >= kMaxDevices) return hipErrorInvalidDevice;
+    const std::lock_guard<std::mutex> lock(g_scratch_mutex);
+    if (!g_scratch[device]) {
+        void* found = nullptr;
+        if (const hipError_t status = hipGetSymbolAddress(&found, HIP_SYMBOL(scratch)); status != hipSuccess) return status;
+        g_scratch[device] = static_cast<float*>(found);
+    }
+    *address = g_scratch[device];
+    return hipSuccess;
+}
 
 size_t gemv_workspace_bytes(uint32_t d, uint32_t h) {
     const size_t up = gemv_splits(h, d, 4), down = gemv_splits(d, h, 4);  // fp32 weights split at least as often

@@ -100,6 +100,11 @@ hipError_t launch_grad_dense(const float* row, const float* mat, const int32_t* 
 // [n, d]; `work` (gemv_workspace_bytes) holds the k-split partial sums.
 constexpr uint32_t kGemvMaxTokens = 64;
 size_t gemv_workspace_bytes(uint32_t d, uint32_t h);
+// The library's own k-split partials for callers that cannot allocate: a file-scope device array of
+// gemv_scratch_bytes() per GPU; gemv_scratch_address gives its address on the current device (looked up once per
+// device with hipGetSymbolAddress). Calls that overlap on one GPU share it and race.
+size_t gemv_scratch_bytes();
+hipError_t gemv_scratch_address(float** address);
 hipError_t launch_gemv_forward(int vt, const float* x, const void* up_planes, const int32_t* up_exps, const float* b_up,
                                const void* down_planes, const int32_t* down_exps, const float* b_down, float* act, float* work,
                                float* y, uint32_t d, uint32_t h, uint32_t n, hipStream_t stream);

@@ -27,7 +27,7 @@
 extern "C" {
 #endif
 
-#define HFFN_ABI_VERSION 9
+#define HFFN_ABI_VERSION 10
 
 #define HFFN_OK 0
 #define HFFN_ERROR_ARGUMENT (-1) /* invalid shape, mode, pointer or workspace */
@@ -177,6 +177,17 @@ int hffn_gemv_workspace(uint32_t d_model, uint32_t d_ff, uint64_t* bytes);
 int hffn_forward_gemv(int value_type, const float* x, const void* up_planes, const int32_t* up_binades, const float* b_up,
                       const void* down_planes, const int32_t* down_binades, const float* b_down, float* act, void* workspace,
                       uint64_t workspace_bytes, float* y, uint32_t d_model, uint32_t d_ff, uint32_t n, void* stream);
+
+/* hffn_forward_gemv without a workspace argument, for callers that cannot allocate device memory (code under HIP graph
+ * capture, tight serving loops, harnesses that forbid hipMalloc). No counterpart in the reference. The k-split partial
+ * sums go to the library's own static device array (HFFN_GEMV_STATIC_SCRATCH_BYTES per GPU, held until the process
+ * ends; its address on the current device is looked up once per device); shapes needing more are refused with
+ * HFFN_ERROR_ARGUMENT, and no call allocates or frees anything. The partials need no initial contents. Every call on
+ * one GPU shares that GPU's array: calls that overlap on one GPU (several streams or threads) race. */
+#define HFFN_GEMV_STATIC_SCRATCH_BYTES (1u << 20)
+int hffn_forward_gemv_static(int value_type, const float* x, const void* up_planes, const int32_t* up_binades, const float* b_up,
+                             const void* down_planes, const int32_t* down_binades, const float* b_down, float* act, float* y,
+                             uint32_t d_model, uint32_t d_ff, uint32_t n, void* stream);
 
 /* Prepared decode-GEMV forward: checks every argument of hffn_forward_gemv but x and the stream and keeps them under a
  * new nonzero handle, launched by hffn_plan_launch (which then checks x's alignment) and dropped by hffn_plan_release,
