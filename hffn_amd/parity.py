@@ -21,10 +21,13 @@ PAIRS = [(None, None)] + [(up, down) for up in GATHER for down in GATHER] + [("m
 
 @dataclass
 class Parity:
-    error: float           # max |y - y_float64| over the pairs
-    relative: float        # max |y - y_float64| / max(1, |y_float64|) over the pairs
-    repeatable: bool       # every pair gives the same bits on a second call
-    pairs: dict            # (up, down) -> max |y - y_float64| of that pair
+    """Worst figures over the pairs run: ``error`` the largest absolute distance to the float64 expectation,
+    ``relative`` the largest distance scaled by max(1, |expected|), ``repeatable`` whether every pair reproduced its
+    own bits on a second call, ``pairs`` the absolute distance of each (up, down) pair."""
+    error: float
+    relative: float
+    repeatable: bool
+    pairs: dict
 
 
 def check(runtime: HFFNRuntime, index: int, x: torch.Tensor, expected: torch.Tensor, pairs=PAIRS) -> Parity:

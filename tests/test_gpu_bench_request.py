@@ -15,7 +15,7 @@ pytestmark = pytest.mark.gpu
 def test_smoke_grid_on_a_tiny_model(tmp_path, device):
     bench_request.prepare(tmp_path / "assets", {1: TINY}, [50])
     out = tmp_path / "out"
-    code = bench_request.orchestrate(bench_request.hip_adapter(), "smoke", tmp_path / "assets", out, densities=[50], sizes=[1])
+    code = bench_request.Campaign(bench_request.hip_adapter(), "smoke", tmp_path / "assets", out, densities=[50], sizes=[1]).run()
     summary = json.loads((out / "summary.json").read_text())
     assert code == 0, summary["failure"]
     assert summary["verdict"]["gate_passed"] and len(summary["cells"]) == 2

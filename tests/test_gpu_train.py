@@ -207,6 +207,43 @@ def test_backward_needs_its_forward(device):
         train.backward(0, gy[:4].contiguous())
     with pytest.raises(ValueError, match="z must be"):
         train.forward(0, x, torch.empty(10, device=device))
+    for pair in ("gemv", "mfma"):  # the planes paths keep no float32 activations: refused, not a KeyError
+        runtime.force(pair, pair)
+        with pytest.raises(ValueError, match="gather kernels"):
+            train.forward(0, x, train._z)
+    runtime.force(None, None)
+
+
+def test_transposed_supports_are_positions_into_the_runtime_arrays(device):
+    """The training supports, built on the device by the stable counting sort with slot positions as its payload: up
+    slots by input (hidden ascending per input) and down edges by neuron (output ascending per neuron), as positions
+    into the runtime's arrays; checked against a brute-force build on a layer with repeated indices in a row and
+    neurons without slots."""
+    from oracle import transpose
+    rng = np.random.default_rng(4)
+    d_model, d_ff = 48, 70
+    degrees = rng.integers(0, 12, d_ff)
+    degrees[::9] = 0
+    offsets = np.zeros(d_ff + 1, np.int32)
+    offsets[1:] = np.cumsum(degrees)
+    up_idx = rng.integers(0, d_model, offsets[-1]).astype(np.int16)
+    down_idx = rng.integers(0, d_model, offsets[-1]).astype(np.int16)
+    values = lambda size: rng.standard_normal(size).astype(np.float32)  # noqa: E731
+    compact = synth.CompactLayer(d_model, d_ff, synth._groups(d_ff), offsets, up_idx, values(up_idx.size), values(d_ff),
+                                 offsets, down_idx, values(down_idx.size), values(d_model))
+    train = HFFNTrainRuntime(HFFNRuntime([hip_layer(compact)], device, dense=False))
+    s = {k: v.cpu().numpy() for k, v in train.supports(0).items()}
+    up_owner = owners(compact.up_offsets, compact.d_ff)
+    by_input = sorted(range(up_owner.size), key=lambda e: (int(compact.up_idx[e]), e))
+    assert s["in_pos"].tolist() == by_input
+    assert s["in_hidden"].tolist() == [int(up_owner[e]) for e in by_input]
+    assert np.array_equal(s["in_offsets"], np.concatenate([[0], np.cumsum(np.bincount(compact.up_idx, minlength=d_model))]))
+    out_offsets, out_hidden, _ = transpose.output_major(d_model, d_ff, compact.down_offsets, compact.down_idx, compact.down_val)
+    out_output = owners(out_offsets, d_model)
+    by_neuron = sorted(range(out_hidden.size), key=lambda q: (int(out_hidden[q]), q))
+    assert s["hid_pos"].tolist() == by_neuron
+    assert s["hid_output"].tolist() == [int(out_output[q]) for q in by_neuron]
+    assert np.array_equal(s["hid_offsets"], np.concatenate([[0], np.cumsum(np.bincount(out_hidden, minlength=d_ff))]))
 
 
 def test_inference_after_training_reads_the_updated_values(device):

@@ -6,7 +6,7 @@
 * the AdamW closed form against ``torch.optim.AdamW`` in float64 over several steps;
 * planted mistakes in the oracle (GELU derivative without its density term, a dropped bias gradient, a transposed
   sampled product) are caught by the autograd comparison;
-* the transposed supports of the training runtime (positions into the runtime's arrays) against a brute-force build.
+* the token tiles of the gather sampled products.
 """
 from __future__ import annotations
 
@@ -15,7 +15,7 @@ import pytest
 import torch
 
 from hffn_amd import synth
-from hffn_amd.train_runtime import grad_tiles, transposed_supports
+from hffn_amd.train_runtime import grad_tiles
 from oracle import train as oracle_train
 from oracle.reference import owners
 
@@ -125,31 +125,6 @@ def test_planted_mistakes_are_caught(mistake, monkeypatch):
             got["g_up"] = dense.T[layer.up_idx.astype(np.int64) % layer.d_model, up_owner % layer.d_model]
     with pytest.raises(AssertionError):
         _assert_groups_close(got, expected)
-
-
-def test_transposed_supports_are_positions_into_the_runtime_arrays():
-    """Input-major up slots and hidden-major down edges, stable (hidden ascending per input, output ascending per
-    neuron), built from the output-major store the runtime holds; checked against a brute-force build."""
-    from oracle import transpose
-    from types import SimpleNamespace
-    compact = _random_layer(40, 70, 9, seed=4, repeats=True)
-    out_offsets, out_hidden, _ = transpose.output_major(compact.d_model, compact.d_ff, compact.down_offsets,
-                                                        compact.down_idx, compact.down_val)
-    t = torch.from_numpy
-    layer = SimpleNamespace(d_model=compact.d_model, d_ff=compact.d_ff, up_offsets=t(compact.up_offsets), up_idx=t(compact.up_idx),
-                            out_offsets=t(out_offsets), out_hidden=t(out_hidden))
-    s = {k: v.numpy() for k, v in transposed_supports(layer).items()}
-    up_owner = owners(compact.up_offsets, compact.d_ff)
-    expected_in = [(int(compact.up_idx[e]), int(up_owner[e]), e) for e in range(len(up_owner))]
-    expected_in.sort(key=lambda item: (item[0], item[2]))
-    assert [int(v) for v in s["in_pos"]] == [e for _, _, e in expected_in]
-    assert [int(v) for v in s["in_hidden"]] == [r for _, r, _ in expected_in]
-    assert np.array_equal(s["in_offsets"], np.concatenate([[0], np.cumsum(np.bincount(compact.up_idx, minlength=compact.d_model))]))
-    out_output = owners(out_offsets, compact.d_model)
-    expected_hid = sorted(range(len(out_hidden)), key=lambda q: (int(out_hidden[q]), q))
-    assert [int(v) for v in s["hid_pos"]] == expected_hid
-    assert [int(v) for v in s["hid_output"]] == [int(out_output[q]) for q in expected_hid]
-    assert np.array_equal(s["hid_offsets"], np.concatenate([[0], np.cumsum(np.bincount(out_hidden, minlength=compact.d_ff))]))
 
 
 def test_grad_tiles():
