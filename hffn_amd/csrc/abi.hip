@@ -198,9 +198,59 @@ struct GemvPlan {
     uint32_t d_model, d_ff, n;
 };
 
-std::mutex g_plans_mutex;  // guards both tables and the handle counter (handles are unique across them)
+std::mutex g_plans_mutex;  // guards the plan tables and the handle counter (handles are unique across them)
 std::unordered_map<uint64_t, Plan> g_plans;
 std::unordered_map<uint64_t, GemvPlan> g_gemv_plans;
+int check_tiles(int value_type, uint32_t d_model, uint32_t d_ff, uint32_t n) {
+    if (!valid_value_type(value_type)) return fail(HFFN_ERROR_ARGUMENT, "unknown value type %d", value_type);
+    if (d_model == 0 || d_model % 16 != 0 || d_model > HFFN_MAX_WIDTH || d_ff == 0 || d_ff % 8 != 0 || d_ff > HFFN_MAX_WIDTH)
+        return fail(HFFN_ERROR_ARGUMENT, "tiles path: d_model=%u must be a multiple of 16 and d_ff=%u of 8, both at most %u", d_model,
+                    d_ff, HFFN_MAX_WIDTH);
+    if (n == 0 || n > hffn::kTilesMaxTokens) return fail(HFFN_ERROR_ARGUMENT, "tiles path: n=%u outside [1, %u]", n, hffn::kTilesMaxTokens);
+    return HFFN_OK;
+}
+
+struct TilesPlan {
+    int value_type;
+    const int16_t* up_idx;
+    const void* up_val;
+    const int32_t* up_index;
+    const float* b_up;
+    const int16_t* out_hidden;
+    const void* out_val;
+    const int32_t* down_index;
+    const float* b_down;
+    float* act;
+    void* workspace;
+    uint64_t workspace_bytes;
+    float* y;
+    uint32_t d_model, d_ff, nnz_up, nnz_down, n;
+};
+
+int check_tiles_call(const TilesPlan& p, const float* x) {
+    if (int status = check_tiles(p.value_type, p.d_model, p.d_ff, p.n)) return status;
+    if (!x || !p.up_idx || !p.up_val || !p.up_index || !p.b_up || !p.out_hidden || !p.out_val || !p.down_index || !p.b_down || !p.act ||
+        !p.workspace || !p.y)
+        return fail(HFFN_ERROR_ARGUMENT, "forward_tiles: null pointer");
+    if (reinterpret_cast<uintptr_t>(x) % 16 != 0 || reinterpret_cast<uintptr_t>(p.act) % 16 != 0)
+        return fail(HFFN_ERROR_ARGUMENT, "forward_tiles: x and act must be 16-byte aligned");
+    if (int status = check_store_alignment(p.up_idx, p.up_val, p.value_type)) return status;
+    if (int status = check_store_alignment(p.out_hidden, p.out_val, p.value_type)) return status;
+    const uint64_t needed = hffn::tiles_workspace_bytes(p.n, p.d_model, p.d_ff);
+    if (p.workspace_bytes < needed)
+        return fail(HFFN_ERROR_ARGUMENT, "forward_tiles: workspace of %llu bytes, %llu needed for n=%u",
+                    static_cast<unsigned long long>(p.workspace_bytes), static_cast<unsigned long long>(needed), p.n);
+    return HFFN_OK;
+}
+
+int launch_tiles(const TilesPlan& p, const float* x, hipStream_t stream) {
+    return launched(hffn::launch_tiles_forward(p.value_type, x, p.up_idx, p.up_val, p.up_index, p.b_up, p.out_hidden, p.out_val,
+                                               p.down_index, p.b_down, p.act, static_cast<float*>(p.workspace), p.y, p.d_model, p.d_ff,
+                                               p.nnz_up, p.nnz_down, p.n, stream),
+                    "forward (tiles)");
+}
+
+std::unordered_map<uint64_t, TilesPlan> g_tiles_plans;
 uint64_t g_next_plan = 1;
 
 }  // namespace
@@ -252,7 +302,8 @@ int hffn_plan_forward(int up_mode, int down_mode, int value_type, const int32_t*
 int hffn_plan_launch(uint64_t plan, const float* x, void* stream) {
     Plan p;
     GemvPlan g;
-    bool gemv = false;
+    TilesPlan t;
+    bool gemv = false, tiles = false;
     {
         const std::lock_guard<std::mutex> lock(g_plans_mutex);
         if (const auto found = g_plans.find(plan); found != g_plans.end()) {
@@ -260,11 +311,18 @@ int hffn_plan_launch(uint64_t plan, const float* x, void* stream) {
         } else if (const auto found_gemv = g_gemv_plans.find(plan); found_gemv != g_gemv_plans.end()) {
             g = found_gemv->second;
             gemv = true;
+        } else if (const auto found_tiles = g_tiles_plans.find(plan); found_tiles != g_tiles_plans.end()) {
+            t = found_tiles->second;
+            tiles = true;
         } else {
             return fail(HFFN_ERROR_ARGUMENT, "plan_launch: unknown plan %llu", static_cast<unsigned long long>(plan));
         }
     }
     if (!x) return fail(HFFN_ERROR_ARGUMENT, "plan_launch: null input");
+    if (tiles) {
+        if (reinterpret_cast<uintptr_t>(x) % 16 != 0) return fail(HFFN_ERROR_ARGUMENT, "plan_launch: x must be 16-byte aligned");
+        return launch_tiles(t, x, static_cast<hipStream_t>(stream));
+    }
     if (gemv)  // the planned arguments passed their checks; x's alignment is checked here
         return hffn_forward_gemv(g.value_type, x, g.up_planes, g.up_binades, g.b_up, g.down_planes, g.down_binades, g.b_down, g.act,
                                  g.workspace, g.workspace_bytes, g.y, g.d_model, g.d_ff, g.n, stream);
@@ -273,7 +331,7 @@ int hffn_plan_launch(uint64_t plan, const float* x, void* stream) {
 
 int hffn_plan_release(uint64_t plan) {
     const std::lock_guard<std::mutex> lock(g_plans_mutex);
-    if (g_plans.erase(plan) == 0 && g_gemv_plans.erase(plan) == 0)
+    if (g_plans.erase(plan) == 0 && g_gemv_plans.erase(plan) == 0 && g_tiles_plans.erase(plan) == 0)
         return fail(HFFN_ERROR_ARGUMENT, "plan_release: unknown plan %llu", static_cast<unsigned long long>(plan));
     return HFFN_OK;
 }
@@ -442,6 +500,54 @@ int hffn_forward_gemv_static(int value_type, const float* x, const void* up_plan
     return launched(hffn::launch_gemv_forward(value_type, x, up_planes, up_binades, b_up, down_planes, down_binades, b_down, act,
                                               scratch, y, d_model, d_ff, n, static_cast<hipStream_t>(stream)),
                     "forward (gemv, static scratch)");
+}
+
+
+int hffn_tiles_index_entries(uint32_t rows, uint32_t k, uint64_t* entries) {
+    if (!entries) return fail(HFFN_ERROR_ARGUMENT, "tiles_index_entries: null result");
+    if (rows == 0 || rows > HFFN_MAX_WIDTH || k == 0 || k > HFFN_MAX_WIDTH)
+        return fail(HFFN_ERROR_ARGUMENT, "tiles_index_entries: rows=%u k=%u must be in [1, %u]", rows, k, HFFN_MAX_WIDTH);
+    *entries = hffn::tiles_index_entries(rows, k);
+    return HFFN_OK;
+}
+
+int hffn_tiles_index(const int32_t* offsets, const int16_t* idx, uint32_t rows, uint32_t k, int32_t* table, void* stream) {
+    uint64_t entries = 0;
+    if (int status = hffn_tiles_index_entries(rows, k, &entries)) return status;
+    if (!offsets || !idx || !table) return fail(HFFN_ERROR_ARGUMENT, "tiles_index: null pointer");
+    return launched(hffn::launch_tiles_index(offsets, idx, rows, k, table, static_cast<hipStream_t>(stream)), "tiles_index");
+}
+
+int hffn_tiles_workspace(uint32_t n, uint32_t d_model, uint32_t d_ff, uint64_t* bytes) {
+    if (!bytes) return fail(HFFN_ERROR_ARGUMENT, "tiles_workspace: null result");
+    if (int status = check_tiles(HFFN_VALUE_F32, d_model, d_ff, n)) return status;
+    *bytes = hffn::tiles_workspace_bytes(n, d_model, d_ff);
+    return HFFN_OK;
+}
+
+int hffn_forward_tiles(int value_type, const float* x, const int16_t* up_idx, const void* up_val, const int32_t* up_index,
+                       const float* b_up, const int16_t* out_hidden, const void* out_val, const int32_t* down_index,
+                       const float* b_down, float* act, void* workspace, uint64_t workspace_bytes, float* y, uint32_t d_model,
+                       uint32_t d_ff, uint32_t nnz_up, uint32_t nnz_down, uint32_t n, void* stream) {
+    const TilesPlan p{value_type, up_idx, up_val, up_index, b_up, out_hidden, out_val, down_index, b_down, act, workspace,
+                      workspace_bytes, y, d_model, d_ff, nnz_up, nnz_down, n};
+    if (int status = check_tiles_call(p, x)) return status;
+    return launch_tiles(p, x, static_cast<hipStream_t>(stream));
+}
+
+int hffn_plan_tiles(int value_type, const int16_t* up_idx, const void* up_val, const int32_t* up_index, const float* b_up,
+                    const int16_t* out_hidden, const void* out_val, const int32_t* down_index, const float* b_down, float* act,
+                    void* workspace, uint64_t workspace_bytes, float* y, uint32_t d_model, uint32_t d_ff, uint32_t nnz_up,
+                    uint32_t nnz_down, uint32_t n, uint64_t* plan) {
+    if (!plan) return fail(HFFN_ERROR_ARGUMENT, "plan_tiles: null result");
+    const TilesPlan p{value_type, up_idx, up_val, up_index, b_up, out_hidden, out_val, down_index, b_down, act, workspace,
+                      workspace_bytes, y, d_model, d_ff, nnz_up, nnz_down, n};
+    const float* some_x = reinterpret_cast<const float*>(uintptr_t{16});  // non-null, aligned: never dereferenced
+    if (int status = check_tiles_call(p, some_x)) return status;
+    const std::lock_guard<std::mutex> lock(g_plans_mutex);
+    *plan = g_next_plan++;
+    g_tiles_plans.emplace(*plan, p);
+    return HFFN_OK;
 }
 
 int hffn_plan_gemv(int value_type, const void* up_planes, const int32_t* up_binades, const float* b_up, const void* down_planes,

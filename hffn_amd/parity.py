@@ -5,7 +5,7 @@ For one input, the runtime runs with its policy and with each forced (up, down) 
 consecutive calls on the same input give the same bits; ``max |y - y64|`` and ``max |y - y64| / max(1, |y64|)`` are
 reported for the caller to compare with its tolerance. The pairs are the policy, the four gather pairs (edges or
 rows up, edges or rows down) and, when the runtime holds densified planes, the MFMA path and (up to 64 tokens) the
-decode GEMVs.
+decode GEMVs, and (up to 64 tokens) the compact-store MFMA path.
 """
 from __future__ import annotations
 
@@ -16,7 +16,7 @@ import torch
 from .runtime import GEMV_MAX_TOKENS, HFFNRuntime
 
 GATHER = ("edges", "rows")
-PAIRS = [(None, None)] + [(up, down) for up in GATHER for down in GATHER] + [("mfma", "mfma"), ("gemv", "gemv")]
+PAIRS = [(None, None)] + [(up, down) for up in GATHER for down in GATHER] + [("mfma", "mfma"), ("gemv", "gemv"), ("tiles", "tiles")]
 
 
 @dataclass
@@ -38,7 +38,9 @@ def check(runtime: HFFNRuntime, index: int, x: torch.Tensor, expected: torch.Ten
         for up, down in pairs:
             if up in ("mfma", "gemv") and not runtime.mfma_available:
                 continue
-            if up == "gemv" and x.shape[0] > GEMV_MAX_TOKENS:
+            if up == "tiles" and not runtime.tiles_available:
+                continue
+            if up in ("gemv", "tiles") and x.shape[0] > GEMV_MAX_TOKENS:
                 continue
             runtime.force(up, down)
             y = runtime.forward(index, x).clone()

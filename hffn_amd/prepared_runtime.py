@@ -1,8 +1,8 @@
 """``PreparedRuntime``: the decode launch path, as ``hffn_pythia_cuda.prepared_runtime``
 (``runtime/gpu/nvidia/llm/inference/hffn_pythia_cuda/prepared_runtime.py:34-82``).
 
-A decode-sized call of layer ``index`` on N tokens (the gather kernels ``edges`` and ``rows``, or the decode GEMVs
-``gemv``) launches from a *plan* that the library builds once per (index, N): every argument of the forward but ``x``
+A decode-sized call of layer ``index`` on N tokens (the gather kernels ``edges`` and ``rows``, the decode GEMVs
+``gemv`` or the compact-store MFMA path ``tiles``) launches from a *plan* that the library builds once per (index, N): every argument of the forward but ``x``
 and the stream is checked and stored on the library side (``hffn_plan_forward``, ``hffn_plan_gemv``), so a call is
 one ctypes call with three arguments (``hffn_plan_launch``) instead of the full argument list and its checks. The
 kernels, modes, work buffers, results and the ``calls`` counter are those of ``HFFNRuntime``; MFMA-path calls (large
@@ -68,6 +68,10 @@ class PreparedRuntime(HFFNRuntime):
                                                 self.d_ff, n, ctypes.byref(handle)),
                        "plan (gemv, gemv)")
             return handle.value, up, down
+        if up == "tiles":
+            _lib.check(self._lib.hffn_plan_tiles(value_type, *self._tiles_args(index), self.d_model, self.d_ff, *self._nnz[index], n,
+                                                 ctypes.byref(handle)), "plan (tiles, tiles)")
+            return handle.value, up, down
         if up not in _GATHER or down not in _GATHER:
             return False
         _lib.check(self._lib.hffn_plan_forward(_lib.UP_MODES[up], _lib.DOWN_MODES[down], value_type, *model, x_t, act, y_t, y,
@@ -91,9 +95,9 @@ class PreparedRuntime(HFFNRuntime):
         if entry is False:
             return super().forward(index, x)
         handle, up, down = entry
-        if up == "gemv":
-            x = _aligned(x)  # the GEMVs read x 16 bytes at a time
-            if index in self._stale:  # a training update changed the values: rebuild the planes in place first
+        if up in ("gemv", "tiles"):
+            x = _aligned(x)  # read 16 bytes at a time
+            if up == "gemv" and index in self._stale:  # a training update changed the values: rebuild the planes first
                 self._densify(self._tensors[index], self._planes[index])
                 self._stale.discard(index)
         stream = self._stream_of(self.device.index) if self._stream_of else torch.cuda.current_stream(self.device).cuda_stream

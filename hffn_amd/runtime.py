@@ -33,10 +33,12 @@ import torch
 
 from . import _lib
 
-UP_MODES = ("edges", "rows", "mfma", "gemv")
-DOWN_MODES = ("edges", "rows", "mfma", "gemv")
-PAIR_MODES = ("mfma", "gemv")  # the planes paths: up and down run together
+UP_MODES = ("edges", "rows", "mfma", "gemv", "tiles")
+DOWN_MODES = ("edges", "rows", "mfma", "gemv", "tiles")
+PAIR_MODES = ("mfma", "gemv", "tiles")  # up and down run together (token-major activations of their own)
+PLANES_MODES = ("mfma", "gemv")         # the paths over densified planes
 GEMV_MAX_TOKENS = 64      # the planes GEMVs' largest call
+TILES_MAX_TOKENS = 64     # the compact-store MFMA path's largest call
 EDGES_MAX_TOKENS = 32     # the policy's last N for the lane-per-slot shapes
 EDGES_PASS_TOKENS = 8     # tokens one pass of the lane-per-slot kernels takes
 MFMA_MIN_DENSITY = 0.05   # the lowest support density the tile-densified MFMA path takes
@@ -265,6 +267,12 @@ class HFFNRuntime:
         self.density = self._slots / (2 * self.d_model * self.d_ff)
         self._planes: list[dict] | None = None
         self._stale: set[int] = set()   # layers whose values changed since their planes were built
+        self._tiles: list[dict] | None = None
+        self._tiles_work = torch.empty(1, device=self.device)
+        if self._tiles_eligible():
+            self._tiles = [self._tiles_index(tensors) for tensors in self._tensors]
+            words = (_lib.query_bytes(self._lib.hffn_tiles_workspace, TILES_MAX_TOKENS, self.d_model, self.d_ff) + 3) // 4
+            self._tiles_work = torch.empty(words, device=self.device)  # the per-chunk partial sums
         self._gemv_work = torch.empty(1, device=self.device)
         if dense and self._mfma_eligible():
             self._planes = [self._densify(tensors) for tensors in self._tensors]
@@ -277,13 +285,39 @@ class HFFNRuntime:
         self._tokens = 0
         self._reserve(1)
 
+    # ------------------------------------------------------------------- compact-store MFMA path (decode sizes)
+
+    def _rows_sorted(self) -> bool:
+        if not hasattr(self, "_sorted"):
+            self._sorted = all(_rows_strictly_increasing(t["up_offsets"], t["up_idx"]) and
+                               _rows_strictly_increasing(t["out_offsets"], t["out_hidden"]) for t in self._tensors)
+        return self._sorted
+
+    def _tiles_eligible(self) -> bool:
+        return self.d_model % 16 == 0 and self.d_ff % 8 == 0 and self._rows_sorted()
+
+    def _tiles_index(self, tensors: dict) -> dict:
+        """Each row's first slot in every 1024-wide chunk of K, for both sides (``hffn_tiles_index``)."""
+        stream = torch.cuda.current_stream(self.device).cuda_stream
+        tables = {}
+        for side, rows, k, names in (("up", self.d_ff, self.d_model, ("up_offsets", "up_idx")),
+                                     ("down", self.d_model, self.d_ff, ("out_offsets", "out_hidden"))):
+            entries = _lib.query_bytes(self._lib.hffn_tiles_index_entries, rows, k)
+            table = torch.empty(entries, dtype=torch.int32, device=self.device)
+            offsets, index = (tensors[name] for name in names)
+            _lib.check(self._lib.hffn_tiles_index(offsets.data_ptr(), index.data_ptr(), rows, k, table.data_ptr(), stream),
+                       f"tiles index {side}")
+            tables[side] = table
+        return tables
+
+    @property
+    def tiles_available(self) -> bool:
+        return self._tiles is not None
+
     # -------------------------------------------------------------------------------- tile-densified MFMA path
 
     def _mfma_eligible(self) -> bool:
-        if not self._lib.hffn_mfma_supported(self.d_model, self.d_ff):
-            return False
-        return all(_rows_strictly_increasing(t["up_offsets"], t["up_idx"]) and
-                   _rows_strictly_increasing(t["out_offsets"], t["out_hidden"]) for t in self._tensors)
+        return bool(self._lib.hffn_mfma_supported(self.d_model, self.d_ff)) and self._rows_sorted()
 
     def _densify(self, tensors: dict, planes: dict | None = None) -> dict:
         """fp16 hi/lo planes (and per-row binades) of W_up [d_ff, d_model] and W_down [d_model, d_ff], built on the
@@ -333,8 +367,10 @@ class HFFNRuntime:
         for pair in PAIR_MODES:
             if (up == pair) != (down == pair):
                 raise ValueError(f"the {pair} path runs up and down together: force ('{pair}', '{pair}')")
-        if up in PAIR_MODES and self._planes is None:
+        if up in PLANES_MODES and self._planes is None:
             raise ValueError(f"the {up} path is not available for these layers")
+        if up == "tiles" and self._tiles is None:
+            raise ValueError("the tiles path needs d_model % 16 == 0, d_ff % 8 == 0 and strictly increasing indices per row")
         self.forced_up, self.forced_down = up, down
 
     def _reserve(self, n: int) -> None:
@@ -353,7 +389,7 @@ class HFFNRuntime:
 
     def workspace_bytes(self) -> int:
         return 4 * (self._x_t.numel() + self._act.numel() + self._y_t.numel() + self._y.numel() + self._mfma_work.numel() +
-                    self._gemv_work.numel())
+                    self._gemv_work.numel() + self._tiles_work.numel())
 
     def modes(self, n: int) -> tuple[str, str]:
         """The (up, down) shapes a call of N tokens takes (forced ones first). The policy's choice depends on N and the
@@ -393,10 +429,25 @@ class HFFNRuntime:
         self.calls[up, down] += 1
         return self._y[:n]
 
+    def _tiles_args(self, index: int) -> tuple:
+        """The arguments of ``hffn_forward_tiles`` / ``hffn_plan_tiles`` between x and the token count."""
+        tensors, tables = self._tensors[index], self._tiles[index]
+        _, act, _, y = self._work
+        return (tensors["up_idx"].data_ptr(), tensors["up_val"].data_ptr(), tables["up"].data_ptr(), tensors["b_up"].data_ptr(),
+                tensors["out_hidden"].data_ptr(), tensors["out_val"].data_ptr(), tables["down"].data_ptr(),
+                tensors["b_down"].data_ptr(), act, self._tiles_work.data_ptr(), 4 * self._tiles_work.numel(), y)
+
     def _launch(self, index: int, x: torch.Tensor, n: int, up: str, down: str) -> None:
         value_type, *model = self._args[index]
         x_t, act, y_t, y = self._work
         stream = torch.cuda.current_stream(self.device).cuda_stream
+        if up == "tiles":
+            if n > TILES_MAX_TOKENS:
+                raise ValueError(f"the tiles path takes at most {TILES_MAX_TOKENS} tokens, not {n}")
+            x = _aligned(x)  # read 16 bytes at a time
+            _lib.check(self._lib.hffn_forward_tiles(value_type, x.data_ptr(), *self._tiles_args(index), self.d_model, self.d_ff,
+                                                    *self._nnz[index], n, stream), "forward (tiles, tiles)")
+            return
         if up in PAIR_MODES:
             x = _aligned(x)  # the planes paths read x 16 bytes at a time
             if index in self._stale:

@@ -27,7 +27,7 @@
 extern "C" {
 #endif
 
-#define HFFN_ABI_VERSION 10
+#define HFFN_ABI_VERSION 11
 
 #define HFFN_OK 0
 #define HFFN_ERROR_ARGUMENT (-1) /* invalid shape, mode, pointer or workspace */
@@ -196,6 +196,45 @@ int hffn_forward_gemv_static(int value_type, const float* x, const void* up_plan
 int hffn_plan_gemv(int value_type, const void* up_planes, const int32_t* up_binades, const float* b_up, const void* down_planes,
                    const int32_t* down_binades, const float* b_down, float* act, void* workspace, uint64_t workspace_bytes, float* y,
                    uint32_t d_model, uint32_t d_ff, uint32_t n, uint64_t* plan);
+
+/* ---- Decode path on the compact store (1-64 tokens). No reference counterpart for the arithmetic: the reference
+ * decodes on its gather kernels (runtime/gpu/nvidia/common/kernels/hffn_cuda/kernels.py:102-191), reading each slot
+ * once per kernel as these do. A block takes 16 rows and one 1024-wide chunk of K: it reads those rows' slots of the
+ * chunk from the compact store (each slot once per call), densifies them in LDS (float32 weights as fp16 hi/lo
+ * scaled by a power of two per row and chunk, bfloat16 weights as they are) and multiplies on 16x16x32 MFMAs
+ * (float32: x split per token and 32-k step into fp16 hi/lo, three products; bfloat16: x split exactly into three
+ * bfloat16 parts). Rows whose K spans several chunks write per-chunk partials, added in chunk order by a second
+ * kernel. Every row's indices must be strictly increasing (the index table and the densified tile assume it; a slot
+ * outside its chunk is skipped, never written out of place). x, act and y token-major; x and act 16-byte aligned; the
+ * index arrays 8-byte and the value arrays 16-byte (fp32) or 8-byte (bf16) aligned, nnz_up / nnz_down their lengths. */
+
+/* Entries of one side's index table (host-only query): rows * (ceil(k / 1024) + 1) int32. */
+int hffn_tiles_index_entries(uint32_t rows, uint32_t k, uint64_t* entries);
+
+/* table[r * (chunks + 1) + c] = the first slot of row r (slots [offsets[r], offsets[r + 1]), indices ascending) whose
+ * index is at least 1024 c, for c = 0 .. chunks; built once per side at load: the up side over (up_offsets, up_idx,
+ * rows = d_ff, k = d_model), the down side over (out_offsets, out_hidden, rows = d_model, k = d_ff). */
+int hffn_tiles_index(const int32_t* offsets, const int16_t* idx, uint32_t rows, uint32_t k, int32_t* table, void* stream);
+
+/* Bytes of the workspace of hffn_forward_tiles for n tokens (host-only query): the per-chunk partials of a side whose K
+ * spans several chunks. No initial contents needed; calls that share it must be ordered (one stream). */
+int hffn_tiles_workspace(uint32_t n, uint32_t d_model, uint32_t d_ff, uint64_t* bytes);
+
+/* act[t, r] = gelu(b_up[r] + sum_k W_up[r, k] x[t, k]) into act (token-major [n, d_ff]), then
+ * y[t, o] = b_down[o] + sum_r W_down[o, r] act[t, r] (token-major [n, d_model]); 1 <= n <= 64, d_model a multiple of
+ * 16, d_ff of 8. The stores are the runtime's (up hidden-major, down output-major) with the two index tables. */
+int hffn_forward_tiles(int value_type, const float* x, const int16_t* up_idx, const void* up_val, const int32_t* up_index,
+                       const float* b_up, const int16_t* out_hidden, const void* out_val, const int32_t* down_index,
+                       const float* b_down, float* act, void* workspace, uint64_t workspace_bytes, float* y, uint32_t d_model,
+                       uint32_t d_ff, uint32_t nnz_up, uint32_t nnz_down, uint32_t n, void* stream);
+
+/* Prepared hffn_forward_tiles (every argument but x and the stream checked and kept under a handle), launched by
+ * hffn_plan_launch and dropped by hffn_plan_release as hffn_plan_forward's: the decode launch path of
+ * PreparedRuntime (runtime/gpu/nvidia/llm/inference/hffn_pythia_cuda/prepared_runtime.py:34-82) for this path. */
+int hffn_plan_tiles(int value_type, const int16_t* up_idx, const void* up_val, const int32_t* up_index, const float* b_up,
+                    const int16_t* out_hidden, const void* out_val, const int32_t* down_index, const float* b_down, float* act,
+                    void* workspace, uint64_t workspace_bytes, float* y, uint32_t d_model, uint32_t d_ff, uint32_t nnz_up,
+                    uint32_t nnz_down, uint32_t n, uint64_t* plan);
 
 /* ------------------------------------------------------------------------------------------------ training (fp32)
  * Layouts: act, z, gz hidden-major [d_ff, ld]; x_t, gy_t, gx_t feature-major [d_model, ld]; x, y, gx token-major

@@ -112,8 +112,8 @@ def test_forced_pairs_match_the_oracle(name, test_layers, device):
         result = parity.check(runtime, 0, torch.from_numpy(x_np).to(device), expected)
         assert result.repeatable, f"{name} N{n}: bits differ on repeat"
         assert result.error <= ATOL, f"{name} N{n}: {result.pairs}"
-    gemv_skipped = sum(n > GEMV_MAX_TOKENS for n in BATCHES)  # the decode GEMVs take at most 64 tokens
-    assert sum(runtime.calls.values()) == 2 * (len(BATCHES) * len(parity.PAIRS) - gemv_skipped)
+    skipped = 2 * sum(n > GEMV_MAX_TOKENS for n in BATCHES)  # the decode GEMVs and the tiles path take at most 64 tokens
+    assert sum(runtime.calls.values()) == 2 * (len(BATCHES) * len(parity.PAIRS) - skipped)
 
 
 def test_shared_buffers_between_calls(test_layers, device):
@@ -189,6 +189,45 @@ def test_gemv_token_result_does_not_depend_on_the_batch(name, test_layers, devic
         assert torch.equal(runtime.forward(0, x[start:start + size].contiguous()), whole[start:start + size]), (start, size)
     expected = reference.forward(compact, x.cpu().numpy())
     assert _relative(whole, expected) <= 1e-5
+
+
+@pytest.mark.parametrize("name", ["homog_512_2048", "irreg_512_2048"])
+def test_tiles_token_result_does_not_depend_on_the_batch(name, test_layers, device):
+    """The compact-store MFMA path densifies each 16-row tile once and multiplies every 16-token tile with the same
+    tile, each token scaled by its own power of two per 32-k step: a token's result is bit-identical alone and in any
+    batch of up to 64 tokens."""
+    compact, case, layer = test_layers[name]
+    runtime = HFFNRuntime([layer], device)
+    runtime.force("tiles", "tiles")
+    x = torch.from_numpy(synth.make_input(case, 64)).to(device)
+    whole = runtime.forward(0, x).clone()
+    for start, size in ((0, 1), (7, 5), (3, 16), (16, 16), (5, 17), (31, 1), (20, 33), (0, 48), (63, 1)):
+        assert torch.equal(runtime.forward(0, x[start:start + size].contiguous()), whole[start:start + size]), (start, size)
+    assert _relative(whole, reference.forward(compact, x.cpu().numpy())) <= 1e-5
+
+
+def test_tiles_index_table(test_layers, device):
+    """The index table of the tiles path: for every row and every 1024-wide chunk of K, the first slot whose index
+    reaches the chunk (a searchsorted over each row's ascending indices)."""
+    from hffn_amd import _lib
+    compact, _, layer = test_layers["irreg_512_2048"]
+    runtime = HFFNRuntime([layer], device)
+    table = runtime._tiles[0]["down"].cpu().numpy()  # rows = d_model outputs over K = d_ff = 2048: two chunks
+    offsets = layer.out_offsets.cpu().numpy().astype(np.int64)
+    hidden = layer.out_hidden.cpu().numpy().astype(np.int64)
+    chunks = (compact.d_ff + 1023) // 1024
+    assert table.size == _lib.query_bytes(_lib.load().hffn_tiles_index_entries, compact.d_model, compact.d_ff)
+    expected = [offsets[o] + np.searchsorted(hidden[offsets[o]:offsets[o + 1]], c * 1024) for o in range(compact.d_model)
+                for c in range(chunks + 1)]
+    assert table.tolist() == [int(v) for v in expected]
+
+
+def test_tiles_refuses_more_than_64_tokens(test_layers, device):
+    compact, case, layer = test_layers["homog_512_2048"]
+    runtime = HFFNRuntime([layer], device)
+    runtime.force("tiles", "tiles")
+    with pytest.raises(ValueError, match="at most 64"):
+        runtime.forward(0, torch.from_numpy(synth.make_input(case, 65)).to(device))
 
 
 def test_gemv_refuses_more_than_64_tokens(test_layers, device):

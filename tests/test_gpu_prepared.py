@@ -1,5 +1,5 @@
 """The decode launch path (``PreparedRuntime``, plans of the C ABI) on the GPU: bit-identical to ``HFFNRuntime`` on
-every gather pair, the decode GEMVs and every token count it serves, the same ``calls`` bookkeeping, plans released when the work buffers move
+every gather pair, the decode GEMVs, the compact-store MFMA path and every token count it serves, the same ``calls`` bookkeeping, plans released when the work buffers move
 or a mode is forced, and the float64 oracle on the reference test layers (2e-5 absolute, as
 runtime/gpu/nvidia/ffn/inference/checks/parity.py:26-61)."""
 from __future__ import annotations
@@ -45,13 +45,13 @@ def test_prepared_matches_control_bitwise(name, runtimes):
 
 
 @pytest.mark.parametrize("pair", [("edges", "edges"), ("edges", "rows"), ("rows", "edges"), ("rows", "rows"),
-                                  ("gemv", "gemv")])
+                                  ("gemv", "gemv"), ("tiles", "tiles")])
 def test_prepared_forced_pairs(pair, runtimes, device):
     compact, case, control, prepared = runtimes["irreg_512_2048"]
     try:
         control.force(*pair)
         prepared.force(*pair)
-        for n in ((1, 4, 7, 24) if pair[0] == "gemv" else (1, 4, 7, 64)):
+        for n in ((1, 4, 7, 24, 33) if pair[0] in ("gemv", "tiles") else (1, 4, 7, 64)):
             x = torch.from_numpy(synth.make_input(case, n)).to(device)
             assert torch.equal(prepared.forward(0, x), control.forward(0, x)), (pair, n)
             assert prepared._plans[(0, n)][1:] == pair
