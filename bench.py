@@ -11,9 +11,13 @@ every step reads its model from HBM.
 
 Prints one JSON line. `roofline` is measured live: HIP events around each kernel of the step (on the stream the
 kernels are launched on) give each kernel's average duration; the dominant one is priced against its algorithmic
-bytes or flops. `cpu_baseline` times the reference x86 AVX2 kernel (built from the reference source into
-oracle/_ref) on this host's cores on a bounded sample of the same workload, after checking it against the float64
-oracle on a token sample.
+bytes or flops: the tile-densified MFMA path against the dense fp16 MFMA peak times the side's useful/dense flop ratio
+(with the fp32-equivalent fraction and the issued fp16 MFMA rate beside it), the gather kernels at large N against the
+fp32 peak, decode-sized calls against HBM on the compact store's bytes (the decode GEMVs also on the bytes of the planes
+they read). `traffic` comes from the committed rocprofv3 counter summary of the same command. `cpu_baseline` times the
+reference x86 AVX2 kernel (built from the reference source into oracle/_ref) on this host's cores, pinned, in child
+processes started before this process touches the GPU (oracle.cpu_bench: the bench workload and the 70M-shape CPU
+configuration, at 8 threads and at every physical core of one NUMA node within the host's CPU share).
 """
 from __future__ import annotations
 
@@ -47,8 +51,7 @@ def parse() -> argparse.Namespace:
     parser.add_argument("--workload", default="pythia410m_d50")
     parser.add_argument("--tokens", type=int, default=None, help="N (default: the workload's first token count)")
     parser.add_argument("--copies", type=int, default=None, help="distinct layer copies in the rotation")
-    parser.add_argument("--cpu-seconds", type=float, default=10.0, help="bound of the CPU-baseline sample")
-    parser.add_argument("--cpu-threads", type=int, default=8)
+    parser.add_argument("--cpu-seconds", type=float, default=5.0, help="timed seconds per CPU-baseline run (4 runs)")
     parser.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     parser.add_argument("--copy-probe-mb", type=int, default=0,
                         help="after the run, copy a buffer of this many MiB 3 times (the plain copy kernel that "
@@ -85,6 +88,7 @@ def layer_costs(compact, n: int) -> dict:
         "model_bytes": up_store + down_store,
         "step_bytes": up_store + down_store + 8 * n * d,
         "step_flops": 2 * (nnz_up + nnz_down) * n,
+        "density_up": nnz_up / (d * h), "density_down": nnz_down / (d * h), "density": (nnz_up + nnz_down) / (2 * d * h),
     }
 
 
@@ -122,23 +126,27 @@ def time_kernels(runtime, x: torch.Tensor, steps: int, copies: int) -> dict:
             for i, name in enumerate(names):
                 totals[name] += events[i].elapsed_time(events[i + 1]) * 1e-3
         return {name: total / steps for name, total in totals.items()}
-    if up == "gemv":
+    if up in ("gemv", "tiles"):  # both projections in one ABI call, timed as one
         total = 0.0
         work, work_bytes = runtime._gemv_work.data_ptr(), 4 * runtime._gemv_work.numel()
         for step in range(steps):
             index = step % copies
             value_type = runtime._args[index][0]
-            planes, tensors = runtime._planes[index], runtime._tensors[index]
             events = [torch.cuda.Event(enable_timing=True) for _ in range(2)]
             events[0].record()
-            _lib.check(lib.hffn_forward_gemv(value_type, x.data_ptr(), planes["up"].data_ptr(), planes["up_binades"].data_ptr(),
-                                             tensors["b_up"].data_ptr(), planes["down"].data_ptr(), planes["down_binades"].data_ptr(),
-                                             tensors["b_down"].data_ptr(), act, work, work_bytes, y, runtime.d_model, runtime.d_ff,
-                                             n, stream), "gemv")
+            if up == "tiles":
+                _lib.check(lib.hffn_forward_tiles(value_type, x.data_ptr(), *runtime._tiles_args(index), runtime.d_model,
+                                                  runtime.d_ff, *runtime._nnz[index], n, stream), "tiles")
+            else:
+                planes, tensors = runtime._planes[index], runtime._tensors[index]
+                _lib.check(lib.hffn_forward_gemv(value_type, x.data_ptr(), planes["up"].data_ptr(), planes["up_binades"].data_ptr(),
+                                                 tensors["b_up"].data_ptr(), planes["down"].data_ptr(),
+                                                 planes["down_binades"].data_ptr(), tensors["b_down"].data_ptr(), act, work,
+                                                 work_bytes, y, runtime.d_model, runtime.d_ff, n, stream), "gemv")
             events[1].record()
             torch.cuda.synchronize()
             total += events[0].elapsed_time(events[1]) * 1e-3
-        return {"gemv": total / steps}
+        return {up: total / steps}
     names = (["transpose_in"] if up == "rows" else []) + ["up", "down"] + (["transpose_out"] if down == "rows" else [])
     totals = {name: 0.0 for name in names}
     for step in range(steps):
@@ -169,32 +177,49 @@ def time_kernels(runtime, x: torch.Tensor, steps: int, copies: int) -> dict:
     return {name: total / steps for name, total in totals.items()}
 
 
-def cpu_baseline(compact, x_np: np.ndarray, seconds: float, threads: int) -> dict | None:
-    """The reference x86 kernel on this host: checked against the float64 oracle on 96 tokens, then timed on whole
-    calls of the workload until `seconds` of work are done (at least 2 calls)."""
-    from oracle import reference, x86_ref
+def _child_json(arguments: list[str]) -> dict:
+    """One pinned child process of oracle.cpu_bench (started before this process touches the GPU); its JSON line."""
+    import subprocess
+    done = subprocess.run([sys.executable, "-m", "oracle.cpu_bench", *arguments], cwd=ROOT, text=True, capture_output=True,
+                          timeout=600)
+    lines = [line for line in done.stdout.splitlines() if line.startswith("{")]
+    if done.returncode != 0 or not lines:
+        raise RuntimeError(f"oracle.cpu_bench {' '.join(arguments)} failed ({done.returncode}): {done.stderr[-2000:]}")
+    return json.loads(lines[-1])
+
+
+def cpu_baseline(workload: str, n: int, seconds: float) -> dict | None:
+    """The reference x86 kernel on this host, pinned (oracle.cpu_bench, the protocol of the reference's
+    bench/threads.py): the bench workload and the 70M-shape CPU configuration (128 tokens), each at T = 8 and at
+    T = every physical core of NUMA node 0 that this process may use (at most 64, and at most the host CPU share
+    OMP_NUM_THREADS names when set). ``value`` is the faster of the two runs of the bench workload, by wall time."""
+    from oracle import cpu_bench, x86_ref
 
     if not x86_ref.available():
         return None
-    threads = max(1, min(threads, len(os.sched_getaffinity(0))))
-    kernel = x86_ref.ReferenceKernel(compact, threads=threads)
-    sample = x_np[:96]
-    error = float(np.max(np.abs(kernel.forward(sample) - reference.forward(compact, sample))))
-    if error > 2e-5:
-        raise RuntimeError(f"reference x86 kernel differs from the oracle by {error:.3e}")
-    kernel.forward(x_np)  # warm-up (thread pool, buffers)
-    calls, wall, inside = 0, 0.0, 0
-    while calls < 2 or wall < seconds:
-        start = time.perf_counter()
-        kernel.forward(x_np)
-        wall += time.perf_counter() - start
-        inside += int(kernel.timing.sum())
-        calls += 1
-    n = x_np.shape[0]
-    return {"value": round(n * calls / wall, 1), "unit": "tokens/s", "cores": threads, "kind": "reference",
-            "sample": f"{calls} whole calls of the same layer and {n}-token input ({wall:.1f} s wall, in-kernel "
-                      f"{inside / calls / 1e6:.2f} ms/call); route dual in 96-token chunks, {threads} threads; "
-                      f"checked against the float64 oracle on 96 tokens (max |dy| {error:.1e})"}
+    host = cpu_bench.machine()
+    node = next(iter(host["numa"].values()), {"cpus": host["affinity"]})
+    cores = cpu_bench.one_core_per_node_cpu(node["cpus"], set(host["affinity"])) or host["affinity"]
+    share = int(os.environ.get("OMP_NUM_THREADS", "0") or 0)
+    every = cores[:min(64, len(cores), share or len(cores))]
+    settings = [("T8", cores[:8]), ("T_all", every)] if len(every) > 8 else [("T8", cores[:8])]
+    runs = []
+    for name, cpus in settings:
+        for wl, tokens, budget in ((workload, n, seconds), ("pythia70m_d20", 128, min(seconds, 4.0))):
+            row = _child_json(["--cpus", ",".join(map(str, cpus)), "--threads", str(len(cpus)), "--workload", wl,
+                               "--tokens", str(tokens), "--seconds", str(budget)])
+            runs.append({"setting": name, **{k: row[k] for k in ("workload", "tokens", "threads", "calls", "kernel_us_median",
+                                                               "wall_us_median", "tokens_per_s_wall", "tokens_per_s_kernel",
+                                                               "max_abs_error_vs_float64")}})
+    main_runs = [r for r in runs if r["workload"] == workload]
+    best = max(main_runs, key=lambda r: r["tokens_per_s_wall"])
+    return {"value": best["tokens_per_s_wall"], "unit": "tokens/s", "cores": best["threads"], "kind": "reference",
+            "sample": f"{best['calls']} whole {n}-token calls of the same layer, median wall "
+                      f"{best['wall_us_median'] / 1e3:.2f} ms (in-kernel {best['kernel_us_median'] / 1e3:.2f} ms), "
+                      f"process pinned to {best['threads']} cores of NUMA node 0, {best['threads']} threads, route dual in "
+                      f"96-token chunks; checked against the float64 oracle on 96 tokens",
+            "runs": runs, "machine": {k: host[k] for k in ("model", "logical_cpus", "governor")} |
+            {"numa_nodes": len(host["numa"]), "node0_physical_cores": node.get("physical_cores"), "allowed_cpus": len(host["affinity"])}}
 
 
 def main() -> int:
@@ -207,9 +232,11 @@ def main() -> int:
     from hffn_amd.ffn import hip_layer
     from hffn_amd.runtime import HFFNRuntime
 
-    device = torch.device("cuda", 0)
     workload = synth.WORKLOADS[args.workload]
     n = args.tokens or workload.tokens[0]
+    # the CPU baseline first, in pinned child processes, while this process has not touched the GPU
+    baseline = None if args.no_cpu else cpu_baseline(workload.name, n, args.cpu_seconds)
+    device = torch.device("cuda", 0)
     base = synth.make_workload_layer(workload)
     costs = layer_costs(base, n)
     copies = args.copies or max(1, math.ceil(MALL_BYTES / costs["model_bytes"]))
@@ -233,26 +260,43 @@ def main() -> int:
     up, down = runtime.modes(n)
 
     kernels = time_kernels(runtime, x, max(20, min(args.steps, 200)), copies)
-    dominant = max((k for k in kernels if k in ("up", "down", "gemv")), key=kernels.get)
-    cost = costs[dominant]
-    compute_bound = cost["flops"] / cost["bytes"] > RIDGE
-    if compute_bound:
-        roofline = {"bound": "mfma", "achieved": round(cost["flops"] / kernels[dominant] / 1e12, 3), "peak": FP32_PEAK / 1e12,
-                    "unit": "TFLOP/s"}
-    else:
-        roofline = {"bound": "hbm", "achieved": round(cost["bytes"] / kernels[dominant] / 1e9, 1), "peak": HBM_PEAK / 1e9,
-                    "unit": "GB/s"}
-    roofline["frac"] = round(roofline["achieved"] / roofline["peak"], 4)
-    roofline["kernel"] = "up+down (gemv)" if dominant == "gemv" else f"{dominant} ({up if dominant == 'up' else down})"
-    roofline["traffic"] = measured_traffic(workload.name, n, roofline["kernel"])
-    if up == "mfma":
-        # what the MFMA units execute: the dense products of the planes, 3 (fp32 values) or 2 (bf16) fp16 MFMAs each
+    dominant = max((k for k in kernels if k in ("up", "down", "gemv", "tiles")), key=kernels.get)
+    cost = costs["gemv" if dominant == "tiles" else dominant]
+    seconds_kernel = kernels[dominant]
+    density = {"up": costs["density_up"], "down": costs["density_down"]}.get(dominant, costs["density"])
+    if up == "mfma" and dominant in ("up", "down"):
+        # The tile-densified MFMA path: its useful flops against the dense fp16 MFMA peak scaled by the useful/dense
+        # flop ratio of the side (its support density); beside it, the same flops against the fp32 peak, and what the
+        # MFMA units issue (the dense products of the planes: 3 fp16 MFMAs per product for fp32 values, 2 for bf16).
+        achieved = cost["flops"] / seconds_kernel
+        peak = FP16_MFMA_PEAK * density
         products = 2 if base.value_dtype == "bf16" else 3
-        dense = 2 * n * base.d_model * base.d_ff * products
-        roofline["fp16_mfma_issued_frac"] = round(dense / kernels[dominant] / FP16_MFMA_PEAK, 4)
-    roofline["kernel_us"] = round(kernels[dominant] * 1e6, 2)
+        roofline = {"bound": "mfma", "achieved": round(achieved / 1e12, 3), "peak": round(peak / 1e12, 1), "unit": "TFLOP/s",
+                    "frac": round(achieved / peak, 4),
+                    "peak_rule": "dense fp16 MFMA 2.5 PFLOP/s x useful/dense flops (the side's support density)",
+                    "fp32_equivalent_frac": round(achieved / FP32_PEAK, 4),
+                    "fp16_mfma_issued_frac": round(2 * n * base.d_model * base.d_ff * products / seconds_kernel / FP16_MFMA_PEAK, 4)}
+    elif cost["flops"] / cost["bytes"] > RIDGE:  # the gather kernels at large N: fp32 FMAs
+        achieved = cost["flops"] / seconds_kernel
+        roofline = {"bound": "mfma", "achieved": round(achieved / 1e12, 3), "peak": FP32_PEAK / 1e12, "unit": "TFLOP/s",
+                    "frac": round(achieved / FP32_PEAK, 4), "peak_rule": "fp32 157.3 TFLOP/s (vector FMAs)"}
+    else:
+        achieved = cost["bytes"] / seconds_kernel
+        roofline = {"bound": "hbm", "achieved": round(achieved / 1e9, 1), "peak": HBM_PEAK / 1e9, "unit": "GB/s",
+                    "frac": round(achieved / HBM_PEAK, 4), "peak_rule": "HBM3E 8 TB/s on the compact store's bytes"}
+        if dominant == "gemv":  # what the decode GEMVs read: the densified planes instead of the compact store
+            # bf16 weights are read from the hi plane only: half of the bytes the planes occupy
+            held = runtime.dense_bytes() // copies // (2 if base.value_dtype == "bf16" else 1)
+            planes = held + costs["step_bytes"] - costs["model_bytes"]
+            roofline["planes_bytes"] = int(planes)
+            roofline["frac_on_planes_bytes"] = round(planes / seconds_kernel / HBM_PEAK, 4)
+    names = {"gemv": "up+down (gemv)", "tiles": "up+down (tiles)"}
+    roofline["kernel"] = names.get(dominant, f"{dominant} ({up if dominant == 'up' else down})")
+    roofline["traffic"] = measured_traffic(workload.name, n, roofline["kernel"])
+    roofline["traffic_source"] = ("rocprofv3 FETCH_SIZE + WRITE_SIZE of this command, per launch, scaled by the copy-kernel "
+                                  "calibration: profiles/traffic.json" if roofline["traffic"] is not None else None)
+    roofline["kernel_us"] = round(seconds_kernel * 1e6, 2)
 
-    baseline = None if args.no_cpu else cpu_baseline(base, x_np, args.cpu_seconds, args.cpu_threads)
     line = {
         "metric": METRIC, "value": round(n * args.steps / seconds, 1), "unit": "tokens/s", "n_gpus": 1,
         "steps": args.steps, "warmup": args.warmup, "ms_per_step": round(seconds / args.steps * 1e3, 4),
@@ -263,6 +307,8 @@ def main() -> int:
                    "modes": [up, down], "kernel_us": {k: round(v * 1e6, 2) for k, v in kernels.items()},
                    "step_hbm_fraction": round(costs["step_bytes"] / (seconds / args.steps) / HBM_PEAK, 4),
                    "step_fp32_fraction": round(costs["step_flops"] / (seconds / args.steps) / FP32_PEAK, 4),
+                   "memory_bytes": {"compact_store": costs["model_bytes"], "planes": runtime.dense_bytes() // copies,
+                                    "workspace": runtime.workspace_bytes()},
                    "wall_s": round(wall, 3)},
         "roofline": roofline,
         "cpu_baseline": baseline,
