@@ -511,11 +511,14 @@ int hffn_tiles_index_entries(uint32_t rows, uint32_t k, uint64_t* entries) {
     return HFFN_OK;
 }
 
-int hffn_tiles_index(const int32_t* offsets, const int16_t* idx, uint32_t rows, uint32_t k, int32_t* table, void* stream) {
+int hffn_tiles_index(int value_type, const int32_t* offsets, const int16_t* idx, const void* val, uint32_t rows, uint32_t k,
+                     int32_t* table, void* stream) {
     uint64_t entries = 0;
     if (int status = hffn_tiles_index_entries(rows, k, &entries)) return status;
-    if (!offsets || !idx || !table) return fail(HFFN_ERROR_ARGUMENT, "tiles_index: null pointer");
-    return launched(hffn::launch_tiles_index(offsets, idx, rows, k, table, static_cast<hipStream_t>(stream)), "tiles_index");
+    if (!valid_value_type(value_type)) return fail(HFFN_ERROR_ARGUMENT, "unknown value type %d", value_type);
+    if (!offsets || !idx || !val || !table) return fail(HFFN_ERROR_ARGUMENT, "tiles_index: null pointer");
+    return launched(hffn::launch_tiles_index(value_type, offsets, idx, val, rows, k, table, static_cast<hipStream_t>(stream)),
+                    "tiles_index");
 }
 
 int hffn_tiles_workspace(uint32_t n, uint32_t d_model, uint32_t d_ff, uint64_t* bytes) {

@@ -111,14 +111,15 @@ hipError_t launch_gemv_forward(int vt, const float* x, const void* up_planes, co
 
 // Decode-sized projections from the compact store (tiles.hip): tiles of 16 rows densified in LDS per 1024-wide chunk
 // of K, MFMA products for 1-kTilesMaxTokens tokens; x, act and y token-major. The index tables (tiles_index_entries
-// int32 per side, built by launch_tiles_index at load) give each row's first slot in every chunk; `work`
+// int32 per side, built by launch_tiles_index at load) give each row's first slot in every chunk and, for float32
+// values, the power of two of the row's largest weight in the chunk; `work`
 // (tiles_workspace_bytes) holds the per-chunk partial sums of a side whose K spans several chunks.
 constexpr uint32_t kTilesChunk = 1024;
 constexpr uint32_t kTilesMaxTokens = 64;
 uint32_t tiles_index_entries(uint32_t rows, uint32_t K);
 size_t tiles_workspace_bytes(uint32_t n, uint32_t d, uint32_t h);
-hipError_t launch_tiles_index(const int32_t* offsets, const int16_t* idx, uint32_t rows, uint32_t K, int32_t* table,
-                              hipStream_t stream);
+hipError_t launch_tiles_index(int vt, const int32_t* offsets, const int16_t* idx, const void* val, uint32_t rows, uint32_t K,
+                              int32_t* table, hipStream_t stream);
 hipError_t launch_tiles_forward(int vt, const float* x, const int16_t* up_idx, const void* up_val, const int32_t* up_table,
                                 const float* b_up, const int16_t* out_hidden, const void* out_val, const int32_t* down_table,
                                 const float* b_down, float* act, float* work, float* y, uint32_t d, uint32_t h, uint32_t nnz_up,

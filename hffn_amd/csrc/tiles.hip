@@ -56,13 +56,6 @@ __device__ __forceinline__ int binade_of(uint32_t magnitude_bits) {
     return magnitude_bits == 0 ? 0 : static_cast<int>((magnitude_bits >> 23) & 0xff) - 127;
 }
 
-__device__ __forceinline__ float wave_max_bits(float v) {
-    uint32_t m = __float_as_uint(v) & 0x7fffffffu;
-#pragma unroll
-    for (int s = 32; s >= 1; s >>= 1) m = max(m, static_cast<uint32_t>(__shfl_xor(static_cast<int>(m), s, kWave)));
-    return __uint_as_float(m);
-}
-
 // A row segment's slots of one chunk, loaded 4 at a time (16-byte fp32 / 8-byte bf16 value loads, 8-byte index loads):
 // group j of lane l starts at slot (b & ~3) + 4 l + 256 j; the slots of a group outside [b, e) are ignored, and the
 // store's last group, when it crosses nnz, is read slot by slot.
@@ -88,7 +81,7 @@ template <typename V, int TT, bool UP>
 __global__ __launch_bounds__(kThreads) void tiles_kernel(const float* __restrict__ in,           // [n, K]
                                                          const int16_t* __restrict__ idx,        // slots' k
                                                          const V* __restrict__ val,              // slots' weights
-                                                         const int32_t* __restrict__ table,      // [R][chunks + 1]
+                                                         const int32_t* __restrict__ table,      // offsets, then binades
                                                          const float* __restrict__ bias,         // [R]
                                                          float* __restrict__ out,                // [n, R]
                                                          float* __restrict__ partials,           // [chunks, n, R]
@@ -110,19 +103,20 @@ __global__ __launch_bounds__(kThreads) void tiles_kernel(const float* __restrict
     const uint32_t width = min(kChunk, K - k0);  // k of this chunk (a multiple of 8)
     const uint32_t r = lane % 16, c = lane / 16;
 
-    // 1. request the wave's inputs and its row segment, then zero the tile while they arrive
+    // 1. request the wave's first inputs and its row segment, zero the tile while they arrive
     const uint32_t row = row0 + wave;
-    int32_t b = 0, e = 0;
+    int32_t b = 0, e = 0, binade = 0;  // binade: the power of two of the segment's largest |weight| (float32 stores)
     if (row < rows) {
         b = table[static_cast<size_t>(row) * (chunks + 1) + chunk];
         e = table[static_cast<size_t>(row) * (chunks + 1) + chunk + 1];
+        if constexpr (kPlanes == 2) binade = table[static_cast<size_t>(rows) * (chunks + 1) + static_cast<size_t>(row) * chunks + chunk];
     }
     const uint32_t steps = (width + kStep - 1) / kStep;
     const uint32_t per_wave = (steps + kWaves - 1) / kWaves;  // at most kWaveSteps
     const uint32_t s0 = min(steps, wave * per_wave), s1 = min(steps, s0 + per_wave);
-    // The inputs of this wave's first 32-k step, requested before the slots (those of its second step are requested
-    // after the scatter, when the slot registers are free). Loaded without branches: an input outside the call
-    // (token >= n, k beyond the chunk) loads x[0, 0..7] and is zeroed at use.
+    // The inputs of the wave's two 32-k steps: the first requested before the slots, the second after the scatter (when
+    // the slot registers are free). Loaded without branches: an input outside the call (token >= n, k beyond the
+    // chunk) loads x[0, 0..7] and is zeroed at use.
     auto request = [&](uint32_t q, float (&xv)[TT][8]) -> uint32_t {
         uint32_t live = 0;  // bit tt: token tile tt of step q is inside the call
         const uint32_t kk = (s0 + q) * kStep + c * 8;
@@ -172,24 +166,10 @@ __global__ __launch_bounds__(kThreads) void tiles_kernel(const float* __restrict
         }
     }
     for (uint32_t i = threadIdx.x; i < kTileHalves / 8; i += kThreads) reinterpret_cast<uint4*>(tile)[i] = make_uint4(0, 0, 0, 0);
-    // groups per lane this segment needs (wave-uniform): the loops below stop there
-    const uint32_t groups = e > b ? static_cast<uint32_t>((e - (b & ~3) + 4 * kWave - 1) / (4 * kWave)) : 0;
-    int binade = 0;
-    if constexpr (kPlanes == 2) {
-        float m = 0.0f;
-#pragma unroll
-        for (uint32_t j = 0; j < kGroups; ++j) {
-            if (j >= groups) break;
-            const int32_t g = first + static_cast<int32_t>(j * 4 * kWave);
-#pragma unroll
-            for (int q = 0; q < 4; ++q)
-                if (g + q >= b && g + q < e) m = fmaxf(m, fabsf(Quad<V>::at(wq[j], q)));
-        }
-        binade = binade_of(__float_as_uint(wave_max_bits(m)));
-    }
-    __syncthreads();
+    __syncthreads();  // the tile is zero (this waits for the LDS only: the loads stay in flight)
 
-    // 2. scatter the row into the dense tile
+    // 2. scatter the row into the tile, each group as its loads arrive
+    const uint32_t groups = e > b ? static_cast<uint32_t>((e - (b & ~3) + 4 * kWave - 1) / (4 * kWave)) : 0;
 #pragma unroll
     for (uint32_t j = 0; j < kGroups; ++j) {
         if (j >= groups) break;
@@ -215,55 +195,63 @@ __global__ __launch_bounds__(kThreads) void tiles_kernel(const float* __restrict
     const uint32_t live1 = request(1, xv1);
     __syncthreads();
 
-    // 3. products over this wave's 32-k steps
+    // 3. products over the wave's two 32-k steps
     static_assert(kWaveSteps == 2, "two 32-k steps per wave");
+    uint4 bh[2], bl[2];
+#pragma unroll
+    for (uint32_t q = 0; q < 2; ++q) {
+        const uint16_t* b_at = tile + tile_at(r, min(s0 + q, steps - 1) * kStep + c * 8);
+        bh[q] = *reinterpret_cast<const uint4*>(b_at);
+        bl[q] = make_uint4(0, 0, 0, 0);
+        if constexpr (kPlanes == 2) bl[q] = *reinterpret_cast<const uint4*>(b_at + kRows * kLdsRow);
+    }
     floatx4 acc[TT];
 #pragma unroll
-    for (int tt = 0; tt < TT; ++tt) acc[tt] = floatx4{0.0f, 0.0f, 0.0f, 0.0f};
+    for (int tt = 0; tt < TT; ++tt) {
+        float v[2][8];
 #pragma unroll
-    for (uint32_t q = 0; q < kWaveSteps; ++q) {
-        if (s0 + q >= s1) break;
-        const uint16_t* b_at = tile + tile_at(r, (s0 + q) * kStep + c * 8);
-        const uint4 b_hi = *reinterpret_cast<const uint4*>(b_at);
-        uint4 b_lo = make_uint4(0, 0, 0, 0);
-        if constexpr (kPlanes == 2) b_lo = *reinterpret_cast<const uint4*>(b_at + kRows * kLdsRow);
+        for (int i = 0; i < 8; ++i) {
+            v[0][i] = (live0 >> tt) & 1u ? xv0[tt][i] : 0.0f;
+            v[1][i] = (live1 >> tt) & 1u ? xv1[tt][i] : 0.0f;
+        }
+        if constexpr (kPlanes == 2) {
+            // the token's power of two over the wave's 64 k: its inputs sit in lanes r, r + 16, r + 32, r + 48
+            uint32_t m = 0;
 #pragma unroll
-        for (int tt = 0; tt < TT; ++tt) {
-            float v[8];
-            const bool inside = ((q == 0 ? live0 : live1) >> tt) & 1u;
+            for (int i = 0; i < 8; ++i) m = max(m, max(__float_as_uint(v[0][i]), __float_as_uint(v[1][i])) & 0x7fffffffu);
+            m = max(m, static_cast<uint32_t>(__shfl_xor(static_cast<int>(m), 16, kWave)));
+            m = max(m, static_cast<uint32_t>(__shfl_xor(static_cast<int>(m), 32, kWave)));
+            const int ex = binade_of(m);
+            floatx4 d = floatx4{0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
-            for (int i = 0; i < 8; ++i) v[i] = inside ? (q == 0 ? xv0[tt][i] : xv1[tt][i]) : 0.0f;
-            if constexpr (kPlanes == 2) {
-                // the token's power of two over this 32-k step: its 32 inputs sit in lanes r, r + 16, r + 32, r + 48
-                uint32_t m = 0;
-#pragma unroll
-                for (int i = 0; i < 8; ++i) m = max(m, __float_as_uint(v[i]) & 0x7fffffffu);
-                m = max(m, static_cast<uint32_t>(__shfl_xor(static_cast<int>(m), 16, kWave)));
-                m = max(m, static_cast<uint32_t>(__shfl_xor(static_cast<int>(m), 32, kWave)));
-                const int ex = binade_of(m);
+            for (int q = 0; q < 2; ++q) {
                 half8 xh, xl;
 #pragma unroll
                 for (int i = 0; i < 8; ++i) {
-                    const float s = ldexpf(v[i], -ex);
-                    const _Float16 hv = static_cast<_Float16>(s);
+                    const float sv = ldexpf(v[q][i], -ex);
+                    const _Float16 hv = static_cast<_Float16>(sv);
                     xh[i] = hv;
-                    xl[i] = static_cast<_Float16>(s - static_cast<float>(hv));
+                    xl[i] = static_cast<_Float16>(sv - static_cast<float>(hv));
                 }
-                const half8 wh = __builtin_bit_cast(half8, b_hi), wl = __builtin_bit_cast(half8, b_lo);
-                floatx4 d = __builtin_amdgcn_mfma_f32_16x16x32_f16(xh, wh, floatx4{0.0f, 0.0f, 0.0f, 0.0f}, 0, 0, 0);
+                const half8 wh = __builtin_bit_cast(half8, bh[q]), wl = __builtin_bit_cast(half8, bl[q]);
+                d = __builtin_amdgcn_mfma_f32_16x16x32_f16(xh, wh, d, 0, 0, 0);
                 d = __builtin_amdgcn_mfma_f32_16x16x32_f16(xh, wl, d, 0, 0, 0);
                 d = __builtin_amdgcn_mfma_f32_16x16x32_f16(xl, wh, d, 0, 0, 0);
-                // D register i holds token 4c + i of the tile: undo its power of two (held by lane 4c + i)
+            }
+            // D register i holds token 4c + i of the tile: undo its power of two (held by lane 4c + i)
 #pragma unroll
-                for (int i = 0; i < 4; ++i) acc[tt][i] += ldexpf(d[i], __shfl(ex, static_cast<int>(4 * c + i), kWave));
-            } else {
+            for (int i = 0; i < 4; ++i) acc[tt][i] = ldexpf(d[i], __shfl(ex, static_cast<int>(4 * c + i), kWave));
+        } else {
+            acc[tt] = floatx4{0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+            for (int q = 0; q < 2; ++q) {
                 uint32_t p1[4], p2[4], p3[4];  // pairs of bfloat16: the three parts of the 8 inputs
 #pragma unroll
                 for (int i = 0; i < 8; i += 2) {
                     uint32_t part[3][2];
 #pragma unroll
                     for (int h = 0; h < 2; ++h) {
-                        const float x0 = v[i + h];
+                        const float x0 = v[q][i + h];
                         const uint32_t b1 = __float_as_uint(x0) & 0xffff0000u;
                         const float rest = x0 - __uint_as_float(b1);
                         const uint32_t b2 = __float_as_uint(rest) & 0xffff0000u;
@@ -276,7 +264,7 @@ __global__ __launch_bounds__(kThreads) void tiles_kernel(const float* __restrict
                     p2[i / 2] = part[1][0] | (part[1][1] << 16);
                     p3[i / 2] = part[2][0] | (part[2][1] << 16);
                 }
-                const bf16x8 wb = __builtin_bit_cast(bf16x8, b_hi);
+                const bf16x8 wb = __builtin_bit_cast(bf16x8, bh[q]);
                 acc[tt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, p1), wb, acc[tt], 0, 0, 0);
                 acc[tt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, p2), wb, acc[tt], 0, 0, 0);
                 acc[tt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, p3), wb, acc[tt], 0, 0, 0);
@@ -338,19 +326,33 @@ __global__ __launch_bounds__(256) void tiles_reduce_kernel(const float* __restri
     out[o] = UP ? gelu(z) : z;
 }
 
-// table[r][c] = the first slot of row r whose index is at least c * kChunk (c = 0 .. chunks); one thread per entry.
+// The index table of one side: offsets[r][c] = the first slot of row r whose index is at least c * kChunk
+// (c = 0 .. chunks), then, for float32 values, binades[r][c] = the power of two of the largest |weight| of row r's slots
+// in chunk c (c < chunks; 0 for an empty segment). One thread per row.
+template <typename V>
 __global__ __launch_bounds__(256) void tiles_index_kernel(const int32_t* __restrict__ offsets, const int16_t* __restrict__ idx,
-                                                          uint32_t rows, uint32_t chunks, int32_t* __restrict__ table) {
-    const uint32_t e = blockIdx.x * 256 + threadIdx.x;
-    if (e >= rows * (chunks + 1)) return;
-    const uint32_t r = e / (chunks + 1), c = e % (chunks + 1);
-    int32_t lo = offsets[r], hi = offsets[r + 1];  // first slot in [lo, hi) with idx >= c * kChunk, else hi
-    const uint32_t bound = c * kChunk;
-    while (lo < hi) {
-        const int32_t mid = lo + (hi - lo) / 2;
-        if (static_cast<uint32_t>(static_cast<uint16_t>(idx[mid])) < bound) lo = mid + 1; else hi = mid;
+                                                          const V* __restrict__ val, uint32_t rows, uint32_t chunks,
+                                                          int32_t* __restrict__ table) {
+    const uint32_t r = blockIdx.x * 256 + threadIdx.x;
+    if (r >= rows) return;
+    const int32_t end = offsets[r + 1];
+    int32_t lo = offsets[r];
+    table[static_cast<size_t>(r) * (chunks + 1)] = lo;
+    for (uint32_t c = 1; c <= chunks; ++c) {
+        // the first slot in [lo, end) whose index reaches c * kChunk, else end (indices ascend within the row)
+        int32_t a = lo, z = end;
+        while (a < z) {
+            const int32_t mid = a + (z - a) / 2;
+            if (static_cast<uint32_t>(static_cast<uint16_t>(idx[mid])) < c * kChunk) a = mid + 1; else z = mid;
+        }
+        table[static_cast<size_t>(r) * (chunks + 1) + c] = a;
+        if constexpr (sizeof(V) == 4) {
+            uint32_t m = 0;
+            for (int32_t s = lo; s < a; ++s) m = max(m, __float_as_uint(val[s]) & 0x7fffffffu);
+            table[static_cast<size_t>(rows) * (chunks + 1) + static_cast<size_t>(r) * chunks + c - 1] = binade_of(m);
+        }
+        lo = a;
     }
-    table[e] = lo;
 }
 
 uint32_t chunks_of(uint32_t K) { return (K + kChunk - 1) / kChunk; }
@@ -377,7 +379,7 @@ hipError_t tiles_side(const float* in, const int16_t* idx, const void* val, cons
 
 }  // namespace
 
-uint32_t tiles_index_entries(uint32_t rows, uint32_t K) { return rows * (chunks_of(K) + 1); }
+uint32_t tiles_index_entries(uint32_t rows, uint32_t K) { return rows * (2 * chunks_of(K) + 1); }
 
 size_t tiles_workspace_bytes(uint32_t n, uint32_t d, uint32_t h) {
     const size_t up = chunks_of(d) > 1 ? size_t(chunks_of(d)) * n * h : 0;
@@ -385,10 +387,16 @@ size_t tiles_workspace_bytes(uint32_t n, uint32_t d, uint32_t h) {
     return std::max<size_t>(std::max(up, down) * sizeof(float), 256);
 }
 
-hipError_t launch_tiles_index(const int32_t* offsets, const int16_t* idx, uint32_t rows, uint32_t K, int32_t* table,
-                              hipStream_t stream) {
-    const uint32_t entries = tiles_index_entries(rows, K);
-    hipLaunchKernelGGL(tiles_index_kernel, dim3((entries + 255) / 256), dim3(256), 0, stream, offsets, idx, rows, chunks_of(K), table);
+hipError_t launch_tiles_index(int vt, const int32_t* offsets, const int16_t* idx, const void* val, uint32_t rows, uint32_t K,
+                              int32_t* table, hipStream_t stream) {
+    const dim3 grid((rows + 255) / 256);
+    if (vt == kBF16) {
+        hipLaunchKernelGGL(tiles_index_kernel<uint16_t>, grid, dim3(256), 0, stream, offsets, idx, static_cast<const uint16_t*>(val), rows,
+                           chunks_of(K), table);
+    } else {
+        hipLaunchKernelGGL(tiles_index_kernel<float>, grid, dim3(256), 0, stream, offsets, idx, static_cast<const float*>(val), rows,
+                           chunks_of(K), table);
+    }
     return hipGetLastError();
 }
 

@@ -297,16 +297,18 @@ class HFFNRuntime:
         return self.d_model % 16 == 0 and self.d_ff % 8 == 0 and self._rows_sorted()
 
     def _tiles_index(self, tensors: dict) -> dict:
-        """Each row's first slot in every 1024-wide chunk of K, for both sides (``hffn_tiles_index``)."""
+        """Each row's first slot in every 1024-wide chunk of K (and, for float32 values, the power of two of the row's
+        largest weight there), for both sides (``hffn_tiles_index``)."""
         stream = torch.cuda.current_stream(self.device).cuda_stream
+        value_type = _value_type(tensors["up_val"], "up_val")
         tables = {}
-        for side, rows, k, names in (("up", self.d_ff, self.d_model, ("up_offsets", "up_idx")),
-                                     ("down", self.d_model, self.d_ff, ("out_offsets", "out_hidden"))):
+        for side, rows, k, names in (("up", self.d_ff, self.d_model, ("up_offsets", "up_idx", "up_val")),
+                                     ("down", self.d_model, self.d_ff, ("out_offsets", "out_hidden", "out_val"))):
             entries = _lib.query_bytes(self._lib.hffn_tiles_index_entries, rows, k)
             table = torch.empty(entries, dtype=torch.int32, device=self.device)
-            offsets, index = (tensors[name] for name in names)
-            _lib.check(self._lib.hffn_tiles_index(offsets.data_ptr(), index.data_ptr(), rows, k, table.data_ptr(), stream),
-                       f"tiles index {side}")
+            offsets, index, values = (tensors[name] for name in names)
+            _lib.check(self._lib.hffn_tiles_index(value_type, offsets.data_ptr(), index.data_ptr(), values.data_ptr(), rows, k,
+                                                  table.data_ptr(), stream), f"tiles index {side}")
             tables[side] = table
         return tables
 
@@ -343,9 +345,11 @@ class HFFNRuntime:
 
     def invalidate_planes(self, index: int) -> None:
         """The compact values of layer ``index`` changed in place (a training update): its densified planes are rebuilt
-        before the MFMA path next reads them."""
+        before the MFMA path next reads them, and the per-chunk powers of two of its tiles index now."""
         if self._planes is not None:
             self._stale.add(index)
+        if self._tiles is not None:
+            self._tiles[index] = self._tiles_index(self._tensors[index])
 
     @property
     def mfma_available(self) -> bool:

@@ -27,7 +27,7 @@
 extern "C" {
 #endif
 
-#define HFFN_ABI_VERSION 11
+#define HFFN_ABI_VERSION 12
 
 #define HFFN_OK 0
 #define HFFN_ERROR_ARGUMENT (-1) /* invalid shape, mode, pointer or workspace */
@@ -208,13 +208,16 @@ int hffn_plan_gemv(int value_type, const void* up_planes, const int32_t* up_bina
  * outside its chunk is skipped, never written out of place). x, act and y token-major; x and act 16-byte aligned; the
  * index arrays 8-byte and the value arrays 16-byte (fp32) or 8-byte (bf16) aligned, nnz_up / nnz_down their lengths. */
 
-/* Entries of one side's index table (host-only query): rows * (ceil(k / 1024) + 1) int32. */
+/* Entries of one side's index table (host-only query): rows * (2 * chunks + 1) int32, chunks = ceil(k / 1024). */
 int hffn_tiles_index_entries(uint32_t rows, uint32_t k, uint64_t* entries);
 
-/* table[r * (chunks + 1) + c] = the first slot of row r (slots [offsets[r], offsets[r + 1]), indices ascending) whose
- * index is at least 1024 c, for c = 0 .. chunks; built once per side at load: the up side over (up_offsets, up_idx,
- * rows = d_ff, k = d_model), the down side over (out_offsets, out_hidden, rows = d_model, k = d_ff). */
-int hffn_tiles_index(const int32_t* offsets, const int16_t* idx, uint32_t rows, uint32_t k, int32_t* table, void* stream);
+/* The index table of one side, built once at load: table[r * (chunks + 1) + c] = the first slot of row r (slots
+ * [offsets[r], offsets[r + 1]), indices ascending) whose index is at least 1024 c, for c = 0 .. chunks; then, for float32
+ * values, table[rows * (chunks + 1) + r * chunks + c] = floor(log2) of the largest |weight| among row r's slots in chunk
+ * c (0 when there are none). The up side over (up_offsets, up_idx, up_val, rows = d_ff, k = d_model), the down side over
+ * (out_offsets, out_hidden, out_val, rows = d_model, k = d_ff). */
+int hffn_tiles_index(int value_type, const int32_t* offsets, const int16_t* idx, const void* val, uint32_t rows, uint32_t k,
+                     int32_t* table, void* stream);
 
 /* Bytes of the workspace of hffn_forward_tiles for n tokens (host-only query): the per-chunk partials of a side whose K
  * spans several chunks. No initial contents needed; calls that share it must be ordered (one stream). */

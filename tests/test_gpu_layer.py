@@ -208,7 +208,8 @@ def test_tiles_token_result_does_not_depend_on_the_batch(name, test_layers, devi
 
 def test_tiles_index_table(test_layers, device):
     """The index table of the tiles path: for every row and every 1024-wide chunk of K, the first slot whose index
-    reaches the chunk (a searchsorted over each row's ascending indices)."""
+    reaches the chunk (a searchsorted over each row's ascending indices), then the power of two of the largest weight
+    of each row's chunk (float32 stores)."""
     from hffn_amd import _lib
     compact, _, layer = test_layers["irreg_512_2048"]
     runtime = HFFNRuntime([layer], device)
@@ -219,7 +220,13 @@ def test_tiles_index_table(test_layers, device):
     assert table.size == _lib.query_bytes(_lib.load().hffn_tiles_index_entries, compact.d_model, compact.d_ff)
     expected = [offsets[o] + np.searchsorted(hidden[offsets[o]:offsets[o + 1]], c * 1024) for o in range(compact.d_model)
                 for c in range(chunks + 1)]
-    assert table.tolist() == [int(v) for v in expected]
+    head = compact.d_model * (chunks + 1)
+    assert table[:head].tolist() == [int(v) for v in expected]
+    values = layer.out_val.cpu().numpy().astype(np.float64)
+    bounds = np.array(expected).reshape(compact.d_model, chunks + 1)
+    binades = [int(np.floor(np.log2(np.abs(values[bounds[o, c]:bounds[o, c + 1]]).max()))) if bounds[o, c + 1] > bounds[o, c] else 0
+               for o in range(compact.d_model) for c in range(chunks)]
+    assert table[head:].tolist() == binades
 
 
 def test_tiles_refuses_more_than_64_tokens(test_layers, device):
