@@ -308,7 +308,7 @@ def main() -> int:
                    "step_hbm_fraction": round(costs["step_bytes"] / (seconds / args.steps) / HBM_PEAK, 4),
                    "step_fp32_fraction": round(costs["step_flops"] / (seconds / args.steps) / FP32_PEAK, 4),
                    "memory_bytes": {"compact_store": costs["model_bytes"], "planes": runtime.dense_bytes() // copies,
-                                    "workspace": runtime.workspace_bytes()},
+                                    "tiled_store": runtime.tiles_bytes() // copies, "workspace": runtime.workspace_bytes()},
                    "wall_s": round(wall, 3)},
         "roofline": roofline,
         "cpu_baseline": baseline,

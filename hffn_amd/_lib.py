@@ -10,7 +10,7 @@ import ctypes
 from pathlib import Path
 
 LIBRARY = Path(__file__).resolve().with_name("libhffn_amd.so")
-ABI_VERSION = 12
+ABI_VERSION = 13
 
 OK = 0
 VALUE_F32, VALUE_BF16 = 0, 1
@@ -54,11 +54,11 @@ SIGNATURES = {
     "hffn_forward_gemv": [_I] + [_P] * 9 + [_U64, _P] + [_U32] * 3 + [_P],
     "hffn_plan_gemv": [_I] + [_P] * 8 + [_U64, _P] + [_U32] * 3 + [_P],
     "hffn_forward_gemv_static": [_I] + [_P] * 9 + [_U32] * 3 + [_P],
-    "hffn_tiles_index_entries": [_U32, _U32, ctypes.POINTER(_U64)],
-    "hffn_tiles_index": [_I, _P, _P, _P, _U32, _U32, _P, _P],
-    "hffn_tiles_workspace": [_U32, _U32, _U32, ctypes.POINTER(_U64)],
-    "hffn_forward_tiles": [_I] + [_P] * 11 + [_U64, _P] + [_U32] * 5 + [_P],
-    "hffn_plan_tiles": [_I] + [_P] * 10 + [_U64, _P] + [_U32] * 5 + [ctypes.POINTER(_U64)],
+    "hffn_tiles_store_size": [_I, _U32, _U32, _U64, ctypes.POINTER(_U64), ctypes.POINTER(_U64)],
+    "hffn_tiles_build": [_I, _P, _P, _P, _U32, _U32, _U64, _P, _U64, _P, _P],
+    "hffn_tiles_workspace": [_I, _U32, _U32, _U32, _U64, _U64, ctypes.POINTER(_U64)],
+    "hffn_forward_tiles": [_I] + [_P] * 9 + [_U64, _P, _U32, _U32, _U64, _U64, _U32, _P],
+    "hffn_plan_tiles": [_I] + [_P] * 8 + [_U64, _P, _U32, _U32, _U64, _U64, _U32, ctypes.POINTER(_U64)],
 }
 
 

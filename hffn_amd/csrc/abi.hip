@@ -212,31 +212,33 @@ int check_tiles(int value_type, uint32_t d_model, uint32_t d_ff, uint32_t n) {
 
 struct TilesPlan {
     int value_type;
-    const int16_t* up_idx;
-    const void* up_val;
-    const int32_t* up_index;
+    const void* up_store;
+    const int32_t* up_table;
     const float* b_up;
-    const int16_t* out_hidden;
-    const void* out_val;
-    const int32_t* down_index;
+    const void* down_store;
+    const int32_t* down_table;
     const float* b_down;
     float* act;
     void* workspace;
     uint64_t workspace_bytes;
     float* y;
-    uint32_t d_model, d_ff, nnz_up, nnz_down, n;
+    uint32_t d_model, d_ff;
+    uint64_t nnz_up, nnz_down;
+    uint32_t n;
 };
 
 int check_tiles_call(const TilesPlan& p, const float* x) {
     if (int status = check_tiles(p.value_type, p.d_model, p.d_ff, p.n)) return status;
-    if (!x || !p.up_idx || !p.up_val || !p.up_index || !p.b_up || !p.out_hidden || !p.out_val || !p.down_index || !p.b_down || !p.act ||
-        !p.workspace || !p.y)
+    if (!x || !p.up_store || !p.up_table || !p.b_up || !p.down_store || !p.down_table || !p.b_down || !p.act || !p.workspace || !p.y)
         return fail(HFFN_ERROR_ARGUMENT, "forward_tiles: null pointer");
     if (reinterpret_cast<uintptr_t>(x) % 16 != 0 || reinterpret_cast<uintptr_t>(p.act) % 16 != 0)
         return fail(HFFN_ERROR_ARGUMENT, "forward_tiles: x and act must be 16-byte aligned");
-    if (int status = check_store_alignment(p.up_idx, p.up_val, p.value_type)) return status;
-    if (int status = check_store_alignment(p.out_hidden, p.out_val, p.value_type)) return status;
-    const uint64_t needed = hffn::tiles_workspace_bytes(p.n, p.d_model, p.d_ff);
+    if (reinterpret_cast<uintptr_t>(p.up_store) % 16 != 0 || reinterpret_cast<uintptr_t>(p.down_store) % 16 != 0)
+        return fail(HFFN_ERROR_ARGUMENT, "forward_tiles: the tiled stores must be 16-byte aligned");
+    if (p.nnz_up > static_cast<uint64_t>(p.d_model) * p.d_ff || p.nnz_down > static_cast<uint64_t>(p.d_model) * p.d_ff)
+        return fail(HFFN_ERROR_ARGUMENT, "forward_tiles: nnz_up=%llu / nnz_down=%llu beyond d_model * d_ff",
+                    static_cast<unsigned long long>(p.nnz_up), static_cast<unsigned long long>(p.nnz_down));
+    const uint64_t needed = hffn::tiles_workspace_bytes(p.value_type, p.n, p.d_model, p.d_ff, p.nnz_up, p.nnz_down);
     if (p.workspace_bytes < needed)
         return fail(HFFN_ERROR_ARGUMENT, "forward_tiles: workspace of %llu bytes, %llu needed for n=%u",
                     static_cast<unsigned long long>(p.workspace_bytes), static_cast<unsigned long long>(needed), p.n);
@@ -244,9 +246,9 @@ int check_tiles_call(const TilesPlan& p, const float* x) {
 }
 
 int launch_tiles(const TilesPlan& p, const float* x, hipStream_t stream) {
-    return launched(hffn::launch_tiles_forward(p.value_type, x, p.up_idx, p.up_val, p.up_index, p.b_up, p.out_hidden, p.out_val,
-                                               p.down_index, p.b_down, p.act, static_cast<float*>(p.workspace), p.y, p.d_model, p.d_ff,
-                                               p.nnz_up, p.nnz_down, p.n, stream),
+    return launched(hffn::launch_tiles_forward(p.value_type, x, p.up_store, p.up_table, p.b_up, p.down_store, p.down_table, p.b_down,
+                                               p.act, static_cast<float*>(p.workspace), p.y, p.d_model, p.d_ff, p.nnz_up, p.nnz_down,
+                                               p.n, stream),
                     "forward (tiles)");
 }
 
@@ -503,48 +505,59 @@ int hffn_forward_gemv_static(int value_type, const float* x, const void* up_plan
 }
 
 
-int hffn_tiles_index_entries(uint32_t rows, uint32_t k, uint64_t* entries) {
-    if (!entries) return fail(HFFN_ERROR_ARGUMENT, "tiles_index_entries: null result");
-    if (rows == 0 || rows > HFFN_MAX_WIDTH || k == 0 || k > HFFN_MAX_WIDTH)
-        return fail(HFFN_ERROR_ARGUMENT, "tiles_index_entries: rows=%u k=%u must be in [1, %u]", rows, k, HFFN_MAX_WIDTH);
-    *entries = hffn::tiles_index_entries(rows, k);
-    return HFFN_OK;
-}
-
-int hffn_tiles_index(int value_type, const int32_t* offsets, const int16_t* idx, const void* val, uint32_t rows, uint32_t k,
-                     int32_t* table, void* stream) {
-    uint64_t entries = 0;
-    if (int status = hffn_tiles_index_entries(rows, k, &entries)) return status;
+int hffn_tiles_store_size(int value_type, uint32_t rows, uint32_t k, uint64_t nnz, uint64_t* store_bytes, uint64_t* table_entries) {
+    if (!store_bytes || !table_entries) return fail(HFFN_ERROR_ARGUMENT, "tiles_store_size: null result");
     if (!valid_value_type(value_type)) return fail(HFFN_ERROR_ARGUMENT, "unknown value type %d", value_type);
-    if (!offsets || !idx || !val || !table) return fail(HFFN_ERROR_ARGUMENT, "tiles_index: null pointer");
-    return launched(hffn::launch_tiles_index(value_type, offsets, idx, val, rows, k, table, static_cast<hipStream_t>(stream)),
-                    "tiles_index");
-}
-
-int hffn_tiles_workspace(uint32_t n, uint32_t d_model, uint32_t d_ff, uint64_t* bytes) {
-    if (!bytes) return fail(HFFN_ERROR_ARGUMENT, "tiles_workspace: null result");
-    if (int status = check_tiles(HFFN_VALUE_F32, d_model, d_ff, n)) return status;
-    *bytes = hffn::tiles_workspace_bytes(n, d_model, d_ff);
+    if (rows == 0 || rows > HFFN_MAX_WIDTH || k == 0 || k > HFFN_MAX_WIDTH)
+        return fail(HFFN_ERROR_ARGUMENT, "tiles_store_size: rows=%u k=%u must be in [1, %u]", rows, k, HFFN_MAX_WIDTH);
+    if (nnz > static_cast<uint64_t>(rows) * k)
+        return fail(HFFN_ERROR_ARGUMENT, "tiles_store_size: nnz=%llu beyond rows * k", static_cast<unsigned long long>(nnz));
+    const hffn::TilesStoreSize size = hffn::tiles_store_size(value_type, rows, k, nnz);
+    *store_bytes = size.store_bytes;
+    *table_entries = size.table_entries;
     return HFFN_OK;
 }
 
-int hffn_forward_tiles(int value_type, const float* x, const int16_t* up_idx, const void* up_val, const int32_t* up_index,
-                       const float* b_up, const int16_t* out_hidden, const void* out_val, const int32_t* down_index,
-                       const float* b_down, float* act, void* workspace, uint64_t workspace_bytes, float* y, uint32_t d_model,
-                       uint32_t d_ff, uint32_t nnz_up, uint32_t nnz_down, uint32_t n, void* stream) {
-    const TilesPlan p{value_type, up_idx, up_val, up_index, b_up, out_hidden, out_val, down_index, b_down, act, workspace,
-                      workspace_bytes, y, d_model, d_ff, nnz_up, nnz_down, n};
+int hffn_tiles_build(int value_type, const int32_t* offsets, const int16_t* idx, const void* val, uint32_t rows, uint32_t k,
+                     uint64_t nnz, void* store, uint64_t store_bytes, int32_t* table, void* stream) {
+    uint64_t needed = 0, entries = 0;
+    if (int status = hffn_tiles_store_size(value_type, rows, k, nnz, &needed, &entries)) return status;
+    if (!offsets || !idx || !val || !store || !table) return fail(HFFN_ERROR_ARGUMENT, "tiles_build: null pointer");
+    if (reinterpret_cast<uintptr_t>(store) % 16 != 0) return fail(HFFN_ERROR_ARGUMENT, "tiles_build: the store must be 16-byte aligned");
+    if (store_bytes < needed)
+        return fail(HFFN_ERROR_ARGUMENT, "tiles_build: store of %llu bytes, %llu needed", static_cast<unsigned long long>(store_bytes),
+                    static_cast<unsigned long long>(needed));
+    return launched(hffn::launch_tiles_build(value_type, offsets, idx, val, rows, k, store, table, static_cast<hipStream_t>(stream)),
+                    "tiles_build");
+}
+
+int hffn_tiles_workspace(int value_type, uint32_t n, uint32_t d_model, uint32_t d_ff, uint64_t nnz_up, uint64_t nnz_down,
+                         uint64_t* bytes) {
+    if (!bytes) return fail(HFFN_ERROR_ARGUMENT, "tiles_workspace: null result");
+    if (int status = check_tiles(value_type, d_model, d_ff, n)) return status;
+    if (nnz_up > static_cast<uint64_t>(d_model) * d_ff || nnz_down > static_cast<uint64_t>(d_model) * d_ff)
+        return fail(HFFN_ERROR_ARGUMENT, "tiles_workspace: nnz_up=%llu / nnz_down=%llu beyond d_model * d_ff",
+                    static_cast<unsigned long long>(nnz_up), static_cast<unsigned long long>(nnz_down));
+    *bytes = hffn::tiles_workspace_bytes(value_type, n, d_model, d_ff, nnz_up, nnz_down);
+    return HFFN_OK;
+}
+
+int hffn_forward_tiles(int value_type, const float* x, const void* up_store, const int32_t* up_table, const float* b_up,
+                       const void* down_store, const int32_t* down_table, const float* b_down, float* act, void* workspace,
+                       uint64_t workspace_bytes, float* y, uint32_t d_model, uint32_t d_ff, uint64_t nnz_up, uint64_t nnz_down,
+                       uint32_t n, void* stream) {
+    const TilesPlan p{value_type, up_store, up_table, b_up, down_store, down_table, b_down, act, workspace, workspace_bytes, y,
+                      d_model, d_ff, nnz_up, nnz_down, n};
     if (int status = check_tiles_call(p, x)) return status;
     return launch_tiles(p, x, static_cast<hipStream_t>(stream));
 }
 
-int hffn_plan_tiles(int value_type, const int16_t* up_idx, const void* up_val, const int32_t* up_index, const float* b_up,
-                    const int16_t* out_hidden, const void* out_val, const int32_t* down_index, const float* b_down, float* act,
-                    void* workspace, uint64_t workspace_bytes, float* y, uint32_t d_model, uint32_t d_ff, uint32_t nnz_up,
-                    uint32_t nnz_down, uint32_t n, uint64_t* plan) {
+int hffn_plan_tiles(int value_type, const void* up_store, const int32_t* up_table, const float* b_up, const void* down_store,
+                    const int32_t* down_table, const float* b_down, float* act, void* workspace, uint64_t workspace_bytes, float* y,
+                    uint32_t d_model, uint32_t d_ff, uint64_t nnz_up, uint64_t nnz_down, uint32_t n, uint64_t* plan) {
     if (!plan) return fail(HFFN_ERROR_ARGUMENT, "plan_tiles: null result");
-    const TilesPlan p{value_type, up_idx, up_val, up_index, b_up, out_hidden, out_val, down_index, b_down, act, workspace,
-                      workspace_bytes, y, d_model, d_ff, nnz_up, nnz_down, n};
+    const TilesPlan p{value_type, up_store, up_table, b_up, down_store, down_table, b_down, act, workspace, workspace_bytes, y,
+                      d_model, d_ff, nnz_up, nnz_down, n};
     const float* some_x = reinterpret_cast<const float*>(uintptr_t{16});  // non-null, aligned: never dereferenced
     if (int status = check_tiles_call(p, some_x)) return status;
     const std::lock_guard<std::mutex> lock(g_plans_mutex);

@@ -109,20 +109,27 @@ hipError_t launch_gemv_forward(int vt, const float* x, const void* up_planes, co
                                const void* down_planes, const int32_t* down_exps, const float* b_down, float* act, float* work,
                                float* y, uint32_t d, uint32_t h, uint32_t n, hipStream_t stream);
 
-// Decode-sized projections from the compact store (tiles.hip): tiles of 16 rows densified in LDS per 1024-wide chunk
-// of K, MFMA products for 1-kTilesMaxTokens tokens; x, act and y token-major. The index tables (tiles_index_entries
-// int32 per side, built by launch_tiles_index at load) give each row's first slot in every chunk and, for float32
-// values, the power of two of the row's largest weight in the chunk; `work`
-// (tiles_workspace_bytes) holds the per-chunk partial sums of a side whose K spans several chunks.
-constexpr uint32_t kTilesChunk = 1024;
+// Decode-sized projections on the tiled store (tiles.hip), 1-kTilesMaxTokens tokens; x, act and y token-major. Each
+// side's tiled store (tiles_store_size: bytes of the store, int32 entries of its table; built at load by
+// launch_tiles_build from the side's compact rows) holds the slots of every 16-row tile and 512-wide sub-chunk of K
+// together in 8-slot groups; `work` (tiles_workspace_bytes) holds the per-chunk partial sums of a side whose blocks
+// split K. tiles_shape: the block shape of a side (row tiles per block, sub-chunks per block, chunks, row blocks),
+// a function of the side's shape and slot count only, so that a token's arithmetic does not depend on the call's token
+// count.
 constexpr uint32_t kTilesMaxTokens = 64;
-uint32_t tiles_index_entries(uint32_t rows, uint32_t K);
-size_t tiles_workspace_bytes(uint32_t n, uint32_t d, uint32_t h);
-hipError_t launch_tiles_index(int vt, const int32_t* offsets, const int16_t* idx, const void* val, uint32_t rows, uint32_t K,
+struct TilesShape {
+    uint32_t tr, s, chunks, blocks;
+};
+struct TilesStoreSize {
+    uint64_t store_bytes, table_entries;
+};
+TilesShape tiles_shape(int vt, uint32_t rows, uint32_t K, uint64_t nnz);
+TilesStoreSize tiles_store_size(int vt, uint32_t rows, uint32_t K, uint64_t nnz);
+size_t tiles_workspace_bytes(int vt, uint32_t n, uint32_t d, uint32_t h, uint64_t nnz_up, uint64_t nnz_down);
+hipError_t launch_tiles_build(int vt, const int32_t* offsets, const int16_t* idx, const void* val, uint32_t rows, uint32_t K, void* store,
                               int32_t* table, hipStream_t stream);
-hipError_t launch_tiles_forward(int vt, const float* x, const int16_t* up_idx, const void* up_val, const int32_t* up_table,
-                                const float* b_up, const int16_t* out_hidden, const void* out_val, const int32_t* down_table,
-                                const float* b_down, float* act, float* work, float* y, uint32_t d, uint32_t h, uint32_t nnz_up,
-                                uint32_t nnz_down, uint32_t n, hipStream_t stream);
+hipError_t launch_tiles_forward(int vt, const float* x, const void* up_store, const int32_t* up_table, const float* b_up,
+                                const void* down_store, const int32_t* down_table, const float* b_down, float* act, float* work,
+                                float* y, uint32_t d, uint32_t h, uint64_t nnz_up, uint64_t nnz_down, uint32_t n, hipStream_t stream);
 
 }  // namespace hffn

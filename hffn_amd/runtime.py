@@ -9,16 +9,22 @@ the chosen shapes need.
 Kernel shapes (the build's own policy, ``up_mode``/``down_mode``):
 
 * ``edges`` - lanes over a row's slots, tokens in registers, input staged in LDS; decode-sized N (N <= 32).
-* ``rows``  - lanes over tokens (1, 2 or 4 per lane), slots walked in order; larger N on layers without the MFMA path.
-* ``mfma``  - tile-densified split-fp16 MFMA GEMMs (up and down together) on layers that qualify (``d_model`` and
-  ``d_ff`` multiples of 256, density at least ``MFMA_MIN_DENSITY``); always above 64 tokens.
-* ``gemv``  - decode GEMVs over the same planes (up and down together, 1-64 tokens): one kernel per projection on
-  16x16x32 MFMAs, the planes read once as whole lines.
+* ``tiles`` - the compact-store MFMA path (up and down together, 1-64 tokens): each side read once from its tiled
+  store (the compact slots regrouped at load by 16-row tile and 512-wide sub-chunk of K, interleaved 16-bit fields),
+  densified per block in LDS and multiplied on 16x16x32 MFMAs.
+* ``rows``  - lanes over tokens (1, 2 or 4 per lane), slots walked in order; large N on layers without the MFMA path.
+* ``mfma``  - tile-densified split-fp16 MFMA GEMMs over dense planes (up and down together) on high-density layers
+  (density at least ``MFMA_MIN_DENSITY``, ``d_model`` and ``d_ff`` multiples of 256), above 64 tokens.
+* ``gemv``  - decode GEMVs over the same planes (1-64 tokens); never chosen by the policy (the planes are kept for
+  large token counts), run when forced.
 
-Up to 64 tokens the policy takes whichever of ``edges`` (up to 32), ``gemv`` and ``mfma`` has the least estimated time
-(``planes_mode``). On the Pythia-410M layer at 50 % (12 rotating copies, MI355X), per call: N = 1: edges 13.7 us,
-gemv 17.5, mfma 28.5; N = 8: gemv 19.7, edges 23.8, mfma 29.8; N = 16: gemv 23.5, mfma 31.2, edges 41.5; N = 32:
-mfma 33.1, gemv 33.1; N = 2048: mfma 140 us.
+The policy reads the compact store up to 64 tokens: ``edges`` (up to 32 tokens) or ``tiles``, whichever has the least
+estimated time (``decode_mode``); above 64 tokens the MFMA path where the layer has planes, else ``rows``. The dense
+planes (4 bytes per weight for float32 values, 2 for bfloat16) are built only for layers of at least
+``MFMA_MIN_DENSITY`` unless asked for (``dense=True``). Per call on the Pythia-410M layer at 50 % (12 rotating
+copies, MI355X, HFFNRuntime.forward): N = 1: tiles 17.4 us, edges 17.6; N = 4: edges 15.3, tiles 17.2; N = 16:
+tiles 18.4, edges 40.6; N = 64: tiles 30.0; N = 2048: mfma 152 us. On the 1.4B layer (bfloat16, 20 %): tiles 21.3,
+22.0, 24.3, 44.9 us at N = 1, 4, 16, 64 (edges 21.6, 25.5, 62.2 at 1, 4, 16).
 
 Model arrays stay on the device. Work buffers are dense, shared by all layers, sized for the largest N seen and
 reused. Kernels are queued on PyTorch's current stream of the device, so they run in call order with the PyTorch
@@ -26,6 +32,7 @@ operations around them (the reference requires the default stream; any current s
 """
 from __future__ import annotations
 
+import ctypes
 from collections import Counter
 from dataclasses import dataclass
 
@@ -41,19 +48,18 @@ GEMV_MAX_TOKENS = 64      # the planes GEMVs' largest call
 TILES_MAX_TOKENS = 64     # the compact-store MFMA path's largest call
 EDGES_MAX_TOKENS = 32     # the policy's last N for the lane-per-slot shapes
 EDGES_PASS_TOKENS = 8     # tokens one pass of the lane-per-slot kernels takes
-MFMA_MIN_DENSITY = 0.05   # the lowest support density the tile-densified MFMA path takes
+MFMA_MIN_DENSITY = 0.5    # the lowest support density whose layers get dense planes by default (the MFMA path)
 # The policy's time estimates (µs per call), fitted to forced-pair timings of HFFNRuntime.forward on MI355X (layer
 # copies rotated so that every call reads HBM; the 70M/20 %, 410M/10 % and 50 %, 1.4B/20 % bf16 and 2.8B/80 % bf16
-# layers, N = 1-256). Lane-per-slot kernels: EDGES_CALL_US per call, plus per pass of up to 8 tokens
-# (EDGES_PASS_US + EDGES_SLOT_US per stored slot of both sides) weighted by EDGES_PASS_WEIGHT of the pass's token
-# width. MFMA path: MFMA_BASE_US + MFMA_ENTRY_US per densified weight of both sides + MFMA_TOKEN_US per token up to
-# 64. Decode GEMVs (N <= 64): GEMV_BASE_US + per densified weight of both sides GEMV_ENTRY_US, plus GEMV_TOKEN_US
-# per weight and token beyond the first up to 16, and beyond 16 (the second and later 16-token MFMA tiles) GEMV_TILE2_US per
-# weight and token plus GEMV_TILE2_TOKEN_US per token.
+# layers). Lane-per-slot kernels: EDGES_CALL_US per call, plus per pass of up to 8 tokens (EDGES_PASS_US +
+# EDGES_SLOT_US per stored slot of both sides) weighted by EDGES_PASS_WEIGHT of the pass's token width. Compact-store
+# MFMA path: TILES_BASE_US + TILES_SLOT_US per stored slot, plus up to (TILES_FILL_US + TILES_FILL_SLOT_US per slot)
+# as the first 16-token tile fills, plus (TILES_TILE_US + TILES_TILE_SLOT_US per slot) per further 16-token tile.
 EDGES_CALL_US, EDGES_PASS_US, EDGES_SLOT_US = 6.0, 4.0, 3.5e-6
 EDGES_PASS_WEIGHT = {1: 0.42, 2: 0.49, 4: 0.52, 8: 1.0}
-MFMA_BASE_US, MFMA_ENTRY_US, MFMA_TOKEN_US = 22.0, 0.93e-6, 0.1
-GEMV_BASE_US, GEMV_ENTRY_US, GEMV_TOKEN_US, GEMV_TILE2_US, GEMV_TILE2_TOKEN_US = 11.9, 0.482e-6, 0.019e-6, 0.038e-6, 0.084
+TILES_BASE_US, TILES_SLOT_US = 12.7, 1.11e-6
+TILES_FILL_US, TILES_FILL_SLOT_US = 2.0, 0.07e-6
+TILES_TILE_US, TILES_TILE_SLOT_US = 4.5, 0.17e-6
 MAX_TOKENS = 1 << 18      # runtime/gpu/nvidia/common/kernels/hffn_cuda/runtime.py:26
 
 _VALUE_TYPES = {torch.float32: _lib.VALUE_F32, torch.bfloat16: _lib.VALUE_BF16}
@@ -85,35 +91,21 @@ def edges_us(n: int, slots: int) -> float:
     return edges
 
 
-def mfma_us(n: int, d_model: int, d_ff: int) -> float:
-    """Estimated µs of a call on the MFMA GEMMs."""
-    return MFMA_BASE_US + MFMA_ENTRY_US * 2 * d_model * d_ff + MFMA_TOKEN_US * min(n, 64)
+def tiles_us(n: int, slots: int) -> float:
+    """Estimated µs of a call on the compact-store MFMA path (N <= 64; ``slots``: stored slots of both sides)."""
+    return (TILES_BASE_US + TILES_SLOT_US * slots + (TILES_FILL_US + TILES_FILL_SLOT_US * slots) * min(n - 1, 15) / 15
+            + (TILES_TILE_US + TILES_TILE_SLOT_US * slots) * ((n - 1) // 16))
 
 
-def gemv_us(n: int, d_model: int, d_ff: int) -> float:
-    """Estimated µs of a call on the decode GEMVs (N <= 64)."""
-    entries = 2 * d_model * d_ff
-    return (GEMV_BASE_US + entries * (GEMV_ENTRY_US + GEMV_TOKEN_US * (min(n, 16) - 1))
-            + max(n - 16, 0) * (GEMV_TILE2_US * entries + GEMV_TILE2_TOKEN_US))
-
-
-def mfma_preferred(n: int, d_model: int, d_ff: int, slots: int) -> bool:
-    """Whether the MFMA path's estimated time beats the lane-per-slot kernels' for N tokens (``slots``: stored slots of
-    both sides); above ``EDGES_MAX_TOKENS`` tokens it always does."""
-    return n > EDGES_MAX_TOKENS or mfma_us(n, d_model, d_ff) < edges_us(n, slots)
-
-
-def planes_mode(n: int, d_model: int, d_ff: int, slots: int, streamed: bool) -> str | None:
-    """The planes path (``gemv`` or ``mfma``) of least estimated time for N tokens when it beats the lane-per-slot
-    kernels (up to ``EDGES_MAX_TOKENS``), else None. Above ``GEMV_MAX_TOKENS`` tokens the MFMA path is taken whenever
-    its GEMMs are streamed (``streamed``)."""
+def decode_mode(n: int, slots: int, edges: bool, tiles: bool) -> str | None:
+    """The compact-store path of least estimated time for N <= 64 tokens: ``edges`` (up to ``EDGES_MAX_TOKENS``, when
+    ``edges``: its LDS stage fits) or ``tiles`` (when ``tiles``: the layer has tiled stores); None when neither
+    applies."""
     options = {}
-    if n <= EDGES_MAX_TOKENS:
-        options[None] = edges_us(n, slots)
-    if n <= GEMV_MAX_TOKENS:
-        options["gemv"] = gemv_us(n, d_model, d_ff)
-    if streamed:
-        options["mfma"] = mfma_us(n, d_model, d_ff) if n <= GEMV_MAX_TOKENS else 0.0
+    if edges and n <= EDGES_MAX_TOKENS:
+        options["edges"] = edges_us(n, slots)
+    if tiles and n <= TILES_MAX_TOKENS:
+        options["tiles"] = tiles_us(n, slots)
     return min(options, key=options.get) if options else None
 
 
@@ -236,9 +228,10 @@ _ARRAYS = ("b_up", "up_offsets", "up_idx", "up_val", "b_down", "out_offsets", "o
 class HFFNRuntime:
     """``HFFNRuntime`` of ``runtime/gpu/nvidia/common/kernels/hffn_cuda/runtime.py:76-163`` on the HIP library."""
 
-    def __init__(self, layers: list[HFFNLayer], device: str | torch.device = "cuda", dense: bool = True) -> None:
-        """``dense``: also build the densified planes of the MFMA path when the layers qualify (``d_model`` and
-        ``d_ff`` multiples of 256, distinct sorted indices per row); without them every call takes the gather kernels."""
+    def __init__(self, layers: list[HFFNLayer], device: str | torch.device = "cuda", dense: bool | None = None) -> None:
+        """``dense``: build the dense planes of the MFMA path and the decode GEMVs (``d_model`` and ``d_ff`` multiples of
+        256, distinct sorted indices per row): None (default) for layers of at least ``MFMA_MIN_DENSITY`` only, True
+        whenever the shapes qualify (the policy still takes them only at that density), False never."""
         self.device = _device(device)
         self.layers = layers
         self.d_model, self.d_ff = layers[0].d_model, layers[0].d_ff
@@ -270,11 +263,13 @@ class HFFNRuntime:
         self._tiles: list[dict] | None = None
         self._tiles_work = torch.empty(1, device=self.device)
         if self._tiles_eligible():
-            self._tiles = [self._tiles_index(tensors) for tensors in self._tensors]
-            words = (_lib.query_bytes(self._lib.hffn_tiles_workspace, TILES_MAX_TOKENS, self.d_model, self.d_ff) + 3) // 4
+            self._tiles = [self._tiles_build(tensors) for tensors in self._tensors]
+            value_type = self._args[0][0]
+            words = max(_lib.query_bytes(self._lib.hffn_tiles_workspace, value_type, TILES_MAX_TOKENS, self.d_model, self.d_ff,
+                                         *nnz) for nnz in self._nnz) // 4
             self._tiles_work = torch.empty(words, device=self.device)  # the per-chunk partial sums
         self._gemv_work = torch.empty(1, device=self.device)
-        if dense and self._mfma_eligible():
+        if (dense or (dense is None and self.density >= MFMA_MIN_DENSITY)) and self._mfma_eligible():
             self._planes = [self._densify(tensors) for tensors in self._tensors]
             words = (_lib.query_bytes(self._lib.hffn_gemv_workspace, self.d_model, self.d_ff) + 3) // 4
             self._gemv_work = torch.empty(words, device=self.device)  # the decode GEMVs' k-split partial sums
@@ -296,21 +291,32 @@ class HFFNRuntime:
     def _tiles_eligible(self) -> bool:
         return self.d_model % 16 == 0 and self.d_ff % 8 == 0 and self._rows_sorted()
 
-    def _tiles_index(self, tensors: dict) -> dict:
-        """Each row's first slot in every 1024-wide chunk of K (and, for float32 values, the power of two of the row's
-        largest weight there), for both sides (``hffn_tiles_index``)."""
+    def _tiles_build(self, tensors: dict, tiles: dict | None = None) -> dict:
+        """The tiled stores of both sides (``hffn_tiles_build``): each side's slots regrouped by 16-row tile and 512-wide
+        sub-chunk of K, with their table; rebuilt into ``tiles`` when given (same sizes: allocates nothing)."""
         stream = torch.cuda.current_stream(self.device).cuda_stream
         value_type = _value_type(tensors["up_val"], "up_val")
-        tables = {}
+        tiles = {} if tiles is None else tiles
         for side, rows, k, names in (("up", self.d_ff, self.d_model, ("up_offsets", "up_idx", "up_val")),
                                      ("down", self.d_model, self.d_ff, ("out_offsets", "out_hidden", "out_val"))):
-            entries = _lib.query_bytes(self._lib.hffn_tiles_index_entries, rows, k)
-            table = torch.empty(entries, dtype=torch.int32, device=self.device)
             offsets, index, values = (tensors[name] for name in names)
-            _lib.check(self._lib.hffn_tiles_index(value_type, offsets.data_ptr(), index.data_ptr(), values.data_ptr(), rows, k,
-                                                  table.data_ptr(), stream), f"tiles index {side}")
-            tables[side] = table
-        return tables
+            store_bytes, entries = ctypes.c_uint64(0), ctypes.c_uint64(0)
+            _lib.check(self._lib.hffn_tiles_store_size(value_type, rows, k, index.numel(), ctypes.byref(store_bytes),
+                                                       ctypes.byref(entries)), f"tiles store size {side}")
+            if side not in tiles:
+                tiles[side] = torch.empty(store_bytes.value, dtype=torch.uint8, device=self.device)
+                tiles[f"{side}_table"] = torch.empty(entries.value, dtype=torch.int32, device=self.device)
+            store, table = tiles[side], tiles[f"{side}_table"]
+            _lib.check(self._lib.hffn_tiles_build(value_type, offsets.data_ptr(), index.data_ptr(), values.data_ptr(), rows, k,
+                                                  index.numel(), store.data_ptr(), store.numel(), table.data_ptr(), stream),
+                       f"tiles build {side}")
+        return tiles
+
+    def tiles_bytes(self) -> int:
+        """Bytes of the tiled stores and their tables held for the tiles path (0 without it)."""
+        if self._tiles is None:
+            return 0
+        return sum(t.numel() * t.element_size() for tiles in self._tiles for t in tiles.values())
 
     @property
     def tiles_available(self) -> bool:
@@ -349,7 +355,7 @@ class HFFNRuntime:
         if self._planes is not None:
             self._stale.add(index)
         if self._tiles is not None:
-            self._tiles[index] = self._tiles_index(self._tensors[index])
+            self._tiles_build(self._tensors[index], self._tiles[index])
 
     @property
     def mfma_available(self) -> bool:
@@ -406,13 +412,16 @@ class HFFNRuntime:
         return chosen
 
     def _modes(self, n: int) -> tuple[str, str]:
-        if self.forced_up is None and self.forced_down is None and self._planes is not None \
-                and self.density >= MFMA_MIN_DENSITY:
-            mode = planes_mode(n, self.d_model, self.d_ff, self._slots, mfma_streamed(n, self.d_model, self.d_ff))
-            if mode is not None:
-                return mode, mode
+        edges = edges_supported(self.d_model, n)
+        if self.forced_up is None and self.forced_down is None:
+            if n <= TILES_MAX_TOKENS:
+                mode = decode_mode(n, self._slots, edges, self._tiles is not None)
+                if mode == "tiles":
+                    return mode, mode
+            elif self._planes is not None and self.density >= MFMA_MIN_DENSITY and mfma_streamed(n, self.d_model, self.d_ff):
+                return "mfma", "mfma"
         up = self.forced_up or up_mode(n, self.d_model)
-        if up == "edges" and not edges_supported(self.d_model, n):
+        if up == "edges" and not edges:
             up = "rows"
         return up, self.forced_down or down_mode(n, self.d_ff)
 
@@ -435,11 +444,11 @@ class HFFNRuntime:
 
     def _tiles_args(self, index: int) -> tuple:
         """The arguments of ``hffn_forward_tiles`` / ``hffn_plan_tiles`` between x and the token count."""
-        tensors, tables = self._tensors[index], self._tiles[index]
+        tensors, tiles = self._tensors[index], self._tiles[index]
         _, act, _, y = self._work
-        return (tensors["up_idx"].data_ptr(), tensors["up_val"].data_ptr(), tables["up"].data_ptr(), tensors["b_up"].data_ptr(),
-                tensors["out_hidden"].data_ptr(), tensors["out_val"].data_ptr(), tables["down"].data_ptr(),
-                tensors["b_down"].data_ptr(), act, self._tiles_work.data_ptr(), 4 * self._tiles_work.numel(), y)
+        return (tiles["up"].data_ptr(), tiles["up_table"].data_ptr(), tensors["b_up"].data_ptr(), tiles["down"].data_ptr(),
+                tiles["down_table"].data_ptr(), tensors["b_down"].data_ptr(), act, self._tiles_work.data_ptr(),
+                4 * self._tiles_work.numel(), y)
 
     def _launch(self, index: int, x: torch.Tensor, n: int, up: str, down: str) -> None:
         value_type, *model = self._args[index]

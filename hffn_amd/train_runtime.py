@@ -33,13 +33,14 @@ from dataclasses import dataclass
 import torch
 
 from . import _lib
-from .runtime import MAX_TOKENS, MFMA_MIN_DENSITY, PAIR_MODES, HFFNRuntime, down_mode, edges_supported, leading_dim, up_mode
+from .runtime import MAX_TOKENS, PAIR_MODES, HFFNRuntime, down_mode, edges_supported, leading_dim, up_mode
 
 PARAMETERS = ("up_val", "b_up", "out_val", "b_down")
 SUPPORTS = ("in_offsets", "in_pos", "in_hidden", "hid_offsets", "hid_pos", "hid_output")
 GRAD_TILE = 256              # tokens per tile of the gather sampled products
 PARTIAL_MAX_TOKENS = 2048    # tokens the tile partials are sized for at construction
 GRAD_DENSE_MIN_TOKENS = 64   # from this N the sampled products may run as dense MFMA products
+GRAD_DENSE_MIN_DENSITY = 0.05  # on layers of at least this support density (the products' dense work over the useful)
 GRAD_MODES = ("gather", "dense")
 
 
@@ -177,7 +178,7 @@ class HFFNTrainRuntime:
 
     def grad_mode(self, n: int) -> str:
         """``dense`` (MFMA products over the tokens, sampled at the support) from ``GRAD_DENSE_MIN_TOKENS`` tokens on
-        layers of at least ``MFMA_MIN_DENSITY`` whose shapes the streamed GEMM takes, else ``gather``;
+        layers of at least ``GRAD_DENSE_MIN_DENSITY`` whose shapes the streamed GEMM takes, else ``gather``;
         ``forced_grad`` overrides the choice."""
         if self.forced_grad is not None:
             if self.forced_grad not in GRAD_MODES:
@@ -185,7 +186,7 @@ class HFFNTrainRuntime:
             if self.forced_grad == "dense" and not self._dense_bytes_at(n):
                 raise ValueError(f"the dense sampled products do not run at N={n} on {self.d_model} x {self.d_ff}")
             return self.forced_grad
-        dense = n >= GRAD_DENSE_MIN_TOKENS and self.runtime.density >= MFMA_MIN_DENSITY and self._dense_bytes_at(n) > 0
+        dense = n >= GRAD_DENSE_MIN_TOKENS and self.runtime.density >= GRAD_DENSE_MIN_DENSITY and self._dense_bytes_at(n) > 0
         return "dense" if dense else "gather"
 
     def _tokens_of(self, t: torch.Tensor, name: str) -> int:

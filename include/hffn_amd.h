@@ -27,7 +27,7 @@
 extern "C" {
 #endif
 
-#define HFFN_ABI_VERSION 12
+#define HFFN_ABI_VERSION 13
 
 #define HFFN_OK 0
 #define HFFN_ERROR_ARGUMENT (-1) /* invalid shape, mode, pointer or workspace */
@@ -199,45 +199,49 @@ int hffn_plan_gemv(int value_type, const void* up_planes, const int32_t* up_bina
 
 /* ---- Decode path on the compact store (1-64 tokens). No reference counterpart for the arithmetic: the reference
  * decodes on its gather kernels (runtime/gpu/nvidia/common/kernels/hffn_cuda/kernels.py:102-191), reading each slot
- * once per kernel as these do. A block takes 16 rows and one 1024-wide chunk of K: it reads those rows' slots of the
- * chunk from the compact store (each slot once per call), densifies them in LDS (float32 weights as fp16 hi/lo
- * scaled by a power of two per row and chunk, bfloat16 weights as they are) and multiplies on 16x16x32 MFMAs
- * (float32: x split per token and 32-k step into fp16 hi/lo, three products; bfloat16: x split exactly into three
- * bfloat16 parts). Rows whose K spans several chunks write per-chunk partials, added in chunk order by a second
- * kernel. Every row's indices must be strictly increasing (the index table and the densified tile assume it; a slot
- * outside its chunk is skipped, never written out of place). x, act and y token-major; x and act 16-byte aligned; the
- * index arrays 8-byte and the value arrays 16-byte (fp32) or 8-byte (bf16) aligned, nnz_up / nnz_down their lengths. */
+ * once per kernel as these do. Each side is read from its tiled store: a copy of the side's compact rows, built once at
+ * load, in which the slots of every 16-row tile and 512-wide sub-chunk of K (an item) are consecutive, in 8-slot groups
+ * of interleaved 16-bit fields ([8 positions][8 bfloat16 weights], 32 bytes; or [8 positions][8 fp16 hi][8 fp16 lo],
+ * 48 bytes, hi + lo = the float32 weight scaled by the power of two of its row's largest |weight|), each item padded
+ * to whole groups with its last slot repeated. A block reads the groups of 16 or 32 rows over a chunk of K (16-byte
+ * loads, each slot once per call), densifies them in LDS and multiplies on 16x16x32 MFMAs (float32: x split per token
+ * into fp16 hi/lo, three products; bfloat16: x split exactly into three bfloat16 parts). Sides whose blocks split K
+ * write per-chunk partials, added in chunk order by a second kernel. x, act and y token-major; x and act 16-byte
+ * aligned. */
 
-/* Entries of one side's index table (host-only query): rows * (2 * chunks + 1) int32, chunks = ceil(k / 1024). */
-int hffn_tiles_index_entries(uint32_t rows, uint32_t k, uint64_t* entries);
+/* Sizes of one side's tiled store for nnz slots over rows x k (host-only query): bytes of the store (an upper bound:
+ * padding of at most one group per item, one spare group) and int32 entries of its table (items + 1, then one per row
+ * for float32 values; items = ceil(rows / 16) * ceil(k / 512)). */
+int hffn_tiles_store_size(int value_type, uint32_t rows, uint32_t k, uint64_t nnz, uint64_t* store_bytes, uint64_t* table_entries);
 
-/* The index table of one side, built once at load: table[r * (chunks + 1) + c] = the first slot of row r (slots
- * [offsets[r], offsets[r + 1]), indices ascending) whose index is at least 1024 c, for c = 0 .. chunks; then, for float32
- * values, table[rows * (chunks + 1) + r * chunks + c] = floor(log2) of the largest |weight| among row r's slots in chunk
- * c (0 when there are none). The up side over (up_offsets, up_idx, up_val, rows = d_ff, k = d_model), the down side over
- * (out_offsets, out_hidden, out_val, rows = d_model, k = d_ff). */
-int hffn_tiles_index(int value_type, const int32_t* offsets, const int16_t* idx, const void* val, uint32_t rows, uint32_t k,
-                     int32_t* table, void* stream);
+/* Builds one side's tiled store and table on the device, once at load: the up side from (up_offsets, up_idx, up_val,
+ * rows = d_ff, k = d_model), the down side from (out_offsets, out_hidden, out_val, rows = d_model, k = d_ff). Every
+ * row's indices must be strictly increasing and below k. table[i] = the first group of item i (items of tile t and
+ * sub-chunk j at i = t * ceil(k / 512) + j), table[items] = the number of groups, then (float32) the rows' powers of
+ * two. store 16-byte aligned, of at least the bytes hffn_tiles_store_size gives. */
+int hffn_tiles_build(int value_type, const int32_t* offsets, const int16_t* idx, const void* val, uint32_t rows, uint32_t k,
+                     uint64_t nnz, void* store, uint64_t store_bytes, int32_t* table, void* stream);
 
-/* Bytes of the workspace of hffn_forward_tiles for n tokens (host-only query): the per-chunk partials of a side whose K
- * spans several chunks. No initial contents needed; calls that share it must be ordered (one stream). */
-int hffn_tiles_workspace(uint32_t n, uint32_t d_model, uint32_t d_ff, uint64_t* bytes);
+/* Bytes of the workspace of hffn_forward_tiles for n tokens (host-only query): the per-chunk partials of a side whose
+ * blocks split K. The block shape of each side depends on its dimensions and slot count (nnz_up, nnz_down), never on n.
+ * No initial contents needed; calls that share it must be ordered (one stream). */
+int hffn_tiles_workspace(int value_type, uint32_t n, uint32_t d_model, uint32_t d_ff, uint64_t nnz_up, uint64_t nnz_down,
+                         uint64_t* bytes);
 
 /* act[t, r] = gelu(b_up[r] + sum_k W_up[r, k] x[t, k]) into act (token-major [n, d_ff]), then
  * y[t, o] = b_down[o] + sum_r W_down[o, r] act[t, r] (token-major [n, d_model]); 1 <= n <= 64, d_model a multiple of
- * 16, d_ff of 8. The stores are the runtime's (up hidden-major, down output-major) with the two index tables. */
-int hffn_forward_tiles(int value_type, const float* x, const int16_t* up_idx, const void* up_val, const int32_t* up_index,
-                       const float* b_up, const int16_t* out_hidden, const void* out_val, const int32_t* down_index,
-                       const float* b_down, float* act, void* workspace, uint64_t workspace_bytes, float* y, uint32_t d_model,
-                       uint32_t d_ff, uint32_t nnz_up, uint32_t nnz_down, uint32_t n, void* stream);
+ * 16, d_ff of 8. The stores and tables are hffn_tiles_build's of the two sides, over nnz_up and nnz_down slots. */
+int hffn_forward_tiles(int value_type, const float* x, const void* up_store, const int32_t* up_table, const float* b_up,
+                       const void* down_store, const int32_t* down_table, const float* b_down, float* act, void* workspace,
+                       uint64_t workspace_bytes, float* y, uint32_t d_model, uint32_t d_ff, uint64_t nnz_up, uint64_t nnz_down,
+                       uint32_t n, void* stream);
 
 /* Prepared hffn_forward_tiles (every argument but x and the stream checked and kept under a handle), launched by
  * hffn_plan_launch and dropped by hffn_plan_release as hffn_plan_forward's: the decode launch path of
  * PreparedRuntime (runtime/gpu/nvidia/llm/inference/hffn_pythia_cuda/prepared_runtime.py:34-82) for this path. */
-int hffn_plan_tiles(int value_type, const int16_t* up_idx, const void* up_val, const int32_t* up_index, const float* b_up,
-                    const int16_t* out_hidden, const void* out_val, const int32_t* down_index, const float* b_down, float* act,
-                    void* workspace, uint64_t workspace_bytes, float* y, uint32_t d_model, uint32_t d_ff, uint32_t nnz_up,
-                    uint32_t nnz_down, uint32_t n, uint64_t* plan);
+int hffn_plan_tiles(int value_type, const void* up_store, const int32_t* up_table, const float* b_up, const void* down_store,
+                    const int32_t* down_table, const float* b_down, float* act, void* workspace, uint64_t workspace_bytes, float* y,
+                    uint32_t d_model, uint32_t d_ff, uint64_t nnz_up, uint64_t nnz_down, uint32_t n, uint64_t* plan);
 
 /* ------------------------------------------------------------------------------------------------ training (fp32)
  * Layouts: act, z, gz hidden-major [d_ff, ld]; x_t, gy_t, gx_t feature-major [d_model, ld]; x, y, gx token-major

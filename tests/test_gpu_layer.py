@@ -105,7 +105,7 @@ def test_gelu_against_float64(device):
 @pytest.mark.parametrize("name", sorted(synth.CASES))
 def test_forced_pairs_match_the_oracle(name, test_layers, device):
     compact, case, layer = test_layers[name]
-    runtime = HFFNRuntime([layer], device)
+    runtime = HFFNRuntime([layer], device, dense=True)
     for n in BATCHES:
         x_np = synth.make_input(case, n)
         expected = torch.from_numpy(reference.forward(compact, x_np)).to(device)
@@ -119,7 +119,7 @@ def test_forced_pairs_match_the_oracle(name, test_layers, device):
 def test_shared_buffers_between_calls(test_layers, device):
     """A call at another N in between does not change a result (runtime/cpu/x86/ffn/inference/tests/test_parity.py:27-35)."""
     compact, case, layer = test_layers["irreg_512_2048"]
-    runtime = HFFNRuntime([layer], device)
+    runtime = HFFNRuntime([layer], device, dense=True)
     x8, x96, x1 = (torch.from_numpy(synth.make_input(case, n)).to(device) for n in (8, 96, 1))
     first = runtime.forward(0, x8).clone()
     runtime.forward(0, x96)
@@ -139,7 +139,7 @@ def test_densified_planes_reconstruct_the_weights(name, test_layers, device):
     """hi + lo of each plane entry, rescaled by its row's power of two, is the weight to 2^-22 of the row's largest
     entry, and exactly zero outside the support."""
     compact, _, layer = test_layers[name]
-    runtime = HFFNRuntime([layer], device)
+    runtime = HFFNRuntime([layer], device, dense=True)
     assert runtime.mfma_available
     planes = runtime._planes[0]
     w_up, w_down = reference.dense_weights(compact)
@@ -161,7 +161,7 @@ def test_token_result_does_not_depend_on_the_batch(up, down, test_layers, device
     into more parts when fewer tokens leave blocks idle, so a token's sums are grouped differently: equal to 1e-6 of
     the output's scale, and bit-identical between calls of the same N."""
     compact, case, layer = test_layers["homog_512_2048"]
-    runtime = HFFNRuntime([layer], device)
+    runtime = HFFNRuntime([layer], device, dense=True)
     runtime.force(up, down)
     x = torch.from_numpy(synth.make_input(case, 300)).to(device)
     whole = runtime.forward(0, x).clone()
@@ -181,7 +181,7 @@ def test_gemv_token_result_does_not_depend_on_the_batch(name, test_layers, devic
     whatever the other tokens (one, two or four 16-token MFMA tiles): a token's result is bit-identical alone and in
     any batch of up to 64 tokens."""
     compact, case, layer = test_layers[name]
-    runtime = HFFNRuntime([layer], device)
+    runtime = HFFNRuntime([layer], device, dense=True)
     runtime.force("gemv", "gemv")
     x = torch.from_numpy(synth.make_input(case, 64)).to(device)
     whole = runtime.forward(0, x).clone()
@@ -197,7 +197,7 @@ def test_tiles_token_result_does_not_depend_on_the_batch(name, test_layers, devi
     tile, each token scaled by its own power of two per 32-k step: a token's result is bit-identical alone and in any
     batch of up to 64 tokens."""
     compact, case, layer = test_layers[name]
-    runtime = HFFNRuntime([layer], device)
+    runtime = HFFNRuntime([layer], device, dense=True)
     runtime.force("tiles", "tiles")
     x = torch.from_numpy(synth.make_input(case, 64)).to(device)
     whole = runtime.forward(0, x).clone()
@@ -206,32 +206,79 @@ def test_tiles_token_result_does_not_depend_on_the_batch(name, test_layers, devi
     assert _relative(whole, reference.forward(compact, x.cpu().numpy())) <= 1e-5
 
 
-def test_tiles_index_table(test_layers, device):
-    """The index table of the tiles path: for every row and every 1024-wide chunk of K, the first slot whose index
-    reaches the chunk (a searchsorted over each row's ascending indices), then the power of two of the largest weight
-    of each row's chunk (float32 stores)."""
-    from hffn_amd import _lib
-    compact, _, layer = test_layers["irreg_512_2048"]
-    runtime = HFFNRuntime([layer], device)
-    table = runtime._tiles[0]["down"].cpu().numpy()  # rows = d_model outputs over K = d_ff = 2048: two chunks
-    offsets = layer.out_offsets.cpu().numpy().astype(np.int64)
-    hidden = layer.out_hidden.cpu().numpy().astype(np.int64)
-    chunks = (compact.d_ff + 1023) // 1024
-    assert table.size == _lib.query_bytes(_lib.load().hffn_tiles_index_entries, compact.d_model, compact.d_ff)
-    expected = [offsets[o] + np.searchsorted(hidden[offsets[o]:offsets[o + 1]], c * 1024) for o in range(compact.d_model)
-                for c in range(chunks + 1)]
-    head = compact.d_model * (chunks + 1)
-    assert table[:head].tolist() == [int(v) for v in expected]
-    values = layer.out_val.cpu().numpy().astype(np.float64)
-    bounds = np.array(expected).reshape(compact.d_model, chunks + 1)
-    binades = [int(np.floor(np.log2(np.abs(values[bounds[o, c]:bounds[o, c + 1]]).max()))) if bounds[o, c + 1] > bounds[o, c] else 0
-               for o in range(compact.d_model) for c in range(chunks)]
-    assert table[head:].tolist() == binades
+def _tiled_store_restated(rows: int, k: int, offsets: np.ndarray, idx: np.ndarray, values: np.ndarray, bf16: bool):
+    """The tiled store of one side restated on the host from its compact rows: items (16-row tile t, 512-wide sub-chunk
+    j) in tile-major order, each item's slots in row order then index order, padded to whole 8-slot groups with the
+    item's last slot; a slot = (row in tile << 12 | index mod 4096, the bfloat16 bits, or fp16 hi and lo of the float32
+    weight scaled by 2^-e, e the power of two of its row's largest |weight|). Returns (table, groups as uint16 rows)."""
+    tiles, subchunks = (rows + 15) // 16, (k + 511) // 512
+    binades = np.zeros(rows, np.int64)
+    for r in range(rows):
+        row = np.abs(values[offsets[r]:offsets[r + 1]].astype(np.float32))
+        if row.size and row.max() > 0:
+            binades[r] = np.frexp(row.max())[1] - 1
+    starts, groups = [0], []
+    for t in range(tiles):
+        for j in range(subchunks):
+            slots = []
+            for rr in range(min(16, rows - 16 * t)):
+                r = 16 * t + rr
+                ks = idx[offsets[r]:offsets[r + 1]].astype(np.int64) & 0xFFFF
+                for s in np.nonzero((ks >= 512 * j) & (ks < 512 * (j + 1)))[0]:
+                    slots.append((rr, r, int(ks[s]), offsets[r] + int(s)))
+            slots += [slots[-1]] * (-len(slots) % 8)
+            for g in range(0, len(slots), 8):
+                fields = [(rr << 12) | (kk & 4095) for rr, _, kk, _ in slots[g:g + 8]]
+                if bf16:
+                    fields += [int(values[s]) for _, _, _, s in slots[g:g + 8]]
+                else:
+                    w = np.array([values[s] for _, _, _, s in slots[g:g + 8]], np.float32)
+                    scaled = np.ldexp(w, -np.array([binades[r] for _, r, _, _ in slots[g:g + 8]])).astype(np.float32)
+                    hi = scaled.astype(np.float16)
+                    lo = (scaled - hi.astype(np.float32)).astype(np.float16)
+                    fields += hi.view(np.uint16).tolist() + lo.view(np.uint16).tolist()
+                groups.append(fields)
+            starts.append(starts[-1] + len(slots) // 8)
+    table = np.array(starts + ([] if bf16 else binades.tolist()), np.int64)
+    return table, np.array(groups, np.uint16).reshape(-1, 16 if bf16 else 24)
+
+
+@pytest.mark.parametrize("shape", [("irreg_512_2048", None), ("odd_f32", (48, 520, 37, "float32")),
+                                   ("odd_bf16", (64, 1032, 300, "bf16"))])
+def test_tiled_store_bitwise(shape, test_layers, device):
+    """The tiled stores built on the device equal their host restatement bit for bit, on both sides: a reference test
+    layer (512 x 2048, four sub-chunks) and two odd shapes (rows not a multiple of 16, K not a multiple of 512, float32
+    and bfloat16 values), table and groups, padding included."""
+    name, dims = shape
+    if dims is None:
+        compact, _, layer = test_layers[name]
+    else:
+        d_model, d_ff, degree, dtype = dims
+        compact = synth.make_workload_layer(synth.Workload(name, d_model, d_ff, min(degree, d_model), 7, value_dtype=dtype))
+        layer = hip_layer(compact)
+    runtime = HFFNRuntime([layer], device, dense=True)
+    bf16 = layer.up_val.dtype == torch.bfloat16
+    tiles = runtime._tiles[0]
+    for side, rows, k, names in (("up", compact.d_ff, compact.d_model, ("up_offsets", "up_idx", "up_val")),
+                                 ("down", compact.d_model, compact.d_ff, ("out_offsets", "out_hidden", "out_val"))):
+        offsets, idx, values = (getattr(layer, n).cpu() for n in names)
+        values = values.view(torch.int16).numpy().view(np.uint16) if bf16 else values.numpy()
+        table, groups = _tiled_store_restated(rows, k, offsets.numpy().astype(np.int64), idx.numpy(), values, bf16)
+        got_table = tiles[f"{side}_table"].cpu().numpy()
+        assert np.array_equal(got_table, table), side
+        store = tiles[side].cpu().numpy().view(np.uint16).reshape(-1, groups.shape[1])
+        assert store.shape[0] > groups.shape[0]  # the spare group past the end
+        assert np.array_equal(store[:groups.shape[0]], groups), side
+    runtime.force("tiles", "tiles")
+    for n in (1, 16, 17, 64):
+        x_np = np.random.default_rng(n).standard_normal((n, compact.d_model)).astype(np.float32)
+        y = runtime.forward(0, torch.from_numpy(x_np).to(device))
+        assert _relative(y, reference.forward(compact, x_np)) <= 1e-5, n
 
 
 def test_tiles_refuses_more_than_64_tokens(test_layers, device):
     compact, case, layer = test_layers["homog_512_2048"]
-    runtime = HFFNRuntime([layer], device)
+    runtime = HFFNRuntime([layer], device, dense=True)
     runtime.force("tiles", "tiles")
     with pytest.raises(ValueError, match="at most 64"):
         runtime.forward(0, torch.from_numpy(synth.make_input(case, 65)).to(device))
@@ -239,7 +286,7 @@ def test_tiles_refuses_more_than_64_tokens(test_layers, device):
 
 def test_gemv_refuses_more_than_64_tokens(test_layers, device):
     compact, case, layer = test_layers["homog_512_2048"]
-    runtime = HFFNRuntime([layer], device)
+    runtime = HFFNRuntime([layer], device, dense=True)
     runtime.force("gemv", "gemv")
     with pytest.raises(ValueError, match="above 64"):
         runtime.forward(0, torch.from_numpy(synth.make_input(case, 65)).to(device))
@@ -249,7 +296,7 @@ def test_mfma_workspace_reused_at_shrinking_token_counts(test_layers, device):
     """The MFMA path's workspace (split-K counters, binades, partials) is shared by calls of any N: calls at falling N
     after a large one stay correct."""
     compact, case, layer = test_layers["homog_512_2048"]
-    runtime = HFFNRuntime([layer], device)
+    runtime = HFFNRuntime([layer], device, dense=True)
     runtime.force("mfma", "mfma")
     for n in (300, 129, 64, 5, 1, 300):
         x_np = synth.make_input(case, n)
@@ -260,7 +307,7 @@ def test_mfma_workspace_reused_at_shrinking_token_counts(test_layers, device):
 def test_stack_of_layers(test_layers, device):
     compact_a, case, layer_a = test_layers["homog_512_2048"]
     compact_b, _, layer_b = test_layers["irreg_512_2048"]
-    runtime = HFFNRuntime([layer_a, layer_b], device)
+    runtime = HFFNRuntime([layer_a, layer_b], device, dense=True)
     x_np = synth.make_input(case, 17)
     x = torch.from_numpy(x_np).to(device)
     for index, compact in ((1, compact_b), (0, compact_a), (1, compact_b)):
@@ -270,7 +317,7 @@ def test_stack_of_layers(test_layers, device):
 
 def test_input_validation(test_layers, device):
     _, case, layer = test_layers["homog_256_1024"]
-    runtime = HFFNRuntime([layer], device)
+    runtime = HFFNRuntime([layer], device, dense=True)
     x = torch.from_numpy(synth.make_input(case, 4)).to(device)
     for bad in (x.double(), x.T, x[:, :128], x.cpu(), x[None], torch.empty(0, 256, device=device)):
         with pytest.raises(ValueError):
@@ -283,7 +330,7 @@ def test_input_validation(test_layers, device):
 
 def test_largest_token_count(test_layers, device):
     compact, case, layer = test_layers["homog_256_1024"]
-    runtime = HFFNRuntime([layer], device)
+    runtime = HFFNRuntime([layer], device, dense=True)
     x = torch.randn(MAX_TOKENS, compact.d_model, generator=torch.Generator().manual_seed(3)).to(device)
     y = runtime.forward(0, x)
     rows = [0, 1, 4097, MAX_TOKENS // 2 + 3, MAX_TOKENS - 1]
@@ -311,7 +358,7 @@ def test_live_row_gemms_equal_the_full_tile(w410m, device):
     the row tiles, hence the k splits, are the same, so the first 64 (100) tokens of a 200-token call (full tile) and
     a call on those tokens alone (live rows) are the same products in the same order: bitwise equal."""
     compact, workload, layer = w410m
-    runtime = HFFNRuntime([layer], device)
+    runtime = HFFNRuntime([layer], device, dense=True)
     runtime.force("mfma", "mfma")
     x = torch.from_numpy(synth.make_input(workload, 200)).to(device)
     full = runtime.forward(0, x).clone()
@@ -324,7 +371,7 @@ def test_410m_gemv_split_token_independence(w410m, device):
     """The 410M down projection runs the decode GEMV with its K split over 4 blocks and a second kernel adding the
     splits in order: still a fixed order per token, so a token alone and in a 32-token batch give the same bits."""
     compact, workload, layer = w410m
-    runtime = HFFNRuntime([layer], device)
+    runtime = HFFNRuntime([layer], device, dense=True)
     runtime.force("gemv", "gemv")
     x = torch.from_numpy(synth.make_input(workload, 32)).to(device)
     whole = runtime.forward(0, x).clone()
@@ -336,7 +383,7 @@ def test_410m_gemv_split_token_independence(w410m, device):
 def test_410m_relative_error(n, w410m, device):
     """Pythia-410M shape, 50 % density, fp32: max |y - y64| / max(1, |y64|) <= 1e-5 for every kernel pair."""
     compact, workload, layer = w410m
-    runtime = HFFNRuntime([layer], device)
+    runtime = HFFNRuntime([layer], device, dense=True)
     x_np = synth.make_input(workload, n)
     expected = reference.forward(compact, x_np)
     pairs = parity.PAIRS if n <= 32 else [(None, None), ("rows", "rows"), ("mfma", "mfma")]
@@ -348,7 +395,7 @@ def test_410m_relative_error(n, w410m, device):
 def test_70m_config(device):
     workload = synth.WORKLOADS["pythia70m_d20"]
     compact = synth.make_workload_layer(workload)
-    runtime = HFFNRuntime([hip_layer(compact)], device)
+    runtime = HFFNRuntime([hip_layer(compact)], device, dense=True)
     x_np = synth.make_input(workload, 128)
     y = runtime.forward(0, torch.from_numpy(x_np).to(device))
     assert float((y.double().cpu() - torch.from_numpy(reference.forward(compact, x_np))).abs().max()) <= ATOL
@@ -363,7 +410,7 @@ def test_1p4b_bf16(n, device):
     layer = hip_layer(compact)
     assert layer.up_val.dtype == torch.bfloat16 and layer.out_val.dtype == torch.bfloat16
     _bitwise_store(layer, compact)
-    runtime = HFFNRuntime([layer], device)
+    runtime = HFFNRuntime([layer], device, dense=True)
     x_np = synth.make_input(workload, n)
     result = parity.check(runtime, 0, torch.from_numpy(x_np).to(device),
                           torch.from_numpy(reference.forward(compact, x_np)).to(device))
@@ -382,7 +429,7 @@ def test_2p8b_zipf_bf16_token_sample(device):
     assert synth.layer_digest(compact) == pins[workload.name]["layer"]
     layer = hip_layer(compact)
     _bitwise_store(layer, compact)
-    runtime = HFFNRuntime([layer], device)
+    runtime = HFFNRuntime([layer], device, dense=True)
     x_np = synth.make_input(workload, 4096)
     y = runtime.forward(0, torch.from_numpy(x_np).to(device)).clone()
     sample = np.random.default_rng(11).choice(4096, 48, replace=False)
@@ -402,7 +449,7 @@ def _cached(name: str):
 def w2p8b(device):
     workload = synth.WORKLOADS["pythia2p8b_d80_zipf_bf16"]
     compact = _cached(workload.name)
-    return compact, workload, HFFNRuntime([hip_layer(compact)], device), reference.dense_weights(compact)
+    return compact, workload, HFFNRuntime([hip_layer(compact)], device, dense=True), reference.dense_weights(compact)
 
 
 @pytest.mark.parametrize("n", [1, 16, 26, 64])
@@ -428,7 +475,7 @@ def test_gemv_wide_calls(name, tokens, device):
     batch."""
     workload = synth.WORKLOADS[name]
     compact = _cached(name)
-    runtime = HFFNRuntime([hip_layer(compact)], device)
+    runtime = HFFNRuntime([hip_layer(compact)], device, dense=True)
     runtime.force("gemv", "gemv")
     weights = reference.dense_weights(compact)
     for n in tokens:
@@ -439,3 +486,19 @@ def test_gemv_wide_calls(name, tokens, device):
         for start, size in ((0, 1), (n - 1, 1), (n // 2, n - n // 2), (3, 16)):
             part = runtime.forward(0, x[start:start + size].contiguous())
             assert torch.equal(part, whole[start:start + size]), (n, start, size)
+
+
+def test_default_policy_reads_the_compact_store(device):
+    """With the default construction, dense planes exist only for layers of at least 50 % density: the 1.4B/20 % bf16
+    layer has none and its calls up to 64 tokens take the compact-store paths (the tiles path at 16 and 64 tokens),
+    above them the gather kernels; the 410M/50 % layer keeps its planes for the MFMA path above 64 tokens and takes the
+    compact store below."""
+    from hffn_amd.runtime import MFMA_MIN_DENSITY
+    sparse = HFFNRuntime([hip_layer(_cached("pythia1p4b_d20_bf16"))], device)
+    assert sparse.density < MFMA_MIN_DENSITY and sparse.dense_bytes() == 0 and not sparse.mfma_available
+    assert sparse.modes(16) == ("tiles", "tiles") and sparse.modes(64) == ("tiles", "tiles")
+    assert sparse.modes(65) == ("rows", "rows")
+    dense = HFFNRuntime([hip_layer(_cached("pythia410m_d50"))], device)
+    assert dense.density >= MFMA_MIN_DENSITY and dense.dense_bytes() > 0
+    assert dense.modes(16) == ("tiles", "tiles") and dense.modes(2048) == ("mfma", "mfma")
+    assert dense.modes(1)[0] == "edges"

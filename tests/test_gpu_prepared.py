@@ -26,7 +26,7 @@ def runtimes(device):
     for name, case in synth.CASES.items():
         compact = synth.make_layer(case)
         layers = [hip_layer(compact)]
-        out[name] = (compact, case, HFFNRuntime(layers, device), PreparedRuntime(layers, device))
+        out[name] = (compact, case, HFFNRuntime(layers, device, dense=True), PreparedRuntime(layers, device, dense=True))
     return out
 
 
@@ -66,7 +66,7 @@ def test_plans_follow_the_buffers(device):
     the calls counter counts plan launches like control calls; an input that is a row-offset view works."""
     case = synth.CASES["homog_256_1024"]
     layers = [hip_layer(synth.make_layer(case))]
-    control, prepared = HFFNRuntime(layers, device), PreparedRuntime(layers, device)
+    control, prepared = HFFNRuntime(layers, device, dense=True), PreparedRuntime(layers, device, dense=True)
     x1 = torch.from_numpy(synth.make_input(case, 1)).to(device)
     x8 = torch.from_numpy(synth.make_input(case, 8)).to(device)
     y1 = control.forward(0, x1).clone()
@@ -85,7 +85,7 @@ def test_plans_follow_the_buffers(device):
 
 def test_prepared_refuses_what_the_control_refuses(device):
     case = synth.CASES["homog_256_1024"]
-    prepared = PreparedRuntime([hip_layer(synth.make_layer(case))], device)
+    prepared = PreparedRuntime([hip_layer(synth.make_layer(case))], device, dense=True)
     with pytest.raises(ValueError, match="contiguous float32"):
         prepared.forward(0, torch.zeros(2, case.d_model + 1, device=device))
     with pytest.raises(ValueError, match="contiguous float32"):
@@ -102,7 +102,7 @@ def test_gemv_plans_see_updated_values(device):
     then invalidate_planes) the planned launch rebuilds the planes first and matches the control bit for bit."""
     case = synth.CASES["homog_512_2048"]
     compact = synth.make_layer(case)
-    control, prepared = HFFNRuntime([hip_layer(compact)], device), PreparedRuntime([hip_layer(compact)], device)
+    control, prepared = HFFNRuntime([hip_layer(compact)], device, dense=True), PreparedRuntime([hip_layer(compact)], device, dense=True)
     control.force("gemv", "gemv")
     prepared.force("gemv", "gemv")
     x = torch.from_numpy(synth.make_input(case, 16)).to(device)

@@ -128,8 +128,8 @@ def test_training_gates(name, n, grad, device):
     layer = synth.make_layer(case)
     x = torch.from_numpy(synth.make_input(case, n)).to(device)
     gy = make_gy(case, n, 0).to(device)
-    baseline = HFFNRuntime([hip_layer(layer)], device)
-    train = HFFNTrainRuntime(HFFNRuntime([hip_layer(layer)], device), **HYPER, max_tokens=max(n, 2048))
+    baseline = HFFNRuntime([hip_layer(layer)], device, dense=True)
+    train = HFFNTrainRuntime(HFFNRuntime([hip_layer(layer)], device, dense=True), **HYPER, max_tokens=max(n, 2048))
     train.forced_grad = grad
     if name.endswith("512_2048") and grad is None:
         assert train.grad_mode(n) == ("dense" if n >= 64 else "gather")
@@ -191,7 +191,7 @@ def test_training_gates(name, n, grad, device):
 
 def test_backward_needs_its_forward(device):
     case = synth.CASES["homog_256_1024"]
-    runtime = HFFNRuntime([hip_layer(synth.make_layer(case))], device)
+    runtime = HFFNRuntime([hip_layer(synth.make_layer(case))], device, dense=True)
     train = HFFNTrainRuntime(runtime, **HYPER)
     train.reserve(8)
     x = torch.from_numpy(synth.make_input(case, 8)).to(device)
@@ -250,7 +250,7 @@ def test_inference_after_training_reads_the_updated_values(device):
     """After steps, the runtime's MFMA path (densified planes, rebuilt in place) agrees with its gather path."""
     case = synth.Case("mfma_256_1024", 256, 1024, 128, 128, False, 1005)
     layer = synth.make_layer(case)
-    runtime = HFFNRuntime([hip_layer(layer)], device)
+    runtime = HFFNRuntime([hip_layer(layer)], device, dense=True)
     assert runtime.mfma_available
     train = HFFNTrainRuntime(runtime, **dict(HYPER, lr=1e-2))
     n = 256

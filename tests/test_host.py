@@ -88,6 +88,48 @@ def test_abi_refuses_bad_shapes_before_launching():
     _expect_argument_error(lib.hffn_plan_gemv(0, p, p, p, p, p, p, ctypes.c_void_p(20), p, big, p, 1024, 4096, 8,
                                               ctypes.byref(handle)), "aligned")
     _expect_argument_error(lib.hffn_plan_gemv(0, p, p, p, p, p, p, p, p, big, p, 1024, 4096, 8, None), "null result")
+    # the tiles path: store sizes (an 8-slot group per 8 slots, one padding group per item at most, one spare group)
+    size, entries = ctypes.c_uint64(0), ctypes.c_uint64(0)
+    assert lib.hffn_tiles_store_size(0, 4096, 1024, 2_097_152, ctypes.byref(size), ctypes.byref(entries)) == _lib.OK
+    items = 256 * 2
+    assert (size.value, entries.value) == ((2_097_152 // 8 + items + 1) * 48, items + 1 + 4096)
+    bf16_size, bf16_entries = ctypes.c_uint64(0), ctypes.c_uint64(0)
+    assert lib.hffn_tiles_store_size(1, 2048, 8192, 3_358_720, ctypes.byref(bf16_size), ctypes.byref(bf16_entries)) == _lib.OK
+    assert (bf16_size.value, bf16_entries.value) == ((3_358_720 // 8 + 128 * 16 + 1) * 32, 128 * 16 + 1)
+    _expect_argument_error(lib.hffn_tiles_store_size(0, 0, 1024, 0, ctypes.byref(size), ctypes.byref(entries)), "rows=0")
+    _expect_argument_error(lib.hffn_tiles_store_size(0, 16, 16, 257, ctypes.byref(size), ctypes.byref(entries)), "nnz=257")
+    _expect_argument_error(lib.hffn_tiles_store_size(5, 16, 16, 1, ctypes.byref(size), ctypes.byref(entries)), "value type")
+    assert lib.hffn_tiles_store_size(0, 4096, 1024, 2_097_152, ctypes.byref(size), ctypes.byref(entries)) == _lib.OK
+    _expect_argument_error(lib.hffn_tiles_build(0, p, p, p, 4096, 1024, 2_097_152, p, size.value - 1, p, None), "store of")
+    _expect_argument_error(lib.hffn_tiles_build(0, p, p, p, 4096, 1024, 2_097_152, ctypes.c_void_p(24), size.value, p, None),
+                           "aligned")
+    _expect_argument_error(lib.hffn_tiles_build(0, None, p, p, 4096, 1024, 2_097_152, p, size.value, p, None), "null")
+    tiles_bytes = ctypes.c_uint64(0)
+    # 410M shape, 16 tokens: the up side in one chunk, the down side's 64 row tiles over 4 chunks of K
+    assert lib.hffn_tiles_workspace(0, 16, 1024, 4096, 2_097_152, 2_097_152, ctypes.byref(tiles_bytes)) == _lib.OK
+    assert tiles_bytes.value == 4 * 16 * 1024 * 4
+    # 1.4B shape, bf16, 20 %, 16 tokens: the up side in 256 blocks of 32 rows x 2048 k, the down side in 32 blocks of
+    # 64 rows per chunk of 1024 (8 chunks)
+    assert lib.hffn_tiles_workspace(1, 16, 2048, 8192, 3_358_720, 3_358_720, ctypes.byref(tiles_bytes)) == _lib.OK
+    assert tiles_bytes.value == 8 * 16 * 2048 * 4
+    _expect_argument_error(lib.hffn_tiles_workspace(1, 16, 2048, 8192, 1 << 40, 0, ctypes.byref(tiles_bytes)), "nnz_up")
+    _expect_argument_error(lib.hffn_tiles_workspace(0, 65, 1024, 4096, 0, 0, ctypes.byref(tiles_bytes)), "n=65")
+    _expect_argument_error(lib.hffn_tiles_workspace(0, 16, 1000, 4096, 0, 0, ctypes.byref(tiles_bytes)), "multiple of 16")
+    assert lib.hffn_tiles_workspace(0, 16, 1024, 4096, 2_097_152, 2_097_152, ctypes.byref(tiles_bytes)) == _lib.OK
+    ws = tiles_bytes.value
+    _expect_argument_error(lib.hffn_forward_tiles(0, p, p, p, p, p, p, p, p, p, ws - 1, p, 1024, 4096, 2_097_152, 2_097_152, 16, None), "workspace")
+    _expect_argument_error(lib.hffn_forward_tiles(0, ctypes.c_void_p(20), p, p, p, p, p, p, p, p, ws, p, 1024, 4096, 2_097_152, 2_097_152, 16,
+                                                  None),
+                           "aligned")
+    _expect_argument_error(lib.hffn_forward_tiles(0, p, ctypes.c_void_p(24), p, p, p, p, p, p, p, ws, p, 1024, 4096, 2_097_152, 2_097_152, 16,
+                                                  None),
+                           "tiled stores")
+    _expect_argument_error(lib.hffn_forward_tiles(0, p, p, None, p, p, p, p, p, p, ws, p, 1024, 4096, 2_097_152, 2_097_152, 16, None), "null")
+    _expect_argument_error(lib.hffn_forward_tiles(0, p, p, p, p, p, p, p, p, p, ws, p, 1024, 4096, 2_097_152, 2_097_152, 65, None), "n=65")
+    handle = ctypes.c_uint64(0)
+    _expect_argument_error(lib.hffn_plan_tiles(0, p, p, p, p, p, p, p, p, ws - 1, p, 1024, 4096, 2_097_152, 2_097_152, 16, ctypes.byref(handle)),
+                           "workspace")
+    _expect_argument_error(lib.hffn_plan_tiles(0, p, p, p, p, p, p, p, p, ws, p, 1024, 4096, 2_097_152, 2_097_152, 16, None), "null result")
     needed = ctypes.c_uint64(0)
     assert lib.hffn_output_major_workspace(2_097_152, 1024, ctypes.byref(needed)) == _lib.OK
     assert needed.value == 1024 * 1024 * 4
@@ -113,37 +155,31 @@ def test_policy():
     assert [runtime.leading_dim(n) for n in (1, 2, 3, 4, 5, 8, 9, 2048, 2049)] == [4, 4, 4, 4, 8, 8, 16, 2048, 2056]
 
 
-def test_mfma_policy_crossovers():
-    """The estimated crossovers land where the forced-pair timings put them: the 410M/50 % layer takes the MFMA path
-    from 9 tokens (a second lane-per-slot pass), the 1.4B/20 % layer from 13, the narrow 70M/20 % layer from 29;
-    above 32 tokens always."""
-    def first(d, h, slots):
-        return next(n for n in range(1, 40) if runtime.mfma_preferred(n, d, h, slots))
-    assert first(1024, 4096, 2 * 4096 * 512) == 9
-    assert first(2048, 8192, 2 * 8192 * 410) == 13
-    assert first(512, 2048, 2 * 2048 * 102) == 29
-    assert runtime.mfma_preferred(33, 512, 2048, 1) and not runtime.mfma_preferred(32, 512, 2048, 1)
+def test_decode_policy():
+    """Up to 64 tokens the policy reads the compact store; the estimated crossovers land where the forced-pair timings
+    put them: the 410M/50 % layer on the lane-per-slot kernels at 1-4 tokens and on the tiles path from 8, the
+    1.4B/20 % bf16 layer on the lane-per-slot kernels at 1-4 tokens (measured 21.6 and 21.3 us at 1 token, a tie; at 4
+    tokens the estimate misses a 14 % gain of the tiles path: 25.5 against 22.0 us) and on the tiles path from 8, the
+    narrow 70M/20 % layer on the lane-per-slot kernels up to 8 tokens, the 2.8B/80 % layer on the tiles path at every
+    count; above 32 tokens only the tiles path remains; without tiled stores the lane-per-slot kernels or nothing."""
+    s410, s1p4, s70, s2p8 = 2 * 4096 * 512, 2 * 8192 * 410, 2 * 2048 * 102, 2 * 10240 * 2048
+    assert [runtime.decode_mode(n, s410, True, True) for n in (1, 2, 4, 8, 16, 32, 64)] == \
+        ["edges", "edges", "edges", "tiles", "tiles", "tiles", "tiles"]
+    assert [runtime.decode_mode(n, s1p4, True, True) for n in (1, 4, 8, 16, 32, 64)] == ["edges", "edges"] + ["tiles"] * 4
+    assert [runtime.decode_mode(n, s70, True, True) for n in (1, 4, 8, 16, 32)] == ["edges", "edges", "edges", "tiles", "tiles"]
+    assert all(runtime.decode_mode(n, s2p8, True, True) == "tiles" for n in (1, 4, 16, 64))
+    assert runtime.decode_mode(33, s410, True, False) is None and runtime.decode_mode(32, s410, True, False) == "edges"
+    assert runtime.decode_mode(65, s410, True, True) is None
+    assert runtime.decode_mode(4, s410, False, True) == "tiles"
 
 
-def test_planes_policy():
-    """Estimates up to 64 tokens: on the Pythia-410M layer at 50 % the lane-per-slot kernels at 1-4 tokens, the decode
-    GEMVs from 8 to 40, the MFMA path at 64 and always above (when its GEMMs are streamed); on the dense 2.8B-shape
-    layer the GEMVs up to 16 tokens and the MFMA path at 32; on the 1.4B layer at 20 % the gather kernels at 1-4
-    tokens and the GEMVs at 16."""
-    slots = 2 * 4096 * 512
-    assert runtime.planes_mode(1, 1024, 4096, slots, True) is None
-    assert runtime.planes_mode(2, 1024, 4096, slots, True) is None and runtime.planes_mode(4, 1024, 4096, slots, True) is None
-    assert all(runtime.planes_mode(n, 1024, 4096, slots, True) == "gemv" for n in (8, 16, 24, 32, 33, 40))
-    assert runtime.planes_mode(64, 1024, 4096, slots, True) == "mfma"
-    assert runtime.planes_mode(65, 1024, 4096, slots, True) == "mfma"
-    assert runtime.planes_mode(65, 1024, 4096, slots, False) is None
-    assert runtime.planes_mode(48, 512, 2048, 2 * 2048 * 102, True) == "gemv"
-    dense = 2 * 10240 * 2048
-    assert all(runtime.planes_mode(n, 2560, 10240, dense, True) == "gemv" for n in (1, 4, 16))
-    assert runtime.planes_mode(32, 2560, 10240, dense, True) == "mfma"
-    sparse = 2 * 8192 * 410
-    assert all(runtime.planes_mode(n, 2048, 8192, sparse, True) is None for n in (1, 4))
-    assert runtime.planes_mode(16, 2048, 8192, sparse, True) == "gemv"
+def test_tiles_estimate():
+    """The tiles path's estimate against the forced-pair timings it was fitted to (within 20 %)."""
+    measured = {(2 * 4096 * 512, 1): 17.4, (2 * 4096 * 512, 16): 18.4, (2 * 4096 * 512, 64): 30.0,
+                (2 * 8192 * 410, 1): 21.3, (2 * 8192 * 410, 16): 24.3, (2 * 8192 * 410, 64): 44.9,
+                (2 * 2048 * 102, 16): 16.5, (2 * 10240 * 2048, 1): 59.3, (2 * 10240 * 2048, 64): 99.3}
+    for (slots, n), us in measured.items():
+        assert abs(runtime.tiles_us(n, slots) / us - 1) < 0.2, (slots, n)
 
 
 def test_mfma_streamed_query():

@@ -39,7 +39,7 @@ def _planes_call(runtime: HFFNRuntime, x: torch.Tensor, static: bool) -> tuple[t
 @pytest.mark.parametrize("name,calls", [("pythia410m_d50", (48, 5)), ("pythia1p4b_d20_bf16", (64, 17))])
 def test_static_scratch_matches_the_workspace_entry(name, calls, device):
     workload = synth.WORKLOADS[name]
-    runtime = HFFNRuntime([hip_layer(synth.make_workload_layer(workload))], device)
+    runtime = HFFNRuntime([hip_layer(synth.make_workload_layer(workload))], device, dense=True)
     for n in calls:
         x = torch.from_numpy(synth.make_input(workload, n)).to(device)
         act, y = _planes_call(runtime, x, static=False)
@@ -51,7 +51,7 @@ def test_static_scratch_matches_the_workspace_entry(name, calls, device):
 
 def test_static_scratch_without_splits(device):
     case = synth.CASES["irreg_512_2048"]
-    runtime = HFFNRuntime([hip_layer(synth.make_layer(case))], device)
+    runtime = HFFNRuntime([hip_layer(synth.make_layer(case))], device, dense=True)
     for n in (33, 2):
         x = torch.from_numpy(synth.make_input(case, n)).to(device)
         assert all(torch.equal(a, b) for a, b in zip(_planes_call(runtime, x, True), _planes_call(runtime, x, False)))
