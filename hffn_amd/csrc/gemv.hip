@@ -11,8 +11,10 @@
 // split that range in W spans of whole 32-k tiles. Per tile, lane (r, c) = (lane % 16, lane / 16) holds row r's
 // chunk c of both planes as the B operand (the 16 lanes of a chunk read 256 contiguous bytes), and the 8 inputs of
 // token r at the same k as the A operand, scaled by the token's power of two over the tile and split into fp16 hi and
-// lo: D[token, row] = x_hi w_hi + x_hi w_lo + x_lo w_hi (x_hi w_hi + x_lo w_hi for bf16 weights, exact in the hi
-// plane), accumulated in fp32 with the token's power of two undone exactly. The waves' sums are added in wave order
+// lo: D[token, row] = x_hi w_hi + x_hi w_lo + x_lo w_hi (x_hi w_hi + x_lo w_hi for bf16 weights, read from the hi
+// plane only: exact for entries down to 2^-14 of their row's largest magnitude; below, fp16 subnormals keep fewer
+// bits, an error of at most ~2^-25 of that magnitude per weight), accumulated in fp32 with the token's power of two
+// undone exactly. The waves' sums are added in wave order
 // (then the splits' partials in split order by gemv_reduce_kernel), then the row's power of two is undone; every
 // output is written by one thread, the sums do not depend on the other tokens of the call, and the bits repeat run to
 // run.

@@ -6,8 +6,9 @@
 // weights are densified once at load (one power of two per row, so that its largest entry lies in [1, 2)); the input
 // X is split by a small kernel before the up GEMM (one power of two per token); the activations are split by the up
 // GEMM's epilogue (one power of two per token and 128-neuron block). Each product is  a_hi b_hi + a_hi b_lo +
-// a_lo b_hi  accumulated in fp32 (the lo*lo term, ~2^-22 relative, is dropped; bf16 weights are exact in the hi
-// plane and take the first and last terms). The powers of two are undone exactly: the down GEMM rescales its
+// a_lo b_hi  accumulated in fp32 (the lo*lo term, ~2^-22 relative, is dropped; bf16 weights take the first and last
+// terms on the hi plane only, which holds them exactly down to 2^-14 of their row's largest magnitude; below that
+// fp16 subnormals keep fewer bits, at most ~2^-25 of that magnitude per weight). The powers of two are undone exactly: the down GEMM rescales its
 // accumulators at each 128-wide k block by the ratio of the blocks' powers of two, and the epilogues apply the last.
 //
 // Plane layout (K-chunk-major): k is cut into 32-wide k-tiles and each k-tile into four 16-byte chunks of 8 halves;

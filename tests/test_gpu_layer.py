@@ -154,6 +154,38 @@ def test_densified_planes_reconstruct_the_weights(name, test_layers, device):
         assert np.all((rowmax == 0) | ((top <= rowmax) & (rowmax < 2 * top))), side
 
 
+def test_bf16_wide_range_row(device):
+    """bf16 weights whose rows span 30 binades: the dense-plane paths read the hi plane only, which holds each entry
+    to ~2^-25 of its row's largest magnitude (entries below 2^-14 of it are fp16 subnormals there), so the planes
+    reconstruct the weights within that bound; every path stays within 1e-5 of float64 (the tiles and gather paths take
+    the bf16 weights as they are)."""
+    import dataclasses
+    base = synth.make_workload_layer(synth.Workload("wide_bf16", 256, 1024, 64, 31, value_dtype="bf16"))
+    spread = lambda v: (v * np.exp2(-(np.arange(v.size) % 31))).astype(np.float32)  # noqa: E731 (exact on bf16 values)
+    compact = dataclasses.replace(base, up_val=spread(base.up_val), down_val=spread(base.down_val))
+    layer = hip_layer(compact)
+    assert layer.up_val.dtype == torch.bfloat16
+    runtime = HFFNRuntime([layer], device, dense=True)
+    planes = runtime._planes[0]
+    w_up, w_down = reference.dense_weights(compact)
+    for side, expected in (("up", w_up), ("down", w_down)):
+        rows, k = expected.shape
+        hi = planes[side].float().cpu().numpy().astype(np.float64).reshape(k // 32, 2, 4, rows, 8).transpose(3, 0, 1, 2, 4)
+        got = hi[:, :, 0].reshape(rows, k) * np.exp2(planes[f"{side}_binades"].cpu().numpy().astype(np.float64))[:, None]
+        rowmax = np.abs(expected).max(axis=1, keepdims=True)
+        small = (expected != 0) & (np.abs(expected) < rowmax * 2.0**-14)
+        assert small.sum() > 1000, side  # the case exercises fp16 subnormals in the hi plane
+        assert np.all(np.abs(got - expected) <= rowmax * 2.0**-25 * 1.0001), side
+    for n in (1, 16, 300):
+        x_np = np.random.default_rng(n).standard_normal((n, 256)).astype(np.float32)
+        expected = reference.forward(compact, x_np)
+        pairs = [("mfma", "mfma"), ("edges", "edges"), ("rows", "rows")] + ([("tiles", "tiles"), ("gemv", "gemv")] if n <= 64 else [])
+        for pair in pairs:
+            runtime.force(*pair)
+            assert _relative(runtime.forward(0, torch.from_numpy(x_np).to(device)), expected) <= 1e-5, (n, pair)
+    runtime.force(None, None)
+
+
 @pytest.mark.parametrize("up,down", [("edges", "edges"), ("rows", "rows"), ("rows", "edges"), ("edges", "rows"),
                                      ("mfma", "mfma")])
 def test_token_result_does_not_depend_on_the_batch(up, down, test_layers, device):
