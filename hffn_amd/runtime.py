@@ -60,6 +60,7 @@ EDGES_PASS_WEIGHT = {1: 0.42, 2: 0.49, 4: 0.52, 8: 1.0}
 TILES_BASE_US, TILES_SLOT_US = 12.7, 1.11e-6
 TILES_FILL_US, TILES_FILL_SLOT_US = 2.0, 0.07e-6
 TILES_TILE_US, TILES_TILE_SLOT_US = 4.5, 0.17e-6
+TILES_TIE = 1.05  # the tiles path wins estimates within 5 % of the lane-per-slot kernels' (its cost is flat in N)
 MAX_TOKENS = 1 << 18      # runtime/gpu/nvidia/common/kernels/hffn_cuda/runtime.py:26
 
 _VALUE_TYPES = {torch.float32: _lib.VALUE_F32, torch.bfloat16: _lib.VALUE_BF16}
@@ -99,13 +100,13 @@ def tiles_us(n: int, slots: int) -> float:
 
 def decode_mode(n: int, slots: int, edges: bool, tiles: bool) -> str | None:
     """The compact-store path of least estimated time for N <= 64 tokens: ``edges`` (up to ``EDGES_MAX_TOKENS``, when
-    ``edges``: its LDS stage fits) or ``tiles`` (when ``tiles``: the layer has tiled stores); None when neither
-    applies."""
+    ``edges``: its LDS stage fits) or ``tiles`` (when ``tiles``: the layer has tiled stores; it also takes estimates
+    within ``TILES_TIE`` of the lane-per-slot kernels'); None when neither applies."""
     options = {}
     if edges and n <= EDGES_MAX_TOKENS:
         options["edges"] = edges_us(n, slots)
     if tiles and n <= TILES_MAX_TOKENS:
-        options["tiles"] = tiles_us(n, slots)
+        options["tiles"] = tiles_us(n, slots) / TILES_TIE
     return min(options, key=options.get) if options else None
 
 
