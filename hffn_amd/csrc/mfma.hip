@@ -260,6 +260,12 @@ __device__ __forceinline__ uint32_t acc_row(uint32_t wm, int i, int r, uint32_t 
     return wm * (BM / 2) + i * 32 + 8 * (r / 4) + 4 * (lane / 32) + r % 4;
 }
 
+// The same for waves of WR rows each (the streamed GEMM's 4- or 8-wave blocks).
+template <uint32_t WR>
+__device__ __forceinline__ uint32_t wave_row(uint32_t wm, int i, int r, uint32_t lane) {
+    return wm * WR + i * 32 + 8 * (r / 4) + 4 * (lane / 32) + r % 4;
+}
+
 // C[M, Ncol] = A[M, K] B[Ncol, K]^T from planes. Up: A = X planes (power of two per row), epilogue bias + GELU,
 // writes the activation planes (K-chunk-major over the d_ff neurons) and one power of two per (row, BN block).
 // Down: A = activation planes (power of two per row and kActBlock-wide k block), epilogue bias, writes Y fp32.
@@ -539,6 +545,7 @@ __global__ __launch_bounds__(kThreads) void gemm_planes_kernel(
 // products and order as gemm_planes_kernel.
 constexpr int kDmaStages = 3;
 constexpr int kDmaBM = 256, kDmaBN = 128;
+constexpr int kDmaWaves = 8;  // waves per block: 8 (two per SIMD, 64 x 64 wave tiles) or 4 (128 x 64)
 constexpr uint32_t kDmaMaxActBlocks = 40;  // activation blocks of one down split held in LDS (int8 binades)
 static_assert(kDmaMaxActBlocks <= 64, "one bit per activation block of a split in two 32-bit masks");
 
@@ -569,11 +576,11 @@ __device__ __forceinline__ void block_barrier() {
 }
 
 // LIVE < BM (one row tile of up to LIVE tokens): only the first LIVE rows of A are transferred and multiplied; the
-// waves of the second row half (all padding) only transfer and meet at the barriers. The live rows get the same
+// waves whose rows are all padding only transfer and meet at the barriers. The live rows get the same
 // products in the same order as with LIVE = BM, and the padding rows' accumulators stay zero, as zero A rows leave
 // them, so the results are bitwise those of the full tile.
-template <Epi EPI, bool LO_B, int LIVE>
-__global__ __launch_bounds__(kThreads) void gemm_dma_kernel(
+template <Epi EPI, bool LO_B, int LIVE, int W>
+__global__ __launch_bounds__(64 * W) void gemm_dma_kernel(
     const _Float16* __restrict__ a_planes,  // [K / 32][8][rows_pad][8]
     const int32_t* __restrict__ a_exp,      // Up: [rows_pad]; Down: [rows_pad, K / kActBlock]
     const _Float16* __restrict__ b_planes,  // [K / 32][8][Ncol][8]
@@ -583,23 +590,28 @@ __global__ __launch_bounds__(kThreads) void gemm_dma_kernel(
     _Float16* __restrict__ out_planes,      // Up: activation planes [Ncol / 32][8][rows_pad][8]
     int32_t* __restrict__ out_exp,          // Up: [rows_pad, Ncol / BN] activation block binades
     uint32_t M, uint32_t rows_pad, uint32_t Ncol, uint32_t K, uint32_t splits) {
-    constexpr int MI = 4, NI = 2, BM = kDmaBM, BN = kDmaBN, S = kDmaStages;
-    static_assert(BM == kThreads, "one thread per block row for the binade tables");
+    // W waves in (W / 2) x 2: 4 waves of 128 x 64 or 8 waves of 64 x 64 (two per SIMD)
+    static_assert(W == 4 || W == 8, "4 or 8 waves");
+    constexpr int MI = W == 4 ? 4 : 2, NI = 2, BM = kDmaBM, BN = kDmaBN, S = kDmaStages;
+    constexpr uint32_t kT = 64 * W, kWaveRows = 32 * MI;
+    static_assert(BM <= kT && kWaveRows * (W / 2) == BM, "a thread per block row for the binade tables; waves cover BM");
     static_assert(LIVE == BM || LIVE == 128 || LIVE == 64, "live rows: the whole tile, its first half or first quarter");
     constexpr uint32_t kStage = kRuns * (BM + BN) * 8;  // halves per stage
     constexpr int kRowRuns = LIVE / 64;                  // 64-row runs of A transferred per (part, chunk)
-    constexpr int kLoadsA = kRowRuns * kRuns / 4, kLoadsB = BN * kRuns / kWave / 4;  // DMA instructions per wave
+    constexpr int kLoadsA = kRowRuns * kRuns / W, kLoadsB = BN * kRuns / kWave / W;  // DMA instructions per wave
+    static_assert(kLoadsA * W == kRowRuns * kRuns && kLoadsB * W == BN * kRuns / kWave, "the transfers divide over the waves");
     constexpr int kLoads = kLoadsA + kLoadsB;
-    constexpr int MIL = LIVE >= BM / 2 ? MI : LIVE / 32;  // multiplied 32-row tiles of a live wave
+    // multiplied 32-row tiles of a live wave (its rows start at wm * kWaveRows; LIVE is a multiple of kWaveRows)
+    constexpr int MIL = LIVE >= static_cast<int>(kWaveRows) ? MI : LIVE / 32;
 
     __shared__ __attribute__((aligned(16))) _Float16 smem[S * kStage];
     __shared__ int32_t e_row[1][BM];  // Up: x binades
     __shared__ __attribute__((aligned(4))) int8_t e_tab[EPI == Epi::Down ? kDmaMaxActBlocks : 1][EPI == Epi::Down ? BM : 1];  // Down: [block][row]
-    __shared__ uint32_t change_masks[EPI == Epi::Down ? kThreads / kWave : 1][2];
+    __shared__ uint32_t change_masks[EPI == Epi::Down ? W : 1][2];
 
     const uint32_t tid = threadIdx.x, lane = tid % kWave, wave = uniform(tid / kWave);
     const uint32_t wm = wave / 2, wn = wave % 2;
-    const bool live = LIVE > BM / 2 || wm == 0;  // wave-uniform: this wave's rows hold tokens
+    const bool live = wm * kWaveRows < static_cast<uint32_t>(LIVE);  // wave-uniform: this wave's rows hold tokens
     const uint32_t tiles_m = rows_pad / BM, tiles_n = Ncol / BN;
     const Tile tile = tile_of(blockIdx.x, tiles_m, tiles_n, splits);
     const uint32_t m0 = tile.m * BM, n0 = tile.n * BN;
@@ -607,11 +619,11 @@ __global__ __launch_bounds__(kThreads) void gemm_dma_kernel(
     const uint32_t k_begin = tile.split * ktiles / splits, k_end = (tile.split + 1) * ktiles / splits;
     const uint32_t a_kblocks = K / kActBlock, kb0 = k_begin / kKtPerActBlock;
     if constexpr (EPI != Epi::Down) {
-        e_row[0][tid] = a_exp[m0 + tid];
+        if (tid < static_cast<uint32_t>(BM)) e_row[0][tid] = a_exp[m0 + tid];
     } else {
         // the row's binades of this split (whole activation blocks), eight loads in flight at a time
-        const uint32_t blocks = (k_end - k_begin) / kKtPerActBlock;
-        const int32_t* row_exp = a_exp + static_cast<size_t>(m0 + tid) * a_kblocks + kb0;
+        const uint32_t blocks = tid < static_cast<uint32_t>(BM) ? (k_end - k_begin) / kKtPerActBlock : 0;
+        const int32_t* row_exp = a_exp + static_cast<size_t>(m0 + (tid < static_cast<uint32_t>(BM) ? tid : 0)) * a_kblocks + kb0;
         for (uint32_t b0 = 0; b0 < blocks; b0 += 8) {
             int32_t v[8];
 #pragma unroll
@@ -640,7 +652,7 @@ __global__ __launch_bounds__(kThreads) void gemm_dma_kernel(
         for (int h = 0; h < 2; ++h) {
             uint32_t c = 0;
 #pragma unroll
-            for (int w = 0; w < kThreads / kWave; ++w) c |= change_masks[w][h];
+            for (int w = 0; w < W; ++w) c |= change_masks[w][h];
             changed[h] = uniform(c);
         }
     }
@@ -682,7 +694,7 @@ __global__ __launch_bounds__(kThreads) void gemm_dma_kernel(
         const uint32_t chunk = kk * 2 + lane / 32;
 #pragma unroll
         for (int i = 0; i < MIL; ++i) {
-            const uint32_t r = wm * (BM / 2) + i * 32 + lane % 32;
+            const uint32_t r = wm * kWaveRows + i * 32 + lane % 32;
             f.ah[i] = *reinterpret_cast<const half8*>(s_a + (chunk * BM + r) * 8);
             f.al[i] = *reinterpret_cast<const half8*>(s_a + ((4 + chunk) * BM + r) * 8);
         }
@@ -755,7 +767,7 @@ __global__ __launch_bounds__(kThreads) void gemm_dma_kernel(
                 for (int i = 0; i < MIL; ++i)
 #pragma unroll
                     for (int g = 0; g < 4; ++g) {
-                        const uint32_t m = acc_row<BM>(wm, i, 4 * g, lane);
+                        const uint32_t m = wave_row<kWaveRows>(wm, i, 4 * g, lane);
                         const uint32_t before = *reinterpret_cast<const uint32_t*>(&e_tab[kb - 1][m]);
                         const uint32_t now = *reinterpret_cast<const uint32_t*>(&e_tab[kb][m]);
 #pragma unroll
@@ -813,23 +825,29 @@ __global__ __launch_bounds__(kThreads) void gemm_dma_kernel(
             for (int i = 0; i < MI; ++i)
 #pragma unroll
                 for (int r = 0; r < 16; ++r) {
-                    const uint32_t m = acc_row<BM>(wm, i, r, lane);
+                    const uint32_t m = wave_row<kWaveRows>(wm, i, r, lane);
                     tile_v[m * kLd + c] = gelu(ldexpf(acc[i][j][r], e_row[0][m] + ce) + cb);
                 }
         }
         __syncthreads();
-        const float* row_v = tile_v + tid * kLd;
+        // H threads per block row (1 with 4 waves, 2 with 8: lanes h of a row are adjacent), each a BN / H-wide part
+        constexpr uint32_t H = kT / BM;
+        const uint32_t row = tid / H, part = tid % H;
+        const float* row_v = tile_v + row * kLd;
         uint32_t largest = 0;
 #pragma unroll 8
-        for (uint32_t c = 0; c < BN; c += 4) {
+        for (uint32_t c = part * (BN / H); c < (part + 1) * (BN / H); c += 4) {
             const float4 v = *reinterpret_cast<const float4*>(row_v + c);
             largest = max(largest, max(max(abs_bits(v.x), abs_bits(v.y)), max(abs_bits(v.z), abs_bits(v.w))));
         }
+#pragma unroll
+        for (uint32_t off = 1; off < H; off <<= 1)
+            largest = max(largest, static_cast<uint32_t>(__shfl_xor(static_cast<int>(largest), static_cast<int>(off), kWave)));
         const int e = act_binade(largest);
-        out_exp[static_cast<size_t>(m0 + tid) * tiles_n + tile.n] = e;
+        if (part == 0) out_exp[static_cast<size_t>(m0 + row) * tiles_n + tile.n] = e;
         const float scale = ldexpf(1.0f, -e);
 #pragma unroll 4
-        for (uint32_t chunk = 0; chunk < BN / 8; ++chunk) {
+        for (uint32_t chunk = part * (BN / 8 / H); chunk < (part + 1) * (BN / 8 / H); ++chunk) {
             const float4 u = *reinterpret_cast<const float4*>(row_v + chunk * 8);
             const float4 w = *reinterpret_cast<const float4*>(row_v + chunk * 8 + 4);
             const float v[8] = {u.x, u.y, u.z, u.w, w.x, w.y, w.z, w.w};
@@ -841,8 +859,8 @@ __global__ __launch_bounds__(kThreads) void gemm_dma_kernel(
                 h[q] = hh;
                 l[q] = ll;
             }
-            *reinterpret_cast<half8*>(out_planes + plane_at(rows_pad, m0 + tid, n0 + chunk * 8, 0)) = h;
-            *reinterpret_cast<half8*>(out_planes + plane_at(rows_pad, m0 + tid, n0 + chunk * 8, 1)) = l;
+            *reinterpret_cast<half8*>(out_planes + plane_at(rows_pad, m0 + row, n0 + chunk * 8, 0)) = h;
+            *reinterpret_cast<half8*>(out_planes + plane_at(rows_pad, m0 + row, n0 + chunk * 8, 1)) = l;
         }
     } else {
         // y (Down, one split) or this split's partial, powers of two undone: through an fp32 [BM][BN] tile in LDS, so
@@ -859,7 +877,7 @@ __global__ __launch_bounds__(kThreads) void gemm_dma_kernel(
             for (int i = 0; i < MI; ++i)
 #pragma unroll
                 for (int r = 0; r < 16; ++r) {
-                    const uint32_t m = acc_row<BM>(wm, i, r, lane);
+                    const uint32_t m = wave_row<kWaveRows>(wm, i, r, lane);
                     const int ea = EPI == Epi::Down ? static_cast<int>(e_tab[kb_last][m]) : e_row[0][m];
                     tile_v[m * kLd + c] = ldexpf(acc[i][j][r], ea + ce);
                 }
@@ -867,7 +885,7 @@ __global__ __launch_bounds__(kThreads) void gemm_dma_kernel(
         __syncthreads();
         float* target = out + (splits > 1 ? static_cast<size_t>(tile.split) * M * Ncol : 0);
         const bool add_bias = EPI == Epi::Down && splits == 1;
-        for (uint32_t q = tid; q < BM * (BN / 4); q += kThreads) {
+        for (uint32_t q = tid; q < BM * (BN / 4); q += kT) {
             const uint32_t m = q / (BN / 4), c = (q % (BN / 4)) * 4;
             if (m0 + m >= M) break;  // rows ascend with q
             float4 v = *reinterpret_cast<const float4*>(tile_v + m * kLd + c);
@@ -1086,16 +1104,17 @@ template <Epi EPI, bool LO_B>
 hipError_t launch_dma(const _Float16* a_planes, const int32_t* a_exp, const _Float16* b_planes, const int32_t* b_exp,
                       const float* bias, float* out, _Float16* out_planes, int32_t* out_exp, uint32_t M, uint32_t Ncol, uint32_t K,
                       uint32_t splits, hipStream_t stream) {
-    const dim3 grid(dma_tiles(M, Ncol) * splits), block(kThreads);
+    constexpr int W = kDmaWaves;
+    const dim3 grid(dma_tiles(M, Ncol) * splits), block(64 * W);
     const uint32_t rows_pad = rows_padded(M), live = rows_live(M);
     if (live == 64)
-        hipLaunchKernelGGL((gemm_dma_kernel<EPI, LO_B, 64>), grid, block, 0, stream, a_planes, a_exp, b_planes, b_exp, bias, out,
+        hipLaunchKernelGGL((gemm_dma_kernel<EPI, LO_B, 64, W>), grid, block, 0, stream, a_planes, a_exp, b_planes, b_exp, bias, out,
                            out_planes, out_exp, M, rows_pad, Ncol, K, splits);
     else if (live == 128)
-        hipLaunchKernelGGL((gemm_dma_kernel<EPI, LO_B, 128>), grid, block, 0, stream, a_planes, a_exp, b_planes, b_exp, bias, out,
+        hipLaunchKernelGGL((gemm_dma_kernel<EPI, LO_B, 128, W>), grid, block, 0, stream, a_planes, a_exp, b_planes, b_exp, bias, out,
                            out_planes, out_exp, M, rows_pad, Ncol, K, splits);
     else
-        hipLaunchKernelGGL((gemm_dma_kernel<EPI, LO_B, kDmaBM>), grid, block, 0, stream, a_planes, a_exp, b_planes, b_exp, bias, out,
+        hipLaunchKernelGGL((gemm_dma_kernel<EPI, LO_B, kDmaBM, W>), grid, block, 0, stream, a_planes, a_exp, b_planes, b_exp, bias, out,
                            out_planes, out_exp, M, rows_pad, Ncol, K, splits);
     return hipGetLastError();
 }
