@@ -545,7 +545,7 @@ __global__ __launch_bounds__(kThreads) void gemm_planes_kernel(
 // products and order as gemm_planes_kernel.
 constexpr int kDmaStages = 3;
 constexpr int kDmaBM = 256, kDmaBN = 128;
-constexpr int kDmaWaves = 8;  // waves per block: 8 (two per SIMD, 64 x 64 wave tiles) or 4 (128 x 64)
+constexpr int kDmaWaves = 8;  // waves per block: two per SIMD, 64 x 64 outputs each
 constexpr uint32_t kDmaMaxActBlocks = 40;  // activation blocks of one down split held in LDS (int8 binades)
 static_assert(kDmaMaxActBlocks <= 64, "one bit per activation block of a split in two 32-bit masks");
 
@@ -556,14 +556,15 @@ __device__ __forceinline__ void wait_loads() {
     __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | (7 << 4));
 }
 
-// 16 bytes per lane from global memory straight into LDS: lane l reads base + 16 l (base wave-uniform, in scalar
-// registers, so that a transfer costs no vector address arithmetic) and its bytes land at lds + 16 l. Written as
-// inline assembly so that the compiler, which cannot tell the ring slots apart, does not wait for every transfer in
-// flight before each LDS read; the kernel orders them itself (wait_loads, then a barrier).
-__device__ __forceinline__ void dma16(const _Float16* base, uint32_t lane, const _Float16* lds) {
+// 16 bytes per lane from global memory straight into LDS: lane l reads base + offset_l (base wave-uniform, in scalar
+// registers; offset_l a 32-bit byte offset in a vector register, the piece's offset plus 16 l, computed once) and its
+// bytes land at lds + 16 l. Written as inline assembly so that the compiler, which cannot tell the ring slots apart,
+// does not wait for every transfer in flight before each LDS read; the kernel orders them itself (wait_loads, then a
+// barrier).
+__device__ __forceinline__ void dma16(const _Float16* base, uint32_t offset, const _Float16* lds) {
     const uint32_t to = static_cast<uint32_t>(__builtin_amdgcn_readfirstlane(
         static_cast<int>(static_cast<uint32_t>(reinterpret_cast<uintptr_t>(lds)))));  // low 32 bits: the LDS address
-    asm volatile("s_mov_b32 m0, %2\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, %1" ::"v"(lane * 16), "s"(base), "s"(to)
+    asm volatile("s_mov_b32 m0, %2\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, %1" ::"v"(offset), "s"(base), "s"(to)
                  : "memory", "m0");
 }
 
@@ -579,8 +580,8 @@ __device__ __forceinline__ void block_barrier() {
 // waves whose rows are all padding only transfer and meet at the barriers. The live rows get the same
 // products in the same order as with LIVE = BM, and the padding rows' accumulators stay zero, as zero A rows leave
 // them, so the results are bitwise those of the full tile.
-template <Epi EPI, bool LO_B, int LIVE, int W>
-__global__ __launch_bounds__(64 * W) void gemm_dma_kernel(
+template <Epi EPI, bool LO_B, int LIVE>
+__global__ __launch_bounds__(64 * kDmaWaves) void gemm_dma_kernel(
     const _Float16* __restrict__ a_planes,  // [K / 32][8][rows_pad][8]
     const int32_t* __restrict__ a_exp,      // Up: [rows_pad]; Down: [rows_pad, K / kActBlock]
     const _Float16* __restrict__ b_planes,  // [K / 32][8][Ncol][8]
@@ -590,90 +591,152 @@ __global__ __launch_bounds__(64 * W) void gemm_dma_kernel(
     _Float16* __restrict__ out_planes,      // Up: activation planes [Ncol / 32][8][rows_pad][8]
     int32_t* __restrict__ out_exp,          // Up: [rows_pad, Ncol / BN] activation block binades
     uint32_t M, uint32_t rows_pad, uint32_t Ncol, uint32_t K, uint32_t splits) {
-    // W waves in (W / 2) x 2: 4 waves of 128 x 64 or 8 waves of 64 x 64 (two per SIMD)
-    static_assert(W == 4 || W == 8, "4 or 8 waves");
-    constexpr int MI = W == 4 ? 4 : 2, NI = 2, BM = kDmaBM, BN = kDmaBN, S = kDmaStages;
-    constexpr uint32_t kT = 64 * W, kWaveRows = 32 * MI;
-    static_assert(BM <= kT && kWaveRows * (W / 2) == BM, "a thread per block row for the binade tables; waves cover BM");
+    // 8 waves in 4 x 2, 64 x 64 outputs each (two waves per SIMD)
+    constexpr int W = kDmaWaves, MI = 2, NI = 2, BM = kDmaBM, BN = kDmaBN, S = kDmaStages;
+    constexpr uint32_t kT = 64 * W, kWaveRows = 32 * MI, kHalf = W / 2;
+    static_assert(kWaveRows * (W / 2) == BM, "the waves cover the block's rows");
+    static_assert(kHalf * kWave == BM, "the upper half of the waves holds a thread per block row");
     static_assert(LIVE == BM || LIVE == 128 || LIVE == 64, "live rows: the whole tile, its first half or first quarter");
     constexpr uint32_t kStage = kRuns * (BM + BN) * 8;  // halves per stage
     constexpr int kRowRuns = LIVE / 64;                  // 64-row runs of A transferred per (part, chunk)
-    constexpr int kLoadsA = kRowRuns * kRuns / W, kLoadsB = BN * kRuns / kWave / W;  // DMA instructions per wave
-    static_assert(kLoadsA * W == kRowRuns * kRuns && kLoadsB * W == BN * kRuns / kWave, "the transfers divide over the waves");
+    // runs of B transferred per k-tile: both planes, or the hi plane alone when the lo plane is not read (LO_B false)
+    constexpr int kRunsB = LO_B ? kRuns : kRuns / 2;
+    constexpr int kLoadsA = kRowRuns * kRuns / W, kLoadsB = BN * kRunsB / kWave / W;  // DMA instructions per wave
+    static_assert(kLoadsA * W == kRowRuns * kRuns && kLoadsB * W == BN * kRunsB / kWave, "the transfers divide over the waves");
     constexpr int kLoads = kLoadsA + kLoadsB;
+    static_assert(2 * kLoads * S < 64, "the prologue's transfers of a lower-half wave fit vmcnt");
     // multiplied 32-row tiles of a live wave (its rows start at wm * kWaveRows; LIVE is a multiple of kWaveRows)
     constexpr int MIL = LIVE >= static_cast<int>(kWaveRows) ? MI : LIVE / 32;
 
     __shared__ __attribute__((aligned(16))) _Float16 smem[S * kStage];
     __shared__ int32_t e_row[1][BM];  // Up: x binades
     __shared__ __attribute__((aligned(4))) int8_t e_tab[EPI == Epi::Down ? kDmaMaxActBlocks : 1][EPI == Epi::Down ? BM : 1];  // Down: [block][row]
-    __shared__ uint32_t change_masks[EPI == Epi::Down ? W : 1][2];
+    __shared__ uint32_t change_masks[EPI == Epi::Down ? kHalf : 1][2];
 
     const uint32_t tid = threadIdx.x, lane = tid % kWave, wave = uniform(tid / kWave);
     const uint32_t wm = wave / 2, wn = wave % 2;
-    const bool live = wm * kWaveRows < static_cast<uint32_t>(LIVE);  // wave-uniform: this wave's rows hold tokens
+    // wave-uniform: this wave's rows hold tokens (a constant for a full tile)
+    const bool live = LIVE == BM || wm * kWaveRows < static_cast<uint32_t>(LIVE);
     const uint32_t tiles_m = rows_pad / BM, tiles_n = Ncol / BN;
     const Tile tile = tile_of(blockIdx.x, tiles_m, tiles_n, splits);
     const uint32_t m0 = tile.m * BM, n0 = tile.n * BN;
     const uint32_t ktiles = K / kBK;
     const uint32_t k_begin = tile.split * ktiles / splits, k_end = (tile.split + 1) * ktiles / splits;
     const uint32_t a_kblocks = K / kActBlock, kb0 = k_begin / kKtPerActBlock;
-    if constexpr (EPI != Epi::Down) {
-        if (tid < static_cast<uint32_t>(BM)) e_row[0][tid] = a_exp[m0 + tid];
-    } else {
-        // the row's binades of this split (whole activation blocks), eight loads in flight at a time
-        const uint32_t blocks = tid < static_cast<uint32_t>(BM) ? (k_end - k_begin) / kKtPerActBlock : 0;
-        const int32_t* row_exp = a_exp + static_cast<size_t>(m0 + (tid < static_cast<uint32_t>(BM) ? tid : 0)) * a_kblocks + kb0;
-        for (uint32_t b0 = 0; b0 < blocks; b0 += 8) {
-            int32_t v[8];
-#pragma unroll
-            for (uint32_t q = 0; q < 8; ++q) v[q] = b0 + q < blocks ? row_exp[b0 + q] : 0;
-#pragma unroll
-            for (uint32_t q = 0; q < 8; ++q)
-                if (b0 + q < blocks) e_tab[b0 + q][tid] = static_cast<int8_t>(v[q]);
+
+    // piece q of wave w's share of a stage: a run of 64 rows (1 KB) of A (pieces below kLoadsA), then of B; its
+    // element offsets within a k-tile's planes and within a ring slot
+    const auto piece = [&](uint32_t w, int q, uint32_t& src, uint32_t& dst) {
+        if (q < kLoadsA) {
+            const uint32_t at = w * kLoadsA + q, run = at / kRowRuns, rb = at % kRowRuns;
+            src = (run * rows_pad + m0 + rb * 64) * 8;
+            dst = (run * BM + rb * 64) * 8;
+        } else {
+            const uint32_t at = w * kLoadsB + (q - kLoadsA), run = at / (BN / 64), rb = at % (BN / 64);
+            src = (run * Ncol + n0 + rb * 64) * 8;
+            dst = kRuns * BM * 8 + (run * BN + rb * 64) * 8;
         }
-        // bit b of `changes`: this row's power of two differs between activation blocks b - 1 and b of the split;
-        // ORed over the wave, then over the block through LDS
-        uint32_t changes[2] = {0, 0};
-        for (uint32_t b = 1; b < blocks; ++b)
-            if (e_tab[b][tid] != e_tab[b - 1][tid]) changes[b / 32] |= 1u << (b % 32);
+    };
+    // this wave's pieces, computed once: the lanes' byte offsets from the k-tile's base (vector registers) and the
+    // LDS offsets (wave-uniform), so that a transfer in the k loop takes the k-tile's base pointer of its operand
+    const size_t a_kt = static_cast<size_t>(kRuns) * rows_pad * 8, b_kt = static_cast<size_t>(kRuns) * Ncol * 8;
+    uint32_t src_lane[kLoads], dst_off[kLoads];
 #pragma unroll
-        for (int h = 0; h < 2; ++h) {
+    for (int q = 0; q < kLoads; ++q) {
+        uint32_t src;
+        piece(wave, q, src, dst_off[q]);
+        src_lane[q] = src * 2 + lane * 16;
+    }
+    const auto issue_piece = [&](uint32_t kt, uint32_t slot, int q) {
+        const _Float16* base = q < kLoadsA ? a_planes + kt * a_kt : b_planes + kt * b_kt;
+        dma16(base, src_lane[q], smem + slot * kStage + dst_off[q]);
+    };
+    const auto issue = [&](uint32_t kt, uint32_t slot) {
 #pragma unroll
-            for (int off = 32; off >= 1; off >>= 1)
-                changes[h] |= static_cast<uint32_t>(__shfl_xor(static_cast<int>(changes[h]), off, kWave));
-            if (lane == 0) change_masks[wave][h] = changes[h];
+        for (int q = 0; q < kLoads; ++q) issue_piece(kt, slot, q);
+    };
+
+    // Prologue: the lower half of the waves transfers the first stages, its own pieces and those of the wave kHalf
+    // above, while the upper half loads the binades. vmcnt retires in order within a wave, so a binade load behind
+    // transfers of its own wave would wait for them; split so, the binades and the first stage arrive together.
+    const uint32_t steps = k_end - k_begin;  // at least 1
+    if (wave < kHalf) {
+#pragma unroll
+        for (int s = 0; s < S; ++s)
+            if (static_cast<uint32_t>(s) < steps) {
+                issue(k_begin + s, s);
+#pragma unroll
+                for (int q = 0; q < kLoads; ++q) {
+                    uint32_t src, dst;
+                    piece(wave + kHalf, q, src, dst);
+                    dma16(q < kLoadsA ? a_planes + (k_begin + s) * a_kt : b_planes + (k_begin + s) * b_kt, src * 2 + lane * 16,
+                          smem + s * kStage + dst);
+                }
+            }
+    } else {
+        const uint32_t t = tid - kHalf * kWave;  // 0 .. BM - 1
+        if constexpr (EPI != Epi::Down) {
+            e_row[0][t] = a_exp[m0 + t];
+        } else {
+            // The tile's binades of this split: `blocks` consecutive ints of each of its BM rows (whole activation
+            // blocks, at least one: the host splits K on activation block boundaries), read coalesced: load i of
+            // thread t takes element q = i BM + t of the table, (row q / blocks, block q % blocks), tracked
+            // incrementally, and the element before it in the row (itself in block 0); the table holds BM blocks
+            // elements, so every thread takes exactly `blocks` (a uniform bound), all in flight at once. Bit b of
+            // `changes`: some row of this thread's elements changes its power of two between blocks b - 1 and b,
+            // ORed over the wave, then over the upper waves through LDS after the prologue's barrier.
+            const uint32_t blocks = (k_end - k_begin) / kKtPerActBlock, dr = BM / blocks, dc = BM % blocks;
+            const int32_t* tab = a_exp + static_cast<size_t>(m0) * a_kblocks + kb0;
+            int32_t v[kDmaMaxActBlocks], u[kDmaMaxActBlocks];
+            uint32_t r = t / blocks, c = t % blocks;
+#pragma unroll
+            for (uint32_t i = 0; i < kDmaMaxActBlocks; ++i) {
+                if (i < blocks) {
+                    const uint32_t at = r * a_kblocks + c;
+                    v[i] = tab[at];
+                    u[i] = tab[c > 0 ? at - 1 : at];
+                }
+                r += dr, c += dc;
+                if (c >= blocks) c -= blocks, ++r;
+            }
+            uint64_t change = 0;  // branch-free: bit c set when the two int8 binades differ
+            r = t / blocks, c = t % blocks;
+#pragma unroll
+            for (uint32_t i = 0; i < kDmaMaxActBlocks; ++i) {
+                if (i < blocks) {
+                    e_tab[c][r] = static_cast<int8_t>(v[i]);
+                    const uint32_t differs = min((static_cast<uint32_t>(v[i]) ^ static_cast<uint32_t>(u[i])) & 0xFFu, 1u);
+                    change |= static_cast<uint64_t>(differs) << c;
+                }
+                r += dr, c += dc;
+                if (c >= blocks) c -= blocks, ++r;
+            }
+            uint32_t changes[2] = {static_cast<uint32_t>(change), static_cast<uint32_t>(change >> 32)};
+#pragma unroll
+            for (int h = 0; h < 2; ++h) {
+#pragma unroll
+                for (int off = 32; off >= 1; off >>= 1)
+                    changes[h] |= static_cast<uint32_t>(__shfl_xor(static_cast<int>(changes[h]), off, kWave));
+                if (lane == 0) change_masks[wave - kHalf][h] = changes[h];
+            }
         }
     }
-    __syncthreads();
+    // stage k_begin has landed (a lower-half wave has two pieces per piece of its share in flight per stage; an
+    // upper-half wave none), the binade tables are written; then the block meets
+    if (steps >= 3) wait_loads<4 * kLoads>();
+    else if (steps == 2) wait_loads<2 * kLoads>();
+    else wait_loads<0>();
+    block_barrier();
     uint32_t changed[2] = {0, 0};  // Down: activation blocks at whose start some row of the tile changes its power of two
     if constexpr (EPI == Epi::Down) {
 #pragma unroll
         for (int h = 0; h < 2; ++h) {
             uint32_t c = 0;
 #pragma unroll
-            for (int w = 0; w < W; ++w) c |= change_masks[w][h];
+            for (int w = 0; w < static_cast<int>(kHalf); ++w) c |= change_masks[w][h];
             changed[h] = uniform(c);
         }
     }
-
-    // piece q of stage kt into ring slot `slot`: wave w copies runs of 64 rows (1 KB each) of A (pieces below
-    // kLoadsA), then of B
-    const auto issue_piece = [&](uint32_t kt, uint32_t slot, int q) {
-        if (q < kLoadsA) {
-            const uint32_t at = wave * kLoadsA + q, run = at / kRowRuns, rb = at % kRowRuns;
-            dma16(a_planes + ((static_cast<size_t>(kt) * kRuns + run) * rows_pad + m0 + rb * 64) * 8, lane,
-                  smem + slot * kStage + (run * BM + rb * 64) * 8);
-        } else {
-            const uint32_t at = wave * kLoadsB + (q - kLoadsA), run = at / (BN / 64), rb = at % (BN / 64);
-            dma16(b_planes + ((static_cast<size_t>(kt) * kRuns + run) * Ncol + n0 + rb * 64) * 8, lane,
-                  smem + slot * kStage + kRuns * BM * 8 + (run * BN + rb * 64) * 8);
-        }
-    };
-    const auto issue = [&](uint32_t kt, uint32_t slot) {
-#pragma unroll
-        for (int q = 0; q < kLoads; ++q) issue_piece(kt, slot, q);
-    };
 
     floatx16 acc[MI][NI];
 #pragma unroll
@@ -749,14 +812,7 @@ __global__ __launch_bounds__(64 * W) void gemm_dma_kernel(
     // Software pipeline over half k-tiles: the fragments of the next 16-wide step are read from LDS while the MFMAs
     // of the current one run, and the block meets once per k-tile, between its two steps (after every wave has read
     // all of k-tile kt and before anyone reads k-tile kt + 1), where the slot of kt is refilled with kt + kDmaStages.
-    const uint32_t steps = k_end - k_begin;  // at least 1
-#pragma unroll
-    for (int s = 0; s < S; ++s)
-        if (static_cast<uint32_t>(s) < steps) issue(k_begin + s, s);
-    if (steps >= 3) wait_loads<2 * kLoads>();  // stage k_begin has landed; the two after it may be in flight
-    else if (steps == 2) wait_loads<kLoads>();
-    else wait_loads<0>();
-    block_barrier();
+    // The first stages went out in the prologue.
     // a new activation block at k-tile kt: bring the accumulators to its power of two (exact); accumulator
     // registers 4g .. 4g + 3 hold 4 consecutive rows, so one 4-byte read per block and group
     const auto rescale = [&](uint32_t kt) {
@@ -1049,17 +1105,30 @@ constexpr uint32_t kDmaMinDownBlocks = 64;
 
 uint32_t dma_tiles(uint32_t m, uint32_t ncol) { return rows_padded(m) / kDmaBM * (ncol / kDmaBN); }
 
-// Splits of the streamed down GEMM: doubled (up to kDmaMaxSplits) until the tiles times the splits reach ~192 blocks
-// or a split's activation binades fit LDS; each split a whole number of activation blocks. 0: not streamed.
+// Splits of the streamed down GEMM by estimated time, over the split counts (powers of two up to kDmaMaxSplits) that
+// cut K on activation blocks, hold a split's binades in LDS and give at least kDmaMinDownBlocks blocks: the blocks
+// run in rounds of one per CU (the LDS ring takes a CU), each block kDmaKtileUs per k-tile plus kDmaBlockUs of
+// prologue and epilogue; a split count above 1 adds its partials' round trip (written, then read by
+// reduce_splits_kernel) and that kernel's launch. The partials are priced on the padded rows, so every token count
+// of one padded row count takes the same splits and a token's sums do not depend on the call's other tokens.
+// Constants measured on MI355X (256 x 128 blocks of 8 waves: a k-tile 1.29-1.46 us, prologue + epilogue 7-9 us,
+// partials at ~4 TB/s). 0: not streamed.
 constexpr uint32_t kDmaMaxSplits = 32;
+constexpr uint32_t kCus = 256;
+constexpr double kDmaKtileUs = 1.35, kDmaBlockUs = 8.0, kPartialBytesPerUs = 4.0e6, kReduceUs = 4.0;
 uint32_t dma_down_splits(uint32_t m, uint32_t ncol, uint32_t k) {
-    const uint32_t tiles = dma_tiles(m, ncol);
-    uint32_t splits = 1;
-    while (splits < kDmaMaxSplits && tiles * splits < 192) splits *= 2;
-    while (splits < kDmaMaxSplits && k / kActBlock / splits > kDmaMaxActBlocks) splits *= 2;  // the split's binades must fit LDS
-    while (splits > 1 && k % (kActBlock * splits) != 0) splits /= 2;
-    if (k / kActBlock / splits > kDmaMaxActBlocks) return 0;
-    return tiles * splits >= kDmaMinDownBlocks ? splits : 0;
+    const uint32_t tiles = dma_tiles(m, ncol), ktiles = k / kBK;
+    uint32_t best = 0;
+    double best_us = 0.0;
+    for (uint32_t splits = 1; splits <= kDmaMaxSplits; splits *= 2) {
+        if (k % (kActBlock * splits) != 0 || k / kActBlock / splits > kDmaMaxActBlocks || tiles * splits < kDmaMinDownBlocks)
+            continue;
+        const double rounds = ceil_div(tiles * splits, kCus);
+        double us = rounds * (static_cast<double>(ktiles) / splits * kDmaKtileUs + kDmaBlockUs);
+        if (splits > 1) us += 8.0 * splits * rows_padded(m) * ncol / kPartialBytesPerUs + kReduceUs;
+        if (best == 0 || us < best_us) best = splits, best_us = us;
+    }
+    return best;
 }
 
 // Splits of the streamed up GEMM: 1 when its tiles alone fill the chip, else doubled (up to 8, each split at least
@@ -1104,17 +1173,16 @@ template <Epi EPI, bool LO_B>
 hipError_t launch_dma(const _Float16* a_planes, const int32_t* a_exp, const _Float16* b_planes, const int32_t* b_exp,
                       const float* bias, float* out, _Float16* out_planes, int32_t* out_exp, uint32_t M, uint32_t Ncol, uint32_t K,
                       uint32_t splits, hipStream_t stream) {
-    constexpr int W = kDmaWaves;
-    const dim3 grid(dma_tiles(M, Ncol) * splits), block(64 * W);
+    const dim3 grid(dma_tiles(M, Ncol) * splits), block(64 * kDmaWaves);
     const uint32_t rows_pad = rows_padded(M), live = rows_live(M);
     if (live == 64)
-        hipLaunchKernelGGL((gemm_dma_kernel<EPI, LO_B, 64, W>), grid, block, 0, stream, a_planes, a_exp, b_planes, b_exp, bias, out,
+        hipLaunchKernelGGL((gemm_dma_kernel<EPI, LO_B, 64>), grid, block, 0, stream, a_planes, a_exp, b_planes, b_exp, bias, out,
                            out_planes, out_exp, M, rows_pad, Ncol, K, splits);
     else if (live == 128)
-        hipLaunchKernelGGL((gemm_dma_kernel<EPI, LO_B, 128, W>), grid, block, 0, stream, a_planes, a_exp, b_planes, b_exp, bias, out,
+        hipLaunchKernelGGL((gemm_dma_kernel<EPI, LO_B, 128>), grid, block, 0, stream, a_planes, a_exp, b_planes, b_exp, bias, out,
                            out_planes, out_exp, M, rows_pad, Ncol, K, splits);
     else
-        hipLaunchKernelGGL((gemm_dma_kernel<EPI, LO_B, kDmaBM, W>), grid, block, 0, stream, a_planes, a_exp, b_planes, b_exp, bias, out,
+        hipLaunchKernelGGL((gemm_dma_kernel<EPI, LO_B, kDmaBM>), grid, block, 0, stream, a_planes, a_exp, b_planes, b_exp, bias, out,
                            out_planes, out_exp, M, rows_pad, Ncol, K, splits);
     return hipGetLastError();
 }
