@@ -8,8 +8,9 @@
 // GEMM's epilogue (one power of two per token and 128-neuron block). Each product is  a_hi b_hi + a_hi b_lo +
 // a_lo b_hi  accumulated in fp32 (the lo*lo term, ~2^-22 relative, is dropped; bf16 weights take the first and last
 // terms on the hi plane only, which holds them exactly down to 2^-14 of their row's largest magnitude; below that
-// fp16 subnormals keep fewer bits, at most ~2^-25 of that magnitude per weight). The powers of two are undone exactly: the down GEMM rescales its
-// accumulators at each 128-wide k block by the ratio of the blocks' powers of two, and the epilogues apply the last.
+// fp16 subnormals keep fewer bits, at most ~2^-25 of that magnitude per weight). The powers of two are undone
+// exactly: the down GEMM rescales its accumulators at each 128-wide k block by the ratio of the blocks' powers of
+// two, and the epilogues apply the last.
 //
 // Plane layout (K-chunk-major): k is cut into 32-wide k-tiles and each k-tile into four 16-byte chunks of 8 halves;
 // for k-tile kt, part p (0 hi, 1 lo) and chunk c, the chunks of all rows follow one another:
@@ -21,7 +22,8 @@
 // the first 64 or 128 rows (rows_live).
 //
 // Two GEMM kernels: the streamed one (gemm_dma_kernel: 256 x 128 tiles whose k-tiles go from global memory straight
-// into LDS, K split 2-32 ways when the tiles alone leave CUs idle, partials added by separate passes) takes every
+// into LDS, K split 2-32 ways by an estimate of the rounds of blocks and the partials' cost, partials added by
+// separate passes) takes every
 // shape whose tiles and splits give enough blocks; the register-staged one below (gemm_planes_kernel) remains for
 // narrower layers at small N.
 //
@@ -537,12 +539,14 @@ __global__ __launch_bounds__(kThreads) void gemm_planes_kernel(
 }
 
 // ------------------------------------------------------------------------------- streamed GEMM (LDS DMA)
-// The large-N GEMM: 256 x 128 block tiles (4 waves of 128 x 64), one block per CU, and k-tiles streamed straight
-// from global memory into a ring of kDmaStages LDS stages by global_load_lds (16 bytes per lane, no registers on
-// the way). In the middle of k-tile kt (its first 16-wide step multiplied, its second read into registers) the block
-// waits for stage kt + 1, meets at a barrier and requests stage kt + kDmaStages into the slot of kt; each stage is
-// thus requested kDmaStages - 1 k-tiles before its wait, and the MFMAs never wait for LDS reads. The down GEMM reads the activation binades of its rows and k range into LDS before the first k-tile. Same
-// products and order as gemm_planes_kernel.
+// The large-N GEMM: 256 x 128 block tiles of 8 waves (4 x 2, 64 x 64 outputs each: two waves per SIMD, so that one
+// wave's barrier and transfer waits are covered by the other's MFMAs), one block per CU, and k-tiles streamed
+// straight from global memory into a ring of kDmaStages LDS stages by global_load_lds (16 bytes per lane, no
+// registers on the way). In the middle of k-tile kt (its first 16-wide step multiplied, its second read into
+// registers) the block waits for stage kt + 1, meets at a barrier and requests stage kt + kDmaStages into the slot of
+// kt; each stage is thus requested kDmaStages - 1 k-tiles before its wait, and the MFMAs never wait for LDS reads.
+// Before the first k-tile the lower half of the waves requests the first stages while the upper half loads the
+// activation binades of the tile's rows and k range (the down GEMM). Same products and order as gemm_planes_kernel.
 constexpr int kDmaStages = 3;
 constexpr int kDmaBM = 256, kDmaBN = 128;
 constexpr int kDmaWaves = 8;  // waves per block: two per SIMD, 64 x 64 outputs each
