@@ -10,7 +10,7 @@ import ctypes
 from pathlib import Path
 
 LIBRARY = Path(__file__).resolve().with_name("libhffn_amd.so")
-ABI_VERSION = 13
+ABI_VERSION = 14
 
 OK = 0
 VALUE_F32, VALUE_BF16 = 0, 1
@@ -34,6 +34,9 @@ SIGNATURES = {
     "hffn_forward_z": [_I, _I] + [_P] * 14 + [_U32] * 6 + [_P],
     "hffn_grad_dense_workspace": [_U32, _U32, _U32, _P],
     "hffn_grad_dense": [_P] * 6 + [_U32] * 4 + [_P, _U64, _P],
+    "hffn_train_mfma_workspace": [_U32, _U32, _U32, ctypes.POINTER(_U64)],
+    "hffn_forward_mfma_z": [_P] * 7 + [_P, _U64] + [_P] * 4 + [_U32] * 4 + [_P],
+    "hffn_backward_mfma": [_P] * 7 + [_U64, _P, _P] + [_U32] * 4 + [_P],
     "hffn_grad_sddmm": [_P] * 6 + [_U32] * 4 + [_P],
     "hffn_grad_hidden": [_P] * 7 + [_U32] * 5 + [_P],
     "hffn_grad_x": [_P] * 6 + [_U32] * 5 + [_P],

@@ -3,7 +3,7 @@ as the reference's FFN training results (``runtime/gpu/nvidia/ffn/training/RESUL
 N = 1, 8, 64, 512; the control is PyTorch's iso-support step: dense weights, masked gradients, fused AdamW,
 ``train_step.py:95-121``).
 
-    python -m hffn_amd.bench_train [--cells 512_2048_d020,1024_4096_d050] [--tokens 1,8,64,512] [--steps 50]
+    python -m hffn_amd.bench_train [--cells 512_2048_d020,1024_4096_d050] [--tokens 1,8,64,512] [--steps 50] [--train gather|mfma]
 
 One JSON line per (cell, N): milliseconds per step of each arm (HIP events around ``steps`` steps after warm-up, inputs
 resident), their ratio, and the memory each arm keeps for its parameters and optimiser state. Layers are synthetic:
@@ -91,12 +91,14 @@ def main(argv: list[str] | None = None) -> int:
     parser.add_argument("--tokens", default="1,8,64,512")
     parser.add_argument("--steps", type=int, default=50)
     parser.add_argument("--warmup", type=int, default=5)
+    parser.add_argument("--train", choices=("gather", "mfma"), help="force the forward with z, gz and gx (default: the policy)")
     args = parser.parse_args(argv)
     device = torch.device("cuda", 0)
     tokens = [int(v) for v in args.tokens.split(",")]
     for name in args.cells.split(","):
         layer = make_cell(name)
         train = HFFNTrainRuntime(HFFNRuntime([hip_layer(layer)], device), **HYPER, max_tokens=max(tokens))
+        train.forced_train = args.train
         dense = DenseControl(layer, device)
         for n in tokens:
             rng = np.random.default_rng(n)
@@ -108,7 +110,8 @@ def main(argv: list[str] | None = None) -> int:
             dense_ms = time_steps(lambda: dense.step(x, gy), args.steps, args.warmup)
             sizes = train.nbytes(0)
             print(json.dumps({"cell": name, "n": n, "hffn_ms": round(hffn_ms, 4), "dense_ms": round(dense_ms, 4),
-                              "hffn_over_dense": round(hffn_ms / dense_ms, 3), "modes": list(train.modes(n)),
+                              "hffn_over_dense": round(hffn_ms / dense_ms, 3), "train_mode": train.train_mode(n),
+                              "grad_mode": train.grad_mode(n), "modes": list(train.modes(n)),
                               "hffn_state_mb": round((sizes["values"] + sizes["gradients"] + sizes["moments"] + sizes["indices"]) / 1e6, 2),
                               "dense_state_mb": round(dense.state_bytes() / 1e6, 2), "growths_in_window": train.growths - growths}),
                   flush=True)

@@ -5,6 +5,7 @@
 
 #include <cstdarg>
 #include <cstdio>
+#include <initializer_list>
 #include <mutex>
 #include <string>
 #include <unordered_map>
@@ -621,6 +622,56 @@ int hffn_grad_dense(const float* row, const float* mat, const int32_t* offsets, 
                     static_cast<unsigned long long>(needed));
     return launched(hffn::launch_grad_dense(row, mat, offsets, index, g, gb, rows, cols, n, ld, workspace, static_cast<hipStream_t>(stream)),
                     "grad_dense");
+}
+
+int hffn_train_mfma_workspace(uint32_t n, uint32_t d_model, uint32_t d_ff, uint64_t* bytes) {
+    if (!bytes) return fail(HFFN_ERROR_ARGUMENT, "train_mfma_workspace: null result");
+    if (int status = check_mfma(HFFN_VALUE_F32, d_model, d_ff, n)) return status;
+    if (!hffn::mfma_streamed(n, d_model, d_ff))
+        return fail(HFFN_ERROR_ARGUMENT, "train_mfma: the streamed GEMM does not take n=%u on %u x %u", n, d_model, d_ff);
+    *bytes = hffn::train_mfma_workspace_bytes(n, d_model, d_ff);
+    return HFFN_OK;
+}
+
+namespace {
+int check_train_mfma(const char* what, uint32_t d_model, uint32_t d_ff, uint32_t n, uint32_t ld, const void* workspace,
+                     uint64_t workspace_bytes, std::initializer_list<const void*> floats, std::initializer_list<const void*> others) {
+    uint64_t needed = 0;
+    if (int status = hffn_train_mfma_workspace(n, d_model, d_ff, &needed)) return status;
+    if (ld < n || ld % 4 != 0) return fail(HFFN_ERROR_ARGUMENT, "%s: ld=%u must be a multiple of 4 and at least n=%u", what, ld, n);
+    for (const void* p : floats)
+        if (!p || reinterpret_cast<uintptr_t>(p) % 16 != 0) return fail(HFFN_ERROR_ARGUMENT, "%s: null or not 16-byte aligned float buffer", what);
+    for (const void* p : others)
+        if (!p) return fail(HFFN_ERROR_ARGUMENT, "%s: null pointer", what);
+    if (!workspace || reinterpret_cast<uintptr_t>(workspace) % 256 != 0)
+        return fail(HFFN_ERROR_ARGUMENT, "%s: the workspace must be 256-byte aligned", what);
+    if (workspace_bytes < needed)
+        return fail(HFFN_ERROR_ARGUMENT, "%s: workspace of %llu bytes, %llu needed", what, static_cast<unsigned long long>(workspace_bytes),
+                    static_cast<unsigned long long>(needed));
+    return HFFN_OK;
+}
+}  // namespace
+
+int hffn_forward_mfma_z(const float* x, const void* up_planes, const int32_t* up_binades, const float* b_up, const void* down_planes,
+                        const int32_t* down_binades, const float* b_down, void* workspace, uint64_t workspace_bytes, float* x_t,
+                        float* act, float* z, float* y, uint32_t d_model, uint32_t d_ff, uint32_t n, uint32_t ld, void* stream) {
+    if (int status = check_train_mfma("forward_mfma_z", d_model, d_ff, n, ld, workspace, workspace_bytes,
+                                      {x, b_up, b_down, x_t, act, z, y, up_planes, down_planes}, {up_binades, down_binades}))
+        return status;
+    return launched(hffn::launch_train_forward(x, up_planes, up_binades, b_up, down_planes, down_binades, b_down, workspace, x_t, act, z, y,
+                                               n, d_model, d_ff, ld, static_cast<hipStream_t>(stream)),
+                    "forward_mfma_z");
+}
+
+int hffn_backward_mfma(const float* gy, const float* z, const void* down_t_planes, const int32_t* down_t_binades, const void* up_t_planes,
+                       const int32_t* up_t_binades, void* workspace, uint64_t workspace_bytes, float* gz, float* gx, uint32_t d_model,
+                       uint32_t d_ff, uint32_t n, uint32_t ld, void* stream) {
+    if (int status = check_train_mfma("backward_mfma", d_model, d_ff, n, ld, workspace, workspace_bytes,
+                                      {gy, z, gz, gx, down_t_planes, up_t_planes}, {down_t_binades, up_t_binades}))
+        return status;
+    return launched(hffn::launch_train_backward(gy, z, down_t_planes, down_t_binades, up_t_planes, up_t_binades, workspace, gz, gx, n,
+                                                d_model, d_ff, ld, static_cast<hipStream_t>(stream)),
+                    "backward_mfma");
 }
 
 int hffn_grad_sddmm(const float* row, const float* mat, const int32_t* offsets, const int16_t* index, float* g, float* gb,

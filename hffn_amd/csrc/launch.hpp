@@ -96,6 +96,18 @@ size_t grad_dense_workspace_bytes(uint32_t rows, uint32_t cols, uint32_t n);
 hipError_t launch_grad_dense(const float* row, const float* mat, const int32_t* off, const int16_t* idx, float* g, float* gb,
                              uint32_t rows, uint32_t cols, uint32_t n, uint32_t ld, void* workspace, hipStream_t stream);
 
+// The training forward (z, act hidden-major; y) and the backward products gz (hidden-major) and gx on the planes
+// (mfma.hip; fp32 weights): the up-shaped products as split products with the training epilogues, the down-shaped ones
+// on the inference down GEMM. The workspace is the MFMA workspace with partials at every split count; both need the
+// streamed GEMM (mfma_streamed).
+size_t train_mfma_workspace_bytes(uint32_t n, uint32_t d, uint32_t h);
+hipError_t launch_train_forward(const float* x, const void* up_planes, const int32_t* up_exp, const float* b_up, const void* down_planes,
+                                const int32_t* down_exp, const float* b_down, void* workspace, float* x_t, float* act, float* z, float* y,
+                                uint32_t n, uint32_t d, uint32_t h, uint32_t ld, hipStream_t stream);
+hipError_t launch_train_backward(const float* gy, const float* z, const void* down_t_planes, const int32_t* down_t_exp,
+                                 const void* up_t_planes, const int32_t* up_t_exp, void* workspace, float* gz, float* gx, uint32_t n,
+                                 uint32_t d, uint32_t h, uint32_t ld, hipStream_t stream);
+
 // Decode-sized projections over the same planes (gemv.hip): act token-major [n, h] (16-byte aligned), y token-major
 // [n, d]; `work` (gemv_workspace_bytes) holds the k-split partial sums.
 constexpr uint32_t kGemvMaxTokens = 64;

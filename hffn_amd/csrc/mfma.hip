@@ -165,39 +165,85 @@ __global__ __launch_bounds__(kThreads) void split_rows_kernel(const float* __res
 }
 
 // --------------------------------------------------------------------------------------------- densify
-// One block per row n of the dense matrix (a neuron of W_up, or an output of W_down^T) with its slots
-// [off[n], off[n+1]) at columns idx[] (distinct within a row; the host checks it). Writes the whole row of both
-// planes (zeros outside the support) and its binade.
+// Row n of the dense matrix (a neuron of W_up, or an output of W_down^T) has its slots [off[n], off[n+1]) at columns
+// idx[] (distinct within a row; the host checks it); densifying writes the whole row of both planes (zeros outside
+// the support) and its binade. A block takes kDensRows consecutive rows and kDensChunk columns (blockIdx.y): the rows'
+// maxima (a wave per row, over all their slots), then their hi/lo parts in its columns assembled in LDS (zeroed, then
+// each slot of the chunk in its column) and written out whole: for every 16-byte chunk run the block's rows are
+// kDensRows consecutive 16-byte pieces, one 128-byte line per (run, row group). The rows are padded by 16 bytes in
+// LDS so that the eight rows of a chunk fall in different banks; the tile (66 KB) leaves room for two blocks per CU.
+constexpr uint32_t kDensRows = 8, kDensChunk = 2048, kDensThreads = 512, kDensPad = 8;
 template <typename V>
-__global__ __launch_bounds__(kThreads) void densify_kernel(const int32_t* __restrict__ off, const int16_t* __restrict__ idx,
-                                                          const V* __restrict__ val, uint32_t rows, uint32_t k,
-                                                          _Float16* __restrict__ planes, int32_t* __restrict__ exps) {
-    __shared__ uint32_t part[kThreads / kWave];
-    const uint32_t n = blockIdx.x;
-    const int32_t begin = off[n], end = off[n + 1];
-    uint32_t m = 0;
-    for (int32_t s = begin + static_cast<int32_t>(threadIdx.x); s < end; s += kThreads) m = max(m, abs_bits(widen(val[s])));
+__global__ __launch_bounds__(kDensThreads) void densify_kernel(const int32_t* __restrict__ off, const int16_t* __restrict__ idx,
+                                                              const V* __restrict__ val, uint32_t rows, uint32_t k,
+                                                              _Float16* __restrict__ planes, int32_t* __restrict__ exps) {
+    static_assert(kDensRows * 16 == 128, "a row group's pieces of one chunk run fill one 128-byte line");
+    __shared__ __attribute__((aligned(16))) _Float16 tile[2][kDensRows][kDensChunk + kDensPad];
+    __shared__ int32_t row_exp[kDensRows];
+    constexpr uint32_t kWaves = kDensThreads / kWave;
+    const uint32_t tid = threadIdx.x, lane = tid % kWave, wave = uniform(tid / kWave);
+    const uint32_t r0 = blockIdx.x * kDensRows;
+    // (the slot loops keep kBatch loads per lane in flight before using any)
+    constexpr int kBatch = 16;
+    for (uint32_t rr = wave; rr < kDensRows; rr += kWaves) {
+        const uint32_t n = r0 + rr;
+        uint32_t m = 0;
+        if (n < rows) {
+            const int32_t end = off[n + 1];
+            for (int32_t s0 = off[n] + static_cast<int32_t>(lane); s0 < end; s0 += kBatch * kWave) {
+                float w[kBatch];
 #pragma unroll
-    for (int s = 32; s >= 1; s >>= 1) m = max(m, static_cast<uint32_t>(__shfl_xor(static_cast<int>(m), s, kWave)));
-    if (threadIdx.x % kWave == 0) part[threadIdx.x / kWave] = m;
-    // zero this row's 16-byte chunk in every (k-tile, part, chunk) run
-    const uint32_t runs = k / kBK * kRuns;
-    for (uint32_t i = threadIdx.x; i < runs; i += kThreads)
-        *reinterpret_cast<uint4*>(planes + (static_cast<size_t>(i) * rows + n) * 8) = make_uint4(0, 0, 0, 0);
-    __syncthreads();
-    uint32_t mx = 0;
+                for (int q = 0; q < kBatch; ++q) w[q] = s0 + q * kWave < end ? widen(val[s0 + q * kWave]) : 0.0f;
 #pragma unroll
-    for (int w = 0; w < kThreads / kWave; ++w) mx = max(mx, part[w]);
-    const int e = binade_of_bits(mx);
-    for (int32_t s = begin + static_cast<int32_t>(threadIdx.x); s < end; s += kThreads) {
-        const uint32_t c = static_cast<uint16_t>(idx[s]);
-        _Float16 hi, lo;
-        split(ldexpf(widen(val[s]), -e), hi, lo);
-        const size_t run = static_cast<size_t>(c / kBK) * kRuns + (c % kBK) / 8;  // part 0
-        planes[(run * rows + n) * 8 + c % 8] = hi;
-        planes[((run + 4) * rows + n) * 8 + c % 8] = lo;
+                for (int q = 0; q < kBatch; ++q) m = max(m, abs_bits(w[q]));
+            }
+        }
+#pragma unroll
+        for (int o = 32; o >= 1; o >>= 1) m = max(m, static_cast<uint32_t>(__shfl_xor(static_cast<int>(m), o, kWave)));
+        if (lane == 0) row_exp[rr] = binade_of_bits(m);
     }
-    if (threadIdx.x == 0) exps[n] = e;
+    __syncthreads();
+    {
+        const uint32_t c0 = blockIdx.y * kDensChunk;
+        const uint32_t width = min(kDensChunk, k - c0), pieces = width / 8;  // width: a multiple of 32
+        for (uint32_t i = tid; i < 2 * kDensRows * pieces; i += kDensThreads) {
+            const uint32_t part = i / (kDensRows * pieces), rr = (i / pieces) % kDensRows, j = i % pieces;
+            *reinterpret_cast<uint4*>(&tile[part][rr][j * 8]) = make_uint4(0, 0, 0, 0);
+        }
+        __syncthreads();
+        for (uint32_t rr = wave; rr < kDensRows; rr += kWaves) {
+            const uint32_t n = r0 + rr;
+            if (n >= rows) continue;
+            const int e = row_exp[rr];
+            const int32_t end = off[n + 1];
+            for (int32_t s0 = off[n] + static_cast<int32_t>(lane); s0 < end; s0 += kBatch * kWave) {
+                uint32_t c[kBatch];
+                float w[kBatch];
+#pragma unroll
+                for (int q = 0; q < kBatch; ++q) {
+                    const bool in = s0 + q * kWave < end;
+                    c[q] = in ? static_cast<uint16_t>(idx[s0 + q * kWave]) : 0xFFFFFFFFu;
+                    w[q] = in ? widen(val[s0 + q * kWave]) : 0.0f;
+                }
+#pragma unroll
+                for (int q = 0; q < kBatch; ++q) {
+                    if (c[q] < c0 || c[q] >= c0 + width) continue;  // another column pass's slot, or past the row
+                    _Float16 hi, lo;
+                    split(ldexpf(w[q], -e), hi, lo);
+                    tile[0][rr][c[q] - c0] = hi;
+                    tile[1][rr][c[q] - c0] = lo;
+                }
+            }
+        }
+        __syncthreads();
+        for (uint32_t i = tid; i < 2 * pieces * kDensRows; i += kDensThreads) {
+            const uint32_t rr = i % kDensRows, j = (i / kDensRows) % pieces, part = i / (kDensRows * pieces);
+            if (r0 + rr < rows)
+                *reinterpret_cast<uint4*>(planes + plane_at(rows, r0 + rr, c0 + j * 8, part)) =
+                    *reinterpret_cast<const uint4*>(&tile[part][rr][j * 8]);
+        }
+    }
+    if (blockIdx.y == 0 && tid < kDensRows && r0 + tid < rows) exps[r0 + tid] = row_exp[tid];
 }
 
 // ------------------------------------------------------------------------------------------------ GEMM
@@ -944,7 +990,7 @@ __global__ __launch_bounds__(64 * kDmaWaves) void gemm_dma_kernel(
         }
         __syncthreads();
         float* target = out + (splits > 1 ? static_cast<size_t>(tile.split) * M * Ncol : 0);
-        const bool add_bias = EPI == Epi::Down && splits == 1;
+        const bool add_bias = EPI == Epi::Down && splits == 1 && bias != nullptr;  // no bias: the training gx product
         for (uint32_t q = tid; q < BM * (BN / 4); q += kT) {
             const uint32_t m = q / (BN / 4), c = (q % (BN / 4)) * 4;
             if (m0 + m >= M) break;  // rows ascend with q
@@ -977,8 +1023,10 @@ __global__ __launch_bounds__(kThreads) void reduce_splits_kernel(const float* __
                 t.x += u[q].x; t.y += u[q].y; t.z += u[q].z; t.w += u[q].w;
             }
     }
-    const float4 b = *reinterpret_cast<const float4*>(bias + (i * 4) % Ncol);
-    t.x += b.x; t.y += b.y; t.z += b.z; t.w += b.w;
+    if (bias != nullptr) {  // none for the training gx product
+        const float4 b = *reinterpret_cast<const float4*>(bias + (i * 4) % Ncol);
+        t.x += b.x; t.y += b.y; t.z += b.z; t.w += b.w;
+    }
     reinterpret_cast<float4*>(y)[i] = t;
 }
 
@@ -1035,6 +1083,108 @@ __global__ __launch_bounds__(kThreads) void act_planes_kernel(const float* __res
     }
     *reinterpret_cast<half8*>(planes + plane_at(rows_pad, m, n, 0)) = hi;
     *reinterpret_cast<half8*>(planes + plane_at(rows_pad, m, n, 1)) = lo;
+}
+
+// Training epilogues of the split up-shaped products [tokens, d_ff] (the sums of the split partials, in split order):
+//   Forward: z = b_up + sum, act = gelu(z): z and act hidden-major [d_ff, ld], act also as planes with its block
+//            binades (read by the down GEMM);
+//   GradZ:   gz = sum * gelu'(z), z read hidden-major: gz hidden-major and as planes with block binades (read by the gx
+//            GEMM).
+// Blocks and threads as act_planes_kernel (16 tokens x one 128-neuron block; 16 threads per token, 8 neurons each). The
+// hidden-major rows go through LDS tiles [128 neurons][16 tokens]: thread i takes neuron i / 4 and tokens 4 (i % 4) ..
+// + 3, 16 bytes at a time (ld and the block's first token are multiples of 4, so a vector that starts below ld ends
+// below it); only tokens below M are written.
+enum class TrainPost { Forward, GradZ };
+template <TrainPost MODE>
+__global__ __launch_bounds__(kThreads) void train_planes_kernel(const float* __restrict__ partials, uint32_t splits,
+                                                               const float* __restrict__ b_up, const float* __restrict__ z_in,
+                                                               float* __restrict__ out_a, float* __restrict__ out_b,
+                                                               _Float16* __restrict__ planes, int32_t* __restrict__ exps, uint32_t M,
+                                                               uint32_t rows_pad, uint32_t H, uint32_t ld) {
+    constexpr uint32_t R = kActRowsPerBlock;
+    static_assert(R == 16 && kActBlock * 4 % kThreads == 0, "16 tokens a block; the tile rows divide over the threads");
+    __shared__ float ta[kActBlock][R + 1], tb[kActBlock][R + 1];  // Forward: z, act; GradZ: z, gz
+    const uint32_t ml = threadIdx.x / 16, sub = threadIdx.x % 16;
+    const uint32_t m0 = blockIdx.x * R, m = m0 + ml;
+    const uint32_t nb = blockIdx.y, n0 = nb * kActBlock, n = n0 + sub * 8;
+    if constexpr (MODE == TrainPost::GradZ) {
+        for (uint32_t i = threadIdx.x; i < kActBlock * 4; i += kThreads) {
+            const uint32_t r = i / 4, c = (i % 4) * 4;
+            float4 q = make_float4(0.f, 0.f, 0.f, 0.f);
+            if (m0 + c < ld) q = *reinterpret_cast<const float4*>(z_in + static_cast<size_t>(n0 + r) * ld + m0 + c);
+            ta[r][c] = q.x, ta[r][c + 1] = q.y, ta[r][c + 2] = q.z, ta[r][c + 3] = q.w;
+        }
+        __syncthreads();
+    }
+    float v[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+    if (m < M) {
+        for (uint32_t s0 = 0; s0 < splits; s0 += 4) {  // 8 loads in flight, added in split order
+            float4 u[4], w[4];
+#pragma unroll
+            for (uint32_t q = 0; q < 4; ++q)
+                if (s0 + q < splits) {
+                    const float* p = partials + (static_cast<size_t>(s0 + q) * M + m) * H + n;
+                    u[q] = *reinterpret_cast<const float4*>(p);
+                    w[q] = *reinterpret_cast<const float4*>(p + 4);
+                }
+#pragma unroll
+            for (uint32_t q = 0; q < 4; ++q)
+                if (s0 + q < splits) {
+                    v[0] += u[q].x; v[1] += u[q].y; v[2] += u[q].z; v[3] += u[q].w;
+                    v[4] += w[q].x; v[5] += w[q].y; v[6] += w[q].z; v[7] += w[q].w;
+                }
+        }
+    }
+    uint32_t largest = 0;
+    if constexpr (MODE == TrainPost::Forward) {
+        const float4 b0 = *reinterpret_cast<const float4*>(b_up + n), b1 = *reinterpret_cast<const float4*>(b_up + n + 4);
+        const float b[8] = {b0.x, b0.y, b0.z, b0.w, b1.x, b1.y, b1.z, b1.w};
+#pragma unroll
+        for (int q = 0; q < 8; ++q) {
+            const float z = v[q] + b[q];
+            ta[sub * 8 + q][ml] = z;
+            v[q] = gelu(z);
+            tb[sub * 8 + q][ml] = v[q];
+            largest = max(largest, abs_bits(v[q]));
+        }
+    } else {
+#pragma unroll
+        for (int q = 0; q < 8; ++q) {
+            v[q] *= gelu_grad(ta[sub * 8 + q][ml]);
+            tb[sub * 8 + q][ml] = v[q];
+            largest = max(largest, abs_bits(v[q]));
+        }
+    }
+#pragma unroll
+    for (int off = 8; off >= 1; off >>= 1) largest = max(largest, static_cast<uint32_t>(__shfl_xor(static_cast<int>(largest), off, kWave)));
+    const int e = act_binade(largest);
+    if (sub == 0) exps[static_cast<size_t>(m) * (H / kActBlock) + nb] = e;
+    const float scale = ldexpf(1.0f, -e);
+    half8 hi, lo;
+#pragma unroll
+    for (int q = 0; q < 8; ++q) {
+        _Float16 hh, ll;
+        split(v[q] * scale, hh, ll);
+        hi[q] = hh;
+        lo[q] = ll;
+    }
+    *reinterpret_cast<half8*>(planes + plane_at(rows_pad, m, n, 0)) = hi;
+    *reinterpret_cast<half8*>(planes + plane_at(rows_pad, m, n, 1)) = lo;
+    __syncthreads();
+    for (uint32_t i = threadIdx.x; i < kActBlock * 4; i += kThreads) {
+        const uint32_t r = i / 4, c = (i % 4) * 4;
+        const size_t at = static_cast<size_t>(n0 + r) * ld + m0 + c;
+#pragma unroll
+        for (uint32_t q = 0; q < 4; ++q) {
+            if (m0 + c + q >= M) break;
+            if constexpr (MODE == TrainPost::Forward) {
+                out_a[at + q] = ta[r][c + q];
+                out_b[at + q] = tb[r][c + q];
+            } else {
+                out_a[at + q] = tb[r][c + q];
+            }
+        }
+    }
 }
 
 uint32_t ceil_div(uint32_t a, uint32_t b) { return (a + b - 1) / b; }
@@ -1228,7 +1378,16 @@ size_t partial_floats(uint32_t m, uint32_t d, uint32_t h) {
     return most;
 }
 
-Workspace workspace_layout(uint32_t m, uint32_t d, uint32_t h) {
+// The training products run the up-shaped GEMMs (the forward's up projection, gz) as split products with partials at
+// every split count, one included: their partials need the largest [max(1, splits), M, d_ff] of any N up to M too.
+size_t train_partial_floats(uint32_t m, uint32_t d, uint32_t h) {
+    size_t most = partial_floats(m, d, h);
+    for (uint32_t rows = kRowPad; rows <= rows_padded(m); rows += kRowPad)
+        most = max(most, static_cast<size_t>(max(1u, dma_up_splits(rows, h, d))) * min(m, rows) * h);
+    return most;
+}
+
+Workspace workspace_layout(uint32_t m, uint32_t d, uint32_t h, bool training = false) {
     const size_t rows = rows_padded(m);
     Workspace w{};
     w.counters = 0;
@@ -1239,7 +1398,7 @@ Workspace workspace_layout(uint32_t m, uint32_t d, uint32_t h) {
     w.x_planes = (words_end + 255) / 256 * 256;  // bytes from here on
     w.act_planes = w.x_planes + rows * d * 4;
     w.partials = w.act_planes + rows * h * 4;
-    w.bytes = w.partials + partial_floats(m, d, h) * 4;
+    w.bytes = w.partials + (training ? train_partial_floats(m, d, h) : partial_floats(m, d, h)) * 4;
     return w;
 }
 
@@ -1307,10 +1466,10 @@ size_t mfma_workspace_bytes(uint32_t n, uint32_t d, uint32_t h) { return workspa
 hipError_t launch_densify(int vt, const int32_t* off, const int16_t* idx, const void* val, uint32_t rows, uint32_t k,
                           void* planes, int32_t* exps, hipStream_t stream) {
     if (vt == kBF16)
-        hipLaunchKernelGGL((densify_kernel<uint16_t>), dim3(rows), dim3(kThreads), 0, stream, off, idx,
+        hipLaunchKernelGGL((densify_kernel<uint16_t>), dim3(ceil_div(rows, kDensRows), ceil_div(k, kDensChunk)), dim3(kDensThreads), 0, stream, off, idx,
                            static_cast<const uint16_t*>(val), rows, k, static_cast<_Float16*>(planes), exps);
     else
-        hipLaunchKernelGGL((densify_kernel<float>), dim3(rows), dim3(kThreads), 0, stream, off, idx,
+        hipLaunchKernelGGL((densify_kernel<float>), dim3(ceil_div(rows, kDensRows), ceil_div(k, kDensChunk)), dim3(kDensThreads), 0, stream, off, idx,
                            static_cast<const float*>(val), rows, k, static_cast<_Float16*>(planes), exps);
     return hipGetLastError();
 }
@@ -1372,6 +1531,62 @@ hipError_t launch_mfma_down(int vt, const void* planes, const int32_t* v_exp, co
                                       words + w.counters, n, d, h, stream);
     return gemm<Epi::Down, true>(shape, act_planes, words + w.act_binades, p, v_exp, b_down, y, nullptr, nullptr, partials,
                                  words + w.counters, n, d, h, stream);
+}
+
+size_t train_mfma_workspace_bytes(uint32_t n, uint32_t d, uint32_t h) { return workspace_layout(n, d, h, true).bytes; }
+
+// Training forward on the planes (fp32 weights): x split into planes, the up projection as a split product (partials
+// at every split count) whose epilogue (train_planes_kernel<Forward>) writes z, act (hidden-major) and the activation
+// planes, then the inference down GEMM: y. x_t = x transposed for the sampled product of g_up. The workspace is laid
+// out as the MFMA workspace with the training partials (train_mfma_workspace_bytes).
+hipError_t launch_train_forward(const float* x, const void* up_planes, const int32_t* up_exp, const float* b_up, const void* down_planes,
+                                const int32_t* down_exp, const float* b_down, void* workspace, float* x_t, float* act, float* z, float* y,
+                                uint32_t n, uint32_t d, uint32_t h, uint32_t ld, hipStream_t stream) {
+    const Workspace w = workspace_layout(n, d, h, true);
+    int32_t* words = static_cast<int32_t*>(workspace);
+    char* bytes = static_cast<char*>(workspace);
+    auto* x_planes = reinterpret_cast<_Float16*>(bytes + w.x_planes);
+    auto* act_planes = reinterpret_cast<_Float16*>(bytes + w.act_planes);
+    float* partials = reinterpret_cast<float*>(bytes + w.partials);
+    if (hipError_t status = launch_transpose(x, x_t, n, d, d, ld, stream); status != hipSuccess) return status;
+    hipLaunchKernelGGL(split_rows_kernel, dim3(rows_live(n) / kSplitBlockRows), dim3(kThreads), 0, stream, x, n, rows_padded(n), d, d,
+                       d, x_planes, words + w.x_binades);
+    if (hipError_t status = hipGetLastError(); status != hipSuccess) return status;
+    const uint32_t splits = max(1u, dma_up_splits(n, h, d));
+    if (hipError_t status = launch_dma<Epi::UpSplit, true>(x_planes, words + w.x_binades, static_cast<const _Float16*>(up_planes), up_exp,
+                                                           nullptr, partials, nullptr, nullptr, n, h, d, splits, stream);
+        status != hipSuccess)
+        return status;
+    hipLaunchKernelGGL(train_planes_kernel<TrainPost::Forward>, dim3(rows_live(n) / kActRowsPerBlock, h / kActBlock), dim3(kThreads), 0,
+                       stream, partials, splits, b_up, nullptr, z, act, act_planes, words + w.act_binades, n, rows_padded(n), h, ld);
+    if (hipError_t status = hipGetLastError(); status != hipSuccess) return status;
+    return launch_mfma_down(kF32, down_planes, down_exp, b_down, y, workspace, n, d, h, stream);
+}
+
+// Training backward products on the planes: gy split into planes; gz = (gy W_down) * gelu'(z) as a split product over
+// the planes of W_down^T [d_ff rows, d_model k] whose epilogue (train_planes_kernel<GradZ>) writes gz hidden-major and
+// as planes; gx = gz W_up by the down GEMM over the planes of W_up^T [d_model rows, d_ff k], without bias.
+hipError_t launch_train_backward(const float* gy, const float* z, const void* down_t_planes, const int32_t* down_t_exp,
+                                 const void* up_t_planes, const int32_t* up_t_exp, void* workspace, float* gz, float* gx, uint32_t n,
+                                 uint32_t d, uint32_t h, uint32_t ld, hipStream_t stream) {
+    const Workspace w = workspace_layout(n, d, h, true);
+    int32_t* words = static_cast<int32_t*>(workspace);
+    char* bytes = static_cast<char*>(workspace);
+    auto* gy_planes = reinterpret_cast<_Float16*>(bytes + w.x_planes);
+    auto* gz_planes = reinterpret_cast<_Float16*>(bytes + w.act_planes);
+    float* partials = reinterpret_cast<float*>(bytes + w.partials);
+    hipLaunchKernelGGL(split_rows_kernel, dim3(rows_live(n) / kSplitBlockRows), dim3(kThreads), 0, stream, gy, n, rows_padded(n), d, d,
+                       d, gy_planes, words + w.x_binades);
+    if (hipError_t status = hipGetLastError(); status != hipSuccess) return status;
+    const uint32_t splits = max(1u, dma_up_splits(n, h, d));
+    if (hipError_t status = launch_dma<Epi::UpSplit, true>(gy_planes, words + w.x_binades, static_cast<const _Float16*>(down_t_planes),
+                                                           down_t_exp, nullptr, partials, nullptr, nullptr, n, h, d, splits, stream);
+        status != hipSuccess)
+        return status;
+    hipLaunchKernelGGL(train_planes_kernel<TrainPost::GradZ>, dim3(rows_live(n) / kActRowsPerBlock, h / kActBlock), dim3(kThreads), 0,
+                       stream, partials, splits, nullptr, z, gz, nullptr, gz_planes, words + w.act_binades, n, rows_padded(n), h, ld);
+    if (hipError_t status = hipGetLastError(); status != hipSuccess) return status;
+    return launch_mfma_down(kF32, up_t_planes, up_t_exp, nullptr, gx, workspace, n, d, h, stream);
 }
 
 }  // namespace hffn

@@ -100,6 +100,8 @@ class PreparedRuntime(HFFNRuntime):
             if up == "gemv" and index in self._stale:  # a training update changed the values: rebuild the planes first
                 self._densify(self._tensors[index], self._planes[index])
                 self._stale.discard(index)
+            if up == "tiles":  # likewise the tiled stores
+                self._fresh_tiles(index)
         stream = self._stream_of(self.device.index) if self._stream_of else torch.cuda.current_stream(self.device).cuda_stream
         _lib.check(self._lib.hffn_plan_launch(handle, x.data_ptr(), stream), f"forward ({up}, {down})")
         self.calls[up, down] += 1

@@ -261,6 +261,7 @@ class HFFNRuntime:
         self.density = self._slots / (2 * self.d_model * self.d_ff)
         self._planes: list[dict] | None = None
         self._stale: set[int] = set()   # layers whose values changed since their planes were built
+        self._tiles_stale: set[int] = set()  # ... since their tiled stores were built
         self._tiles: list[dict] | None = None
         self._tiles_work = torch.empty(1, device=self.device)
         if self._tiles_eligible():
@@ -351,12 +352,17 @@ class HFFNRuntime:
         return planes
 
     def invalidate_planes(self, index: int) -> None:
-        """The compact values of layer ``index`` changed in place (a training update): its densified planes are rebuilt
-        before the MFMA path next reads them, and the per-chunk powers of two of its tiles index now."""
+        """The compact values of layer ``index`` changed in place (a training update): its densified planes and its tiled
+        stores are rebuilt, in place, before a call next reads them (a training loop rebuilds nothing it does not read)."""
         if self._planes is not None:
             self._stale.add(index)
         if self._tiles is not None:
+            self._tiles_stale.add(index)
+
+    def _fresh_tiles(self, index: int) -> None:
+        if index in self._tiles_stale:
             self._tiles_build(self._tensors[index], self._tiles[index])
+            self._tiles_stale.discard(index)
 
     @property
     def mfma_available(self) -> bool:
@@ -459,6 +465,7 @@ class HFFNRuntime:
             if n > TILES_MAX_TOKENS:
                 raise ValueError(f"the tiles path takes at most {TILES_MAX_TOKENS} tokens, not {n}")
             x = _aligned(x)  # read 16 bytes at a time
+            self._fresh_tiles(index)
             _lib.check(self._lib.hffn_forward_tiles(value_type, x.data_ptr(), *self._tiles_args(index), self.d_model, self.d_ff,
                                                     *self._nnz[index], n, stream), "forward (tiles, tiles)")
             return

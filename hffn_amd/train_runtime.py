@@ -22,6 +22,9 @@ and ``g_up``/``gb_up`` as gathers over 256-token tiles (``hffn_grad_sddmm``, til
 ``hffn_reduce_tiles``) or, from ``GRAD_DENSE_MIN_TOKENS`` tokens on dense enough layers, as split-fp16 MFMA products
 sampled at the support (``hffn_grad_dense``); ``gz`` by ``hffn_grad_hidden``; ``gx`` by ``hffn_grad_x``; AdamW per
 array by ``hffn_adamw``. After an update the runtime's densified planes of that layer are rebuilt before their next use.
+On layers whose runtime holds densified planes, from ``TRAIN_MFMA_MIN_TOKENS`` tokens (``train_mode``), the forward
+with z (``hffn_forward_mfma_z``) and gz, gx (``hffn_backward_mfma``) run as split-fp16 MFMA products instead, the
+backward over planes of W_down^T and W_up^T densified at every backward from the values in the transposed orders.
 """
 from __future__ import annotations
 
@@ -33,7 +36,7 @@ from dataclasses import dataclass
 import torch
 
 from . import _lib
-from .runtime import MAX_TOKENS, PAIR_MODES, HFFNRuntime, down_mode, edges_supported, leading_dim, up_mode
+from .runtime import MAX_TOKENS, PAIR_MODES, HFFNRuntime, _aligned, down_mode, edges_supported, leading_dim, mfma_streamed, up_mode
 
 PARAMETERS = ("up_val", "b_up", "out_val", "b_down")
 SUPPORTS = ("in_offsets", "in_pos", "in_hidden", "hid_offsets", "hid_pos", "hid_output")
@@ -42,6 +45,8 @@ PARTIAL_MAX_TOKENS = 2048    # tokens the tile partials are sized for at constru
 GRAD_DENSE_MIN_TOKENS = 64   # from this N the sampled products may run as dense MFMA products
 GRAD_DENSE_MIN_DENSITY = 0.05  # on layers of at least this support density (the products' dense work over the useful)
 GRAD_MODES = ("gather", "dense")
+TRAIN_MFMA_MIN_TOKENS = 64   # from this N the forward with z, gz and gx may run on the planes
+TRAIN_MODES = ("gather", "mfma")
 
 
 def grad_tiles(n: int) -> int:
@@ -80,6 +85,7 @@ class _LayerState:
     supports: dict
     values: dict          # in_val, hid_val: the compact values in the transposed orders
     columns: tuple        # g_down [0, c1), gb_down [c1, c2), g_up [c2, c3), gb_up [c3, width) of the partials
+    planes_t: dict | None = None  # planes of W_down^T and W_up^T (the MFMA backward), allocated by reserve
 
 
 class HFFNTrainRuntime:
@@ -95,6 +101,8 @@ class HFFNTrainRuntime:
         self.steps = [0] * len(self._layers)   # AdamW steps taken per layer
         self.calls: Counter = Counter()        # (up, down) of the forwards that kept z
         self.forced_grad: str | None = None    # diagnostic: the sampled products' formulation, else the policy's
+        self.forced_train: str | None = None   # diagnostic: the forward with z, gz and gx on gathers or planes
+        self._mfma_work: torch.Tensor | None = None
         self._tokens = 0                        # N the dense buffers hold
         self._tiles = 1                         # token tiles the partials hold (none allocated for 1)
         self._partials: torch.Tensor | None = None
@@ -146,6 +154,28 @@ class HFFNTrainRuntime:
             self.growths += 1
         self._grow_partials(n)
         self._grow_dense(n)
+        self._grow_mfma(n)
+
+    def _mfma_possible(self, n: int) -> bool:
+        return self.runtime.mfma_available and mfma_streamed(n, self.d_model, self.d_ff)
+
+    def _grow_mfma(self, n: int) -> None:
+        """The MFMA workspace at N and every layer's transposed planes, when the planes products may run at N."""
+        if not self._mfma_possible(n):
+            return
+        need = _lib.query_bytes(self._lib.hffn_train_mfma_workspace, n, self.d_model, self.d_ff)
+        if self._mfma_work is None or need > self._mfma_work.numel():
+            self._mfma_work = torch.zeros(need, dtype=torch.uint8, device=self.runtime.device)
+            self.growths += 1
+        for state in self._layers:
+            if state.planes_t is None:
+                device, planes = self.runtime.device, {}
+                for side, rows, k in (("down_t", self.d_ff, self.d_model), ("up_t", self.d_model, self.d_ff)):
+                    size = _lib.query_bytes(self._lib.hffn_dense_planes_bytes, rows, k)
+                    planes[side] = torch.empty(size // 2, dtype=torch.float16, device=device)
+                    planes[f"{side}_binades"] = torch.empty(rows, dtype=torch.int32, device=device)
+                state.planes_t = planes
+                self.growths += 1
 
     def _grow_partials(self, n: int) -> None:
         tiles = grad_tiles(n)
@@ -189,6 +219,29 @@ class HFFNTrainRuntime:
         dense = n >= GRAD_DENSE_MIN_TOKENS and self.runtime.density >= GRAD_DENSE_MIN_DENSITY and self._dense_bytes_at(n) > 0
         return "dense" if dense else "gather"
 
+    def train_mode(self, n: int) -> str:
+        """``mfma`` (the forward with z, gz and gx as split-fp16 MFMA products over densified planes) from
+        ``TRAIN_MFMA_MIN_TOKENS`` tokens when the runtime holds planes, runs its policy (no forced pair) and the streamed
+        GEMM takes N, else ``gather``; ``forced_train`` overrides the choice."""
+        possible = self._mfma_possible(n)
+        if self.forced_train is not None:
+            if self.forced_train not in TRAIN_MODES:
+                raise ValueError(f"training mode is one of {TRAIN_MODES}, not {self.forced_train!r}")
+            if self.forced_train == "mfma" and not possible:
+                raise ValueError(f"the planes products do not run at N={n} on {self.d_model} x {self.d_ff} (no planes, or "
+                                 "a shape the streamed GEMM refuses)")
+            return self.forced_train
+        policy = self.runtime.forced_up is None and self.runtime.forced_down is None
+        return "mfma" if possible and policy and n >= TRAIN_MFMA_MIN_TOKENS else "gather"
+
+    def _runtime_planes(self, index: int) -> dict:
+        """The runtime's planes of layer ``index``, rebuilt first if an update made them stale."""
+        runtime = self.runtime
+        if index in runtime._stale:
+            runtime._densify(runtime._tensors[index], runtime._planes[index])
+            runtime._stale.discard(index)
+        return runtime._planes[index]
+
     def _tokens_of(self, t: torch.Tensor, name: str) -> int:
         if not (t.dim() == 2 and t.shape[1] == self.d_model and t.dtype == torch.float32 and t.device == self.runtime._y.device
                 and t.is_contiguous()):
@@ -222,13 +275,23 @@ class HFFNTrainRuntime:
         if not (z.dtype == torch.float32 and z.device == runtime._y.device and z.is_contiguous() and z.numel() >= self.d_ff * ld):
             raise ValueError(f"z must be a contiguous float32 device tensor of at least {self.d_ff * ld} entries")
         self.reserve(n)
-        up, down = self.modes(n)
-        _, *model = runtime._args[index]
         x_t, act, y_t, y = runtime._work
-        _lib.check(self._lib.hffn_forward_z(_lib.UP_MODES[up], _lib.DOWN_MODES[down], x.data_ptr(), *model, x_t, act, y_t, y,
-                                            z.data_ptr(), self.d_model, self.d_ff, *runtime._nnz[index], n, ld,
-                                            _stream(runtime.device)), f"forward with z ({up}, {down})")
-        self.calls[up, down] += 1
+        if self.train_mode(n) == "mfma":
+            planes, tensors, x = self._runtime_planes(index), runtime._tensors[index], _aligned(x)
+            _lib.check(self._lib.hffn_forward_mfma_z(x.data_ptr(), planes["up"].data_ptr(), planes["up_binades"].data_ptr(),
+                                                     tensors["b_up"].data_ptr(), planes["down"].data_ptr(),
+                                                     planes["down_binades"].data_ptr(), tensors["b_down"].data_ptr(),
+                                                     self._mfma_work.data_ptr(), self._mfma_work.numel(), x_t, act, z.data_ptr(),
+                                                     y, self.d_model, self.d_ff, n, ld, _stream(runtime.device)),
+                       "forward with z (mfma)")
+            self.calls["mfma", "mfma"] += 1
+        else:
+            up, down = self.modes(n)
+            _, *model = runtime._args[index]
+            _lib.check(self._lib.hffn_forward_z(_lib.UP_MODES[up], _lib.DOWN_MODES[down], x.data_ptr(), *model, x_t, act, y_t, y,
+                                                z.data_ptr(), self.d_model, self.d_ff, *runtime._nnz[index], n, ld,
+                                                _stream(runtime.device)), f"forward with z ({up}, {down})")
+            self.calls[up, down] += 1
         self._last_forward = (index, n, z.data_ptr(), sum(runtime.calls.values()))
         return runtime._y[:n]
 
@@ -251,6 +314,21 @@ class HFFNTrainRuntime:
         for source, position, target in (("out_val", "hid_pos", "hid_val"), ("up_val", "in_pos", "in_val")):
             _lib.check(lib.hffn_gather_values(arrays[source].data_ptr(), supports[position].data_ptr(), values[target].data_ptr(),
                                               values[target].numel(), stream), f"{target} refresh")
+        planes_mode = self.train_mode(n) == "mfma"
+        if planes_mode:  # gz and gx on the planes of W_down^T and W_up^T, densified from the values just gathered
+            planes_t = state.planes_t
+            for side, rows, k, (offsets, owner, vals) in (("down_t", h, d, ("hid_offsets", "hid_output", "hid_val")),
+                                                          ("up_t", d, h, ("in_offsets", "in_hidden", "in_val"))):
+                source = values[vals]
+                _lib.check(lib.hffn_densify(_lib.VALUE_F32, supports[offsets].data_ptr(), supports[owner].data_ptr(),
+                                            source.data_ptr(), rows, k, planes_t[side].data_ptr(),
+                                            planes_t[f"{side}_binades"].data_ptr(), stream), f"densify {side}")
+            gy_in = _aligned(gy)
+            _lib.check(lib.hffn_backward_mfma(gy_in.data_ptr(), z_ptr, planes_t["down_t"].data_ptr(),
+                                              planes_t["down_t_binades"].data_ptr(), planes_t["up_t"].data_ptr(),
+                                              planes_t["up_t_binades"].data_ptr(), self._mfma_work.data_ptr(),
+                                              self._mfma_work.numel(), self._gz.data_ptr(), self._gx.data_ptr(), d, h, n, ld, stream),
+                       "gz, gx (mfma)")
         dense = self.grad_mode(n) == "dense"
         if dense:
             self._grow_dense(n)
@@ -273,18 +351,20 @@ class HFFNTrainRuntime:
 
         sampled(self._gy_t.data_ptr(), act, arrays["out_offsets"].data_ptr(), arrays["out_hidden"].data_ptr(), into["g_down"],
                 into["gb_down"], d, h, "g_down")
-        _lib.check(lib.hffn_grad_hidden(gy.data_ptr(), self._gy_t.data_ptr(), z_ptr, supports["hid_offsets"].data_ptr(),
-                                        supports["hid_output"].data_ptr(), values["hid_val"].data_ptr(), self._gz.data_ptr(), d, h,
-                                        values["hid_val"].numel(), n, ld, stream), "gz")
+        if not planes_mode:
+            _lib.check(lib.hffn_grad_hidden(gy.data_ptr(), self._gy_t.data_ptr(), z_ptr, supports["hid_offsets"].data_ptr(),
+                                            supports["hid_output"].data_ptr(), values["hid_val"].data_ptr(), self._gz.data_ptr(), d, h,
+                                            values["hid_val"].numel(), n, ld, stream), "gz")
         sampled(self._gz.data_ptr(), x_t, arrays["up_offsets"].data_ptr(), arrays["up_idx"].data_ptr(), into["g_up"], into["gb_up"],
                 h, d, "g_up")
         if tiled:
             _lib.check(lib.hffn_reduce_tiles(self._partials.data_ptr(), width, grad_tiles(n), c1, c2, c3,
                                              grads["out_val"].data_ptr(), grads["b_down"].data_ptr(), grads["up_val"].data_ptr(),
                                              grads["b_up"].data_ptr(), stream), "tile partials")
-        _lib.check(lib.hffn_grad_x(self._gz.data_ptr(), supports["in_offsets"].data_ptr(), supports["in_hidden"].data_ptr(),
-                                   values["in_val"].data_ptr(), self._gx_t.data_ptr(), self._gx.data_ptr(), d, h,
-                                   values["in_val"].numel(), n, ld, stream), "gx")
+        if not planes_mode:
+            _lib.check(lib.hffn_grad_x(self._gz.data_ptr(), supports["in_offsets"].data_ptr(), supports["in_hidden"].data_ptr(),
+                                       values["in_val"].data_ptr(), self._gx_t.data_ptr(), self._gx.data_ptr(), d, h,
+                                       values["in_val"].numel(), n, ld, stream), "gx")
         return self._gx[:n]
 
     def adamw(self, index: int) -> None:
@@ -343,5 +423,7 @@ class HFFNTrainRuntime:
                 "indices": size(arrays[name] for name in ("up_offsets", "up_idx", "out_offsets", "out_hidden"))
                 + size(state.supports.values()) + size(state.values.values()),
                 "workspace": self.runtime.workspace_bytes() + size((self._z, self._gz, self._gy_t, self._gx_t, self._gx))
-                + (self._dense_work.numel() if self._dense_work is not None else 0),
+                + (self._dense_work.numel() if self._dense_work is not None else 0)
+                + (self._mfma_work.numel() if self._mfma_work is not None else 0),
+                "planes_t": size(state.planes_t.values()) if state.planes_t is not None else 0,
                 "partials": size((self._partials,)) if self._partials is not None else 0}

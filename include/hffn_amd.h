@@ -27,7 +27,7 @@
 extern "C" {
 #endif
 
-#define HFFN_ABI_VERSION 13
+#define HFFN_ABI_VERSION 14
 
 #define HFFN_OK 0
 #define HFFN_ERROR_ARGUMENT (-1) /* invalid shape, mode, pointer or workspace */
@@ -268,6 +268,25 @@ int hffn_forward_z(int up_mode, int down_mode, const float* x, const int32_t* up
 int hffn_grad_dense_workspace(uint32_t rows, uint32_t cols, uint32_t n, uint64_t* bytes);
 int hffn_grad_dense(const float* row, const float* mat, const int32_t* offsets, const int16_t* index, float* g, float* gb,
                     uint32_t rows, uint32_t cols, uint32_t n, uint32_t ld, void* workspace, uint64_t workspace_bytes, void* stream);
+
+/* The training step's dense products on the planes (fp32 values; layers whose planes the runtime holds), for the
+ * token counts the streamed GEMM takes (hffn_train_mfma_workspace refuses the others). hffn_forward_mfma_z: the forward
+ * with z of hffn_forward_z on the planes of W_up [d_ff, d_model] and W_down [d_model, d_ff] (hffn_densify):
+ * z = b_up + W_up x and act = gelu(z) hidden-major [d_ff, ld], x_t = x transposed, y = W_down act + b_down.
+ * hffn_backward_mfma: gz = (gy W_down) * gelu'(z) hidden-major and gx = gz W_up [n, d_model], on the planes of
+ * W_down^T [d_ff rows, d_model k] and W_up^T [d_model rows, d_ff k] (hffn_densify of the hidden-major down support and
+ * of the input-major up support, with the values gathered into those orders). Every product is split fp16 on MFMA
+ * (hi*hi + hi*lo + lo*hi, fp32 accumulation); every result is written by one lane. Float buffers 16-byte aligned, the
+ * workspace (hffn_train_mfma_workspace bytes) 256-byte aligned; it holds the token planes and split partials, and the
+ * calls that share it must be ordered. No reference counterpart: the reference's training kernels are gathers
+ * (kernels_train.py:101-231); these replace the forward with z, grad_hidden and grad_x at high density and many tokens. */
+int hffn_train_mfma_workspace(uint32_t n, uint32_t d_model, uint32_t d_ff, uint64_t* bytes);
+int hffn_forward_mfma_z(const float* x, const void* up_planes, const int32_t* up_binades, const float* b_up, const void* down_planes,
+                        const int32_t* down_binades, const float* b_down, void* workspace, uint64_t workspace_bytes, float* x_t,
+                        float* act, float* z, float* y, uint32_t d_model, uint32_t d_ff, uint32_t n, uint32_t ld, void* stream);
+int hffn_backward_mfma(const float* gy, const float* z, const void* down_t_planes, const int32_t* down_t_binades, const void* up_t_planes,
+                       const int32_t* up_t_binades, void* workspace, uint64_t workspace_bytes, float* gz, float* gx, uint32_t d_model,
+                       uint32_t d_ff, uint32_t n, uint32_t ld, void* stream);
 
 /* Sampled product over an owner-row support: for each owner o < rows, token tile k and slot q of o,
  * g[k*stride + q] = sum_t row[o, t] mat[index[q], t] and gb[k*stride + o] = sum_t row[o, t] (t over tile k, below n);

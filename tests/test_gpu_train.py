@@ -13,7 +13,9 @@ inference runtime reading the updated values.
 N covers one tile (1, 33, 100, 128), a one-token last tile (257), partial last tiles (300, 2100) and exact tiles (512).
 The sampled products run as gathers (``gather``) or as dense split-fp16 MFMA products sampled at the support
 (``dense``, the policy's choice from 64 tokens on the 512 x 2048 layers); cases force either where the policy would
-not take it, so both meet every gate.
+not take it, so both meet every gate. The forward with z, gz and gx run as gathers or on the planes (``mfma``, the
+policy's choice from 64 tokens where the streamed GEMM takes N); planes cases check gate 1 against the inference
+runtime's MFMA call (the same products: its bits).
 """
 from __future__ import annotations
 
@@ -35,9 +37,11 @@ HYPER = dict(lr=1e-3, betas=(0.9, 0.999), eps=1e-8, weight_decay=1e-2)
 GROUPS = ("y", "gb_down", "g_down", "gz", "g_up", "gb_up", "gx")
 GATE2_FACTOR, GATE2_FLOOR = 10.0, 1e-7
 GATE3_CONDITIONING, GATE3_RELATIVE = 100.0, 1e-5
-CASES = ([("homog_256_1024", n, None) for n in (1, 33, 100, 128, 257, 300, 512, 2100)]
-         + [("irreg_512_2048", 4, None), ("irreg_512_2048", 300, None), ("irreg_512_2048", 300, "gather"),
-            ("irreg_512_2048", 33, "dense"), ("homog_512_2048", 64, None), ("homog_512_2048", 2100, None)])
+CASES = ([("homog_256_1024", n, None, None) for n in (1, 33, 100, 128, 257, 300, 512, 2100)]
+         + [("homog_256_1024", 2100, None, "gather"), ("irreg_512_2048", 4, None, None), ("irreg_512_2048", 300, None, "gather"),
+            ("irreg_512_2048", 300, "gather", "gather"), ("irreg_512_2048", 33, "dense", "gather"), ("irreg_512_2048", 300, None, "mfma"),
+            ("irreg_512_2048", 33, None, "mfma"), ("homog_512_2048", 64, None, None), ("homog_512_2048", 2100, None, None),
+            ("homog_512_2048", 2100, "gather", "gather")])
 
 
 def make_gy(case, n: int, salt: int) -> torch.Tensor:
@@ -122,8 +126,8 @@ def _update_errors(pre: dict, post: dict, groups: dict, masks: dict, step: int) 
     return worst
 
 
-@pytest.mark.parametrize("name,n,grad", CASES)
-def test_training_gates(name, n, grad, device):
+@pytest.mark.parametrize("name,n,grad,mode", CASES)
+def test_training_gates(name, n, grad, mode, device):
     case = synth.CASES[name]
     layer = synth.make_layer(case)
     x = torch.from_numpy(synth.make_input(case, n)).to(device)
@@ -131,16 +135,26 @@ def test_training_gates(name, n, grad, device):
     baseline = HFFNRuntime([hip_layer(layer)], device, dense=True)
     train = HFFNTrainRuntime(HFFNRuntime([hip_layer(layer)], device, dense=True), **HYPER, max_tokens=max(n, 2048))
     train.forced_grad = grad
+    train.forced_train = mode
     if name.endswith("512_2048") and grad is None:
         assert train.grad_mode(n) == ("dense" if n >= 64 else "gather")
+    if name.endswith("512_2048") and mode is None:
+        assert train.train_mode(n) == ("mfma" if n >= 64 else "gather")
+    planes = train.train_mode(n) == "mfma"
     train.reserve(n)
-    # gate 1: the inference call is untouched; the forward with z has the bits of the same gather forward
-    for pair in ((None, None), ("edges", "edges"), ("rows", "rows"), ("edges", "rows"), ("rows", "edges")):
+    # gate 1: the inference call is untouched; the forward with z has the bits of the same gather forward, or on the
+    # planes those of the inference MFMA call
+    pairs = ((None, None),) if planes else ((None, None), ("edges", "edges"), ("rows", "rows"), ("edges", "rows"), ("rows", "edges"))
+    for pair in pairs:
         baseline.force(*pair)
         train.runtime.force(*pair)
         assert torch.equal(baseline.forward(0, x).clone(), train.forward(0, x).clone()), pair
         if pair != (None, None):
             assert torch.equal(train.forward(0, x, train._z).clone(), baseline.forward(0, x)), pair
+    if planes:
+        baseline.force("mfma", "mfma")
+        assert torch.equal(train.forward(0, x, train._z).clone(), baseline.forward(0, x))
+        assert train.calls["mfma", "mfma"] == 1
     baseline.force(None, None)
     train.runtime.force(None, None)
     train.reserve(n)
@@ -247,7 +261,8 @@ def test_transposed_supports_are_positions_into_the_runtime_arrays(device):
 
 
 def test_inference_after_training_reads_the_updated_values(device):
-    """After steps, the runtime's MFMA path (densified planes, rebuilt in place) agrees with its gather path."""
+    """After steps, the runtime's MFMA path (densified planes, rebuilt in place) and its tiles path (tiled stores, rebuilt
+    in place) agree with its gather path."""
     case = synth.Case("mfma_256_1024", 256, 1024, 128, 128, False, 1005)
     layer = synth.make_layer(case)
     runtime = HFFNRuntime([hip_layer(layer)], device, dense=True)
@@ -264,6 +279,13 @@ def test_inference_after_training_reads_the_updated_values(device):
     assert not torch.equal(runtime._planes[0]["up"], planes_before)
     runtime.force("rows", "rows")
     y_rows = runtime.forward(0, x).clone()
-    runtime.force(None, None)
     scale = float(y_rows.abs().max())
     assert float((y_mfma - y_rows).abs().max()) <= 1e-5 * max(1.0, scale)
+    # the tiled stores, rebuilt in place before the decode path next reads them, agree with the gathers too
+    few = x[:16].contiguous()
+    y_few = runtime.forward(0, few).clone()
+    runtime.force("tiles", "tiles")
+    y_tiles = runtime.forward(0, few).clone()
+    assert runtime.calls["tiles", "tiles"] == 1 and not runtime._tiles_stale
+    runtime.force(None, None)
+    assert float((y_tiles - y_few).abs().max()) <= 1e-5 * max(1.0, float(y_few.abs().max()))

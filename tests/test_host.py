@@ -182,6 +182,36 @@ def test_tiles_estimate():
         assert abs(runtime.tiles_us(n, slots) / us - 1) < 0.2, (slots, n)
 
 
+@pytest.mark.skipif(torch.cuda.is_available(), reason="uses placeholder pointers: never run where a launch could reach a GPU")
+def test_training_planes_entries_refuse_bad_arguments():
+    """The planes training products: sized only where the streamed GEMM takes N; the forward with z and the backward
+    refuse a small or misaligned workspace, a bad ld and misaligned or null buffers before any launch."""
+    lib = _lib.load()
+    p, odd = ctypes.c_void_p(256), ctypes.c_void_p(264)
+    need = ctypes.c_uint64(0)
+    assert lib.hffn_train_mfma_workspace(512, 1024, 4096, ctypes.byref(need)) == _lib.OK
+    mfma = ctypes.c_uint64(0)
+    assert lib.hffn_mfma_workspace(512, 1024, 4096, ctypes.byref(mfma)) == _lib.OK
+    assert need.value >= mfma.value  # the same layout with partials at every split count
+    _expect_argument_error(lib.hffn_train_mfma_workspace(1, 256, 1024, ctypes.byref(need)), "streamed GEMM")
+    _expect_argument_error(lib.hffn_train_mfma_workspace(512, 1040, 4096, ctypes.byref(need)), "multiples of 256")
+    assert lib.hffn_train_mfma_workspace(512, 1024, 4096, ctypes.byref(need)) == _lib.OK
+    ws = need.value
+    fwd = lambda x, work, size, ld: lib.hffn_forward_mfma_z(x, p, p, p, p, p, p, work, size, p, p, p, p,  # noqa: E731
+                                                            1024, 4096, 512, ld, None)
+    _expect_argument_error(fwd(p, p, ws - 1, 512), "workspace")
+    _expect_argument_error(fwd(p, odd, ws, 512), "256-byte aligned")
+    _expect_argument_error(fwd(odd, p, ws, 512), "16-byte aligned")
+    _expect_argument_error(fwd(None, p, ws, 512), "16-byte aligned")
+    _expect_argument_error(fwd(p, p, ws, 510), "ld=510")
+    _expect_argument_error(fwd(p, p, ws, 514), "ld=514")
+    bwd = lambda gy, binades, size: lib.hffn_backward_mfma(gy, p, p, binades, p, p, p, size, p, p, 1024, 4096, 512, 512,  # noqa: E731
+                                                           None)
+    _expect_argument_error(bwd(p, p, ws - 1), "workspace")
+    _expect_argument_error(bwd(odd, p, ws), "16-byte aligned")
+    _expect_argument_error(bwd(p, None, ws), "null pointer")
+
+
 def test_mfma_streamed_query():
     """Both projections stream for the model shapes at every token count; a 256 x 1024 layer's up projection has too
     few 128-column tiles below 512 tokens and falls back to the register-staged GEMM."""
