@@ -168,82 +168,97 @@ __global__ __launch_bounds__(kThreads) void split_rows_kernel(const float* __res
 // Row n of the dense matrix (a neuron of W_up, or an output of W_down^T) has its slots [off[n], off[n+1]) at columns
 // idx[] (distinct within a row; the host checks it); densifying writes the whole row of both planes (zeros outside
 // the support) and its binade. A block takes kDensRows consecutive rows and kDensChunk columns (blockIdx.y): the rows'
-// maxima (a wave per row, over all their slots), then their hi/lo parts in its columns assembled in LDS (zeroed, then
-// each slot of the chunk in its column) and written out whole: for every 16-byte chunk run the block's rows are
+// maxima (two waves per row, over all their slots), then their hi/lo parts in its columns assembled in LDS (zeroed
+// meanwhile, then each slot of the chunk in its column) and written out whole: for every 16-byte chunk run the block's rows are
 // kDensRows consecutive 16-byte pieces, one 128-byte line per (run, row group). The rows are padded by 16 bytes in
 // LDS so that the eight rows of a chunk fall in different banks; the tile (66 KB) leaves room for two blocks per CU.
-constexpr uint32_t kDensRows = 8, kDensChunk = 2048, kDensThreads = 512, kDensPad = 8;
+constexpr uint32_t kDensRows = 8, kDensChunk = 2048, kDensThreads = 1024, kDensPad = 8;
 template <typename V>
 __global__ __launch_bounds__(kDensThreads) void densify_kernel(const int32_t* __restrict__ off, const int16_t* __restrict__ idx,
                                                               const V* __restrict__ val, uint32_t rows, uint32_t k,
                                                               _Float16* __restrict__ planes, int32_t* __restrict__ exps) {
+    const auto value = [&](int32_t s) { return widen(val[s]); };
     static_assert(kDensRows * 16 == 128, "a row group's pieces of one chunk run fill one 128-byte line");
     __shared__ __attribute__((aligned(16))) _Float16 tile[2][kDensRows][kDensChunk + kDensPad];
-    __shared__ int32_t row_exp[kDensRows];
+    __shared__ uint32_t row_max[2][kDensRows];
     constexpr uint32_t kWaves = kDensThreads / kWave;
+    static_assert(kWaves == 2 * kDensRows, "two waves per row");
     const uint32_t tid = threadIdx.x, lane = tid % kWave, wave = uniform(tid / kWave);
-    const uint32_t r0 = blockIdx.x * kDensRows;
-    // (the slot loops keep kBatch loads per lane in flight before using any)
-    constexpr int kBatch = 16;
-    for (uint32_t rr = wave; rr < kDensRows; rr += kWaves) {
-        const uint32_t n = r0 + rr;
-        uint32_t m = 0;
-        if (n < rows) {
-            const int32_t end = off[n + 1];
-            for (int32_t s0 = off[n] + static_cast<int32_t>(lane); s0 < end; s0 += kBatch * kWave) {
-                float w[kBatch];
+    const uint32_t row = wave % kDensRows, half = wave / kDensRows;  // wave-uniform
+    const uint32_t r0 = blockIdx.x * kDensRows, n = r0 + row;
+    const uint32_t c0 = blockIdx.y * kDensChunk;
+    const uint32_t width = min(kDensChunk, k - c0), pieces = width / 8;  // width: a multiple of 32
+    // the block's tile zeroed while the slots are in flight
+    for (uint32_t i = tid; i < 2 * kDensRows * pieces; i += kDensThreads) {
+        const uint32_t part = i / (kDensRows * pieces), rr = (i / pieces) % kDensRows, j = i % pieces;
+        *reinterpret_cast<uint4*>(&tile[part][rr][j * 8]) = make_uint4(0, 0, 0, 0);
+    }
+    // Waves w and w + kDensRows take row r0 + w, slots interleaved by 64 (lane l of half h: begin + 64 h + l + 128 q).
+    // A row of at most kHeld slots per lane is read once, into registers, for both its maximum and its scatter; a
+    // longer row is read twice, kBatch slots per lane in flight. The two halves' maxima meet in LDS.
+    constexpr int kHeld = 16, kBatch = 16, kStride = 2 * kWave;
+    const int32_t begin = n < rows ? off[n] : 0, end = n < rows ? off[n + 1] : 0;
+    const int32_t first = begin + static_cast<int32_t>(half * kWave + lane);
+    const bool held = end - begin <= kHeld * kStride;  // wave-uniform
+    uint32_t hc[kHeld];
+    float hw[kHeld];
+    uint32_t m = 0;
+    if (held) {
 #pragma unroll
-                for (int q = 0; q < kBatch; ++q) w[q] = s0 + q * kWave < end ? widen(val[s0 + q * kWave]) : 0.0f;
-#pragma unroll
-                for (int q = 0; q < kBatch; ++q) m = max(m, abs_bits(w[q]));
-            }
+        for (int q = 0; q < kHeld; ++q) {
+            const int32_t s = first + q * kStride;
+            const bool in = s < end;
+            hc[q] = in ? static_cast<uint16_t>(idx[s]) : 0xFFFFFFFFu;
+            hw[q] = in ? value(s) : 0.0f;
         }
 #pragma unroll
-        for (int o = 32; o >= 1; o >>= 1) m = max(m, static_cast<uint32_t>(__shfl_xor(static_cast<int>(m), o, kWave)));
-        if (lane == 0) row_exp[rr] = binade_of_bits(m);
+        for (int q = 0; q < kHeld; ++q) m = max(m, abs_bits(hw[q]));
+    } else {
+        for (int32_t s0 = first; s0 < end; s0 += kBatch * kStride) {
+            float w[kBatch];
+#pragma unroll
+            for (int q = 0; q < kBatch; ++q) w[q] = s0 + q * kStride < end ? value(s0 + q * kStride) : 0.0f;
+#pragma unroll
+            for (int q = 0; q < kBatch; ++q) m = max(m, abs_bits(w[q]));
+        }
+    }
+#pragma unroll
+    for (int o = 32; o >= 1; o >>= 1) m = max(m, static_cast<uint32_t>(__shfl_xor(static_cast<int>(m), o, kWave)));
+    if (lane == 0) row_max[half][row] = m;
+    __syncthreads();  // the tile is zeroed, the halves' maxima are in
+    const int e = binade_of_bits(max(row_max[0][row], row_max[1][row]));
+    const auto place = [&](uint32_t c, float w) {
+        if (c < c0 || c >= c0 + width) return;  // another column block's slot, or past the row
+        _Float16 hi, lo;
+        split(ldexpf(w, -e), hi, lo);
+        tile[0][row][c - c0] = hi;
+        tile[1][row][c - c0] = lo;
+    };
+    if (held) {
+#pragma unroll
+        for (int q = 0; q < kHeld; ++q) place(hc[q], hw[q]);
+    } else {
+        for (int32_t s0 = first; s0 < end; s0 += kBatch * kStride) {
+            uint32_t c[kBatch];
+            float w[kBatch];
+#pragma unroll
+            for (int q = 0; q < kBatch; ++q) {
+                const bool in = s0 + q * kStride < end;
+                c[q] = in ? static_cast<uint16_t>(idx[s0 + q * kStride]) : 0xFFFFFFFFu;
+                w[q] = in ? value(s0 + q * kStride) : 0.0f;
+            }
+#pragma unroll
+            for (int q = 0; q < kBatch; ++q) place(c[q], w[q]);
+        }
     }
     __syncthreads();
-    {
-        const uint32_t c0 = blockIdx.y * kDensChunk;
-        const uint32_t width = min(kDensChunk, k - c0), pieces = width / 8;  // width: a multiple of 32
-        for (uint32_t i = tid; i < 2 * kDensRows * pieces; i += kDensThreads) {
-            const uint32_t part = i / (kDensRows * pieces), rr = (i / pieces) % kDensRows, j = i % pieces;
-            *reinterpret_cast<uint4*>(&tile[part][rr][j * 8]) = make_uint4(0, 0, 0, 0);
-        }
-        __syncthreads();
-        for (uint32_t rr = wave; rr < kDensRows; rr += kWaves) {
-            const uint32_t n = r0 + rr;
-            if (n >= rows) continue;
-            const int e = row_exp[rr];
-            const int32_t end = off[n + 1];
-            for (int32_t s0 = off[n] + static_cast<int32_t>(lane); s0 < end; s0 += kBatch * kWave) {
-                uint32_t c[kBatch];
-                float w[kBatch];
-#pragma unroll
-                for (int q = 0; q < kBatch; ++q) {
-                    const bool in = s0 + q * kWave < end;
-                    c[q] = in ? static_cast<uint16_t>(idx[s0 + q * kWave]) : 0xFFFFFFFFu;
-                    w[q] = in ? widen(val[s0 + q * kWave]) : 0.0f;
-                }
-#pragma unroll
-                for (int q = 0; q < kBatch; ++q) {
-                    if (c[q] < c0 || c[q] >= c0 + width) continue;  // another column pass's slot, or past the row
-                    _Float16 hi, lo;
-                    split(ldexpf(w[q], -e), hi, lo);
-                    tile[0][rr][c[q] - c0] = hi;
-                    tile[1][rr][c[q] - c0] = lo;
-                }
-            }
-        }
-        __syncthreads();
-        for (uint32_t i = tid; i < 2 * pieces * kDensRows; i += kDensThreads) {
-            const uint32_t rr = i % kDensRows, j = (i / kDensRows) % pieces, part = i / (kDensRows * pieces);
-            if (r0 + rr < rows)
-                *reinterpret_cast<uint4*>(planes + plane_at(rows, r0 + rr, c0 + j * 8, part)) =
-                    *reinterpret_cast<const uint4*>(&tile[part][rr][j * 8]);
-        }
+    for (uint32_t i = tid; i < 2 * pieces * kDensRows; i += kDensThreads) {
+        const uint32_t rr = i % kDensRows, j = (i / kDensRows) % pieces, part = i / (kDensRows * pieces);
+        if (r0 + rr < rows)
+            *reinterpret_cast<uint4*>(planes + plane_at(rows, r0 + rr, c0 + j * 8, part)) =
+                *reinterpret_cast<const uint4*>(&tile[part][rr][j * 8]);
     }
-    if (blockIdx.y == 0 && tid < kDensRows && r0 + tid < rows) exps[r0 + tid] = row_exp[tid];
+    if (blockIdx.y == 0 && half == 0 && lane == 0 && n < rows) exps[n] = e;
 }
 
 // ------------------------------------------------------------------------------------------------ GEMM
@@ -1307,18 +1322,37 @@ __global__ __launch_bounds__(kThreads) void gather_dense_kernel(const float* __r
                                                                uint32_t cols) {
     const uint32_t o = blockIdx.x * (kThreads / kWave) + uniform(threadIdx.x / kWave), lane = threadIdx.x % kWave;
     if (o >= rows) return;
+    // (kBatch loads per lane in flight; each lane's sums in the order of its tokens and splits)
+    constexpr int kBatch = 16;
     float s = 0.0f;
-    for (uint32_t t = lane; t < n; t += kWave) s += a[static_cast<size_t>(o) * ld + t];
+    const float* arow = a + static_cast<size_t>(o) * ld;
+    for (uint32_t t0 = lane; t0 < n; t0 += kBatch * kWave) {
+        float v[kBatch];
+#pragma unroll
+        for (int j = 0; j < kBatch; ++j) v[j] = t0 + j * kWave < n ? arow[t0 + j * kWave] : 0.0f;
+#pragma unroll
+        for (int j = 0; j < kBatch; ++j)
+            if (t0 + j * kWave < n) s += v[j];
+    }
     s = wave_sum(s);
     if (lane == 0) gb[o] = s;
     const size_t plane = static_cast<size_t>(rows) * cols;
     const float* row = partials + static_cast<size_t>(o) * cols;
     const int32_t end = off[o + 1];
-    for (int32_t q = off[o] + static_cast<int32_t>(lane); q < end; q += kWave) {
-        const uint32_t c = static_cast<uint16_t>(idx[q]);
-        float v = row[c];
-        for (uint32_t sp = 1; sp < splits; ++sp) v += row[sp * plane + c];
-        g[q] = v;
+    for (int32_t q0 = off[o] + static_cast<int32_t>(lane); q0 < end; q0 += kBatch * kWave) {
+        uint32_t c[kBatch];
+        float v[kBatch];
+#pragma unroll
+        for (int j = 0; j < kBatch; ++j) c[j] = q0 + j * kWave < end ? static_cast<uint16_t>(idx[q0 + j * kWave]) : 0u;
+#pragma unroll
+        for (int j = 0; j < kBatch; ++j) v[j] = q0 + j * kWave < end ? row[c[j]] : 0.0f;
+        for (uint32_t sp = 1; sp < splits; ++sp)
+#pragma unroll
+            for (int j = 0; j < kBatch; ++j)
+                if (q0 + j * kWave < end) v[j] += row[sp * plane + c[j]];
+#pragma unroll
+        for (int j = 0; j < kBatch; ++j)
+            if (q0 + j * kWave < end) g[q0 + j * kWave] = v[j];
     }
 }
 
@@ -1465,12 +1499,13 @@ size_t mfma_workspace_bytes(uint32_t n, uint32_t d, uint32_t h) { return workspa
 
 hipError_t launch_densify(int vt, const int32_t* off, const int16_t* idx, const void* val, uint32_t rows, uint32_t k,
                           void* planes, int32_t* exps, hipStream_t stream) {
+    const dim3 grid(ceil_div(rows, kDensRows), ceil_div(k, kDensChunk)), block(kDensThreads);
     if (vt == kBF16)
-        hipLaunchKernelGGL((densify_kernel<uint16_t>), dim3(ceil_div(rows, kDensRows), ceil_div(k, kDensChunk)), dim3(kDensThreads), 0, stream, off, idx,
-                           static_cast<const uint16_t*>(val), rows, k, static_cast<_Float16*>(planes), exps);
+        hipLaunchKernelGGL((densify_kernel<uint16_t>), grid, block, 0, stream, off, idx, static_cast<const uint16_t*>(val), rows, k,
+                           static_cast<_Float16*>(planes), exps);
     else
-        hipLaunchKernelGGL((densify_kernel<float>), dim3(ceil_div(rows, kDensRows), ceil_div(k, kDensChunk)), dim3(kDensThreads), 0, stream, off, idx,
-                           static_cast<const float*>(val), rows, k, static_cast<_Float16*>(planes), exps);
+        hipLaunchKernelGGL((densify_kernel<float>), grid, block, 0, stream, off, idx, static_cast<const float*>(val), rows, k,
+                           static_cast<_Float16*>(planes), exps);
     return hipGetLastError();
 }
 
