@@ -68,6 +68,15 @@ __device__ __forceinline__ int act_binade(uint32_t bits) {
     return e >= 0 ? (e + kActBinadeStep - 1) / kActBinadeStep * kActBinadeStep : -(-e / kActBinadeStep * kActBinadeStep);
 }
 
+// Activation block binades are int8 (multiples of kActBinadeStep, |e| < 128), block-major [d_ff / kActBlock][rows_pad]:
+// the down GEMM transfers each activation block's binades of its 256 rows, one contiguous 256-byte run, straight into
+// LDS. They travel through the GEMMs' int32 binade pointers (Up: out_exp; Down: a_exp), read and written as bytes.
+__device__ __forceinline__ size_t act_exp_at(uint32_t rows_pad, uint32_t m, uint32_t block) {
+    return static_cast<size_t>(block) * rows_pad + m;
+}
+__device__ __forceinline__ const int8_t* act_exps(const int32_t* p) { return reinterpret_cast<const int8_t*>(p); }
+__device__ __forceinline__ int8_t* act_exps(int32_t* p) { return reinterpret_cast<int8_t*>(p); }
+
 __device__ __forceinline__ uint32_t abs_bits(float v) { return __float_as_uint(v) & 0x7fffffffu; }
 
 __device__ __forceinline__ void split(float v, _Float16& hi, _Float16& lo) {
@@ -335,13 +344,13 @@ __device__ __forceinline__ uint32_t wave_row(uint32_t wm, int i, int r, uint32_t
 template <Epi EPI, int MI, int NI, bool LO_B, int SPLITS>
 __global__ __launch_bounds__(kThreads) void gemm_planes_kernel(
     const _Float16* __restrict__ a_planes,  // [K / 32][8][rows_pad][8]
-    const int32_t* __restrict__ a_exp,      // Up: [rows_pad]; Down: [rows_pad, K / kActBlock]
+    const int32_t* __restrict__ a_exp,      // Up: [rows_pad]; Down: [K / kActBlock, rows_pad] (act_exp_at)
     const _Float16* __restrict__ b_planes,  // [K / 32][8][Ncol][8]
     const int32_t* __restrict__ b_exp,      // [Ncol]
     const float* __restrict__ bias,         // [Ncol]
     float* __restrict__ out,                // Down: [M, Ncol] fp32 row-major
     _Float16* __restrict__ out_planes,      // Up: activation planes [Ncol / 32][8][rows_pad][8]
-    int32_t* __restrict__ out_exp,          // Up: [rows_pad, Ncol / BN] activation block binades
+    int32_t* __restrict__ out_exp,          // Up: [Ncol / BN, rows_pad] activation block binades (act_exp_at)
     float* __restrict__ partials,           // SPLITS > 1: [SPLITS, M, Ncol] partial sums
     int32_t* __restrict__ counters,         // SPLITS > 1: [tiles], zero between calls
     uint32_t M, uint32_t rows_pad, uint32_t Ncol, uint32_t K) {
@@ -363,11 +372,10 @@ __global__ __launch_bounds__(kThreads) void gemm_planes_kernel(
     const uint32_t m0 = tile.m * BM, n0 = tile.n * BN;
     const uint32_t ktiles = K / kBK;
     const uint32_t k_begin = tile.split * ktiles / SPLITS, k_end = (tile.split + 1) * ktiles / SPLITS;
-    const uint32_t a_kblocks = K / kActBlock;
 
     if (tid < BM) {
         if constexpr (EPI == Epi::Up) row_e[0][tid] = a_exp[m0 + tid];
-        else row_e[(k_begin / kKtPerActBlock) & 1][tid] = a_exp[static_cast<size_t>(m0 + tid) * a_kblocks + k_begin / kKtPerActBlock];
+        else row_e[(k_begin / kKtPerActBlock) & 1][tid] = act_exps(a_exp)[act_exp_at(rows_pad, m0 + tid, k_begin / kKtPerActBlock)];
     }
 
     const uint32_t run = tid / 32, row = tid % 32;
@@ -392,7 +400,7 @@ __global__ __launch_bounds__(kThreads) void gemm_planes_kernel(
             load_stage<ARPT, BRPT>(regs, a_src, a_stride, b_src, b_stride, k_begin + 1);
             if constexpr (EPI == Epi::Down) {
                 if ((k_begin + 1) % kKtPerActBlock == 0 && tid < BM)
-                    next_e = a_exp[static_cast<size_t>(m0 + tid) * a_kblocks + (k_begin + 1) / kKtPerActBlock];
+                    next_e = act_exps(a_exp)[act_exp_at(rows_pad, m0 + tid, (k_begin + 1) / kKtPerActBlock)];
             }
         }
     }
@@ -450,7 +458,7 @@ __global__ __launch_bounds__(kThreads) void gemm_planes_kernel(
                 load_stage<ARPT, BRPT>(regs, a_src, a_stride, b_src, b_stride, kt + 2);
                 if constexpr (EPI == Epi::Down) {
                     if ((kt + 2) % kKtPerActBlock == 0 && tid < BM)
-                        next_e = a_exp[static_cast<size_t>(m0 + tid) * a_kblocks + (kt + 2) / kKtPerActBlock];
+                        next_e = act_exps(a_exp)[act_exp_at(rows_pad, m0 + tid, (kt + 2) / kKtPerActBlock)];
                 }
             }
         }
@@ -488,7 +496,7 @@ __global__ __launch_bounds__(kThreads) void gemm_planes_kernel(
         if (tid < BM) {
             const int e = act_binade(max(row_max[0][tid], row_max[1][tid]));
             row_e[1][tid] = e;
-            out_exp[static_cast<size_t>(m0 + tid) * tiles_n + tile.n] = e;
+            act_exps(out_exp)[act_exp_at(rows_pad, m0 + tid, tile.n)] = static_cast<int8_t>(e);
         }
         // the planes go out through LDS, half the block's rows (one wave row) at a time: the waves of that row store
         // v as fp32 [row][col], then every thread splits 8 consecutive columns of one row and writes 16 bytes per
@@ -612,7 +620,6 @@ constexpr int kDmaStages = 3;
 constexpr int kDmaBM = 256, kDmaBN = 128;
 constexpr int kDmaWaves = 8;  // waves per block: two per SIMD, 64 x 64 outputs each
 constexpr uint32_t kDmaMaxActBlocks = 40;  // activation blocks of one down split held in LDS (int8 binades)
-static_assert(kDmaMaxActBlocks <= 64, "one bit per activation block of a split in two 32-bit masks");
 
 // s_waitcnt vmcnt(N) lgkmcnt(0): at most N vector-memory loads of this wave still in flight, its LDS accesses done.
 template <int N>
@@ -626,10 +633,18 @@ __device__ __forceinline__ void wait_loads() {
 // bytes land at lds + 16 l. Written as inline assembly so that the compiler, which cannot tell the ring slots apart,
 // does not wait for every transfer in flight before each LDS read; the kernel orders them itself (wait_loads, then a
 // barrier).
-__device__ __forceinline__ void dma16(const _Float16* base, uint32_t offset, const _Float16* lds) {
+__device__ __forceinline__ void dma16(const void* base, uint32_t offset, const void* lds) {
     const uint32_t to = static_cast<uint32_t>(__builtin_amdgcn_readfirstlane(
         static_cast<int>(static_cast<uint32_t>(reinterpret_cast<uintptr_t>(lds)))));  // low 32 bits: the LDS address
     asm volatile("s_mov_b32 m0, %2\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, %1" ::"v"(offset), "s"(base), "s"(to)
+                 : "memory", "m0");
+}
+
+// The same with 4 bytes per lane (lane l's land at lds + 4 l).
+__device__ __forceinline__ void dma4(const void* base, uint32_t offset, const void* lds) {
+    const uint32_t to = static_cast<uint32_t>(__builtin_amdgcn_readfirstlane(
+        static_cast<int>(static_cast<uint32_t>(reinterpret_cast<uintptr_t>(lds)))));
+    asm volatile("s_mov_b32 m0, %2\n\ts_nop 0\n\tglobal_load_lds_dword %0, %1" ::"v"(offset), "s"(base), "s"(to)
                  : "memory", "m0");
 }
 
@@ -648,13 +663,13 @@ __device__ __forceinline__ void block_barrier() {
 template <Epi EPI, bool LO_B, int LIVE>
 __global__ __launch_bounds__(64 * kDmaWaves) void gemm_dma_kernel(
     const _Float16* __restrict__ a_planes,  // [K / 32][8][rows_pad][8]
-    const int32_t* __restrict__ a_exp,      // Up: [rows_pad]; Down: [rows_pad, K / kActBlock]
+    const int32_t* __restrict__ a_exp,      // Up: [rows_pad]; Down: [K / kActBlock, rows_pad] (act_exp_at)
     const _Float16* __restrict__ b_planes,  // [K / 32][8][Ncol][8]
     const int32_t* __restrict__ b_exp,      // [Ncol]
     const float* __restrict__ bias,         // [Ncol]
     float* __restrict__ out,                // Down: y [M, Ncol] (splits == 1) or partials [splits, M, Ncol]; UpSplit: partials
     _Float16* __restrict__ out_planes,      // Up: activation planes [Ncol / 32][8][rows_pad][8]
-    int32_t* __restrict__ out_exp,          // Up: [rows_pad, Ncol / BN] activation block binades
+    int32_t* __restrict__ out_exp,          // Up: [Ncol / BN, rows_pad] activation block binades (act_exp_at)
     uint32_t M, uint32_t rows_pad, uint32_t Ncol, uint32_t K, uint32_t splits) {
     // 8 waves in 4 x 2, 64 x 64 outputs each (two waves per SIMD)
     constexpr int W = kDmaWaves, MI = 2, NI = 2, BM = kDmaBM, BN = kDmaBN, S = kDmaStages;
@@ -669,14 +684,13 @@ __global__ __launch_bounds__(64 * kDmaWaves) void gemm_dma_kernel(
     constexpr int kLoadsA = kRowRuns * kRuns / W, kLoadsB = BN * kRunsB / kWave / W;  // DMA instructions per wave
     static_assert(kLoadsA * W == kRowRuns * kRuns && kLoadsB * W == BN * kRunsB / kWave, "the transfers divide over the waves");
     constexpr int kLoads = kLoadsA + kLoadsB;
-    static_assert(2 * kLoads * S < 64, "the prologue's transfers of a lower-half wave fit vmcnt");
+    static_assert(kLoads * S + (kDmaMaxActBlocks + W - 1) / W < 64, "the prologue's transfers of a wave fit vmcnt");
     // multiplied 32-row tiles of a live wave (its rows start at wm * kWaveRows; LIVE is a multiple of kWaveRows)
     constexpr int MIL = LIVE >= static_cast<int>(kWaveRows) ? MI : LIVE / 32;
 
     __shared__ __attribute__((aligned(16))) _Float16 smem[S * kStage];
-    __shared__ int32_t e_row[1][BM];  // Up: x binades
-    __shared__ __attribute__((aligned(4))) int8_t e_tab[EPI == Epi::Down ? kDmaMaxActBlocks : 1][EPI == Epi::Down ? BM : 1];  // Down: [block][row]
-    __shared__ uint32_t change_masks[EPI == Epi::Down ? kHalf : 1][2];
+    __shared__ __attribute__((aligned(16))) int32_t e_row[1][BM];  // Up: x binades
+    __shared__ __attribute__((aligned(16))) int8_t e_tab[EPI == Epi::Down ? kDmaMaxActBlocks : 1][EPI == Epi::Down ? BM : 1];  // Down: [block][row]
 
     const uint32_t tid = threadIdx.x, lane = tid % kWave, wave = uniform(tid / kWave);
     const uint32_t wm = wave / 2, wn = wave % 2;
@@ -687,7 +701,7 @@ __global__ __launch_bounds__(64 * kDmaWaves) void gemm_dma_kernel(
     const uint32_t m0 = tile.m * BM, n0 = tile.n * BN;
     const uint32_t ktiles = K / kBK;
     const uint32_t k_begin = tile.split * ktiles / splits, k_end = (tile.split + 1) * ktiles / splits;
-    const uint32_t a_kblocks = K / kActBlock, kb0 = k_begin / kKtPerActBlock;
+    const uint32_t kb0 = k_begin / kKtPerActBlock;
 
     // piece q of wave w's share of a stage: a run of 64 rows (1 KB) of A (pieces below kLoadsA), then of B; its
     // element offsets within a k-tile's planes and within a ring slot
@@ -721,87 +735,29 @@ __global__ __launch_bounds__(64 * kDmaWaves) void gemm_dma_kernel(
         for (int q = 0; q < kLoads; ++q) issue_piece(kt, slot, q);
     };
 
-    // Prologue: the lower half of the waves transfers the first stages, its own pieces and those of the wave kHalf
-    // above, while the upper half loads the binades. vmcnt retires in order within a wave, so a binade load behind
-    // transfers of its own wave would wait for them; split so, the binades and the first stage arrive together.
+    // Prologue: every wave requests its pieces of the first stages, after the binades of the tile's rows, which go
+    // straight into LDS as well (Up: the x binades, one 1 KB run; Down: the split's activation blocks, one 256-byte run
+    // of int8 each, block c from wave c % W). vmcnt retires in order within a wave, so once the first stage has landed
+    // so have they: the block meets once, and no wave holds a register for them. (Loaded into registers by half of the
+    // waves and reduced to change masks there, the down GEMM's binades kept the block 6.5 us in its prologue, where
+    // the first stage lands in 2.5-3 us.)
     const uint32_t steps = k_end - k_begin;  // at least 1
-    if (wave < kHalf) {
-#pragma unroll
-        for (int s = 0; s < S; ++s)
-            if (static_cast<uint32_t>(s) < steps) {
-                issue(k_begin + s, s);
-#pragma unroll
-                for (int q = 0; q < kLoads; ++q) {
-                    uint32_t src, dst;
-                    piece(wave + kHalf, q, src, dst);
-                    dma16(q < kLoadsA ? a_planes + (k_begin + s) * a_kt : b_planes + (k_begin + s) * b_kt, src * 2 + lane * 16,
-                          smem + s * kStage + dst);
-                }
-            }
+    if constexpr (EPI == Epi::Down) {
+        const uint32_t blocks = (k_end - k_begin) / kKtPerActBlock;  // at least one: K is split on activation blocks
+        const int8_t* tab = act_exps(a_exp);
+        for (uint32_t c = wave; c < blocks; c += W)
+            dma4(tab + act_exp_at(rows_pad, m0, kb0 + c), lane * 4, &e_tab[c][0]);
     } else {
-        const uint32_t t = tid - kHalf * kWave;  // 0 .. BM - 1
-        if constexpr (EPI != Epi::Down) {
-            e_row[0][t] = a_exp[m0 + t];
-        } else {
-            // The tile's binades of this split: `blocks` consecutive ints of each of its BM rows (whole activation
-            // blocks, at least one: the host splits K on activation block boundaries), read coalesced: load i of
-            // thread t takes element q = i BM + t of the table, (row q / blocks, block q % blocks), tracked
-            // incrementally, and the element before it in the row (itself in block 0); the table holds BM blocks
-            // elements, so every thread takes exactly `blocks` (a uniform bound), all in flight at once. Bit b of
-            // `changes`: some row of this thread's elements changes its power of two between blocks b - 1 and b,
-            // ORed over the wave, then over the upper waves through LDS after the prologue's barrier.
-            const uint32_t blocks = (k_end - k_begin) / kKtPerActBlock, dr = BM / blocks, dc = BM % blocks;
-            const int32_t* tab = a_exp + static_cast<size_t>(m0) * a_kblocks + kb0;
-            int32_t v[kDmaMaxActBlocks], u[kDmaMaxActBlocks];
-            uint32_t r = t / blocks, c = t % blocks;
-#pragma unroll
-            for (uint32_t i = 0; i < kDmaMaxActBlocks; ++i) {
-                if (i < blocks) {
-                    const uint32_t at = r * a_kblocks + c;
-                    v[i] = tab[at];
-                    u[i] = tab[c > 0 ? at - 1 : at];
-                }
-                r += dr, c += dc;
-                if (c >= blocks) c -= blocks, ++r;
-            }
-            uint64_t change = 0;  // branch-free: bit c set when the two int8 binades differ
-            r = t / blocks, c = t % blocks;
-#pragma unroll
-            for (uint32_t i = 0; i < kDmaMaxActBlocks; ++i) {
-                if (i < blocks) {
-                    e_tab[c][r] = static_cast<int8_t>(v[i]);
-                    const uint32_t differs = min((static_cast<uint32_t>(v[i]) ^ static_cast<uint32_t>(u[i])) & 0xFFu, 1u);
-                    change |= static_cast<uint64_t>(differs) << c;
-                }
-                r += dr, c += dc;
-                if (c >= blocks) c -= blocks, ++r;
-            }
-            uint32_t changes[2] = {static_cast<uint32_t>(change), static_cast<uint32_t>(change >> 32)};
-#pragma unroll
-            for (int h = 0; h < 2; ++h) {
-#pragma unroll
-                for (int off = 32; off >= 1; off >>= 1)
-                    changes[h] |= static_cast<uint32_t>(__shfl_xor(static_cast<int>(changes[h]), off, kWave));
-                if (lane == 0) change_masks[wave - kHalf][h] = changes[h];
-            }
-        }
+        if (wave == 0) dma16(a_exp + m0, lane * 16, &e_row[0][0]);
     }
-    // stage k_begin has landed (a lower-half wave has two pieces per piece of its share in flight per stage; an
-    // upper-half wave none), the binade tables are written; then the block meets
-    if (steps >= 3) wait_loads<4 * kLoads>();
-    else if (steps == 2) wait_loads<2 * kLoads>();
+#pragma unroll
+    for (int s = 0; s < S; ++s)
+        if (static_cast<uint32_t>(s) < steps) issue(k_begin + s, s);
+    // stage k_begin has landed (later stages may be in flight), and with it the binades; then the block meets
+    if (steps >= 3) wait_loads<2 * kLoads>();
+    else if (steps == 2) wait_loads<kLoads>();
     else wait_loads<0>();
     block_barrier();
-    uint32_t changed[2] = {0, 0};  // Down: activation blocks at whose start some row of the tile changes its power of two
-    if constexpr (EPI == Epi::Down) {
-#pragma unroll
-        for (int h = 0; h < 2; ++h) {
-            uint32_t c = 0;
-#pragma unroll
-            for (int w = 0; w < static_cast<int>(kHalf); ++w) c |= change_masks[w][h];
-            changed[h] = uniform(c);
-        }
-    }
 
     floatx16 acc[MI][NI];
 #pragma unroll
@@ -878,12 +834,16 @@ __global__ __launch_bounds__(64 * kDmaWaves) void gemm_dma_kernel(
     // of the current one run, and the block meets once per k-tile, between its two steps (after every wave has read
     // all of k-tile kt and before anyone reads k-tile kt + 1), where the slot of kt is refilled with kt + kDmaStages.
     // The first stages went out in the prologue.
-    // a new activation block at k-tile kt: bring the accumulators to its power of two (exact); accumulator
-    // registers 4g .. 4g + 3 hold 4 consecutive rows, so one 4-byte read per block and group
+    // a new activation block at k-tile kt: bring the accumulators to its power of two (exact), when some row of the
+    // wave changes it (lane l checks the wave's row l; binades are multiples of kActBinadeStep, so changes are rare;
+    // checked here rather than for all blocks after the prologue, which measured 0.5 % slower); accumulator registers
+    // 4g .. 4g + 3 hold 4 consecutive rows, so one 4-byte read per block and group
     const auto rescale = [&](uint32_t kt) {
         if constexpr (EPI == Epi::Down) {
             const uint32_t kb = kt / kKtPerActBlock - kb0;
-            if (kt % kKtPerActBlock == 0 && kt != k_begin && live && ((changed[kb / 32] >> (kb % 32)) & 1)) {
+            if (kt % kKtPerActBlock != 0 || kt == k_begin || !live) return;
+            const uint32_t own = wm * kWaveRows + lane;
+            if (__builtin_amdgcn_ballot_w64(e_tab[kb - 1][own] != e_tab[kb][own]) != 0) {
 #pragma unroll
                 for (int i = 0; i < MIL; ++i)
 #pragma unroll
@@ -965,7 +925,7 @@ __global__ __launch_bounds__(64 * kDmaWaves) void gemm_dma_kernel(
         for (uint32_t off = 1; off < H; off <<= 1)
             largest = max(largest, static_cast<uint32_t>(__shfl_xor(static_cast<int>(largest), static_cast<int>(off), kWave)));
         const int e = act_binade(largest);
-        if (part == 0) out_exp[static_cast<size_t>(m0 + row) * tiles_n + tile.n] = e;
+        if (part == 0) act_exps(out_exp)[act_exp_at(rows_pad, m0 + row, tile.n)] = static_cast<int8_t>(e);
         const float scale = ldexpf(1.0f, -e);
 #pragma unroll 4
         for (uint32_t chunk = part * (BN / 8 / H); chunk < (part + 1) * (BN / 8 / H); ++chunk) {
@@ -1053,7 +1013,7 @@ __global__ __launch_bounds__(kThreads) void reduce_splits_kernel(const float* __
 constexpr uint32_t kActRowsPerBlock = kThreads / 16;
 __global__ __launch_bounds__(kThreads) void act_planes_kernel(const float* __restrict__ partials, uint32_t splits,
                                                              const float* __restrict__ b_up, _Float16* __restrict__ planes,
-                                                             int32_t* __restrict__ exps, uint32_t M, uint32_t rows_pad, uint32_t H) {
+                                                             int8_t* __restrict__ exps, uint32_t M, uint32_t rows_pad, uint32_t H) {
     const uint32_t m = blockIdx.x * kActRowsPerBlock + threadIdx.x / 16, sub = threadIdx.x % 16;
     const uint32_t nb = blockIdx.y, n = nb * kActBlock + sub * 8;
     const float4 b0 = *reinterpret_cast<const float4*>(b_up + n), b1 = *reinterpret_cast<const float4*>(b_up + n + 4);
@@ -1086,7 +1046,7 @@ __global__ __launch_bounds__(kThreads) void act_planes_kernel(const float* __res
 #pragma unroll
     for (int off = 8; off >= 1; off >>= 1) largest = max(largest, static_cast<uint32_t>(__shfl_xor(static_cast<int>(largest), off, kWave)));
     const int e = act_binade(largest);
-    if (sub == 0) exps[static_cast<size_t>(m) * (H / kActBlock) + nb] = e;
+    if (sub == 0) exps[act_exp_at(rows_pad, m, nb)] = static_cast<int8_t>(e);
     const float scale = ldexpf(1.0f, -e);
     half8 hi, lo;
 #pragma unroll
@@ -1114,7 +1074,7 @@ template <TrainPost MODE>
 __global__ __launch_bounds__(kThreads) void train_planes_kernel(const float* __restrict__ partials, uint32_t splits,
                                                                const float* __restrict__ b_up, const float* __restrict__ z_in,
                                                                float* __restrict__ out_a, float* __restrict__ out_b,
-                                                               _Float16* __restrict__ planes, int32_t* __restrict__ exps, uint32_t M,
+                                                               _Float16* __restrict__ planes, int8_t* __restrict__ exps, uint32_t M,
                                                                uint32_t rows_pad, uint32_t H, uint32_t ld) {
     constexpr uint32_t R = kActRowsPerBlock;
     static_assert(R == 16 && kActBlock * 4 % kThreads == 0, "16 tokens a block; the tile rows divide over the threads");
@@ -1173,7 +1133,7 @@ __global__ __launch_bounds__(kThreads) void train_planes_kernel(const float* __r
 #pragma unroll
     for (int off = 8; off >= 1; off >>= 1) largest = max(largest, static_cast<uint32_t>(__shfl_xor(static_cast<int>(largest), off, kWave)));
     const int e = act_binade(largest);
-    if (sub == 0) exps[static_cast<size_t>(m) * (H / kActBlock) + nb] = e;
+    if (sub == 0) exps[act_exp_at(rows_pad, m, nb)] = static_cast<int8_t>(e);
     const float scale = ldexpf(1.0f, -e);
     half8 hi, lo;
 #pragma unroll
@@ -1426,9 +1386,10 @@ Workspace workspace_layout(uint32_t m, uint32_t d, uint32_t h, bool training = f
     Workspace w{};
     w.counters = 0;
     const size_t counter_words = static_cast<size_t>(ceil_div(kMaxTokens, 64)) * (d / 64);
-    w.x_binades = w.counters + counter_words;
-    w.act_binades = w.x_binades + rows;
-    const size_t words_end = (w.act_binades + rows * (h / kActBlock)) * 4;
+    // both binade tables start on 256-byte boundaries: the streamed GEMM transfers them into LDS 16 or 4 bytes a lane
+    w.x_binades = (w.counters + counter_words + 63) / 64 * 64;
+    w.act_binades = (w.x_binades + rows + 63) / 64 * 64;
+    const size_t words_end = (w.act_binades + rows * (h / kActBlock) / 4) * 4;  // int8 activation binades
     w.x_planes = (words_end + 255) / 256 * 256;  // bytes from here on
     w.act_planes = w.x_planes + rows * d * 4;
     w.partials = w.act_planes + rows * h * 4;
@@ -1529,7 +1490,7 @@ hipError_t launch_mfma_up(int vt, const float* x, const void* planes, const int3
                                                          h, d, splits, stream);
         if (status != hipSuccess) return status;
         hipLaunchKernelGGL(act_planes_kernel, dim3(rows_live(n) / kActRowsPerBlock, h / kActBlock), dim3(kThreads), 0, stream, partials,
-                           splits, b_up, act_planes, words + w.act_binades, n, rows_padded(n), h);
+                           splits, b_up, act_planes, reinterpret_cast<int8_t*>(words + w.act_binades), n, rows_padded(n), h);
         return hipGetLastError();
     }
     if (dma_tiles(n, h) >= kDmaMinBlocks) {
@@ -1593,7 +1554,8 @@ hipError_t launch_train_forward(const float* x, const void* up_planes, const int
         status != hipSuccess)
         return status;
     hipLaunchKernelGGL(train_planes_kernel<TrainPost::Forward>, dim3(rows_live(n) / kActRowsPerBlock, h / kActBlock), dim3(kThreads), 0,
-                       stream, partials, splits, b_up, nullptr, z, act, act_planes, words + w.act_binades, n, rows_padded(n), h, ld);
+                       stream, partials, splits, b_up, nullptr, z, act, act_planes, reinterpret_cast<int8_t*>(words + w.act_binades), n,
+                       rows_padded(n), h, ld);
     if (hipError_t status = hipGetLastError(); status != hipSuccess) return status;
     return launch_mfma_down(kF32, down_planes, down_exp, b_down, y, workspace, n, d, h, stream);
 }
@@ -1619,7 +1581,8 @@ hipError_t launch_train_backward(const float* gy, const float* z, const void* do
         status != hipSuccess)
         return status;
     hipLaunchKernelGGL(train_planes_kernel<TrainPost::GradZ>, dim3(rows_live(n) / kActRowsPerBlock, h / kActBlock), dim3(kThreads), 0,
-                       stream, partials, splits, nullptr, z, gz, nullptr, gz_planes, words + w.act_binades, n, rows_padded(n), h, ld);
+                       stream, partials, splits, nullptr, z, gz, nullptr, gz_planes, reinterpret_cast<int8_t*>(words + w.act_binades), n,
+                       rows_padded(n), h, ld);
     if (hipError_t status = hipGetLastError(); status != hipSuccess) return status;
     return launch_mfma_down(kF32, up_t_planes, up_t_exp, nullptr, gx, workspace, n, d, h, stream);
 }
