@@ -10,6 +10,8 @@
 """
 from __future__ import annotations
 
+import math
+
 import numpy as np
 import pytest
 import torch
@@ -98,6 +100,33 @@ def test_gelu_against_float64(device):
     expected = torch.tensor([0.5 * v * math.erfc(-v / math.sqrt(2.0)) for v in zf.tolist()], dtype=torch.float64)
     error = (got - expected).abs()
     assert bool((error <= 4e-7 * zf.abs().clamp(min=1.0)).all()), float(error.max())
+
+
+def test_mfma_gelu_against_float64(device):
+    """The device GELU through the MFMA path (the streamed up GEMM's epilogue, then the activation planes and the down
+    GEMM) of an identity layer (d_model = d_ff = 4096, neuron r reads input r with weight 1, output r reads neuron r
+    with weight 1, zero biases): at 2048 tokens y = gelu(x) for 8M arguments in [-12, 12], each token's inputs within
+    0.012 of each other, against float64: within 4e-7 max(1, |z|) plus 1e-6 for the activation planes (a 128-neuron
+    block's power of two rounded up to a multiple of 4 binades leaves 2^-24 of it per value)."""
+    from hffn_amd.synth import CompactLayer
+    d = h = 4096
+    n = 2048
+    ramp = np.arange(h, dtype=np.int32)
+    one = np.ones(h, dtype=np.float32)
+    zero = np.zeros(h, dtype=np.float32)
+    layer = CompactLayer(d, h, np.zeros(5, dtype=np.int32), np.arange(h + 1, dtype=np.int32), ramp.astype(np.int16), one,
+                         zero, np.arange(h + 1, dtype=np.int32), ramp.astype(np.int16), one, zero)
+    runtime = HFFNRuntime([hip_layer(layer)], device, dense=True)
+    runtime.force("mfma", "mfma")
+    z = torch.linspace(-12.0, 12.0, n * d, dtype=torch.float64)
+    x = z.float().reshape(n, d)
+    got = runtime.forward(0, x.to(device)).double().cpu().reshape(-1)
+    zf = x.double().reshape(-1)
+    expected = 0.5 * zf * torch.special.erfc(-zf / math.sqrt(2.0))
+    error = (got - expected).abs()
+    assert bool((error <= 4e-7 * zf.abs().clamp(min=1.0) + 1e-6).all()), float(error.max())
+    # the tanh form of GELU is far outside that bound
+    assert float((0.5 * zf * (1 + torch.tanh(0.7978845608 * (zf + 0.044715 * zf ** 3))) - expected).abs().max()) > 1e-4
     big = expected.abs() > 1e-6
     assert float((error[big] / expected[big].abs()).max()) <= 2e-6
 
