@@ -39,8 +39,13 @@ constexpr uint32_t kGemvTile = 16;   // tokens per MFMA row tile
 constexpr uint32_t kGemvK = 32;      // k per MFMA, one plane k-tile
 constexpr uint32_t kGemvMinBlocks = 256;  // blocks of one round (one per CU); fewer row tiles call for splits or 16 waves
 
-// floor(log2(m)) of a non-negative float given by its bits; 0 for zero.
-__device__ __forceinline__ int gemv_binade(uint32_t bits) { return bits == 0 ? 0 : static_cast<int>((bits >> 23) & 0xff) - 127; }
+// Power of two of a token's 32 inputs of a k-tile: floor(log2(m)) - 12, clamped, so that the largest scaled input lies
+// in 2^12 .. 2^13 and lo stays a normal fp16 down to 2^-15 of it (the weight planes are lifted the same way: scaled
+// products stay below 2^26); -12 for zero.
+__device__ __forceinline__ int gemv_binade(uint32_t bits) {
+    const int e = bits == 0 ? 0 : static_cast<int>((bits >> 23) & 0xff) - 127;
+    return min(max(e, -100), 100) - 12;
+}
 
 template <int W, int TT, bool LO_B, bool UP>
 __global__ __launch_bounds__(W* kWave) void gemv_mfma_kernel(const float* __restrict__ in,        // [n, K]

@@ -53,22 +53,38 @@ constexpr uint32_t kRowPad = 256;  // token planes hold a multiple of this many 
 constexpr uint32_t kActBlock = 128;  // neurons per activation power of two (the up GEMM's column tile)
 constexpr uint32_t kKtPerActBlock = kActBlock / kBK;
 
-// floor(log2(m)) of a non-negative float given by its bits; 0 for zero (any scale is exact for zeros).
+// Every plane row (a token's inputs, a weight row, a token's activation block) is stored as hi + lo = v * 2^-e, e
+// its power of two. e puts the row's largest |v| at 2^kPlaneLift .. 2^(kPlaneLift + 1) (below fp16's 65504 with room
+// to spare), far above fp16's smallest normal 2^-14: lo, the residual of hi (at most 2^-11 of |hi|), is then a
+// normal fp16 for every entry down to 2^-(kPlaneLift + 3) of the row's largest, and below that its absolute error
+// (2^-25 after scaling) is 2^-(25 + kPlaneLift) of the largest. Scaled products stay below 2^26 per term, so fp32
+// accumulation has no overflow at any K. Whoever reads a plane undoes e exactly (ldexp), so the lift is invisible
+// outside the planes.
+constexpr int kPlaneLift = 12;
+// binades are clamped to +-kBinadeClamp before the lift: 2^(kBinadeClamp + kPlaneLift) is a finite float scale, and an
+// activation block's binade fits an int8 (a row of only tiny entries, below 2^-100, keeps less than fp32's precision)
+constexpr int kBinadeClamp = 100;
+
+// floor(log2(m)) - kPlaneLift of a non-negative float given by its bits (clamped); -kPlaneLift for zero (any scale is
+// exact for zeros). inf and NaN give the clamp's top, which scales them to themselves.
 __device__ __forceinline__ int binade_of_bits(uint32_t bits) {
-    return bits == 0 ? 0 : static_cast<int>((bits >> 23) & 0xff) - 127;
+    const int e = bits == 0 ? 0 : static_cast<int>((bits >> 23) & 0xff) - 127;
+    return min(max(e, -kBinadeClamp), kBinadeClamp) - kPlaneLift;
 }
 
-// Power of two of an activation block (a token's kActBlock neurons): the binade of its largest |v| rounded up to a
-// multiple of kActBinadeStep. The block's largest value scaled still lies below 2, and the planes' resolution (2^-24
-// after scaling, fp16's smallest subnormal) stays within 2^-21 of it; neighbouring blocks of a token then mostly
-// share their power of two, and the down GEMM has nothing to rescale between them.
+// Power of two of an activation block (a token's kActBlock neurons): binade_of_bits of its largest |v| rounded up to a
+// multiple of kActBinadeStep (kPlaneLift is one, so the rounding is that of the true binade). The block's largest
+// value scaled lies in 2^(kPlaneLift - 3) .. 2^(kPlaneLift + 1); neighbouring blocks of a token then mostly share their
+// power of two, and the down GEMM has nothing to rescale between them. Range: -112 .. 88, an int8.
 constexpr int kActBinadeStep = 4;
+static_assert(kPlaneLift % kActBinadeStep == 0, "the lift keeps activation binades on their grid");
+static_assert(kBinadeClamp + kPlaneLift + kActBinadeStep < 128, "activation binades fit an int8");
 __device__ __forceinline__ int act_binade(uint32_t bits) {
     const int e = binade_of_bits(bits);
     return e >= 0 ? (e + kActBinadeStep - 1) / kActBinadeStep * kActBinadeStep : -(-e / kActBinadeStep * kActBinadeStep);
 }
 
-// Activation block binades are int8 (multiples of kActBinadeStep, |e| < 128), block-major [d_ff / kActBlock][rows_pad]:
+// Activation block binades are int8 (multiples of kActBinadeStep, -112 .. 88), block-major [d_ff / kActBlock][rows_pad]:
 // the down GEMM transfers each activation block's binades of its 256 rows, one contiguous 256-byte run, straight into
 // LDS. They travel through the GEMMs' int32 binade pointers (Up: out_exp; Down: a_exp), read and written as bytes.
 __device__ __forceinline__ size_t act_exp_at(uint32_t rows_pad, uint32_t m, uint32_t block) {
@@ -91,7 +107,7 @@ __device__ __forceinline__ size_t plane_at(uint32_t rows, uint32_t row, uint32_t
 
 // ------------------------------------------------------------------------------------------ input planes
 // X [M, K] fp32 (row stride ld; entries at k >= k_real read as zeros) -> planes of X [rows_pad, K] and e[row] =
-// binade of max |x[row, :]| (rows M .. 8 * gridDim.x: zeros, e = 0; K a multiple of 256). A block takes 8 rows; its wave w takes k in [w K/4, (w + 1) K/4) in steps of 64,
+// binade of max |x[row, :]| (rows M .. 8 * gridDim.x: zeros, e = -kPlaneLift; K a multiple of 256). A block takes 8 rows; its wave w takes k in [w K/4, (w + 1) K/4) in steps of 64,
 // up to 4 steps (a chunk) at a time: in a step, lane l holds 8 consecutive k (piece l / 8) of row l % 8, so that the
 // 8 lanes of a row read 256 contiguous bytes of it and the 8 lanes of a piece write the 8 rows' 16 bytes of one
 // 128-byte run of the planes. First the row maxima (lanes, then the 4 waves through LDS), then the split; a wave

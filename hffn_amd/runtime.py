@@ -62,6 +62,12 @@ TILES_FILL_US, TILES_FILL_SLOT_US = 2.0, 0.07e-6
 TILES_TILE_US, TILES_TILE_SLOT_US = 4.5, 0.17e-6
 TILES_TIE = 1.05  # the tiles path wins estimates within 5 % of the lane-per-slot kernels' (its cost is flat in N)
 MAX_TOKENS = 1 << 18      # runtime/gpu/nvidia/common/kernels/hffn_cuda/runtime.py:26
+# The reference's policy constants (runtime.py:24-25), with this policy's meaning: COOP_MAX_TOKENS, the largest N the
+# policy may run on the cooperative (lane-per-slot, wave-reduced) kernels; BLOCK_MAX_WIDTH, the widest d_ff up to which
+# the down choice is the same as for narrower FFNs - every d_ff the 16-bit hidden ids of the output-major store can
+# address, since the choice here does not depend on d_ff.
+COOP_MAX_TOKENS = EDGES_MAX_TOKENS
+BLOCK_MAX_WIDTH = 1 << 15
 
 _VALUE_TYPES = {torch.float32: _lib.VALUE_F32, torch.bfloat16: _lib.VALUE_BF16}
 

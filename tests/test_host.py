@@ -300,3 +300,37 @@ def test_plans_are_checked_once_and_released():
     _expect_argument_error(lib.hffn_plan_launch(handle.value, ctypes.c_void_p(20), None), "aligned")
     assert lib.hffn_plan_release(handle.value) == _lib.OK
     _expect_argument_error(lib.hffn_plan_release(handle.value), "unknown plan")
+
+
+class _StubRuntime:
+    """The runtime interface parity.check uses, on the CPU: each pair adds a fixed offset to x (rows, rows: none),
+    and the (edges, edges) pair changes its bits between calls."""
+    mfma_available = tiles_available = True
+
+    def __init__(self):
+        self.pair, self.calls = (None, None), 0
+
+    def force(self, up, down):
+        self.pair = (up, down)
+
+    def forward(self, index, x):
+        self.calls += 1
+        offset = {("rows", "rows"): 0.0, ("edges", "edges"): 1e-3 * (self.calls % 2)}.get(self.pair, 1e-4)
+        return x + offset
+
+
+def test_parity_result_reads_as_the_reference_callers_read_it():
+    """runtime/gpu/nvidia/llm/inference/checks/parity_layers.py:51-53 and ffn/inference/checks/parity.py:49-51 read
+    ``repeatable``, ``sequential_bits``, ``relative`` and ``error`` of each result; the reference runtime's module
+    constants exist."""
+    from hffn_amd import parity
+    x = torch.linspace(-2, 2, 12, dtype=torch.float32).reshape(3, 4)
+    result = parity.check(_StubRuntime(), 0, x, x.double())
+    assert result.repeatable is False  # (edges, edges) changed its bits
+    assert result.sequential_bits is True  # (rows, rows): same bits whole and in halves
+    assert 1e-4 <= result.relative <= 2e-3 and result.error == pytest.approx(1e-3, rel=1e-3)
+    assert result.pairs[("rows", "rows")] == 0.0
+    steady = parity.check(_StubRuntime(), 0, x, x.double(), pairs=[("rows", "rows")])
+    assert steady.repeatable and steady.sequential_bits and steady.error == 0.0
+    assert runtime.COOP_MAX_TOKENS == runtime.EDGES_MAX_TOKENS
+    assert runtime.BLOCK_MAX_WIDTH == 32768 and runtime.MAX_TOKENS == 1 << 18
