@@ -53,6 +53,12 @@ def parse() -> argparse.Namespace:
     parser.add_argument("--copies", type=int, default=None, help="distinct layer copies in the rotation")
     parser.add_argument("--cpu-seconds", type=float, default=5.0, help="timed seconds per CPU-baseline run (4 runs)")
     parser.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
+    parser.add_argument("--settle-ms", type=float, default=500.0,
+                        help="after the warm-up steps, untimed rotations over the copies for this long (GPU clocks ramp "
+                             "up under load: 20 steps after 5 warm-up steps measured 0.141 ms per step, 200 after 20 "
+                             "0.122 ms)")
+    parser.add_argument("--no-decode", action="store_true", help="skip the decode record")
+    parser.add_argument("--decode-rotations", type=int, default=20, help="passes over the copies per decode entry")
     parser.add_argument("--copy-probe-mb", type=int, default=0,
                         help="after the run, copy a buffer of this many MiB 3 times (the plain copy kernel that "
                              "calibrates rocprofv3 FETCH_SIZE/WRITE_SIZE)")
@@ -92,9 +98,15 @@ def layer_costs(compact, n: int) -> dict:
     }
 
 
+def _kernel_seconds(recorded: list, names: list[str], steps: int) -> dict:
+    torch.cuda.synchronize()
+    return {name: sum(e[i].elapsed_time(e[i + 1]) for e in recorded) * 1e-3 / steps for i, name in enumerate(names)}
+
+
 def time_kernels(runtime, x: torch.Tensor, steps: int, copies: int) -> dict:
     """Average duration (s) of each kernel of the step, from HIP events recorded between the launches on the
-    current stream (the stream the C ABI launches on)."""
+    current stream (the stream the C ABI launches on); the steps are issued back to back, without a synchronisation
+    between them, so that no launch latency of an idle device enters the figures."""
     from hffn_amd import _lib
     from hffn_amd.runtime import leading_dim
 
@@ -104,30 +116,30 @@ def time_kernels(runtime, x: torch.Tensor, steps: int, copies: int) -> dict:
     up, down = runtime.modes(n)
     x_t, act, y_t, y = runtime._work
     stream = torch.cuda.current_stream().cuda_stream
+    recorded = []  # the steps run back to back; the events are read after the last one
     if up == "mfma":
-        names = ["up", "down"]
-        totals = {name: 0.0 for name in names}
+        # hffn_mfma_up's two halves apart (the input split, then the up GEMM), so that the GEMM is priced alone
+        names = ["split", "up", "down"]
         work, work_bytes = runtime._mfma_work.data_ptr(), 4 * runtime._mfma_work.numel()
         for step in range(steps):
             index = step % copies
             value_type = runtime._args[index][0]
             planes, tensors = runtime._planes[index], runtime._tensors[index]
-            events = [torch.cuda.Event(enable_timing=True) for _ in range(3)]
+            events = [torch.cuda.Event(enable_timing=True) for _ in range(4)]
             events[0].record()
-            _lib.check(lib.hffn_mfma_up(value_type, x.data_ptr(), planes["up"].data_ptr(), planes["up_binades"].data_ptr(),
-                                        tensors["b_up"].data_ptr(), work, work_bytes, runtime.d_model, runtime.d_ff, n, stream),
-                       "mfma up")
+            _lib.check(lib.hffn_mfma_split(x.data_ptr(), work, work_bytes, runtime.d_model, runtime.d_ff, n, stream), "mfma split")
             events[1].record()
+            _lib.check(lib.hffn_mfma_up_planes(value_type, planes["up"].data_ptr(), planes["up_binades"].data_ptr(),
+                                               tensors["b_up"].data_ptr(), work, work_bytes, runtime.d_model, runtime.d_ff, n,
+                                               stream), "mfma up")
+            events[2].record()
             _lib.check(lib.hffn_mfma_down(value_type, planes["down"].data_ptr(), planes["down_binades"].data_ptr(),
                                           tensors["b_down"].data_ptr(), y, work, work_bytes, runtime.d_model, runtime.d_ff, n, stream),
                        "mfma down")
-            events[2].record()
-            torch.cuda.synchronize()
-            for i, name in enumerate(names):
-                totals[name] += events[i].elapsed_time(events[i + 1]) * 1e-3
-        return {name: total / steps for name, total in totals.items()}
+            events[3].record()
+            recorded.append(events)
+        return _kernel_seconds(recorded, names, steps)
     if up in ("gemv", "tiles"):  # both projections in one ABI call, timed as one
-        total = 0.0
         work, work_bytes = runtime._gemv_work.data_ptr(), 4 * runtime._gemv_work.numel()
         for step in range(steps):
             index = step % copies
@@ -144,11 +156,9 @@ def time_kernels(runtime, x: torch.Tensor, steps: int, copies: int) -> dict:
                                                  planes["down_binades"].data_ptr(), tensors["b_down"].data_ptr(), act, work,
                                                  work_bytes, y, runtime.d_model, runtime.d_ff, n, stream), "gemv")
             events[1].record()
-            torch.cuda.synchronize()
-            total += events[0].elapsed_time(events[1]) * 1e-3
-        return {up: total / steps}
+            recorded.append(events)
+        return _kernel_seconds(recorded, [up], steps)
     names = (["transpose_in"] if up == "rows" else []) + ["up", "down"] + (["transpose_out"] if down == "rows" else [])
-    totals = {name: 0.0 for name in names}
     for step in range(steps):
         value_type, up_off, up_idx, up_val, b_up, out_off, out_hid, out_val, b_down = runtime._args[step % copies]
         nnz_up, nnz_down = runtime._nnz[step % copies]
@@ -171,10 +181,77 @@ def time_kernels(runtime, x: torch.Tensor, steps: int, copies: int) -> dict:
         if down == "rows":
             _lib.check(lib.hffn_transpose(y_t, y, runtime.d_model, n, ld, runtime.d_model, stream), "transpose")
             events[k].record(); k += 1
-        torch.cuda.synchronize()
-        for i, name in enumerate(names):
-            totals[name] += events[i].elapsed_time(events[i + 1]) * 1e-3
-    return {name: total / steps for name, total in totals.items()}
+        recorded.append(events)
+    return _kernel_seconds(recorded, names, steps)
+
+
+DECODE_TOKENS = {"pythia410m_d50": (1, 8, 16), "pythia1p4b_d20_bf16": (1, 4, 16)}
+DECODE_STEP_BATCHES = (1, 8)
+DECODE_STEP_LAYERS = 24
+
+
+def device_copies(layer, count: int) -> list:
+    """``layer`` and count - 1 clones of its device arrays: the same store at distinct addresses, so that a rotation
+    over them reads HBM on every call as distinct layers would (the timing does not depend on the values)."""
+    from hffn_amd.runtime import HFFNLayer
+    return [layer] + [HFFNLayer(**{k: v.clone() if isinstance(v, torch.Tensor) else v for k, v in vars(layer).items()})
+                      for _ in range(count - 1)]
+
+
+def call_us(runtime, x: torch.Tensor, copies: int, rotations: int) -> float:
+    """Mean µs of one ``forward`` over ``rotations`` passes through the copies (HIP events around all of them), after
+    one untimed pass (inputs resident)."""
+    for index in range(copies):
+        runtime.forward(index, x)
+    torch.cuda.synchronize()
+    start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    start.record()
+    for _ in range(rotations):
+        for index in range(copies):
+            runtime.forward(index, x)
+    end.record()
+    torch.cuda.synchronize()
+    return start.elapsed_time(end) * 1e3 / (rotations * copies)
+
+
+def decode_entry(runtime, workload, compact, n: int, copies: int, rotations: int, device) -> dict:
+    from hffn_amd import synth
+    x = torch.from_numpy(synth.make_input(workload, n)).to(device)
+    us = call_us(runtime, x, copies, rotations)
+    moved = layer_costs(compact, n)["step_bytes"]  # the compact store, x read, y written
+    return {"tokens": n, "modes": list(runtime.modes(n)), "us_per_call": round(us, 2), "tokens_per_s": round(n / us * 1e6, 1),
+            "hbm_fraction": round(moved / (us * 1e-6) / HBM_PEAK, 4)}
+
+
+def decode_record(runtime, base, device, rotations: int, steps: int) -> dict:
+    """Decode-sized calls in the same process after the headline: the Pythia-410M-shape layer (the headline's copies)
+    at 1, 8 and 16 tokens; the Pythia-1.4B-shape bf16 layer at 20 % at 1, 4 and 16 tokens (one generated layer and
+    device clones, more than 300 MB in the rotation); and the FFN calls of one decode step of the 24-layer
+    Pythia-410M-shape model at batch 1 and 8, eager and replayed from a HIP graph (hffn_amd.bench_decode). Every
+    entry: µs per call (or step) and the HBM fraction on the compact bytes it reads."""
+    from hffn_amd import bench_decode, synth
+    from hffn_amd.ffn import hip_layer
+    from hffn_amd.prepared_runtime import PreparedRuntime
+    from hffn_amd.runtime import HFFNRuntime
+
+    record = {"rotation": f"{rotations} passes over each layer's copies after one untimed pass; HIP events around all"}
+    copies = len(runtime.layers)
+    record["pythia410m_d50"] = [decode_entry(runtime, synth.WORKLOADS["pythia410m_d50"], base, n, copies, rotations, device)
+                                for n in DECODE_TOKENS["pythia410m_d50"]]
+    workload = synth.WORKLOADS["pythia1p4b_d20_bf16"]
+    compact = synth.make_workload_layer(workload)
+    count = max(1, math.ceil(MALL_BYTES / layer_costs(compact, 1)["model_bytes"]))
+    bf16 = HFFNRuntime(device_copies(hip_layer(compact, device), count), device)
+    record["pythia1p4b_d20_bf16"] = [decode_entry(bf16, workload, compact, n, count, rotations, device)
+                                     for n in DECODE_TOKENS["pythia1p4b_d20_bf16"]]
+    del bf16
+    layers = runtime.layers + device_copies(runtime.layers[0], DECODE_STEP_LAYERS - copies + 1)[1:]
+    model = PreparedRuntime(layers[:DECODE_STEP_LAYERS], device)
+    record["pythia410m_model_step"] = [bench_decode.measure(model, [base] * DECODE_STEP_LAYERS, batch, steps)
+                                       for batch in DECODE_STEP_BATCHES]
+    del model
+    torch.cuda.empty_cache()
+    return record
 
 
 def _child_json(arguments: list[str]) -> dict:
@@ -247,7 +324,15 @@ def main() -> int:
 
     for step in range(args.warmup):
         runtime.forward(step % copies, x)
+    for index in range(copies):  # every copy once, untimed: none is first used inside the timed steps
+        runtime.forward(index, x)
     torch.cuda.synchronize()
+    settle = time.perf_counter()
+    while time.perf_counter() - settle < args.settle_ms * 1e-3:  # untimed rotations until the clocks have ramped up
+        for index in range(copies):
+            runtime.forward(index, x)
+        torch.cuda.synchronize()
+    settle = time.perf_counter() - settle
     start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     wall = time.perf_counter()
     start.record()
@@ -260,6 +345,7 @@ def main() -> int:
     up, down = runtime.modes(n)
 
     kernels = time_kernels(runtime, x, max(20, min(args.steps, 200)), copies)
+    decode = None if args.no_decode else decode_record(runtime, base, device, args.decode_rotations, 50)
     dominant = max((k for k in kernels if k in ("up", "down", "gemv", "tiles")), key=kernels.get)
     cost = costs["gemv" if dominant == "tiles" else dominant]
     seconds_kernel = kernels[dominant]
@@ -304,6 +390,8 @@ def main() -> int:
         "dtype": "f32" if base.value_dtype == "float32" else "bf16-weights/f32-accumulate", "data": "synthetic",
         "config": {"workload": f"{workload.name}: isolated HFFN layer d_model={base.d_model} d_ff={base.d_ff}, "
                                f"{workload.degree}-slot supports, {n} tokens", "tokens": n, "copies": copies,
+                   "warmup_rotation": "after the warm-up steps, every copy called once untimed, then untimed "
+                                      f"rotations for {settle:.2f} s (clock ramp)",
                    "modes": [up, down], "kernel_us": {k: round(v * 1e6, 2) for k, v in kernels.items()},
                    "step_hbm_fraction": round(costs["step_bytes"] / (seconds / args.steps) / HBM_PEAK, 4),
                    "step_fp32_fraction": round(costs["step_flops"] / (seconds / args.steps) / FP32_PEAK, 4),
@@ -312,6 +400,7 @@ def main() -> int:
                    "wall_s": round(wall, 3)},
         "roofline": roofline,
         "cpu_baseline": baseline,
+        "decode": decode,
     }
     print(json.dumps(line), flush=True)
     if args.copy_probe_mb:

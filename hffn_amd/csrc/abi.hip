@@ -426,6 +426,24 @@ int hffn_mfma_up(int value_type, const float* x, const void* up_planes, const in
                                          static_cast<hipStream_t>(stream)), "mfma up");
 }
 
+int hffn_mfma_split(const float* x, void* workspace, uint64_t workspace_bytes, uint32_t d_model, uint32_t d_ff, uint32_t n,
+                    void* stream) {
+    if (int status = check_mfma(HFFN_VALUE_F32, d_model, d_ff, n)) return status;
+    if (!x || !workspace) return fail(HFFN_ERROR_ARGUMENT, "mfma_split: null pointer");
+    if (reinterpret_cast<uintptr_t>(x) % 16 != 0) return fail(HFFN_ERROR_ARGUMENT, "mfma_split: x must be 16-byte aligned");
+    if (int status = check_workspace(workspace_bytes, d_model, d_ff, n, "mfma_split")) return status;
+    return launched(hffn::launch_mfma_split(x, workspace, n, d_model, d_ff, static_cast<hipStream_t>(stream)), "mfma split");
+}
+
+int hffn_mfma_up_planes(int value_type, const void* up_planes, const int32_t* up_binades, const float* b_up, void* workspace,
+                        uint64_t workspace_bytes, uint32_t d_model, uint32_t d_ff, uint32_t n, void* stream) {
+    if (int status = check_mfma(value_type, d_model, d_ff, n)) return status;
+    if (!up_planes || !up_binades || !b_up || !workspace) return fail(HFFN_ERROR_ARGUMENT, "mfma_up_planes: null pointer");
+    if (int status = check_workspace(workspace_bytes, d_model, d_ff, n, "mfma_up_planes")) return status;
+    return launched(hffn::launch_mfma_up_planes(value_type, up_planes, up_binades, b_up, workspace, n, d_model, d_ff,
+                                                static_cast<hipStream_t>(stream)), "mfma up planes");
+}
+
 int hffn_mfma_down(int value_type, const void* down_planes, const int32_t* down_binades, const float* b_down, float* y,
                    void* workspace, uint64_t workspace_bytes, uint32_t d_model, uint32_t d_ff, uint32_t n, void* stream) {
     if (int status = check_mfma(value_type, d_model, d_ff, n)) return status;

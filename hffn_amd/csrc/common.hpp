@@ -95,4 +95,31 @@ __device__ __forceinline__ void load_vec(const float* p, float (&out)[N]) {
     }
 }
 
+// s_waitcnt vmcnt(N) lgkmcnt(0): at most N vector-memory loads of this wave still in flight, its LDS accesses done.
+template <int N>
+__device__ __forceinline__ void wait_loads() {
+    static_assert(N >= 0 && N < 64, "vmcnt is 6 bits");
+    __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | (7 << 4));
+}
+
+// 16 bytes per lane from global memory straight into LDS (global_load_lds_dwordx4): lane l reads base + offset_l
+// (base wave-uniform, in scalar registers; offset_l a 32-bit byte offset in a vector register) and its bytes land at
+// lds + 16 l. Inactive lanes transfer nothing. Written as inline assembly so that the compiler, which cannot tell the
+// transfers' LDS destinations apart, does not wait for every transfer in flight before each LDS read; the kernel
+// orders them itself (wait_loads, then a barrier).
+__device__ __forceinline__ void dma16(const void* base, uint32_t offset, const void* lds) {
+    const uint32_t to = static_cast<uint32_t>(__builtin_amdgcn_readfirstlane(
+        static_cast<int>(static_cast<uint32_t>(reinterpret_cast<uintptr_t>(lds)))));  // low 32 bits: the LDS address
+    asm volatile("s_mov_b32 m0, %2\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, %1" ::"v"(offset), "s"(base), "s"(to)
+                 : "memory", "m0");
+}
+
+// The same with 4 bytes per lane (lane l's land at lds + 4 l).
+__device__ __forceinline__ void dma4(const void* base, uint32_t offset, const void* lds) {
+    const uint32_t to = static_cast<uint32_t>(__builtin_amdgcn_readfirstlane(
+        static_cast<int>(static_cast<uint32_t>(reinterpret_cast<uintptr_t>(lds)))));
+    asm volatile("s_mov_b32 m0, %2\n\ts_nop 0\n\tglobal_load_lds_dword %0, %1" ::"v"(offset), "s"(base), "s"(to)
+                 : "memory", "m0");
+}
+
 }  // namespace hffn

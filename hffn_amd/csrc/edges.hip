@@ -13,181 +13,16 @@
 // Tokens are processed NT at a time (NT = 1, 2, 4 or 8); every activation and output is written by one lane: no
 // atomics, bitwise repeatable, and a token's result does not depend on the other tokens of the call.
 #include "common.hpp"
+#include "edges.hpp"
 #include "launch.hpp"
 
 namespace hffn {
 namespace {
 
+using namespace edges;
+
 constexpr uint32_t kBlock = 256;
 constexpr uint32_t kWaves = kBlock / kWave;
-
-template <typename V> struct Group;
-template <> struct Group<float> {
-    using type = float4;
-    __device__ static float at(const float4& g, int s) { return s == 0 ? g.x : s == 1 ? g.y : s == 2 ? g.z : g.w; }
-};
-template <> struct Group<uint16_t> {
-    using type = uint2;
-    __device__ static float at(const uint2& g, int s) {
-        const uint32_t word = s < 2 ? g.x : g.y;
-        return __uint_as_float((s % 2 == 0 ? word << 16 : word & 0xffff0000u));
-    }
-};
-
-__device__ __forceinline__ uint32_t index_at(const uint2& g, int s) {
-    const uint32_t word = s < 2 ? g.x : g.y;
-    return s % 2 == 0 ? (word & 0xffffu) : (word >> 16);
-}
-
-// Where a token's input for feature i lives: LDS [i][NT] (staged) or global [i * ld] + t (act of the down kernel).
-struct StagedInput {
-    const float* lds;
-    template <int NT> __device__ void load(uint32_t i, float (&v)[NT]) const { load_vec<NT>(lds + i * NT, v); }
-};
-struct GlobalInput {
-    const float* base;  // act + c0
-    uint32_t ld;
-    template <int NT> __device__ void load(uint32_t i, float (&v)[NT]) const {
-        load_vec<NT>(base + static_cast<size_t>(i) * ld, v);
-    }
-};
-
-// A wave's slots of one row segment [pb, pe), held in registers: up to G groups of 4 slots per lane, loaded before
-// the inputs are staged so that the store's bytes are in flight while the block waits for its inputs.
-template <typename V, int G>
-struct Segment {
-    typename Group<V>::type vals[G];
-    uint2 ids[G];
-    int32_t first;  // slot of this lane's group 0
-};
-
-// Issues the loads of groups [chunk * G, chunk * G + G) of this lane (4-slot groups strided by the wave); groups
-// that cross nnz, or lie past pe, are loaded slot by slot or left empty.
-template <typename V, int G>
-__device__ __forceinline__ void load_segment(Segment<V, G>& seg, const int16_t* __restrict__ idx, const V* __restrict__ val,
-                                             int32_t pb, int32_t pe, int32_t nnz, uint32_t lane, uint32_t chunk) {
-    seg.first = (pb & ~3) + 4 * static_cast<int32_t>(lane) + static_cast<int32_t>(chunk) * G * 4 * kWave;
-#pragma unroll
-    for (int k = 0; k < G; ++k) {
-        const int32_t g = seg.first + k * 4 * kWave;
-        if (g < pe && g + 4 <= nnz) {
-            seg.vals[k] = *reinterpret_cast<const typename Group<V>::type*>(val + g);
-            seg.ids[k] = *reinterpret_cast<const uint2*>(idx + g);
-        } else if (g < pe) {
-            // the store's last group: pack the slots below nnz by hand
-            uint16_t i4[4] = {0, 0, 0, 0};
-            V v4[4] = {V(0), V(0), V(0), V(0)};
-            for (int s = 0; s < 4; ++s)
-                if (g + s < nnz) {
-                    i4[s] = static_cast<uint16_t>(idx[g + s]);
-                    v4[s] = val[g + s];
-                }
-            seg.ids[k] = make_uint2(i4[0] | (static_cast<uint32_t>(i4[1]) << 16), i4[2] | (static_cast<uint32_t>(i4[3]) << 16));
-            seg.vals[k] = *reinterpret_cast<const typename Group<V>::type*>(v4);
-        }
-    }
-}
-
-template <int NT, typename V, int G, typename Input>
-__device__ __forceinline__ void accumulate_segment(const Segment<V, G>& seg, int32_t pb, int32_t pe, const Input& input,
-                                                   float (&acc)[NT]) {
-#pragma unroll
-    for (int k = 0; k < G; ++k) {
-        const int32_t g = seg.first + k * 4 * kWave;
-        if (g < pe) {
-#pragma unroll
-            for (int s = 0; s < 4; ++s) {
-                if (g + s >= pb && g + s < pe) {
-                    float xv[NT];
-                    input.template load<NT>(index_at(seg.ids[k], s), xv);
-                    const float w = Group<V>::at(seg.vals[k], s);
-#pragma unroll
-                    for (int t = 0; t < NT; ++t) acc[t] = fmaf(w, xv[t], acc[t]);
-                }
-            }
-        }
-    }
-}
-
-// Groups per lane held at once (768 slots per wave); longer segments take several chunks.
-constexpr int kGroups = 3;
-
-// Partial sums of one wave over slots [pb, pe) of a row, NT tokens: the first chunk's loads come from `first`
-// (issued by the caller before the inputs were staged); the next chunks are loaded here.
-template <int NT, typename V, typename Input>
-__device__ __forceinline__ void row_partials(const Segment<V, kGroups>& first, const int16_t* __restrict__ idx,
-                                             const V* __restrict__ val, int32_t pb, int32_t pe, int32_t nnz,
-                                             const Input& input, uint32_t lane, float (&acc)[NT]) {
-#pragma unroll
-    for (int t = 0; t < NT; ++t) acc[t] = 0.0f;
-    accumulate_segment<NT>(first, pb, pe, input, acc);
-    const int32_t span = kGroups * 4 * kWave;
-    for (uint32_t chunk = 1; (pb & ~3) + static_cast<int32_t>(chunk) * span < pe; ++chunk) {
-        Segment<V, kGroups> seg;
-        load_segment(seg, idx, val, pb, pe, nnz, lane, chunk);
-        accumulate_segment<NT>(seg, pb, pe, input, acc);
-    }
-}
-
-// Adds the wave's lane partials, then (P > 1) the block's P segment totals of the row in segment order; returns, in
-// lane t < NT of the row's first wave, the row total of token t (other lanes: unspecified).
-template <int NT, int P>
-__device__ __forceinline__ float row_total(float (&acc)[NT], uint32_t lane, uint32_t part, uint32_t row_in_block,
-                                           float* __restrict__ totals /* LDS [kWaves][NT] */) {
-    float mine = 0.0f;
-#pragma unroll
-    for (int t = 0; t < NT; ++t) {
-        const float s = wave_sum(acc[t]);
-        if (lane == static_cast<uint32_t>(t)) mine = s;
-    }
-    if constexpr (P > 1) {
-        const uint32_t wave = row_in_block * P + part;
-        if (lane < NT) totals[wave * NT + lane] = mine;
-        __syncthreads();
-        if (part == 0 && lane < NT) {
-            float s = totals[(row_in_block * P) * NT + lane];
-#pragma unroll
-            for (int p = 1; p < P; ++p) s += totals[(row_in_block * P + p) * NT + lane];
-            mine = s;
-        }
-        __syncthreads();
-    }
-    return mine;
-}
-
-// Segment [pb, pe) of part `part` of a row [begin, end) split in P: the parts cut the row on the 4-slot grid, so
-// each starts on a group boundary and no group is shared by two waves.
-template <int P>
-__device__ __forceinline__ void segment(int32_t begin, int32_t end, uint32_t part, int32_t& pb, int32_t& pe) {
-    if constexpr (P == 1) {
-        pb = begin;
-        pe = end;
-    } else {
-        const int32_t base = begin & ~3;
-        const int32_t seg = ((end - base + P - 1) / P + 3) & ~3;
-        const int32_t start = base + static_cast<int32_t>(part) * seg;
-        pb = max(begin, min(end, start));
-        pe = min(end, start + seg);
-    }
-}
-
-// A wave's first chunk of one row segment, requested ahead of its use.
-template <typename V>
-struct Slots {
-    Segment<V, kGroups> seg;
-    int32_t pb = 0, pe = 0;  // empty unless requested
-};
-
-// Requests the first chunk of part `part` of row r (nothing when r >= rows).
-template <int P, typename V>
-__device__ __forceinline__ void request_row(Slots<V>& s, const int32_t* __restrict__ off, const int16_t* __restrict__ idx,
-                                            const V* __restrict__ val, uint32_t r, uint32_t rows, uint32_t part, int32_t nnz,
-                                            uint32_t lane) {
-    if (r < rows) {
-        segment<P>(off[r], off[r + 1], part, s.pb, s.pe);
-        load_segment(s.seg, idx, val, s.pb, s.pe, nnz, lane, 0);
-    }
-}
 
 // ------------------------------------------------------------------------------------------------- up
 template <int NT, int P, typename V, int WAVES, bool GRAD = false>

@@ -85,7 +85,10 @@ size_t mfma_workspace_bytes(uint32_t n, uint32_t d, uint32_t h);
 hipError_t launch_densify(int vt, const int32_t* off, const int16_t* idx, const void* val, uint32_t rows, uint32_t k,
                           void* planes, int32_t* exps, hipStream_t stream);
 hipError_t launch_mfma_up(int vt, const float* x, const void* planes, const int32_t* w_exp, const float* b_up, void* workspace,
-                          uint32_t n, uint32_t d, uint32_t h, hipStream_t stream);
+                          uint32_t n, uint32_t d, uint32_t h, hipStream_t stream);  // launch_mfma_split, then launch_mfma_up_planes
+hipError_t launch_mfma_split(const float* x, void* workspace, uint32_t n, uint32_t d, uint32_t h, hipStream_t stream);
+hipError_t launch_mfma_up_planes(int vt, const void* planes, const int32_t* w_exp, const float* b_up, void* workspace, uint32_t n,
+                                 uint32_t d, uint32_t h, hipStream_t stream);
 hipError_t launch_mfma_down(int vt, const void* planes, const int32_t* v_exp, const float* b_down, float* y, void* workspace,
                             uint32_t n, uint32_t d, uint32_t h, hipStream_t stream);
 

@@ -637,33 +637,6 @@ constexpr int kDmaBM = 256, kDmaBN = 128;
 constexpr int kDmaWaves = 8;  // waves per block: two per SIMD, 64 x 64 outputs each
 constexpr uint32_t kDmaMaxActBlocks = 40;  // activation blocks of one down split held in LDS (int8 binades)
 
-// s_waitcnt vmcnt(N) lgkmcnt(0): at most N vector-memory loads of this wave still in flight, its LDS accesses done.
-template <int N>
-__device__ __forceinline__ void wait_loads() {
-    static_assert(N >= 0 && N < 64, "vmcnt is 6 bits");
-    __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | (7 << 4));
-}
-
-// 16 bytes per lane from global memory straight into LDS: lane l reads base + offset_l (base wave-uniform, in scalar
-// registers; offset_l a 32-bit byte offset in a vector register, the piece's offset plus 16 l, computed once) and its
-// bytes land at lds + 16 l. Written as inline assembly so that the compiler, which cannot tell the ring slots apart,
-// does not wait for every transfer in flight before each LDS read; the kernel orders them itself (wait_loads, then a
-// barrier).
-__device__ __forceinline__ void dma16(const void* base, uint32_t offset, const void* lds) {
-    const uint32_t to = static_cast<uint32_t>(__builtin_amdgcn_readfirstlane(
-        static_cast<int>(static_cast<uint32_t>(reinterpret_cast<uintptr_t>(lds)))));  // low 32 bits: the LDS address
-    asm volatile("s_mov_b32 m0, %2\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, %1" ::"v"(offset), "s"(base), "s"(to)
-                 : "memory", "m0");
-}
-
-// The same with 4 bytes per lane (lane l's land at lds + 4 l).
-__device__ __forceinline__ void dma4(const void* base, uint32_t offset, const void* lds) {
-    const uint32_t to = static_cast<uint32_t>(__builtin_amdgcn_readfirstlane(
-        static_cast<int>(static_cast<uint32_t>(reinterpret_cast<uintptr_t>(lds)))));
-    asm volatile("s_mov_b32 m0, %2\n\ts_nop 0\n\tglobal_load_lds_dword %0, %1" ::"v"(offset), "s"(base), "s"(to)
-                 : "memory", "m0");
-}
-
 // Workgroup barrier without the memory fence of __syncthreads (whose release would also wait for every LDS DMA in
 // flight); LDS visibility is ensured by the wait_loads before it.
 __device__ __forceinline__ void block_barrier() {
@@ -1486,16 +1459,28 @@ hipError_t launch_densify(int vt, const int32_t* off, const int16_t* idx, const 
     return hipGetLastError();
 }
 
+hipError_t launch_mfma_split(const float* x, void* workspace, uint32_t n, uint32_t d, uint32_t h, hipStream_t stream) {
+    const Workspace w = workspace_layout(n, d, h);
+    int32_t* words = static_cast<int32_t*>(workspace);
+    auto* x_planes = reinterpret_cast<_Float16*>(static_cast<char*>(workspace) + w.x_planes);
+    hipLaunchKernelGGL(split_rows_kernel, dim3(rows_live(n) / kSplitBlockRows), dim3(kThreads), 0, stream, x, n, rows_padded(n), d, d,
+                       d, x_planes, words + w.x_binades);  // 8 rows per block
+    return hipGetLastError();
+}
+
 hipError_t launch_mfma_up(int vt, const float* x, const void* planes, const int32_t* w_exp, const float* b_up, void* workspace,
                           uint32_t n, uint32_t d, uint32_t h, hipStream_t stream) {
+    if (hipError_t status = launch_mfma_split(x, workspace, n, d, h, stream); status != hipSuccess) return status;
+    return launch_mfma_up_planes(vt, planes, w_exp, b_up, workspace, n, d, h, stream);
+}
+
+hipError_t launch_mfma_up_planes(int vt, const void* planes, const int32_t* w_exp, const float* b_up, void* workspace, uint32_t n,
+                                 uint32_t d, uint32_t h, hipStream_t stream) {
     const Workspace w = workspace_layout(n, d, h);
     int32_t* words = static_cast<int32_t*>(workspace);
     char* bytes = static_cast<char*>(workspace);
     auto* x_planes = reinterpret_cast<_Float16*>(bytes + w.x_planes);
     auto* act_planes = reinterpret_cast<_Float16*>(bytes + w.act_planes);
-    hipLaunchKernelGGL(split_rows_kernel, dim3(rows_live(n) / kSplitBlockRows), dim3(kThreads), 0, stream, x, n, rows_padded(n), d, d,
-                       d, x_planes, words + w.x_binades);  // 8 rows per block
-    if (hipError_t status = hipGetLastError(); status != hipSuccess) return status;
     const auto* p = static_cast<const _Float16*>(planes);
     if (const uint32_t splits = dma_up_splits(n, h, d); splits > 1) {
         float* partials = reinterpret_cast<float*>(bytes + w.partials);

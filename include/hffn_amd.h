@@ -27,7 +27,7 @@
 extern "C" {
 #endif
 
-#define HFFN_ABI_VERSION 14
+#define HFFN_ABI_VERSION 15
 
 #define HFFN_OK 0
 #define HFFN_ERROR_ARGUMENT (-1) /* invalid shape, mode, pointer or workspace */
@@ -150,6 +150,14 @@ int hffn_mfma_workspace(uint32_t n, uint32_t d_model, uint32_t d_ff, uint64_t* b
  * 128-neuron block (read by hffn_mfma_down); also splits x (16-byte aligned) into the workspace. */
 int hffn_mfma_up(int value_type, const float* x, const void* up_planes, const int32_t* up_binades, const float* b_up,
                  void* workspace, uint64_t workspace_bytes, uint32_t d_model, uint32_t d_ff, uint32_t n, void* stream);
+
+/* The two halves of hffn_mfma_up, for callers that time or reuse them apart (no reference counterpart):
+ * hffn_mfma_split splits x (16-byte aligned) into the workspace's token planes and binades; hffn_mfma_up_planes runs
+ * the up GEMM on them (act as hffn_mfma_up leaves it). hffn_mfma_up = hffn_mfma_split, then hffn_mfma_up_planes. */
+int hffn_mfma_split(const float* x, void* workspace, uint64_t workspace_bytes, uint32_t d_model, uint32_t d_ff, uint32_t n,
+                    void* stream);
+int hffn_mfma_up_planes(int value_type, const void* up_planes, const int32_t* up_binades, const float* b_up, void* workspace,
+                        uint64_t workspace_bytes, uint32_t d_model, uint32_t d_ff, uint32_t n, void* stream);
 
 /* y[t, o] = sum_r W_down[o, r] act[t, r] + b_down[o], y token-major [n, d_model]; the activations as left in the
  * workspace by hffn_mfma_up for the same n. */

@@ -147,9 +147,11 @@ def test_forced_pairs_match_the_oracle(name, test_layers, device):
         expected = torch.from_numpy(reference.forward(compact, x_np)).to(device)
         result = parity.check(runtime, 0, torch.from_numpy(x_np).to(device), expected)
         assert result.repeatable, f"{name} N{n}: bits differ on repeat"
+        assert result.sequential_bits, f"{name} N{n}: the sequential pair depends on the batch"
         assert result.error <= ATOL, f"{name} N{n}: {result.pairs}"
     skipped = 2 * sum(n > GEMV_MAX_TOKENS for n in BATCHES)  # the decode GEMVs and the tiles path take at most 64 tokens
-    assert sum(runtime.calls.values()) == 2 * (len(BATCHES) * len(parity.PAIRS) - skipped)
+    halves = 2 * sum(n >= 2 for n in BATCHES)  # the sequential pair also runs the input's two halves
+    assert sum(runtime.calls.values()) == 2 * (len(BATCHES) * len(parity.PAIRS) - skipped) + halves
 
 
 def test_shared_buffers_between_calls(test_layers, device):

@@ -85,7 +85,7 @@ def test_pythia410m_export_layer_parity(index, leaf_runtime, device):
         x = generator.standard_normal((n, compact.d_model)).astype(np.float32)
         expected = torch.from_numpy(reference.forward_dense(compact, x, weights)).to(device)
         result = parity.check(runtime, index, torch.from_numpy(x).to(device), expected)
-        assert result.repeatable, f"layer {index} N{n}: bits differ on repeat"
+        assert result.repeatable and result.sequential_bits, f"layer {index} N{n}: bits differ on repeat"
         worst[n] = result.relative
         assert result.relative <= 1e-5, (index, n, result.pairs)
     print(f"layer {index}: max relative " + " ".join(f"N{n}={e:.1e}" for n, e in worst.items()), flush=True)

@@ -334,3 +334,4 @@ def test_parity_result_reads_as_the_reference_callers_read_it():
     assert steady.repeatable and steady.sequential_bits and steady.error == 0.0
     assert runtime.COOP_MAX_TOKENS == runtime.EDGES_MAX_TOKENS
     assert runtime.BLOCK_MAX_WIDTH == 32768 and runtime.MAX_TOKENS == 1 << 18
+
