@@ -8,10 +8,11 @@ Arms: ``hffn`` and ``hffn_copy`` (two ``HFFNRuntime`` of the same layer), ``dens
 ``F.linear -> gelu -> F.linear`` in float32 on dense weights holding the support's values and zeros elsewhere). One
 fresh process per session (``--worker``), all cells in it. A window is ``repeats`` calls of one arm on one resident
 input between two synchronisations (host wall time), after an untimed window of the same arm; a block is eight
-windows in one of the two orders, each arm twice with equal time centroid. Per cell: every arm's output within 2e-5
-of the float64 dense result computed here, the copies bitwise equal, memory steady. A/A: every cell-session's
-hffn/hffn_copy and dense/dense_copy ratio of medians within 3 %, else the session grid is not admissible and no ratio
-is read. One JSON line per cell and a summary line.
+windows in one of the two orders, each arm twice with equal time centroid. ``repeats`` makes the slowest arm's window
+last the grid's window time. The worker reports every timed window as one observation (block, slot, arm, µs); the
+summary groups them. Per cell: every arm's output within 2e-5 of the float64 dense result computed here, the copies
+bitwise equal, memory steady. A/A: every cell-session's hffn/hffn_copy and dense/dense_copy ratio of medians within
+3 %, else the session grid is not admissible and no ratio is read. One JSON line per cell and a summary line.
 """
 from __future__ import annotations
 
@@ -65,95 +66,137 @@ def load_cell(name: str):
     return synth.make_workload_layer(workload), workload, synth.make_input
 
 
-def window(fn, repeats: int) -> float:
-    """Milliseconds of `repeats` calls between two synchronisations."""
-    import torch
-    torch.cuda.synchronize()
-    start = time.perf_counter_ns()
-    for _ in range(repeats):
-        fn()
-    torch.cuda.synchronize()
-    return (time.perf_counter_ns() - start) / 1e6
+ARMS = ("hffn", "hffn_copy", "dense", "dense_copy")
+
+
+def schedule() -> list[tuple[int, int, str]]:
+    """(block, slot, arm) of every timed window of a cell: the blocks of ``BLOCK_ORDERS`` one after the other."""
+    return [(block, slot, arm) for block, order in enumerate(BLOCK_ORDERS) for slot, arm in enumerate(order)]
+
+
+class LayerCell:
+    """One (layer, N) cell in a worker: the input on the device, its float64 expectation, and the four arms as
+    callables (two HFFNRuntime of the same layer; two dense iso-support PyTorch layers)."""
+
+    def __init__(self, name: str, n: int, device) -> None:
+        import torch
+        import torch.nn.functional as F
+
+        from .ffn import hip_layer
+        from .runtime import HFFNRuntime
+
+        self.name, self.n = name, n
+        layer, case, make_input = load_cell(name)
+        x_np = make_input(case, n)
+        w_up, w_down = dense_weights(layer)
+        self.expected = torch.from_numpy(float64_forward(layer, x_np, w_up, w_down)).to(device)
+        self.x = torch.from_numpy(x_np).to(device)
+        self.runtimes = [HFFNRuntime([hip_layer(layer, device)], device) for _ in range(2)]
+        dense = [tuple(torch.from_numpy(np.ascontiguousarray(a)).to(device) for a in (w_up, layer.b_up, w_down, layer.b_down))
+                 for _ in range(2)]
+        x = self.x
+        self.arms = {
+            "hffn": lambda: self.runtimes[0].forward(0, x),
+            "hffn_copy": lambda: self.runtimes[1].forward(0, x),
+            "dense": lambda p=dense[0]: F.linear(F.gelu(F.linear(x, p[0], p[1]), approximate="none"), p[2], p[3]),
+            "dense_copy": lambda p=dense[1]: F.linear(F.gelu(F.linear(x, p[0], p[1]), approximate="none"), p[2], p[3]),
+        }
+        self.record = {"layer": name, "n": n, "modes": list(self.runtimes[0].modes(n)),
+                       "model_bytes": self.runtimes[0].layers[0].model_bytes(),
+                       "workspace_bytes": self.runtimes[0].workspace_bytes(),
+                       "dense_weight_bytes": 4 * 2 * layer.d_model * layer.d_ff}
+
+    def gates(self) -> dict:
+        """Before any timing: every arm within TOLERANCE of the float64 layer (relative to max(1, max |y64|)), and the
+        two HFFN runtimes bitwise equal."""
+        import torch
+        out = {arm: fn().clone() for arm, fn in self.arms.items()}
+        scale = float(self.expected.abs().max().clamp(min=1.0))
+        errors = {arm: float((y.double() - self.expected).abs().max()) / scale for arm, y in out.items()}
+        self.record["errors"] = errors
+        return {"oracle": max(errors.values()) <= TOLERANCE, "copy_bitwise": bool(torch.equal(out["hffn"], out["hffn_copy"]))}
+
+    def window_us(self, arm: str, repeats: int) -> float:
+        """µs per call over ``repeats`` calls of ``arm`` between two synchronisations (host wall clock)."""
+        import torch
+        fn = self.arms[arm]
+        torch.cuda.synchronize()
+        began = time.perf_counter_ns()
+        for _ in range(repeats):
+            fn()
+        torch.cuda.synchronize()
+        return (time.perf_counter_ns() - began) / repeats / 1e3
+
+    def repeats_for(self, window_ms: float) -> int:
+        """Calls per window: enough that the slowest arm's window lasts ``window_ms`` (its single-call time is the best
+        of three after a warm-up call of every arm), so that no arm's window is shorter."""
+        for arm in ARMS:
+            self.window_us(arm, 1)
+        slowest = max(min(self.window_us(arm, 1) for _ in range(3)) for arm in ARMS)
+        return max(1, min(MAX_REPEATS, math.ceil(window_ms * 1e3 / slowest)))
+
+    def observe(self, repeats: int) -> list[dict]:
+        """The schedule's windows, each after an untimed window of the same arm: one observation per timed window."""
+        rows = []
+        for block, slot, arm in schedule():
+            self.window_us(arm, repeats)
+            rows.append({"block": block, "slot": slot, "arm": arm, "us": self.window_us(arm, repeats)})
+        return rows
 
 
 def worker(job: dict) -> int:
+    """One session: every cell of the job in this process, one JSON line per cell (gates, then the observations)."""
     import torch
-    import torch.nn.functional as F
-
-    from .ffn import hip_layer
-    from .runtime import HFFNRuntime
-
     device = torch.device("cuda", 0)
     print(json.dumps({"event": "session", "session": job["session"]}), flush=True)
     with torch.inference_mode():
         for name, n in job["cells"]:
-            layer, case, make_input = load_cell(name)
-            x_np = make_input(case, n)
-            x = torch.from_numpy(x_np).to(device)
-            w_up, w_down = dense_weights(layer)
-            expected = torch.from_numpy(float64_forward(layer, x_np, w_up, w_down)).to(device)
-
-            def dense_arm():
-                wu, wd = torch.from_numpy(w_up).to(device), torch.from_numpy(w_down).to(device)
-                bu, bd = torch.from_numpy(layer.b_up.copy()).to(device), torch.from_numpy(layer.b_down.copy()).to(device)
-                return lambda: F.linear(F.gelu(F.linear(x, wu, bu), approximate="none"), wd, bd)
-
-            runtimes = [HFFNRuntime([hip_layer(layer, device)], device) for _ in range(2)]
-            arms = {"dense": dense_arm(), "dense_copy": dense_arm(),
-                    "hffn": lambda: runtimes[0].forward(0, x), "hffn_copy": lambda: runtimes[1].forward(0, x)}
-            outputs = {arm: fn().clone() for arm, fn in arms.items()}
-            scale = float(expected.abs().max().clamp(min=1.0))
-            errors = {arm: float((y.double() - expected).abs().max()) / scale for arm, y in outputs.items()}
-            gates = {"oracle": all(e <= TOLERANCE for e in errors.values()),
-                     "copy_bitwise": bool(torch.equal(outputs["hffn"], outputs["hffn_copy"]))}
-            for _ in range(3):
-                for fn in arms.values():
-                    fn()
+            cell = LayerCell(name, n, device)
+            gates = cell.gates()
+            repeats = cell.repeats_for(job["window_ms"])
             torch.cuda.synchronize()
-            allocated = torch.cuda.memory_allocated()
-            once = min(window(arms["dense"], 1) for _ in range(3))
-            repeats = min(MAX_REPEATS, max(1, math.ceil(job["window_ms"] / once)))
-            samples = {arm: [] for arm in arms}
-            for order in BLOCK_ORDERS:
-                for arm in order:
-                    window(arms[arm], repeats)  # untimed lead-in of the same arm
-                    samples[arm].append(window(arms[arm], repeats) / repeats * 1e3)  # µs per call
-            gates["memory_steady"] = torch.cuda.memory_allocated() == allocated
-            print(json.dumps({"event": "cell", "session": job["session"], "layer": name, "n": n, "repeats": repeats,
-                              "samples_us": samples, "errors": errors, "gates": gates, "modes": list(runtimes[0].modes(n)),
-                              "model_bytes": runtimes[0].layers[0].model_bytes(),
-                              "dense_weight_bytes": 4 * 2 * layer.d_model * layer.d_ff}), flush=True)
-            del arms, runtimes, outputs
+            held = torch.cuda.memory_allocated()
+            observations = cell.observe(repeats)
+            gates["memory_steady"] = torch.cuda.memory_allocated() == held
+            print(json.dumps({"event": "cell", "session": job["session"], **cell.record, "repeats": repeats, "gates": gates,
+                              "observations": observations}), flush=True)
+            del cell
             torch.cuda.empty_cache()
     print(json.dumps({"event": "session_end", "session": job["session"]}), flush=True)
     return 0
 
 
-def median_ratio(samples: dict, a: str, b: str) -> float:
-    return statistics.median(samples[a]) / statistics.median(samples[b])
+def arm_medians(cell: dict) -> dict:
+    """Median µs per call of each arm over a cell-session's observations."""
+    by_arm: dict = {}
+    for row in cell["observations"]:
+        by_arm.setdefault(row["arm"], []).append(row["us"])
+    return {arm: statistics.median(values) for arm, values in by_arm.items()}
 
 
 def summarise(cells: list[dict]) -> dict:
-    """A/A verdict over every cell-session, then (when admissible) the HFFN/dense ratios per cell."""
-    aa = {pair: [median_ratio(c["samples_us"], pair, f"{pair}_copy") for c in cells] for pair in ("hffn", "dense")}
-    verdict = {pair: {"within": sum(abs(v - 1) <= AA_TOLERANCE for v in values), "of": len(values),
-                      "max_abs_dev": round(max((abs(v - 1) for v in values), default=1.0), 4)} for pair, values in aa.items()}
-    gates = all(all(c["gates"].values()) for c in cells)
-    admissible = bool(cells) and gates and all(v["within"] == v["of"] for v in verdict.values())
-    rows = {}
-    for c in cells:
-        rows.setdefault((c["layer"], c["n"]), []).append(c)
-    out = []
-    for (layer, n), entries in rows.items():
-        row = {"layer": layer, "n": n, "sessions": len(entries), "modes": entries[0]["modes"]}
+    """Per cell-session, the arm medians; A/A (each arm over its copy) must hold within AA_TOLERANCE in every
+    cell-session, and every gate must pass, before any HFFN/dense ratio is reported (median, min and max over the
+    sessions of each cell)."""
+    table = [{"key": (c["layer"], c["n"]), "modes": c["modes"], "gates": c["gates"], **arm_medians(c)} for c in cells]
+    deviations = {pair: [abs(t[pair] / t[f"{pair}_copy"] - 1.0) for t in table] for pair in ("hffn", "dense")}
+    aa = {pair: {"within": sum(d <= AA_TOLERANCE for d in devs), "of": len(devs), "max_abs_dev": round(max(devs, default=1.0), 4)}
+          for pair, devs in deviations.items()}
+    gates = all(all(t["gates"].values()) for t in table)
+    admissible = bool(table) and gates and all(v["within"] == v["of"] for v in aa.values())
+    keys = list(dict.fromkeys(t["key"] for t in table))
+    rows = []
+    for key in keys:
+        sessions = [t for t in table if t["key"] == key]
+        row = {"layer": key[0], "n": key[1], "sessions": len(sessions), "modes": sessions[0]["modes"]}
         if admissible:
-            ratios = [median_ratio(e["samples_us"], "hffn", "dense") for e in entries]
-            row["hffn_over_dense"] = {"median": round(statistics.median(ratios), 4), "min": round(min(ratios), 4),
-                                      "max": round(max(ratios), 4)}
-            row["hffn_us"] = round(statistics.median(statistics.median(e["samples_us"]["hffn"]) for e in entries), 2)
-            row["dense_us"] = round(statistics.median(statistics.median(e["samples_us"]["dense"]) for e in entries), 2)
-        out.append(row)
-    return {"event": "summary", "aa": verdict, "gates": gates, "admissible": admissible, "cells": out}
+            ratios = sorted(t["hffn"] / t["dense"] for t in sessions)
+            row["hffn_over_dense"] = {"median": round(statistics.median(ratios), 4), "min": round(ratios[0], 4),
+                                      "max": round(ratios[-1], 4)}
+            row["hffn_us"] = round(statistics.median(t["hffn"] for t in sessions), 2)
+            row["dense_us"] = round(statistics.median(t["dense"] for t in sessions), 2)
+        rows.append(row)
+    return {"event": "summary", "aa": aa, "gates": gates, "admissible": admissible, "cells": rows}
 
 
 def parse_cells(text: str) -> list[tuple[str, int]]:
@@ -188,8 +231,7 @@ def main(argv: list[str] | None = None) -> int:
                 lines.append(record)
                 if record["event"] == "cell":
                     print(json.dumps({k: record[k] for k in ("session", "layer", "n", "repeats", "gates", "modes")}
-                                     | {"median_us": {a: round(statistics.median(v), 2) for a, v in record["samples_us"].items()}}),
-                          flush=True)
+                                     | {"median_us": {a: round(v, 2) for a, v in arm_medians(record).items()}}), flush=True)
         if result.returncode != 0:
             print(result.stderr[-2000:], file=sys.stderr)
             return result.returncode
