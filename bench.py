@@ -147,8 +147,7 @@ def time_kernels(runtime, x: torch.Tensor, steps: int, copies: int) -> dict:
             events = [torch.cuda.Event(enable_timing=True) for _ in range(2)]
             events[0].record()
             if up == "tiles":
-                _lib.check(lib.hffn_forward_tiles(value_type, x.data_ptr(), *runtime._tiles_args(index), runtime.d_model,
-                                                  runtime.d_ff, *runtime._nnz[index], n, stream), "tiles")
+                runtime._tiles_forward(index, x, n, stream)
             else:
                 planes, tensors = runtime._planes[index], runtime._tensors[index]
                 _lib.check(lib.hffn_forward_gemv(value_type, x.data_ptr(), planes["up"].data_ptr(), planes["up_binades"].data_ptr(),

@@ -10,7 +10,7 @@ import ctypes
 from pathlib import Path
 
 LIBRARY = Path(__file__).resolve().with_name("libhffn_amd.so")
-ABI_VERSION = 15
+ABI_VERSION = 16
 
 OK = 0
 VALUE_F32, VALUE_BF16 = 0, 1
@@ -52,6 +52,10 @@ SIGNATURES = {
     "hffn_mfma_streamed": [_U32, _U32, _U32],
     "hffn_mfma_up": [_I, _P, _P, _P, _P, _P, _U64, _U32, _U32, _U32, _P],
     "hffn_mfma_split": [_P, _P, _U64, _U32, _U32, _U32, _P],
+    "hffn_tiles_table_size": [_I, _U32, _U32, ctypes.POINTER(_U64)],
+    "hffn_tiles_table_build": [_I, _P, _P, _P, _U32, _U32, _P, _P],
+    "hffn_forward_tiles_compact": [_I] + [_P] * 11 + [_U64, _P, _U32, _U32, _U64, _U64, _U32, _P],
+    "hffn_plan_tiles_compact": [_I] + [_P] * 10 + [_U64, _P, _U32, _U32, _U64, _U64, _U32, ctypes.POINTER(_U64)],
     "hffn_mfma_up_planes": [_I, _P, _P, _P, _P, _U64, _U32, _U32, _U32, _P],
     "hffn_mfma_down": [_I, _P, _P, _P, _P, _P, _U64, _U32, _U32, _U32, _P],
     "hffn_forward_mfma": [_I] + [_P] * 8 + [_U64, _P] + [_U32] * 3 + [_P],

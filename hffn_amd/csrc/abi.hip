@@ -213,7 +213,7 @@ int check_tiles(int value_type, uint32_t d_model, uint32_t d_ff, uint32_t n) {
 
 struct TilesPlan {
     int value_type;
-    const void* up_store;
+    const void* up_store;  // the tiled stores; null for a plan on the compact rows
     const int32_t* up_table;
     const float* b_up;
     const void* down_store;
@@ -226,15 +226,24 @@ struct TilesPlan {
     uint32_t d_model, d_ff;
     uint64_t nnz_up, nnz_down;
     uint32_t n;
+    const int16_t* up_idx = nullptr;  // the compact rows (hffn_forward_tiles_compact)
+    const void* up_val = nullptr;
+    const int16_t* out_hidden = nullptr;
+    const void* out_val = nullptr;
 };
 
 int check_tiles_call(const TilesPlan& p, const float* x) {
     if (int status = check_tiles(p.value_type, p.d_model, p.d_ff, p.n)) return status;
-    if (!x || !p.up_store || !p.up_table || !p.b_up || !p.down_store || !p.down_table || !p.b_down || !p.act || !p.workspace || !p.y)
+    const bool compact = p.up_idx != nullptr;
+    if (!x || !p.up_table || !p.b_up || !p.down_table || !p.b_down || !p.act || !p.workspace || !p.y ||
+        (compact ? !p.up_val || !p.out_hidden || !p.out_val : !p.up_store || !p.down_store))
         return fail(HFFN_ERROR_ARGUMENT, "forward_tiles: null pointer");
     if (reinterpret_cast<uintptr_t>(x) % 16 != 0 || reinterpret_cast<uintptr_t>(p.act) % 16 != 0)
         return fail(HFFN_ERROR_ARGUMENT, "forward_tiles: x and act must be 16-byte aligned");
-    if (reinterpret_cast<uintptr_t>(p.up_store) % 16 != 0 || reinterpret_cast<uintptr_t>(p.down_store) % 16 != 0)
+    if (compact && (reinterpret_cast<uintptr_t>(p.up_idx) % 16 != 0 || reinterpret_cast<uintptr_t>(p.up_val) % 16 != 0 ||
+                    reinterpret_cast<uintptr_t>(p.out_hidden) % 16 != 0 || reinterpret_cast<uintptr_t>(p.out_val) % 16 != 0))
+        return fail(HFFN_ERROR_ARGUMENT, "forward_tiles_compact: the index and value arrays must be 16-byte aligned");
+    if (!compact && (reinterpret_cast<uintptr_t>(p.up_store) % 16 != 0 || reinterpret_cast<uintptr_t>(p.down_store) % 16 != 0))
         return fail(HFFN_ERROR_ARGUMENT, "forward_tiles: the tiled stores must be 16-byte aligned");
     if (p.nnz_up > static_cast<uint64_t>(p.d_model) * p.d_ff || p.nnz_down > static_cast<uint64_t>(p.d_model) * p.d_ff)
         return fail(HFFN_ERROR_ARGUMENT, "forward_tiles: nnz_up=%llu / nnz_down=%llu beyond d_model * d_ff",
@@ -247,6 +256,11 @@ int check_tiles_call(const TilesPlan& p, const float* x) {
 }
 
 int launch_tiles(const TilesPlan& p, const float* x, hipStream_t stream) {
+    if (p.up_idx)
+        return launched(hffn::launch_tiles_compact(p.value_type, x, p.up_idx, p.up_val, p.up_table, p.b_up, p.out_hidden, p.out_val,
+                                                   p.down_table, p.b_down, p.act, static_cast<float*>(p.workspace), p.y, p.d_model,
+                                                   p.d_ff, p.nnz_up, p.nnz_down, p.n, stream),
+                        "forward (tiles, compact rows)");
     return launched(hffn::launch_tiles_forward(p.value_type, x, p.up_store, p.up_table, p.b_up, p.down_store, p.down_table, p.b_down,
                                                p.act, static_cast<float*>(p.workspace), p.y, p.d_model, p.d_ff, p.nnz_up, p.nnz_down,
                                                p.n, stream),
@@ -523,6 +537,51 @@ int hffn_forward_gemv_static(int value_type, const float* x, const void* up_plan
                     "forward (gemv, static scratch)");
 }
 
+
+int hffn_tiles_table_size(int value_type, uint32_t rows, uint32_t k, uint64_t* entries) {
+    if (!entries) return fail(HFFN_ERROR_ARGUMENT, "tiles_table_size: null result");
+    if (!valid_value_type(value_type)) return fail(HFFN_ERROR_ARGUMENT, "unknown value type %d", value_type);
+    if (rows == 0 || rows > HFFN_MAX_WIDTH || k == 0 || k > HFFN_MAX_WIDTH)
+        return fail(HFFN_ERROR_ARGUMENT, "tiles_table_size: rows=%u k=%u must be in [1, %u]", rows, k, HFFN_MAX_WIDTH);
+    *entries = hffn::tiles_table_entries(value_type, rows, k);
+    return HFFN_OK;
+}
+
+int hffn_tiles_table_build(int value_type, const int32_t* offsets, const int16_t* idx, const void* val, uint32_t rows, uint32_t k,
+                           int32_t* table, void* stream) {
+    uint64_t entries = 0;
+    if (int status = hffn_tiles_table_size(value_type, rows, k, &entries)) return status;
+    if (!offsets || !idx || !val || !table) return fail(HFFN_ERROR_ARGUMENT, "tiles_table_build: null pointer");
+    return launched(hffn::launch_tiles_table(value_type, offsets, idx, val, rows, k, table, static_cast<hipStream_t>(stream)),
+                    "tiles table build");
+}
+
+int hffn_forward_tiles_compact(int value_type, const float* x, const int16_t* up_idx, const void* up_val, const int32_t* up_table,
+                               const float* b_up, const int16_t* out_hidden, const void* out_val, const int32_t* down_table,
+                               const float* b_down, float* act, void* workspace, uint64_t workspace_bytes, float* y, uint32_t d_model,
+                               uint32_t d_ff, uint64_t nnz_up, uint64_t nnz_down, uint32_t n, void* stream) {
+    TilesPlan p{value_type, nullptr, up_table, b_up, nullptr, down_table, b_down, act, workspace, workspace_bytes, y, d_model, d_ff, nnz_up,
+                nnz_down, n, up_idx, up_val, out_hidden, out_val};
+    if (!up_idx) return fail(HFFN_ERROR_ARGUMENT, "forward_tiles_compact: null pointer");
+    if (int status = check_tiles_call(p, x)) return status;
+    return launch_tiles(p, x, static_cast<hipStream_t>(stream));
+}
+
+int hffn_plan_tiles_compact(int value_type, const int16_t* up_idx, const void* up_val, const int32_t* up_table, const float* b_up,
+                            const int16_t* out_hidden, const void* out_val, const int32_t* down_table, const float* b_down, float* act,
+                            void* workspace, uint64_t workspace_bytes, float* y, uint32_t d_model, uint32_t d_ff, uint64_t nnz_up,
+                            uint64_t nnz_down, uint32_t n, uint64_t* plan) {
+    if (!plan) return fail(HFFN_ERROR_ARGUMENT, "plan_tiles_compact: null result");
+    TilesPlan p{value_type, nullptr, up_table, b_up, nullptr, down_table, b_down, act, workspace, workspace_bytes, y, d_model, d_ff, nnz_up,
+                nnz_down, n, up_idx, up_val, out_hidden, out_val};
+    if (!up_idx) return fail(HFFN_ERROR_ARGUMENT, "plan_tiles_compact: null pointer");
+    const float* some_x = reinterpret_cast<const float*>(uintptr_t{16});  // non-null, aligned: never dereferenced
+    if (int status = check_tiles_call(p, some_x)) return status;
+    const std::lock_guard<std::mutex> lock(g_plans_mutex);
+    *plan = g_next_plan++;
+    g_tiles_plans.emplace(*plan, p);
+    return HFFN_OK;
+}
 
 int hffn_tiles_store_size(int value_type, uint32_t rows, uint32_t k, uint64_t nnz, uint64_t* store_bytes, uint64_t* table_entries) {
     if (!store_bytes || !table_entries) return fail(HFFN_ERROR_ARGUMENT, "tiles_store_size: null result");

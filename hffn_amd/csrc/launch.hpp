@@ -141,6 +141,15 @@ struct TilesStoreSize {
 TilesShape tiles_shape(int vt, uint32_t rows, uint32_t K, uint64_t nnz);
 TilesStoreSize tiles_store_size(int vt, uint32_t rows, uint32_t K, uint64_t nnz);
 size_t tiles_workspace_bytes(int vt, uint32_t n, uint32_t d, uint32_t h, uint64_t nnz_up, uint64_t nnz_down);
+// The tiles path on the compact rows: a side's table (tiles_table_entries int32, built by launch_tiles_table) holds,
+// per row, the first slot of each 512-wide sub-chunk of K and the row's end, then (float32) the row's power of two.
+uint64_t tiles_table_entries(int vt, uint32_t rows, uint32_t K);
+hipError_t launch_tiles_table(int vt, const int32_t* offsets, const int16_t* idx, const void* val, uint32_t rows, uint32_t K,
+                              int32_t* table, hipStream_t stream);
+hipError_t launch_tiles_compact(int vt, const float* x, const int16_t* up_idx, const void* up_val, const int32_t* up_table,
+                                const float* b_up, const int16_t* out_hidden, const void* out_val, const int32_t* down_table,
+                                const float* b_down, float* act, float* work, float* y, uint32_t d, uint32_t h, uint64_t nnz_up,
+                                uint64_t nnz_down, uint32_t n, hipStream_t stream);
 hipError_t launch_tiles_build(int vt, const int32_t* offsets, const int16_t* idx, const void* val, uint32_t rows, uint32_t K, void* store,
                               int32_t* table, hipStream_t stream);
 hipError_t launch_tiles_forward(int vt, const float* x, const void* up_store, const int32_t* up_table, const float* b_up,

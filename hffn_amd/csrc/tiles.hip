@@ -80,7 +80,38 @@ constexpr bool shape_fits() {
     return TR * S * Planes<V>::count * kRows * kSub * 2 <= kTileBudget;
 }
 
-template <typename V, int TT, int S, int TR>
+// One 8-slot piece of a row of the compact store, slots [8 q, 8 q + 8): its 8 indices (one 16-byte load) and values
+// (one or two 16-byte loads); a piece across the end of the arrays is read slot by slot, the slots past nnz zero.
+template <typename V>
+__device__ __forceinline__ void load_piece(const int16_t* __restrict__ idx, const V* __restrict__ val, int32_t q, int32_t nnz,
+                                           uint4 (&pc)[1 + Planes<V>::count]) {
+    constexpr uint32_t P = Planes<V>::count;
+    const int32_t s = 8 * q;
+    if (s + 8 <= nnz) {
+        pc[0] = *reinterpret_cast<const uint4*>(idx + s);
+#pragma unroll
+        for (uint32_t p = 0; p < P; ++p) pc[1 + p] = reinterpret_cast<const uint4*>(val + s)[p];
+    } else {
+        uint16_t ids[8] = {0, 0, 0, 0, 0, 0, 0, 0};
+        V vals[8] = {V(0), V(0), V(0), V(0), V(0), V(0), V(0), V(0)};
+        for (int u = 0; u < 8; ++u)
+            if (s + u < nnz) {
+                ids[u] = static_cast<uint16_t>(idx[s + u]);
+                vals[u] = val[s + u];
+            }
+        pc[0] = *reinterpret_cast<const uint4*>(ids);
+#pragma unroll
+        for (uint32_t p = 0; p < P; ++p) pc[1 + p] = reinterpret_cast<const uint4*>(vals)[p];
+    }
+}
+
+// Value u (0..7) of a piece: float32 (fields 4 per uint4) or bfloat16 bits.
+__device__ __forceinline__ float piece_value(const uint4 (&pc)[3], int u) {
+    const uint4& q = pc[1 + u / 4];
+    return __uint_as_float(u % 4 == 0 ? q.x : u % 4 == 1 ? q.y : u % 4 == 2 ? q.z : q.w);
+}
+
+template <typename V, int TT, int S, int TR, bool COMPACT>
 __global__ __launch_bounds__(kThreads) void tiles_kernel(const float* __restrict__ in,         // [n, K]
                                                          const uint4* __restrict__ store,      // groups
                                                          const int32_t* __restrict__ table,    // items' first groups
@@ -89,7 +120,8 @@ __global__ __launch_bounds__(kThreads) void tiles_kernel(const float* __restrict
                                                          float* __restrict__ out,              // [n, R]
                                                          float* __restrict__ partials,         // [chunks, n, R]
                                                          uint32_t rows, uint32_t K, uint32_t n, uint32_t subchunks,
-                                                         uint32_t up) {
+                                                         uint32_t up, const int16_t* __restrict__ cidx, const V* __restrict__ cval,
+                                                         int32_t nnz) {
     constexpr uint32_t P = Planes<V>::count;
     constexpr uint32_t W = S * kSub;  // k per block
     constexpr uint32_t kTileRows = TR * kRows;
@@ -109,11 +141,23 @@ __global__ __launch_bounds__(kThreads) void tiles_kernel(const float* __restrict
 
     // 1. the block's group ranges (one per tile; a tile past the side owns none)
     int32_t first[TR], count[TR], total = 0;
+    // compact: the slot range [s0, s1) of each of the wave's rows (row 16 tr + wave of the block) in this chunk, and
+    // (float32) the row's power of two
+    int32_t s0[TR], s1[TR], row_e[TR];
 #pragma unroll
     for (int tr = 0; tr < TR; ++tr) {
         first[tr] = 0;
         count[tr] = 0;
-        if (tile0 + tr < tiles) {
+        if constexpr (COMPACT) {
+            const uint32_t row = (tile0 + tr) * kRows + wave;
+            s0[tr] = s1[tr] = 0;
+            row_e[tr] = 0;
+            if (row < rows) {
+                s0[tr] = table[row * (subchunks + 1) + j0];
+                s1[tr] = table[row * (subchunks + 1) + j1];
+                if constexpr (P == 2) row_e[tr] = binades[row];
+            }
+        } else if (tile0 + tr < tiles) {
             first[tr] = table[(tile0 + tr) * subchunks + j0];
             count[tr] = table[(tile0 + tr) * subchunks + j1] - first[tr];
         }
@@ -168,6 +212,69 @@ __global__ __launch_bounds__(kThreads) void tiles_kernel(const float* __restrict
             }
         }
     };
+    if constexpr (COMPACT) {
+        // 1'. the wave's rows' 8-slot pieces as one list (row tr's pieces q0[tr] .. q0[tr] + count - 1 after those of
+        // rows 0 .. tr - 1), over the lanes: piece g of the list in lane g % 64, round g / 64. The first two rounds are
+        // requested before the tile is zeroed.
+        int32_t q0[TR], cum[TR], pieces = 0;
+#pragma unroll
+        for (int tr = 0; tr < TR; ++tr) {
+            q0[tr] = s0[tr] >> 3;
+            cum[tr] = pieces;
+            pieces += s0[tr] < s1[tr] ? ((s1[tr] + 7) >> 3) - q0[tr] : 0;
+        }
+        auto locate = [&](int32_t g, int& tr, int32_t& q) {  // a later row with cum <= g overrides: empty rows are passed
+            tr = 0;
+#pragma unroll
+            for (int t = 1; t < TR; ++t)
+                if (g >= cum[t]) tr = t;
+            q = q0[tr] + (g - cum[tr]);
+        };
+        auto fetch = [&](int32_t g, int& tr, int32_t& q, uint4 (&part)[3]) {
+            if (g >= pieces) return;
+            locate(g, tr, q);
+            load_piece(cidx, cval, q, nnz, reinterpret_cast<uint4(&)[1 + P]>(part));
+        };
+        // 2'. scatter: a piece's slots inside its row's range, at (row, index - kb); float32 weights split into fp16
+        // hi + lo = w 2^-e(row), as the tile would hold them from any source
+        auto place = [&](int32_t g, int tr, int32_t q, const uint4 (&part)[3]) {
+            if (g >= pieces) return;
+            const uint32_t rr = tr * kRows + wave;
+#pragma unroll
+            for (int u = 0; u < 8; ++u) {
+                const int32_t slot = 8 * q + u;
+                if (slot >= s0[tr] && slot < s1[tr]) {
+                    const uint32_t at = tile_at<W>(rr, field(part[0], u) - kb);
+                    if constexpr (P == 1) {
+                        tile[at] = static_cast<uint16_t>(field(part[1], u));
+                    } else {
+                        const float sv = ldexpf(piece_value(part, u), -row_e[tr]);
+                        const _Float16 hi = static_cast<_Float16>(sv);
+                        tile[at] = __builtin_bit_cast(uint16_t, hi);
+                        tile[kPlane + at] = __builtin_bit_cast(uint16_t, static_cast<_Float16>(sv - static_cast<float>(hi)));
+                    }
+                }
+            }
+        };
+        const int32_t ga_at = static_cast<int32_t>(lane), gb_at = ga_at + kWave;
+        uint4 pa[3], pb[3];
+        int tra = 0, trb = 0;
+        int32_t qa = 0, qb = 0;
+        fetch(ga_at, tra, qa, pa);
+        fetch(gb_at, trb, qb, pb);
+        for (uint32_t i = threadIdx.x; i < kTileBytes / 16; i += kThreads) reinterpret_cast<uint4*>(tile)[i] = make_uint4(0, 0, 0, 0);
+        __syncthreads();  // the tile is zero (this waits for the LDS only: the loads stay in flight)
+        place(ga_at, tra, qa, pa);
+        place(gb_at, trb, qb, pb);
+        for (int32_t g = ga_at + 2 * kWave; g - static_cast<int32_t>(lane) < pieces; g += kWave) {
+            uint4 pc[3];
+            int tr = 0;
+            int32_t q = 0;
+            fetch(g, tr, q, pc);
+            place(g, tr, q, pc);
+        }
+        __syncthreads();
+    } else {
     uint4 ga[1 + P], gb[1 + P];
     const uint32_t rows_a = load_group(threadIdx.x, ga), rows_b = load_group(threadIdx.x + kThreads, gb);
     for (uint32_t i = threadIdx.x; i < kTileBytes / 16; i += kThreads) reinterpret_cast<uint4*>(tile)[i] = make_uint4(0, 0, 0, 0);
@@ -181,6 +288,7 @@ __global__ __launch_bounds__(kThreads) void tiles_kernel(const float* __restrict
         scatter(g, gc, load_group(g, gc));
     }
     __syncthreads();
+    }
 
     // 3. products over the wave's S steps, one token tile after the other. With few steps (2; 4 for bfloat16) the
     // tile's A operands are all formed before the next tile's inputs are requested (their arrival overlaps the
@@ -454,6 +562,16 @@ __global__ __launch_bounds__(256) void tiles_place_kernel(const int32_t* __restr
 
 // ---------------------------------------------------------------------------------------------- launches
 
+// table[r (subchunks + 1) + j] = the first slot of row r whose index reaches 512 j (j = subchunks: the row's end).
+__global__ __launch_bounds__(256) void tiles_bounds_kernel(const int32_t* __restrict__ offsets, const int16_t* __restrict__ idx,
+                                                           uint32_t rows, uint32_t subchunks, int32_t* __restrict__ table) {
+    const uint32_t e = blockIdx.x * 256 + threadIdx.x;
+    if (e >= rows * (subchunks + 1)) return;
+    const uint32_t r = e / (subchunks + 1), j = e % (subchunks + 1);
+    const int32_t lo = offsets[r], hi = offsets[r + 1];
+    table[e] = j == 0 ? lo : j == subchunks ? hi : first_reaching(idx, lo, hi, j * kSub);
+}
+
 struct Side {
     const float* in;
     const uint4* store;
@@ -464,33 +582,36 @@ struct Side {
     float* partials;
     uint32_t rows, K, n, subchunks, up;
     uint64_t nnz;
+    const int16_t* cidx;  // the compact rows (COMPACT launches)
+    const void* cval;
 };
 
-template <typename V, int TT, int S, int TR>
+template <typename V, int TT, int S, int TR, bool COMPACT>
 bool launch_shape(const Side& a, const TilesShape& shape, hipStream_t stream) {
     if constexpr (!shape_fits<V, TT, S, TR>()) {
         return false;
     } else {
         if (shape.s != S || shape.tr != TR) return false;
-        hipLaunchKernelGGL((tiles_kernel<V, TT, S, TR>), dim3(shape.blocks, shape.chunks), dim3(kThreads), 0, stream, a.in, a.store, a.table,
-                           a.binades, a.bias, a.out, a.partials, a.rows, a.K, a.n, a.subchunks, a.up);
+        hipLaunchKernelGGL((tiles_kernel<V, TT, S, TR, COMPACT>), dim3(shape.blocks, shape.chunks), dim3(kThreads), 0, stream, a.in, a.store,
+                           a.table, a.binades, a.bias, a.out, a.partials, a.rows, a.K, a.n, a.subchunks, a.up, a.cidx,
+                           static_cast<const V*>(a.cval), static_cast<int32_t>(a.nnz));
         return true;
     }
 }
 
-template <typename V, int TT>
+template <typename V, int TT, bool COMPACT>
 bool launch_tokens(const Side& a, const TilesShape& shape, hipStream_t stream) {
-    return launch_shape<V, TT, 2, 1>(a, shape, stream) || launch_shape<V, TT, 4, 1>(a, shape, stream) ||
-           launch_shape<V, TT, 8, 1>(a, shape, stream) || launch_shape<V, TT, 2, 2>(a, shape, stream) ||
-           launch_shape<V, TT, 4, 2>(a, shape, stream) || launch_shape<V, TT, 2, 4>(a, shape, stream);
+    return launch_shape<V, TT, 2, 1, COMPACT>(a, shape, stream) || launch_shape<V, TT, 4, 1, COMPACT>(a, shape, stream) ||
+           launch_shape<V, TT, 8, 1, COMPACT>(a, shape, stream) || launch_shape<V, TT, 2, 2, COMPACT>(a, shape, stream) ||
+           launch_shape<V, TT, 4, 2, COMPACT>(a, shape, stream) || launch_shape<V, TT, 2, 4, COMPACT>(a, shape, stream);
 }
 
-template <typename V>
+template <typename V, bool COMPACT = false>
 hipError_t tiles_side(const Side& a, hipStream_t stream) {
     const TilesShape shape = tiles_shape(Planes<V>::count == 1 ? kBF16 : kF32, a.rows, a.K, a.nnz);
-    const bool launched = a.n <= kTokenTile       ? launch_tokens<V, 1>(a, shape, stream)
-                          : a.n <= 2 * kTokenTile ? launch_tokens<V, 2>(a, shape, stream)
-                                                  : launch_tokens<V, 4>(a, shape, stream);
+    const bool launched = a.n <= kTokenTile       ? launch_tokens<V, 1, COMPACT>(a, shape, stream)
+                          : a.n <= 2 * kTokenTile ? launch_tokens<V, 2, COMPACT>(a, shape, stream)
+                                                  : launch_tokens<V, 4, COMPACT>(a, shape, stream);
     if (!launched) return hipErrorInvalidValue;
     if (hipError_t status = hipGetLastError(); status != hipSuccess || shape.chunks == 1) return status;
     hipLaunchKernelGGL(tiles_reduce_kernel, dim3((a.n * a.rows + 255) / 256), dim3(256), 0, stream, a.partials, shape.chunks, a.bias, a.out,
@@ -562,14 +683,42 @@ hipError_t launch_tiles_build(int vt, const int32_t* offsets, const int16_t* idx
     return hipGetLastError();
 }
 
+uint64_t tiles_table_entries(int vt, uint32_t rows, uint32_t K) {
+    return static_cast<uint64_t>(rows) * ((K + kSub - 1) / kSub + 1) + (vt == kBF16 ? 0 : rows);
+}
+
+hipError_t launch_tiles_table(int vt, const int32_t* offsets, const int16_t* idx, const void* val, uint32_t rows, uint32_t K,
+                              int32_t* table, hipStream_t stream) {
+    const uint32_t subchunks = (K + kSub - 1) / kSub, entries = rows * (subchunks + 1);
+    hipLaunchKernelGGL(tiles_bounds_kernel, dim3((entries + 255) / 256), dim3(256), 0, stream, offsets, idx, rows, subchunks, table);
+    if (vt != kBF16)
+        hipLaunchKernelGGL(tiles_binade_kernel, dim3((rows + 255) / 256), dim3(256), 0, stream, offsets, static_cast<const float*>(val), rows,
+                           table + entries);
+    return hipGetLastError();
+}
+
+hipError_t launch_tiles_compact(int vt, const float* x, const int16_t* up_idx, const void* up_val, const int32_t* up_table,
+                                const float* b_up, const int16_t* out_hidden, const void* out_val, const int32_t* down_table,
+                                const float* b_down, float* act, float* work, float* y, uint32_t d, uint32_t h, uint64_t nnz_up,
+                                uint64_t nnz_down, uint32_t n, hipStream_t stream) {
+    const uint32_t up_sub = (d + kSub - 1) / kSub, down_sub = (h + kSub - 1) / kSub;
+    const Side up{x, nullptr, up_table, up_table + static_cast<size_t>(h) * (up_sub + 1), b_up, act, work, h, d, n, up_sub, 1, nnz_up,
+                  up_idx, up_val};
+    const Side down{act, nullptr, down_table, down_table + static_cast<size_t>(d) * (down_sub + 1), b_down, y, work, d, h, n, down_sub, 0,
+                    nnz_down, out_hidden, out_val};
+    const hipError_t status = vt == kBF16 ? tiles_side<uint16_t, true>(up, stream) : tiles_side<float, true>(up, stream);
+    if (status != hipSuccess) return status;
+    return vt == kBF16 ? tiles_side<uint16_t, true>(down, stream) : tiles_side<float, true>(down, stream);
+}
+
 hipError_t launch_tiles_forward(int vt, const float* x, const void* up_store, const int32_t* up_table, const float* b_up,
                                 const void* down_store, const int32_t* down_table, const float* b_down, float* act, float* work,
                                 float* y, uint32_t d, uint32_t h, uint64_t nnz_up, uint64_t nnz_down, uint32_t n, hipStream_t stream) {
     const uint32_t up_items = items_of(h, d), down_items = items_of(d, h);
     const Side up{x, static_cast<const uint4*>(up_store), up_table, up_table + up_items + 1, b_up, act, work, h, d, n,
-                  (d + kSub - 1) / kSub, 1, nnz_up};
+                  (d + kSub - 1) / kSub, 1, nnz_up, nullptr, nullptr};
     const Side down{act, static_cast<const uint4*>(down_store), down_table, down_table + down_items + 1, b_down, y, work, d, h, n,
-                    (h + kSub - 1) / kSub, 0, nnz_down};
+                    (h + kSub - 1) / kSub, 0, nnz_down, nullptr, nullptr};
     const hipError_t status = vt == kBF16 ? tiles_side<uint16_t>(up, stream) : tiles_side<float>(up, stream);
     if (status != hipSuccess) return status;
     return vt == kBF16 ? tiles_side<uint16_t>(down, stream) : tiles_side<float>(down, stream);

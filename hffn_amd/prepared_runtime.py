@@ -28,9 +28,9 @@ _GATHER = ("edges", "rows")
 class PreparedRuntime(HFFNRuntime):
     """``HFFNRuntime`` whose gather-mode calls launch from per-(layer, N) plans of the HIP library."""
 
-    def __init__(self, layers, device="cuda", dense: bool | None = None) -> None:
+    def __init__(self, layers, device="cuda", dense: bool | None = None, tiled: bool = True) -> None:
         self._plans: dict = {}
-        super().__init__(layers, device, dense)
+        super().__init__(layers, device, dense, tiled)
         self._stream_of = getattr(torch._C, "_cuda_getCurrentRawStream", None)
 
     def _release_plans(self) -> None:
@@ -69,8 +69,9 @@ class PreparedRuntime(HFFNRuntime):
                        "plan (gemv, gemv)")
             return handle.value, up, down
         if up == "tiles":
-            _lib.check(self._lib.hffn_plan_tiles(value_type, *self._tiles_args(index), self.d_model, self.d_ff, *self._nnz[index], n,
-                                                 ctypes.byref(handle)), "plan (tiles, tiles)")
+            entry = self._lib.hffn_plan_tiles if self.tiled else self._lib.hffn_plan_tiles_compact
+            _lib.check(entry(value_type, *self._tiles_args(index), self.d_model, self.d_ff, *self._nnz[index], n, ctypes.byref(handle)),
+                       "plan (tiles, tiles)")
             return handle.value, up, down
         if up not in _GATHER or down not in _GATHER:
             return False

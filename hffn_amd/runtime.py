@@ -235,11 +235,16 @@ _ARRAYS = ("b_up", "up_offsets", "up_idx", "up_val", "b_down", "out_offsets", "o
 class HFFNRuntime:
     """``HFFNRuntime`` of ``runtime/gpu/nvidia/common/kernels/hffn_cuda/runtime.py:76-163`` on the HIP library."""
 
-    def __init__(self, layers: list[HFFNLayer], device: str | torch.device = "cuda", dense: bool | None = None) -> None:
+    def __init__(self, layers: list[HFFNLayer], device: str | torch.device = "cuda", dense: bool | None = None,
+                 tiled: bool = True) -> None:
         """``dense``: build the dense planes of the MFMA path and the decode GEMVs (``d_model`` and ``d_ff`` multiples of
         256, distinct sorted indices per row): None (default) for layers of at least ``MFMA_MIN_DENSITY`` only, True
-        whenever the shapes qualify (the policy still takes them only at that density), False never."""
+        whenever the shapes qualify (the policy still takes them only at that density), False never. ``tiled``: the
+        tiles path reads a tiled copy of each layer's store (True, the default: its interleaved groups make the decode
+        kernels 8-35 % faster) or the compact rows themselves through a small table of row bounds (False: the same
+        bits, and no second copy of the store)."""
         self.device = _device(device)
+        self.tiled = tiled
         self.layers = layers
         self.d_model, self.d_ff = layers[0].d_model, layers[0].d_ff
         if any((layer.d_model, layer.d_ff) != (self.d_model, self.d_ff) for layer in layers):
@@ -301,13 +306,22 @@ class HFFNRuntime:
 
     def _tiles_build(self, tensors: dict, tiles: dict | None = None) -> dict:
         """The tiled stores of both sides (``hffn_tiles_build``): each side's slots regrouped by 16-row tile and 512-wide
-        sub-chunk of K, with their table; rebuilt into ``tiles`` when given (same sizes: allocates nothing)."""
+        sub-chunk of K, with their table; or, for ``tiled=False``, each side's table of row bounds over the compact rows
+        (``hffn_tiles_table_build``). Rebuilt into ``tiles`` when given (same sizes: allocates nothing)."""
         stream = torch.cuda.current_stream(self.device).cuda_stream
         value_type = _value_type(tensors["up_val"], "up_val")
         tiles = {} if tiles is None else tiles
         for side, rows, k, names in (("up", self.d_ff, self.d_model, ("up_offsets", "up_idx", "up_val")),
                                      ("down", self.d_model, self.d_ff, ("out_offsets", "out_hidden", "out_val"))):
             offsets, index, values = (tensors[name] for name in names)
+            if not self.tiled:
+                if side not in tiles:
+                    entries = ctypes.c_uint64(0)
+                    _lib.check(self._lib.hffn_tiles_table_size(value_type, rows, k, ctypes.byref(entries)), f"tiles table size {side}")
+                    tiles[side] = torch.empty(entries.value, dtype=torch.int32, device=self.device)
+                _lib.check(self._lib.hffn_tiles_table_build(value_type, offsets.data_ptr(), index.data_ptr(), values.data_ptr(), rows, k,
+                                                            tiles[side].data_ptr(), stream), f"tiles table {side}")
+                continue
             store_bytes, entries = ctypes.c_uint64(0), ctypes.c_uint64(0)
             _lib.check(self._lib.hffn_tiles_store_size(value_type, rows, k, index.numel(), ctypes.byref(store_bytes),
                                                        ctypes.byref(entries)), f"tiles store size {side}")
@@ -321,7 +335,8 @@ class HFFNRuntime:
         return tiles
 
     def tiles_bytes(self) -> int:
-        """Bytes of the tiled stores and their tables held for the tiles path (0 without it)."""
+        """Bytes held for the tiles path beyond the compact store: the tiled stores and their tables, or (``tiled=False``)
+        the tables of row bounds; 0 without it."""
         if self._tiles is None:
             return 0
         return sum(t.numel() * t.element_size() for tiles in self._tiles for t in tiles.values())
@@ -456,12 +471,23 @@ class HFFNRuntime:
         return self._y[:n]
 
     def _tiles_args(self, index: int) -> tuple:
-        """The arguments of ``hffn_forward_tiles`` / ``hffn_plan_tiles`` between x and the token count."""
+        """The arguments of ``hffn_forward_tiles`` / ``hffn_plan_tiles`` (or, for ``tiled=False``, of
+        ``hffn_forward_tiles_compact`` / ``hffn_plan_tiles_compact``) between x and the widths."""
         tensors, tiles = self._tensors[index], self._tiles[index]
         _, act, _, y = self._work
+        work = (act, self._tiles_work.data_ptr(), 4 * self._tiles_work.numel(), y)
+        if not self.tiled:
+            return (tensors["up_idx"].data_ptr(), tensors["up_val"].data_ptr(), tiles["up"].data_ptr(), tensors["b_up"].data_ptr(),
+                    tensors["out_hidden"].data_ptr(), tensors["out_val"].data_ptr(), tiles["down"].data_ptr(),
+                    tensors["b_down"].data_ptr(), *work)
         return (tiles["up"].data_ptr(), tiles["up_table"].data_ptr(), tensors["b_up"].data_ptr(), tiles["down"].data_ptr(),
-                tiles["down_table"].data_ptr(), tensors["b_down"].data_ptr(), act, self._tiles_work.data_ptr(),
-                4 * self._tiles_work.numel(), y)
+                tiles["down_table"].data_ptr(), tensors["b_down"].data_ptr(), *work)
+
+    def _tiles_forward(self, index: int, x: torch.Tensor, n: int, stream) -> None:
+        """One call of the tiles path on x (16-byte aligned), from the tiled store or the compact rows."""
+        entry = self._lib.hffn_forward_tiles if self.tiled else self._lib.hffn_forward_tiles_compact
+        _lib.check(entry(self._args[index][0], x.data_ptr(), *self._tiles_args(index), self.d_model, self.d_ff, *self._nnz[index], n,
+                         stream), "forward (tiles, tiles)")
 
     def _launch(self, index: int, x: torch.Tensor, n: int, up: str, down: str) -> None:
         value_type, *model = self._args[index]
@@ -472,8 +498,7 @@ class HFFNRuntime:
                 raise ValueError(f"the tiles path takes at most {TILES_MAX_TOKENS} tokens, not {n}")
             x = _aligned(x)  # read 16 bytes at a time
             self._fresh_tiles(index)
-            _lib.check(self._lib.hffn_forward_tiles(value_type, x.data_ptr(), *self._tiles_args(index), self.d_model, self.d_ff,
-                                                    *self._nnz[index], n, stream), "forward (tiles, tiles)")
+            self._tiles_forward(index, x, n, stream)
             return
         if up in PAIR_MODES:
             x = _aligned(x)  # the planes paths read x 16 bytes at a time

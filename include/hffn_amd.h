@@ -27,7 +27,7 @@
 extern "C" {
 #endif
 
-#define HFFN_ABI_VERSION 15
+#define HFFN_ABI_VERSION 16
 
 #define HFFN_OK 0
 #define HFFN_ERROR_ARGUMENT (-1) /* invalid shape, mode, pointer or workspace */
@@ -250,6 +250,24 @@ int hffn_forward_tiles(int value_type, const float* x, const void* up_store, con
 int hffn_plan_tiles(int value_type, const void* up_store, const int32_t* up_table, const float* b_up, const void* down_store,
                     const int32_t* down_table, const float* b_down, float* act, void* workspace, uint64_t workspace_bytes, float* y,
                     uint32_t d_model, uint32_t d_ff, uint64_t nnz_up, uint64_t nnz_down, uint32_t n, uint64_t* plan);
+
+/* The tiles path on the compact rows themselves (no tiled copy: the layer's only resident store), the same products
+ * and the same bits as hffn_forward_tiles, the tiles read by per-row ranges of 8-slot pieces (16-byte loads of the
+ * index and value arrays). A side's table (hffn_tiles_table_size int32 entries, built by hffn_tiles_table_build from its
+ * compact rows) holds, per row, the first slot of each 512-wide sub-chunk of k and the row's end, then (float32) each
+ * row's power of two. The index and value arrays must be 16-byte aligned; the rest as hffn_forward_tiles.
+ * hffn_plan_tiles_compact keeps every argument but x and the stream under a plan handle (hffn_plan_launch). */
+int hffn_tiles_table_size(int value_type, uint32_t rows, uint32_t k, uint64_t* entries);
+int hffn_tiles_table_build(int value_type, const int32_t* offsets, const int16_t* idx, const void* val, uint32_t rows, uint32_t k,
+                           int32_t* table, void* stream);
+int hffn_forward_tiles_compact(int value_type, const float* x, const int16_t* up_idx, const void* up_val, const int32_t* up_table,
+                               const float* b_up, const int16_t* out_hidden, const void* out_val, const int32_t* down_table,
+                               const float* b_down, float* act, void* workspace, uint64_t workspace_bytes, float* y, uint32_t d_model,
+                               uint32_t d_ff, uint64_t nnz_up, uint64_t nnz_down, uint32_t n, void* stream);
+int hffn_plan_tiles_compact(int value_type, const int16_t* up_idx, const void* up_val, const int32_t* up_table, const float* b_up,
+                            const int16_t* out_hidden, const void* out_val, const int32_t* down_table, const float* b_down, float* act,
+                            void* workspace, uint64_t workspace_bytes, float* y, uint32_t d_model, uint32_t d_ff, uint64_t nnz_up,
+                            uint64_t nnz_down, uint32_t n, uint64_t* plan);
 
 /* ------------------------------------------------------------------------------------------------ training (fp32)
  * Layouts: act, z, gz hidden-major [d_ff, ld]; x_t, gy_t, gx_t feature-major [d_model, ld]; x, y, gx token-major

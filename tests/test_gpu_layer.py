@@ -370,6 +370,43 @@ def test_tiled_store_bitwise(shape, test_layers, device):
         assert _relative(y, reference.forward(compact, x_np)) <= 1e-5, n
 
 
+@pytest.mark.parametrize("shape", [("irreg_512_2048", None), ("odd_f32", (48, 520, 37, "float32")),
+                                   ("odd_bf16", (64, 1032, 60, "bf16")), ("empty_items", "empty"),
+                                   ("pythia1p4b_d20_bf16", "workload")])
+def test_tiles_on_the_compact_rows_equal_the_tiled_store(shape, test_layers, device):
+    """With tiled=False the tiles path reads the compact rows through the table of row bounds: the same dense tiles,
+    so the same bits as the tiled store at every token count (eager and planned); the layer then holds its compact
+    store plus tables of row bounds (about 1 % of a real layer's store)."""
+    from hffn_amd.prepared_runtime import PreparedRuntime
+    name, dims = shape
+    if dims is None:
+        compact, _, layer = test_layers[name]
+    elif dims == "empty":
+        compact = _layer_with_empty_items()
+        layer = hip_layer(compact)
+    elif dims == "workload":
+        compact = synth.make_workload_layer(synth.WORKLOADS[name])
+        layer = hip_layer(compact)
+    else:
+        d_model, d_ff, degree, dtype = dims
+        compact = synth.make_workload_layer(synth.Workload(name, d_model, d_ff, min(degree, d_model), 7, value_dtype=dtype))
+        layer = hip_layer(compact)
+    tiled, rows = HFFNRuntime([layer], device), PreparedRuntime([layer], device, tiled=False)
+    tiled.force("tiles", "tiles")
+    rows.force("tiles", "tiles")
+    assert rows.tiles_bytes() < 0.5 * tiled.tiles_bytes()
+    if dims == "workload":  # a real layer (1.4B shape, bfloat16, 20 %): the tables are 1.1 % of its compact store
+        assert rows.tiles_bytes() <= 0.015 * layer.model_bytes()
+    for n in (1, 2, 7, 16, 17, 33, 64):
+        x_np = np.random.default_rng(n).standard_normal((n, compact.d_model)).astype(np.float32)
+        x = torch.from_numpy(x_np).to(device)
+        expected = tiled.forward(0, x).clone()
+        assert torch.equal(rows.forward(0, x), expected), n  # planned launch
+        assert torch.equal(HFFNRuntime.forward(rows, 0, x), expected), n  # eager launch
+        if n in (1, 17, 64):
+            assert _relative(expected, reference.forward(compact, x_np)) <= 1e-5, n
+
+
 def test_tiles_refuses_more_than_64_tokens(test_layers, device):
     compact, case, layer = test_layers["homog_512_2048"]
     runtime = HFFNRuntime([layer], device, dense=True)
