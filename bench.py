@@ -4,8 +4,8 @@
 Workload (default): the Pythia-410M-shape HFFN layer, d_model 1024, d_ff 4096, 50 % density (512-slot up and down
 supports per neuron, uniform without replacement, sorted), fp32 values ~N(0, 0.02), biases ~N(0, 0.01), x = 2048 tokens
 ~N(0, 1), exact-erf GELU. A step is one forward of the whole layer on the 2048 resident tokens. The timed loop rotates
-over enough distinct copies of the layer (different seeds) that their stores exceed the 256 MB Infinity Cache, so
-every step reads its model from HBM.
+over enough copies of the layer (device clones of its arrays, each at its own addresses) that their stores exceed the
+256 MB Infinity Cache, so every step reads its model from HBM.
 
     python bench.py [--steps K] [--warmup W] [--workload NAME] [--tokens N]
 
@@ -58,6 +58,8 @@ def parse() -> argparse.Namespace:
                              "up under load: 20 steps after 5 warm-up steps measured 0.141 ms per step, 200 after 20 "
                              "0.122 ms)")
     parser.add_argument("--no-decode", action="store_true", help="skip the decode record")
+    parser.add_argument("--untiled", action="store_true",
+                        help="the runtime without tiled copies of the stores (tiled=False: the tiles path reads the compact rows)")
     parser.add_argument("--decode-rotations", type=int, default=20, help="passes over the copies per decode entry")
     parser.add_argument("--copy-probe-mb", type=int, default=0,
                         help="after the run, copy a buffer of this many MiB 3 times (the plain copy kernel that "
@@ -316,8 +318,7 @@ def main() -> int:
     base = synth.make_workload_layer(workload)
     costs = layer_costs(base, n)
     copies = args.copies or max(1, math.ceil(MALL_BYTES / costs["model_bytes"]))
-    compacts = [base] + [synth.make_workload_layer(workload, seed=workload.seed * 1000 + c) for c in range(1, copies)]
-    runtime = HFFNRuntime([hip_layer(c, device) for c in compacts], device)
+    runtime = HFFNRuntime(device_copies(hip_layer(base, device), copies), device, tiled=not args.untiled)
     x_np = synth.make_input(workload, n)
     x = torch.from_numpy(x_np).to(device)
 
@@ -395,7 +396,9 @@ def main() -> int:
                    "step_hbm_fraction": round(costs["step_bytes"] / (seconds / args.steps) / HBM_PEAK, 4),
                    "step_fp32_fraction": round(costs["step_flops"] / (seconds / args.steps) / FP32_PEAK, 4),
                    "memory_bytes": {"compact_store": costs["model_bytes"], "planes": runtime.dense_bytes() // copies,
-                                    "tiled_store": runtime.tiles_bytes() // copies, "workspace": runtime.workspace_bytes()},
+                                    ("tiled_store" if runtime.tiled else "row_bounds_tables"): runtime.tiles_bytes() // copies,
+                                    "workspace": runtime.workspace_bytes()},
+                   "tiled": runtime.tiled,
                    "wall_s": round(wall, 3)},
         "roofline": roofline,
         "cpu_baseline": baseline,

@@ -505,13 +505,16 @@ __global__ __launch_bounds__(1024) void tiles_scan_kernel(int32_t* __restrict__ 
 }
 
 // binades[r] = the power of two of row r's largest |weight| (0 for a row without a non-zero weight); float32 stores.
+// One wave per row: the lanes' maxima over the row's slots (64 apart), then a wave maximum.
 __global__ __launch_bounds__(256) void tiles_binade_kernel(const int32_t* __restrict__ offsets, const float* __restrict__ val,
                                                            uint32_t rows, int32_t* __restrict__ binades) {
-    const uint32_t r = blockIdx.x * 256 + threadIdx.x;
+    const uint32_t r = blockIdx.x * 4 + threadIdx.x / kWave, lane = threadIdx.x % kWave;
     if (r >= rows) return;
     uint32_t m = 0;
-    for (int32_t s = offsets[r]; s < offsets[r + 1]; ++s) m = max(m, __float_as_uint(val[s]) & 0x7fffffffu);
-    binades[r] = binade_of(m);
+    for (int32_t s = offsets[r] + static_cast<int32_t>(lane); s < offsets[r + 1]; s += kWave) m = max(m, __float_as_uint(val[s]) & 0x7fffffffu);
+#pragma unroll
+    for (int o = 32; o >= 1; o >>= 1) m = max(m, static_cast<uint32_t>(__shfl_xor(static_cast<int>(m), o, kWave)));
+    if (lane == 0) binades[r] = binade_of(m);
 }
 
 // One wave per item: its rows' slots in row order, then the padding (the item's last slot again).
@@ -675,7 +678,7 @@ hipError_t launch_tiles_build(int vt, const int32_t* offsets, const int16_t* idx
         hipLaunchKernelGGL(tiles_place_kernel<uint16_t>, place, dim3(256), 0, stream, offsets, idx, static_cast<const uint16_t*>(val), table,
                            binades, rows, subchunks, items, static_cast<uint16_t*>(store));
     } else {
-        hipLaunchKernelGGL(tiles_binade_kernel, dim3((rows + 255) / 256), dim3(256), 0, stream, offsets, static_cast<const float*>(val), rows,
+        hipLaunchKernelGGL(tiles_binade_kernel, dim3((rows + 3) / 4), dim3(256), 0, stream, offsets, static_cast<const float*>(val), rows,
                            binades);
         hipLaunchKernelGGL(tiles_place_kernel<float>, place, dim3(256), 0, stream, offsets, idx, static_cast<const float*>(val), table,
                            binades, rows, subchunks, items, static_cast<uint16_t*>(store));
@@ -692,7 +695,7 @@ hipError_t launch_tiles_table(int vt, const int32_t* offsets, const int16_t* idx
     const uint32_t subchunks = (K + kSub - 1) / kSub, entries = rows * (subchunks + 1);
     hipLaunchKernelGGL(tiles_bounds_kernel, dim3((entries + 255) / 256), dim3(256), 0, stream, offsets, idx, rows, subchunks, table);
     if (vt != kBF16)
-        hipLaunchKernelGGL(tiles_binade_kernel, dim3((rows + 255) / 256), dim3(256), 0, stream, offsets, static_cast<const float*>(val), rows,
+        hipLaunchKernelGGL(tiles_binade_kernel, dim3((rows + 3) / 4), dim3(256), 0, stream, offsets, static_cast<const float*>(val), rows,
                            table + entries);
     return hipGetLastError();
 }
