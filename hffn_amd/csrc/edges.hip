@@ -6,7 +6,8 @@
 // A row is read as groups of 4 consecutive slots per lane (16-byte value and 8-byte index loads, i.e. 1 KB and
 // 512 B per wave instruction; groups are aligned to 4 slots, so a group may straddle the row's ends and its outside
 // slots are skipped). A wave requests its first 3 groups per lane (768 slots) before its block stages the inputs in
-// LDS, so the store streams while the block waits: at decode sizes these kernels are HBM-bound on the store.
+// LDS (by DMA, every transfer issued before any is waited for), so the store streams while the block waits: one
+// memory round trip for the row offsets, then one for the slots and the inputs together.
 // Long rows are split over P waves of the block (each takes a contiguous segment cut on the 4-slot grid); the P
 // partial sums are added in segment order. Within a wave the 64 lane partials are added by a fixed xor butterfly. Inputs are
 // staged in LDS when they fit (x for up, act for down at small n), otherwise act is gathered from L2.
@@ -45,10 +46,8 @@ __global__ __launch_bounds__(WAVES * kWave) void up_edges_kernel(const float* __
         Slots<V> cur;
         request_row<P>(cur, off, idx, w, r0 + row_in_pass, r1, part, nnz, lane);
         if (c0) __syncthreads();
-        for (uint32_t i = threadIdx.x; i < d * NT; i += WAVES * kWave) {
-            const uint32_t feature = i / NT, t = i % NT;
-            xs[i] = t < tokens ? x[static_cast<size_t>(c0 + t) * d + feature] : 0.0f;
-        }
+        stage_inputs<NT, WAVES>(xs, x + static_cast<size_t>(c0) * d, d, 1, d, tokens, wave, lane);
+        wait_loads<0>();
         __syncthreads();
         const StagedInput input{xs};
         for (uint32_t base = r0; base < r1; base += kRowsPerPass) {  // uniform trip count across the block
@@ -99,10 +98,8 @@ __global__ __launch_bounds__(WAVES * kWave) void down_edges_kernel(const float* 
         request_row<P>(cur, off, hid, v, o0 + row_in_pass, o1, part, nnz, lane);
         if constexpr (STAGE) {
             if (c0) __syncthreads();
-            for (uint32_t i = threadIdx.x; i < h * NT; i += WAVES * kWave) {
-                const uint32_t r = i / NT, t = i % NT;
-                as[i] = t < tokens ? act[static_cast<size_t>(r) * ld + c0 + t] : 0.0f;
-            }
+            stage_inputs<NT, WAVES>(as, act + c0, h, ld, 1, tokens, wave, lane);
+            wait_loads<0>();
             __syncthreads();
         }
         for (uint32_t base = o0; base < o1; base += kRowsPerPass) {

@@ -50,29 +50,58 @@ struct Segment {
     int32_t first;  // slot of this lane's group 0
 };
 
-// Issues the loads of groups [chunk * G, chunk * G + G) of this lane (4-slot groups strided by the wave); groups
-// that cross nnz, or lie past pe, are loaded slot by slot or left empty.
+// Issues the loads of groups [chunk * G, chunk * G + G) of this lane (4-slot groups strided by the wave). The whole
+// groups (below pe and nnz) are loaded as one value and one index load each, all issued back to back with no branch
+// between them, so they are in flight together (a lane without a whole group reads the store's group 0, which it never
+// uses). A group that crosses nnz is loaded slot by slot, only in a wave whose segment reaches past the last whole group
+// of the store (nnz not a multiple of 4).
 template <typename V, int G>
 __device__ __forceinline__ void load_segment(Segment<V, G>& seg, const int16_t* __restrict__ idx, const V* __restrict__ val,
                                              int32_t pb, int32_t pe, int32_t nnz, uint32_t lane, uint32_t chunk) {
     seg.first = (pb & ~3) + 4 * static_cast<int32_t>(lane) + static_cast<int32_t>(chunk) * G * 4 * kWave;
+    if (nnz >= 4) {
 #pragma unroll
-    for (int k = 0; k < G; ++k) {
-        const int32_t g = seg.first + k * 4 * kWave;
-        if (g < pe && g + 4 <= nnz) {
-            seg.vals[k] = *reinterpret_cast<const typename Group<V>::type*>(val + g);
-            seg.ids[k] = *reinterpret_cast<const uint2*>(idx + g);
-        } else if (g < pe) {
-            // the store's last group: pack the slots below nnz by hand
-            uint16_t i4[4] = {0, 0, 0, 0};
-            V v4[4] = {V(0), V(0), V(0), V(0)};
-            for (int s = 0; s < 4; ++s)
-                if (g + s < nnz) {
-                    i4[s] = static_cast<uint16_t>(idx[g + s]);
-                    v4[s] = val[g + s];
-                }
-            seg.ids[k] = make_uint2(i4[0] | (static_cast<uint32_t>(i4[1]) << 16), i4[2] | (static_cast<uint32_t>(i4[3]) << 16));
-            seg.vals[k] = *reinterpret_cast<const typename Group<V>::type*>(v4);
+        for (int k = 0; k < G; ++k) {
+            const int32_t g = seg.first + k * 4 * kWave;
+            const int32_t at = g < pe && g + 4 <= nnz ? g : 0;
+            seg.vals[k] = *reinterpret_cast<const typename Group<V>::type*>(val + at);
+            seg.ids[k] = *reinterpret_cast<const uint2*>(idx + at);
+        }
+    }
+    if (pe > (nnz & ~3)) {
+#pragma unroll
+        for (int k = 0; k < G; ++k) {
+            const int32_t g = seg.first + k * 4 * kWave;
+            if (g < pe && g + 4 > nnz) {
+                uint16_t i4[4] = {0, 0, 0, 0};
+                V v4[4] = {V(0), V(0), V(0), V(0)};
+                for (int s = 0; s < 4; ++s)
+                    if (g + s < nnz) {
+                        i4[s] = static_cast<uint16_t>(idx[g + s]);
+                        v4[s] = val[g + s];
+                    }
+                seg.ids[k] = make_uint2(i4[0] | (static_cast<uint32_t>(i4[1]) << 16), i4[2] | (static_cast<uint32_t>(i4[3]) << 16));
+                seg.vals[k] = *reinterpret_cast<const typename Group<V>::type*>(v4);
+            }
+        }
+    }
+}
+
+// Stages NT tokens of `rows` inputs into LDS [rows][NT] by DMA (global_load_lds, 4 bytes per lane): element (r, t)
+// from src[r * rstride + min(t, tokens - 1) * tstride] (a padded token repeats the block's last token; its sums are
+// never written). Every transfer of the block is issued before any is waited for; the caller waits (wait_loads<0>)
+// and synchronises the block before reading the stage.
+template <int NT, int WAVES>
+__device__ __forceinline__ void stage_inputs(float* lds, const float* src, uint32_t rows, uint32_t rstride, uint32_t tstride,
+                                             uint32_t tokens, uint32_t wave, uint32_t lane) {
+    const uint32_t total = rows * NT;
+    for (uint32_t base = wave * kWave; base < total; base += WAVES * kWave) {
+        const uint32_t r0 = base / NT;  // the piece's first row: its address is the wave-uniform base of the transfer
+        const float* from = src + static_cast<size_t>(r0) * rstride;
+        const uint32_t i = base + lane;
+        if (i < total) {
+            const uint32_t r = i / NT - r0, t = min(i % NT, tokens - 1);
+            dma4(from, (r * rstride + t * tstride) * static_cast<uint32_t>(sizeof(float)), lds + base);
         }
     }
 }
