@@ -139,6 +139,20 @@ __global__ __launch_bounds__(kThreads) void tiles_kernel(const float* __restrict
     const uint32_t kb = chunk * W, width = min(W, K - kb), kbase = kb % kSuper;
     const uint32_t j0 = chunk * S, j1 = min(j0 + S, subchunks);
 
+    // the epilogue's per-row constants of this thread's outputs (output o = threadIdx.x + kThreads i: row o % the block's
+    // rows), requested first so that their round trip overlaps the store's; a row past the side reads the last row's
+    constexpr uint32_t kOutputs = TT * kTokenTile * kTileRows, kOuts = (kOutputs + kThreads - 1) / kThreads;
+    int32_t out_e[kOuts];
+    float out_b[kOuts];
+#pragma unroll
+    for (uint32_t i = 0; i < kOuts; ++i) {
+        const uint32_t row = min(tile0 * kRows + (threadIdx.x + i * kThreads) % kTileRows, rows - 1);
+        out_e[i] = 0;
+        out_b[i] = 0.0f;
+        if constexpr (P == 2) out_e[i] = binades[row];
+        if (gridDim.y == 1) out_b[i] = bias[row];
+    }
+
     // 1. the block's group ranges (one per tile; a tile past the side owns none)
     int32_t first[TR], count[TR], total = 0;
     // compact: the slot range [s0, s1) of each of the wave's rows (row 16 tr + wave of the block) in this chunk, and
@@ -420,7 +434,10 @@ __global__ __launch_bounds__(kThreads) void tiles_kernel(const float* __restrict
                 }
     }
     __syncthreads();
-    for (uint32_t o = threadIdx.x; o < TT * kTokenTile * kTileRows; o += kThreads) {
+#pragma unroll
+    for (uint32_t i = 0; i < kOuts; ++i) {
+        const uint32_t o = threadIdx.x + i * kThreads;
+        if (o >= kOutputs) break;
         const uint32_t t = o / kTileRows, rr = o % kTileRows, row = tile0 * kRows + rr;
         if (t >= n) break;
         if (row >= rows) continue;
@@ -428,11 +445,11 @@ __global__ __launch_bounds__(kThreads) void tiles_kernel(const float* __restrict
         float s = sums[at];
 #pragma unroll
         for (uint32_t h = 1; h < kWaves / 2; ++h) s += sums[h * kWaveSums + at];
-        if constexpr (P == 2) s = ldexpf(s, binades[row]);
+        if constexpr (P == 2) s = ldexpf(s, out_e[i]);
         if (gridDim.y > 1) {
             partials[(static_cast<size_t>(chunk) * n + t) * rows + row] = s;
         } else {
-            const float z = s + bias[row];
+            const float z = s + out_b[i];
             out[static_cast<size_t>(t) * rows + row] = up ? gelu(z) : z;
         }
     }
@@ -445,9 +462,19 @@ __global__ __launch_bounds__(256) void tiles_reduce_kernel(const float* __restri
     const uint32_t o = blockIdx.x * 256 + threadIdx.x;
     if (o >= n * rows) return;
     const size_t stride = static_cast<size_t>(n) * rows;
+    // every load of a batch of 8 chunks (and the bias) is issued before the first is added: one memory round trip per
+    // batch; a chunk past the last reloads the last one and is not added
+    const float b = bias[o % rows];
     float s = partials[o];
-    for (uint32_t k = 1; k < chunks; ++k) s += partials[k * stride + o];
-    const float z = s + bias[o % rows];
+    for (uint32_t k0 = 1; k0 < chunks; k0 += 8) {
+        float p[8];
+#pragma unroll
+        for (uint32_t u = 0; u < 8; ++u) p[u] = partials[min(k0 + u, chunks - 1) * stride + o];
+#pragma unroll
+        for (uint32_t u = 0; u < 8; ++u)
+            if (k0 + u < chunks) s += p[u];
+    }
+    const float z = s + b;
     out[o] = up ? gelu(z) : z;
 }
 
