@@ -1,8 +1,10 @@
 // Lane-per-token ("rows") gather kernels of the HFFN forward on CDNA4 (wave64), and the layout transpose:
 // up projection with fused bias + exact GELU, and the atomics-free down projection over the output-major store.
 // One wave per neuron/output; the lanes own consecutive tokens (TPL per lane, vector loads), the wave walks the row's
-// slots in order with wave-uniform index/value loads, and each slot is one coalesced read of a feature-major input
-// row. (The lane-per-slot decode shapes are in edges.hip.)
+// slots in order, and each slot is one coalesced read of a feature-major input row. The slots' indices and values
+// are read 64 at a time (one coalesced load per lane) and broadcast from their lanes, and the input rows of a batch of
+// slots are all requested before the first is used: a walk costs a memory round trip per batch, not per slot, while
+// each output stays the sequential sum in stored slot order. (The lane-per-slot decode shapes are in edges.hip.)
 // Every activation and every output is written by exactly one lane: no atomics, bitwise
 // repeatable. Semantics follow runtime/gpu/nvidia/common/kernels/hffn_cuda/kernels.py:1-22.
 #include "common.hpp"
@@ -13,6 +15,55 @@ namespace {
 
 constexpr uint32_t kBlock = 256;
 constexpr uint32_t kWaves = kBlock / kWave;
+
+// The wave's walk of one row's slots [begin, end) for the TPL tokens of each lane (base: the lane's first token in the
+// feature-major input, rows ld apart). Lane l holds slot e0 + l of the current 64 (the next 64 are requested after the
+// first batch's inputs); a batch takes kBatch slots, broadcasting each slot's index from its lane, requesting every
+// input row of the batch, then adding the products one slot after the other in stored order. A slot past the row's end
+// repeats the row's last slot and is not added.
+template <int TPL, typename V>
+__device__ __forceinline__ void walk_row(const float* __restrict__ base, const int16_t* __restrict__ idx, const V* __restrict__ w,
+                                         int32_t begin, int32_t end, uint32_t ld, uint32_t lane, float (&acc)[TPL]) {
+    constexpr int32_t kBatch = TPL == 4 ? 16 : 32;
+#pragma unroll
+    for (int j = 0; j < TPL; ++j) acc[j] = 0.0f;
+    if (begin >= end) return;
+    const int32_t last = end - 1;
+    int32_t at = min(begin + static_cast<int32_t>(lane), last);
+    int32_t my_i = static_cast<uint16_t>(idx[at]);
+    float my_w = widen(w[at]);
+    for (int32_t e0 = begin; e0 < end; e0 += kWave) {
+        const int32_t count = min(static_cast<int32_t>(kWave), end - e0);
+        float xv[kBatch][TPL];
+        auto request = [&](int32_t u0) {
+#pragma unroll
+            for (int32_t u = 0; u < kBatch; ++u) {
+                const uint32_t i = static_cast<uint32_t>(__builtin_amdgcn_readlane(my_i, min(u0 + u, count - 1)));
+                load_vec<TPL>(base + static_cast<size_t>(i) * ld, xv[u]);
+            }
+        };
+        auto add = [&](int32_t u0) {
+#pragma unroll
+            for (int32_t u = 0; u < kBatch; ++u)
+                if (u0 + u < count) {
+                    const float wv = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(my_w), u0 + u));
+#pragma unroll
+                    for (int j = 0; j < TPL; ++j) acc[j] = fmaf(wv, xv[u][j], acc[j]);
+                }
+        };
+        request(0);
+        at = min(e0 + static_cast<int32_t>(kWave + lane), last);  // the next 64 slots, behind the first batch's inputs
+        const int32_t next_i = static_cast<uint16_t>(idx[at]);
+        const float next_w = widen(w[at]);
+        add(0);
+        for (int32_t u0 = kBatch; u0 < count; u0 += kBatch) {
+            request(u0);
+            add(u0);
+        }
+        my_i = next_i;
+        my_w = next_w;
+    }
+}
 
 // ------------------------------------------------------------------------------------------- up, rows
 // EPI kGelu: act = gelu(b + acc), and z = b + acc where z is not null (the training forward keeps it). EPI kGeluGrad
@@ -26,40 +77,16 @@ __global__ __launch_bounds__(kBlock) void up_rows_kernel(const float* __restrict
                                                         float* __restrict__ z, uint32_t h, uint32_t n, uint32_t ld) {
     const uint32_t r = blockIdx.x * kWaves + uniform(threadIdx.x / kWave);
     if (r >= h) return;
+    // every lane walks (the slots are spread over the wave's lanes); a lane past the tokens reads token 0 and stores nothing
     const uint32_t t0 = (blockIdx.y * kWave + threadIdx.x % kWave) * TPL;
-    if (t0 >= n) return;
-    const int32_t begin = off[r], end = off[r + 1];
-    const float* base = x_t + t0;
+    const bool live = t0 < n;
+    const float bias = EPI == kGelu ? b[r] : 0.0f;  // requested with the row's first slots
     float acc[TPL];
-#pragma unroll
-    for (int j = 0; j < TPL; ++j) acc[j] = 0.0f;
-    int32_t e = begin;
-    for (; e + 8 <= end; e += 8) {
-        float xv[8][TPL];
-        float wv[8];
-#pragma unroll
-        for (int u = 0; u < 8; ++u) {
-            const uint32_t i = static_cast<uint16_t>(idx[e + u]);
-            wv[u] = widen(w[e + u]);
-            load_vec<TPL>(base + static_cast<size_t>(i) * ld, xv[u]);
-        }
-#pragma unroll
-        for (int u = 0; u < 8; ++u)
-#pragma unroll
-            for (int j = 0; j < TPL; ++j) acc[j] = fmaf(wv[u], xv[u][j], acc[j]);
-    }
-    for (; e < end; ++e) {
-        const uint32_t i = static_cast<uint16_t>(idx[e]);
-        const float wv = widen(w[e]);
-        float xv[TPL];
-        load_vec<TPL>(base + static_cast<size_t>(i) * ld, xv);
-#pragma unroll
-        for (int j = 0; j < TPL; ++j) acc[j] = fmaf(wv, xv[j], acc[j]);
-    }
+    walk_row<TPL>(x_t + (live ? t0 : 0), idx, w, off[r], off[r + 1], ld, threadIdx.x % kWave, acc);
+    if (!live) return;
     float* out = act + static_cast<size_t>(r) * ld + t0;
     float* zr = z ? z + static_cast<size_t>(r) * ld + t0 : nullptr;
     if constexpr (EPI == kGelu) {
-        const float bias = b[r];
 #pragma unroll
         for (int j = 0; j < TPL; ++j)
             if (t0 + j < n) {
@@ -83,36 +110,11 @@ __global__ __launch_bounds__(kBlock) void down_rows_kernel(const float* __restri
     const uint32_t o = blockIdx.x * kWaves + uniform(threadIdx.x / kWave);
     if (o >= d) return;
     const uint32_t t0 = (blockIdx.y * kWave + threadIdx.x % kWave) * TPL;
-    if (t0 >= n) return;
-    const int32_t begin = off[o], end = off[o + 1];
-    const float* base = act + t0;
+    const bool live = t0 < n;
+    const float bo = bias ? bias[o] : 0.0f;  // no bias: the backward's gx; requested with the row's first slots
     float acc[TPL];
-#pragma unroll
-    for (int j = 0; j < TPL; ++j) acc[j] = 0.0f;
-    int32_t q = begin;
-    for (; q + 8 <= end; q += 8) {
-        float av[8][TPL];
-        float vv[8];
-#pragma unroll
-        for (int u = 0; u < 8; ++u) {
-            const uint32_t hh = static_cast<uint16_t>(hid[q + u]);
-            vv[u] = widen(v[q + u]);
-            load_vec<TPL>(base + static_cast<size_t>(hh) * ld, av[u]);
-        }
-#pragma unroll
-        for (int u = 0; u < 8; ++u)
-#pragma unroll
-            for (int j = 0; j < TPL; ++j) acc[j] = fmaf(vv[u], av[u][j], acc[j]);
-    }
-    for (; q < end; ++q) {
-        const uint32_t hh = static_cast<uint16_t>(hid[q]);
-        const float vv = widen(v[q]);
-        float av[TPL];
-        load_vec<TPL>(base + static_cast<size_t>(hh) * ld, av);
-#pragma unroll
-        for (int j = 0; j < TPL; ++j) acc[j] = fmaf(vv, av[j], acc[j]);
-    }
-    const float bo = bias ? bias[o] : 0.0f;  // no bias: the backward's gx
+    walk_row<TPL>(act + (live ? t0 : 0), hid, v, off[o], off[o + 1], ld, threadIdx.x % kWave, acc);
+    if (!live) return;
     float* out = y_t + static_cast<size_t>(o) * ld + t0;
 #pragma unroll
     for (int j = 0; j < TPL; ++j)

@@ -52,7 +52,7 @@ def check(runtime: HFFNRuntime, index: int, x: torch.Tensor, expected: torch.Ten
                 continue
             if up == "tiles" and not runtime.tiles_available:
                 continue
-            if up in ("gemv", "tiles") and x.shape[0] > GEMV_MAX_TOKENS:
+            if up == "gemv" and x.shape[0] > GEMV_MAX_TOKENS:
                 continue
             runtime.force(up, down)
             y = runtime.forward(index, x).clone()

@@ -20,7 +20,7 @@ import ctypes
 import torch
 
 from . import _lib
-from .runtime import MAX_TOKENS, HFFNRuntime, _aligned, leading_dim
+from .runtime import MAX_TOKENS, TILES_MAX_TOKENS, HFFNRuntime, _aligned, leading_dim
 
 _GATHER = ("edges", "rows")
 
@@ -68,6 +68,8 @@ class PreparedRuntime(HFFNRuntime):
                                                 self.d_ff, n, ctypes.byref(handle)),
                        "plan (gemv, gemv)")
             return handle.value, up, down
+        if up == "tiles" and n > TILES_MAX_TOKENS:
+            return False  # pieces of TILES_MAX_TOKENS tokens: the control's loop
         if up == "tiles":
             entry = self._lib.hffn_plan_tiles if self.tiled else self._lib.hffn_plan_tiles_compact
             _lib.check(entry(value_type, *self._tiles_args(index), self.d_model, self.d_ff, *self._nnz[index], n, ctypes.byref(handle)),

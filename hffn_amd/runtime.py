@@ -19,7 +19,11 @@ Kernel shapes (the build's own policy, ``up_mode``/``down_mode``):
   large token counts), run when forced.
 
 The policy reads the compact store up to 64 tokens: ``edges`` (up to 32 tokens) or ``tiles``, whichever has the least
-estimated time (``decode_mode``); above 64 tokens the MFMA path where the layer has planes, else ``rows``. The dense
+estimated time (``decode_mode``); above 64 tokens the MFMA path where the layer has planes, else ``tiles`` in pieces of
+64 tokens or ``rows``, whichever has the least estimated time (``pieces_us``, ``rows_us``: the tiles path reads the
+store once per piece, the lane-per-token kernels read an input row per slot and token, so the tiles path takes the
+larger layers, e.g. the 1.4B layer at 20 %, 59 against 223 us at 65 tokens and 1.32 against 2.00 ms at 2048, and the
+lane-per-token kernels the smallest, e.g. the 70M layer at 20 % from 128 tokens on, 53 against 63 us). The dense
 planes (4 bytes per weight for float32 values, 2 for bfloat16) are built only for layers of at least
 ``MFMA_MIN_DENSITY`` unless asked for (``dense=True``). Per call on the Pythia-410M layer at 50 % (12 rotating
 copies, MI355X, HFFNRuntime.forward): N = 1: tiles 17.4 us, edges 17.6; N = 4: edges 15.3, tiles 17.2; N = 16:
@@ -61,6 +65,10 @@ TILES_BASE_US, TILES_SLOT_US = 12.7, 1.11e-6
 TILES_FILL_US, TILES_FILL_SLOT_US = 2.0, 0.07e-6
 TILES_TILE_US, TILES_TILE_SLOT_US = 4.5, 0.17e-6
 TILES_TIE = 1.05  # the tiles path wins estimates within 5 % of the lane-per-slot kernels' (its cost is flat in N)
+# Lane-per-token kernels above 64 tokens: ROWS_CALL_US per call plus ROWS_SLOT_US per stored slot (both sides) and token
+# (each slot reads its input row of every token from L2), fitted to forced-pair timings of the 70M/20 %, 410M/50 % and
+# 1.4B/20 % bf16 layers at 65-2048 tokens; against it the tiles path in pieces of 64 tokens (one tiles_us each).
+ROWS_CALL_US, ROWS_SLOT_US = 45.0, 0.14e-6
 MAX_TOKENS = 1 << 18      # runtime/gpu/nvidia/common/kernels/hffn_cuda/runtime.py:26
 # The reference's policy constants (runtime.py:24-25), with this policy's meaning: COOP_MAX_TOKENS, the largest N the
 # policy may run on the cooperative (lane-per-slot, wave-reduced) kernels; BLOCK_MAX_WIDTH, the widest d_ff up to which
@@ -102,6 +110,17 @@ def tiles_us(n: int, slots: int) -> float:
     """Estimated µs of a call on the compact-store MFMA path (N <= 64; ``slots``: stored slots of both sides)."""
     return (TILES_BASE_US + TILES_SLOT_US * slots + (TILES_FILL_US + TILES_FILL_SLOT_US * slots) * min(n - 1, 15) / 15
             + (TILES_TILE_US + TILES_TILE_SLOT_US * slots) * ((n - 1) // 16))
+
+
+def rows_us(n: int, slots: int) -> float:
+    """Estimated µs of a call on the lane-per-token kernels above 64 tokens (``slots``: stored slots of both sides)."""
+    return ROWS_CALL_US + ROWS_SLOT_US * slots * n
+
+
+def pieces_us(n: int, slots: int) -> float:
+    """Estimated µs of N tokens on the tiles path, in calls of up to ``TILES_MAX_TOKENS`` tokens."""
+    whole, rest = divmod(n, TILES_MAX_TOKENS)
+    return whole * tiles_us(TILES_MAX_TOKENS, slots) + (tiles_us(rest, slots) if rest else 0.0)
 
 
 def decode_mode(n: int, slots: int, edges: bool, tiles: bool) -> str | None:
@@ -448,6 +467,8 @@ class HFFNRuntime:
                     return mode, mode
             elif self._planes is not None and self.density >= MFMA_MIN_DENSITY and mfma_streamed(n, self.d_model, self.d_ff):
                 return "mfma", "mfma"
+            elif self._tiles is not None and pieces_us(n, self._slots) < rows_us(n, self._slots):
+                return "tiles", "tiles"
         up = self.forced_up or up_mode(n, self.d_model)
         if up == "edges" and not edges:
             up = "rows"
@@ -470,12 +491,13 @@ class HFFNRuntime:
         self.calls[up, down] += 1
         return self._y[:n]
 
-    def _tiles_args(self, index: int) -> tuple:
+    def _tiles_args(self, index: int, y: int | None = None) -> tuple:
         """The arguments of ``hffn_forward_tiles`` / ``hffn_plan_tiles`` (or, for ``tiled=False``, of
-        ``hffn_forward_tiles_compact`` / ``hffn_plan_tiles_compact``) between x and the widths."""
+        ``hffn_forward_tiles_compact`` / ``hffn_plan_tiles_compact``) between x and the widths; the output at ``y``
+        (default: the start of the output buffer)."""
         tensors, tiles = self._tensors[index], self._tiles[index]
-        _, act, _, y = self._work
-        work = (act, self._tiles_work.data_ptr(), 4 * self._tiles_work.numel(), y)
+        _, act, _, y0 = self._work
+        work = (act, self._tiles_work.data_ptr(), 4 * self._tiles_work.numel(), y0 if y is None else y)
         if not self.tiled:
             return (tensors["up_idx"].data_ptr(), tensors["up_val"].data_ptr(), tiles["up"].data_ptr(), tensors["b_up"].data_ptr(),
                     tensors["out_hidden"].data_ptr(), tensors["out_val"].data_ptr(), tiles["down"].data_ptr(),
@@ -484,18 +506,20 @@ class HFFNRuntime:
                 tiles["down_table"].data_ptr(), tensors["b_down"].data_ptr(), *work)
 
     def _tiles_forward(self, index: int, x: torch.Tensor, n: int, stream) -> None:
-        """One call of the tiles path on x (16-byte aligned), from the tiled store or the compact rows."""
+        """The tiles path on x (16-byte aligned), from the tiled store or the compact rows: one call per piece of up to
+        ``TILES_MAX_TOKENS`` tokens (token-major rows of x and y, one after the other on the stream)."""
         entry = self._lib.hffn_forward_tiles if self.tiled else self._lib.hffn_forward_tiles_compact
-        _lib.check(entry(self._args[index][0], x.data_ptr(), *self._tiles_args(index), self.d_model, self.d_ff, *self._nnz[index], n,
-                         stream), "forward (tiles, tiles)")
+        row = 4 * self.d_model  # bytes of one token's x or y
+        for t0 in range(0, n, TILES_MAX_TOKENS):
+            m = min(TILES_MAX_TOKENS, n - t0)
+            _lib.check(entry(self._args[index][0], x.data_ptr() + row * t0, *self._tiles_args(index, self._y.data_ptr() + row * t0),
+                             self.d_model, self.d_ff, *self._nnz[index], m, stream), "forward (tiles, tiles)")
 
     def _launch(self, index: int, x: torch.Tensor, n: int, up: str, down: str) -> None:
         value_type, *model = self._args[index]
         x_t, act, y_t, y = self._work
         stream = torch.cuda.current_stream(self.device).cuda_stream
         if up == "tiles":
-            if n > TILES_MAX_TOKENS:
-                raise ValueError(f"the tiles path takes at most {TILES_MAX_TOKENS} tokens, not {n}")
             x = _aligned(x)  # read 16 bytes at a time
             self._fresh_tiles(index)
             self._tiles_forward(index, x, n, stream)

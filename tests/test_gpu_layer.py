@@ -149,7 +149,7 @@ def test_forced_pairs_match_the_oracle(name, test_layers, device):
         assert result.repeatable, f"{name} N{n}: bits differ on repeat"
         assert result.sequential_bits, f"{name} N{n}: the sequential pair depends on the batch"
         assert result.error <= ATOL, f"{name} N{n}: {result.pairs}"
-    skipped = 2 * sum(n > GEMV_MAX_TOKENS for n in BATCHES)  # the decode GEMVs and the tiles path take at most 64 tokens
+    skipped = sum(n > GEMV_MAX_TOKENS for n in BATCHES)  # the decode GEMVs take at most 64 tokens
     halves = 2 * sum(n >= 2 for n in BATCHES)  # the sequential pair also runs the input's two halves
     assert sum(runtime.calls.values()) == 2 * (len(BATCHES) * len(parity.PAIRS) - skipped) + halves
 
@@ -407,12 +407,20 @@ def test_tiles_on_the_compact_rows_equal_the_tiled_store(shape, test_layers, dev
             assert _relative(expected, reference.forward(compact, x_np)) <= 1e-5, n
 
 
-def test_tiles_refuses_more_than_64_tokens(test_layers, device):
-    compact, case, layer = test_layers["homog_512_2048"]
-    runtime = HFFNRuntime([layer], device, dense=True)
+@pytest.mark.parametrize("n", (65, 129, 200))
+def test_tiles_above_64_tokens_run_in_pieces(n, test_layers, device):
+    """Above 64 tokens the tiles path runs pieces of 64 tokens one after the other: the output is, token for token, the
+    bits of the pieces run as separate calls, and it matches the oracle."""
+    compact, case, layer = test_layers["irreg_512_2048"]
+    runtime = HFFNRuntime([layer], device)
     runtime.force("tiles", "tiles")
-    with pytest.raises(ValueError, match="at most 64"):
-        runtime.forward(0, torch.from_numpy(synth.make_input(case, 65)).to(device))
+    x_np = synth.make_input(case, n)
+    x = torch.from_numpy(x_np).to(device)
+    whole = runtime.forward(0, x).clone()
+    for start in range(0, n, 64):
+        piece = runtime.forward(0, x[start:start + 64].contiguous())
+        assert torch.equal(piece, whole[start:start + 64]), (n, start)
+    assert float((whole.double().cpu() - torch.from_numpy(reference.forward(compact, x_np))).abs().max()) <= ATOL
 
 
 def test_gemv_refuses_more_than_64_tokens(test_layers, device):
@@ -621,14 +629,16 @@ def test_gemv_wide_calls(name, tokens, device):
 
 def test_default_policy_reads_the_compact_store(device):
     """With the default construction, dense planes exist only for layers of at least 50 % density: the 1.4B/20 % bf16
-    layer has none and its calls up to 64 tokens take the compact-store paths (the tiles path at 16 and 64 tokens),
-    above them the gather kernels; the 410M/50 % layer keeps its planes for the MFMA path above 64 tokens and takes the
-    compact store below."""
+    layer has none and its calls take the compact-store MFMA path (tiles; above 64 tokens in pieces of 64) at every
+    size; the 70M/20 % layer takes the lane-per-token kernels from 128 tokens on; the 410M/50 % layer keeps its planes
+    for the MFMA path above 64 tokens and takes the compact store below."""
     from hffn_amd.runtime import MFMA_MIN_DENSITY
     sparse = HFFNRuntime([hip_layer(_cached("pythia1p4b_d20_bf16"))], device)
     assert sparse.density < MFMA_MIN_DENSITY and sparse.dense_bytes() == 0 and not sparse.mfma_available
     assert sparse.modes(16) == ("tiles", "tiles") and sparse.modes(64) == ("tiles", "tiles")
-    assert sparse.modes(65) == ("rows", "rows")
+    assert sparse.modes(65) == ("tiles", "tiles") and sparse.modes(2048) == ("tiles", "tiles")
+    small = HFFNRuntime([hip_layer(_cached("pythia70m_d20"))], device)
+    assert small.modes(128) == ("rows", "rows") and small.modes(2048) == ("rows", "rows")
     dense = HFFNRuntime([hip_layer(_cached("pythia410m_d50"))], device)
     assert dense.density >= MFMA_MIN_DENSITY and dense.dense_bytes() > 0
     assert dense.modes(16) == ("tiles", "tiles") and dense.modes(2048) == ("mfma", "mfma")

@@ -182,6 +182,25 @@ def test_tiles_estimate():
         assert abs(runtime.tiles_us(n, slots) / us - 1) < 0.2, (slots, n)
 
 
+def test_large_n_estimates():
+    """Above 64 tokens, without planes, the tiles path in pieces of 64 against the lane-per-token kernels: the estimates
+    pick the faster of the forced-pair timings they were fitted to (MI355X, µs per call): the 1.4B/20 % bf16 layer on
+    the tiles path at every count (65: 59 against 223; 512: 332 against 500; 2048: 1321 against 1998), the 410M/50 %
+    layer too (128: 57 against 203), the 70M/20 % layer on the lane-per-token kernels from 128 tokens (53 against 63;
+    2048: 145 against 998); the rows estimate within 30 % of those timings from 128 tokens on."""
+    s410, s1p4, s70 = 2 * 4096 * 512, 2 * 8192 * 410, 2 * 2048 * 102
+    faster = lambda n, slots: "tiles" if runtime.pieces_us(n, slots) < runtime.rows_us(n, slots) else "rows"
+    assert [faster(n, s1p4) for n in (65, 128, 512, 2048)] == ["tiles"] * 4
+    assert [faster(n, s410) for n in (65, 128, 2048)] == ["tiles"] * 3
+    assert [faster(n, s70) for n in (128, 256, 2048)] == ["rows"] * 3
+    assert runtime.pieces_us(128, s70) == 2 * runtime.tiles_us(64, s70)
+    assert runtime.pieces_us(65, s70) == runtime.tiles_us(64, s70) + runtime.tiles_us(1, s70)
+    rows_measured = {(s70, 128): 52.6, (s70, 512): 69.1, (s70, 2048): 145.2, (s1p4, 512): 499.8, (s1p4, 2048): 1997.7,
+                     (s410, 512): 313.4, (s410, 2048): 1085.7, (s1p4, 128): 234.7}
+    for (slots, n), us in rows_measured.items():
+        assert abs(runtime.rows_us(n, slots) / us - 1) < 0.3, (slots, n)
+
+
 @pytest.mark.skipif(torch.cuda.is_available(), reason="uses placeholder pointers: never run where a launch could reach a GPU")
 def test_training_planes_entries_refuse_bad_arguments():
     """The planes training products: sized only where the streamed GEMM takes N; the forward with z and the backward
