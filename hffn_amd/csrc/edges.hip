@@ -42,9 +42,10 @@ __global__ __launch_bounds__(WAVES * kWave) void up_edges_kernel(const float* __
     const uint32_t r1 = min(h, r0 + per_block);
     for (uint32_t c0 = 0; c0 < n; c0 += NT) {
         const uint32_t tokens = min(n - c0, static_cast<uint32_t>(NT));
-        // the first row's slots are requested before the block stages x and waits for it
+        // the first row's slots (and bias) are requested before the block stages x and waits for it
         Slots<V> cur;
         request_row<P>(cur, off, idx, w, r0 + row_in_pass, r1, part, nnz, lane);
+        float b_cur = GRAD ? 0.0f : row_bias(b, r0 + row_in_pass, r1);
         if (c0) __syncthreads();
         stage_inputs<NT, WAVES>(xs, x + static_cast<size_t>(c0) * d, d, 1, d, tokens, wave, lane);
         wait_loads<0>();
@@ -55,6 +56,7 @@ __global__ __launch_bounds__(WAVES * kWave) void up_edges_kernel(const float* __
             // the wave's next row is requested before this row's sums, so its slots stream meanwhile
             Slots<V> next;
             request_row<P>(next, off, idx, w, r + kRowsPerPass, r1, part, nnz, lane);
+            const float b_next = GRAD ? 0.0f : row_bias(b, r + kRowsPerPass, r1);
             float acc[NT];
             if (r < r1) {
                 row_partials<NT>(cur.seg, idx, w, cur.pb, cur.pe, nnz, input, lane, acc);
@@ -68,12 +70,13 @@ __global__ __launch_bounds__(WAVES * kWave) void up_edges_kernel(const float* __
                 if constexpr (GRAD) {  // the backward's gz: z holds the forward's pre-activations
                     act[at] = total * gelu_grad(z[at]);
                 } else {
-                    const float pre = b[r] + total;
+                    const float pre = b_cur + total;
                     if (z) z[at] = pre;  // the training forward keeps the pre-activation
                     act[at] = gelu(pre);
                 }
             }
             cur = next;
+            b_cur = b_next;
         }
     }
 }
@@ -96,6 +99,7 @@ __global__ __launch_bounds__(WAVES * kWave) void down_edges_kernel(const float* 
         const uint32_t tokens = min(n - c0, static_cast<uint32_t>(NT));
         Slots<V> cur;
         request_row<P>(cur, off, hid, v, o0 + row_in_pass, o1, part, nnz, lane);
+        float b_cur = row_bias(bias, o0 + row_in_pass, o1);
         if constexpr (STAGE) {
             if (c0) __syncthreads();
             stage_inputs<NT, WAVES>(as, act + c0, h, ld, 1, tokens, wave, lane);
@@ -106,6 +110,7 @@ __global__ __launch_bounds__(WAVES * kWave) void down_edges_kernel(const float* 
             const uint32_t o = base + row_in_pass;
             Slots<V> next;
             request_row<P>(next, off, hid, v, o + kRowsPerPass, o1, part, nnz, lane);
+            const float b_next = row_bias(bias, o + kRowsPerPass, o1);
             float acc[NT];
             if (o < o1) {
                 if constexpr (STAGE) row_partials<NT>(cur.seg, hid, v, cur.pb, cur.pe, nnz, StagedInput{as}, lane, acc);
@@ -115,8 +120,9 @@ __global__ __launch_bounds__(WAVES * kWave) void down_edges_kernel(const float* 
                 for (int t = 0; t < NT; ++t) acc[t] = 0.0f;
             }
             const float total = row_total<NT, P>(acc, lane, part, row_in_pass, totals);
-            if (o < o1 && part == 0 && lane < tokens) y[static_cast<size_t>(c0 + lane) * d + o] = bias ? total + bias[o] : total;
+            if (o < o1 && part == 0 && lane < tokens) y[static_cast<size_t>(c0 + lane) * d + o] = bias ? total + b_cur : total;
             cur = next;
+            b_cur = b_next;
         }
     }
 }

@@ -189,6 +189,12 @@ __device__ __forceinline__ void segment(int32_t begin, int32_t end, uint32_t par
     }
 }
 
+// Row r's bias (0 past the rows, or without biases), requested with the row's slots so that the epilogue does not
+// wait for it.
+__device__ __forceinline__ float row_bias(const float* __restrict__ b, uint32_t r, uint32_t rows) {
+    return b != nullptr && r < rows ? b[r] : 0.0f;
+}
+
 // A wave's first chunk of one row segment, requested ahead of its use.
 template <typename V>
 struct Slots {
