@@ -170,8 +170,12 @@ int launch_forward(const Plan& p, const float* x, hipStream_t s, float* z = null
         if (int status = launched(hffn::launch_transpose(x, p.x_t, p.n, p.d_model, p.d_model, p.ld, s), "input transpose")) return status;
     }
     if (p.up_mode == HFFN_UP_ROWS) x = p.x_t;
+    // One or two tokens on the lane-per-slot pair (without z): the activations are packed [d_ff, n] in the workspace,
+    // so that the down kernel's blocks read them from contiguous memory (in the [d_ff, ld] layout a row's n values are
+    // followed by ld - n unused ones).
+    const uint32_t act_ld = !z && p.n <= 2 && p.up_mode == HFFN_UP_EDGES && p.down_mode == HFFN_DOWN_EDGES ? p.n : p.ld;
     if (int status = launch_up(p.up_mode, p.value_type, x, p.up_offsets, p.up_idx, p.up_val, p.b_up, p.act, p.d_model, p.d_ff,
-                               p.nnz_up, p.n, p.ld, s, z))
+                               p.nnz_up, p.n, act_ld, s, z))
         return status;
     if (p.down_mode == HFFN_DOWN_ROWS) {
         if (int status = launch_down(p.down_mode, p.value_type, p.act, p.out_offsets, p.out_hidden, p.out_val, p.b_down, p.y_t,
@@ -180,7 +184,7 @@ int launch_forward(const Plan& p, const float* x, hipStream_t s, float* z = null
         return launched(hffn::launch_transpose(p.y_t, p.y, p.d_model, p.n, p.ld, p.d_model, s), "output transpose");
     }
     return launch_down(p.down_mode, p.value_type, p.act, p.out_offsets, p.out_hidden, p.out_val, p.b_down, p.y, p.d_model, p.d_ff,
-                       p.nnz_down, p.n, p.ld, s);
+                       p.nnz_down, p.n, act_ld, s);
 }
 
 // Everything of one decode-GEMV forward (hffn_forward_gemv) but x and the stream.
