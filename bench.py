@@ -215,13 +215,60 @@ def call_us(runtime, x: torch.Tensor, copies: int, rotations: int) -> float:
     return start.elapsed_time(end) * 1e3 / (rotations * copies)
 
 
-def decode_entry(runtime, workload, compact, n: int, copies: int, rotations: int, device) -> dict:
+def read_floor(compact, copies: int, rotations: int, device) -> dict:
+    """The plain-read floor of a decode call (``hffn_read_probe``): the bytes of the layer's up and down stores (offsets,
+    slots, bias) read by a kernel that does nothing else, from ``copies`` distinct buffers in rotation, as one launch
+    per side back to back (the call's two dependent kernels) and as one launch for both; µs per call, events around
+    ``rotations`` passes after one untimed pass."""
+    from hffn_amd import _lib
+    lib = _lib.load()
+    costs = layer_costs(compact, 1)
+    sides = [costs["up"]["bytes"] - 4 * (compact.d_model + compact.d_ff), costs["down"]["bytes"] - 4 * (compact.d_model + compact.d_ff)]
+    sides = [(b + 15) // 16 * 16 for b in sides]
+    buffers = [torch.empty(sum(sides), dtype=torch.uint8, device=device) for _ in range(copies)]
+    blocks = lambda size: min(8192, max(256, size // 12288))  # ~3 KB per wave  # noqa: E731
+    sink = torch.empty(4 * blocks(sum(sides)), dtype=torch.int32, device=device)
+    stream = torch.cuda.current_stream(device).cuda_stream
+
+    def read(pointer: int, size: int) -> None:
+        _lib.check(lib.hffn_read_probe(pointer, size, sink.data_ptr(), sink.numel(), blocks(size), stream), "read probe")
+
+    def timed(one_launch: bool) -> float:
+        def run(buffer):
+            if one_launch:
+                read(buffer.data_ptr(), sum(sides))
+            else:
+                read(buffer.data_ptr(), sides[0])
+                read(buffer.data_ptr() + sides[0], sides[1])
+        for buffer in buffers:
+            run(buffer)
+        torch.cuda.synchronize()
+        start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        start.record()
+        for _ in range(rotations):
+            for buffer in buffers:
+                run(buffer)
+        end.record()
+        torch.cuda.synchronize()
+        return start.elapsed_time(end) * 1e3 / (rotations * copies)
+
+    two, one = timed(False), timed(True)
+    del buffers
+    return {"bytes_per_side": sides, "two_launches_us": round(two, 2), "one_launch_us": round(one, 2),
+            "two_launches_hbm_fraction": round(sum(sides) / (two * 1e-6) / HBM_PEAK, 4),
+            "one_launch_hbm_fraction": round(sum(sides) / (one * 1e-6) / HBM_PEAK, 4)}
+
+
+def decode_entry(runtime, workload, compact, n: int, copies: int, rotations: int, device, floor: dict | None = None) -> dict:
     from hffn_amd import synth
     x = torch.from_numpy(synth.make_input(workload, n)).to(device)
     us = call_us(runtime, x, copies, rotations)
     moved = layer_costs(compact, n)["step_bytes"]  # the compact store, x read, y written
-    return {"tokens": n, "modes": list(runtime.modes(n)), "us_per_call": round(us, 2), "tokens_per_s": round(n / us * 1e6, 1),
-            "hbm_fraction": round(moved / (us * 1e-6) / HBM_PEAK, 4)}
+    entry = {"tokens": n, "modes": list(runtime.modes(n)), "us_per_call": round(us, 2), "tokens_per_s": round(n / us * 1e6, 1),
+             "hbm_fraction": round(moved / (us * 1e-6) / HBM_PEAK, 4)}
+    if floor:  # the call's time against a plain read of its stores in two launches
+        entry["of_read_floor"] = round(floor["two_launches_us"] / us, 3)
+    return entry
 
 
 def decode_record(runtime, base, device, rotations: int, steps: int) -> dict:
@@ -229,7 +276,8 @@ def decode_record(runtime, base, device, rotations: int, steps: int) -> dict:
     at 1, 8 and 16 tokens; the Pythia-1.4B-shape bf16 layer at 20 % at 1, 4 and 16 tokens (one generated layer and
     device clones, more than 300 MB in the rotation); and the FFN calls of one decode step of the 24-layer
     Pythia-410M-shape model at batch 1 and 8, eager and replayed from a HIP graph (hffn_amd.bench_decode). Every
-    entry: µs per call (or step) and the HBM fraction on the compact bytes it reads."""
+    entry: µs per call (or step), the HBM fraction on the compact bytes it reads, and the fraction of the plain-read
+    floor (``read_floor``: the same bytes read by a kernel that does nothing else, one launch per side)."""
     from hffn_amd import bench_decode, synth
     from hffn_amd.ffn import hip_layer
     from hffn_amd.prepared_runtime import PreparedRuntime
@@ -237,19 +285,25 @@ def decode_record(runtime, base, device, rotations: int, steps: int) -> dict:
 
     record = {"rotation": f"{rotations} passes over each layer's copies after one untimed pass; HIP events around all"}
     copies = len(runtime.layers)
-    record["pythia410m_d50"] = [decode_entry(runtime, synth.WORKLOADS["pythia410m_d50"], base, n, copies, rotations, device)
+    floor = read_floor(base, copies, rotations, device)
+    record["pythia410m_d50_read_floor"] = floor
+    record["pythia410m_d50"] = [decode_entry(runtime, synth.WORKLOADS["pythia410m_d50"], base, n, copies, rotations, device, floor)
                                 for n in DECODE_TOKENS["pythia410m_d50"]]
     workload = synth.WORKLOADS["pythia1p4b_d20_bf16"]
     compact = synth.make_workload_layer(workload)
     count = max(1, math.ceil(MALL_BYTES / layer_costs(compact, 1)["model_bytes"]))
     bf16 = HFFNRuntime(device_copies(hip_layer(compact, device), count), device)
-    record["pythia1p4b_d20_bf16"] = [decode_entry(bf16, workload, compact, n, count, rotations, device)
+    bf16_floor = read_floor(compact, count, rotations, device)
+    record["pythia1p4b_d20_bf16_read_floor"] = bf16_floor
+    record["pythia1p4b_d20_bf16"] = [decode_entry(bf16, workload, compact, n, count, rotations, device, bf16_floor)
                                      for n in DECODE_TOKENS["pythia1p4b_d20_bf16"]]
     del bf16
     layers = runtime.layers + device_copies(runtime.layers[0], DECODE_STEP_LAYERS - copies + 1)[1:]
     model = PreparedRuntime(layers[:DECODE_STEP_LAYERS], device)
     record["pythia410m_model_step"] = [bench_decode.measure(model, [base] * DECODE_STEP_LAYERS, batch, steps)
                                        for batch in DECODE_STEP_BATCHES]
+    for entry in record["pythia410m_model_step"]:  # against the plain read of every layer's stores, two launches each
+        entry["of_read_floor"] = round(DECODE_STEP_LAYERS * floor["two_launches_us"] / entry["calls_us_per_step"], 3)
     del model
     torch.cuda.empty_cache()
     return record

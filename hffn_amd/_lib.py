@@ -10,7 +10,7 @@ import ctypes
 from pathlib import Path
 
 LIBRARY = Path(__file__).resolve().with_name("libhffn_amd.so")
-ABI_VERSION = 16
+ABI_VERSION = 17
 
 OK = 0
 VALUE_F32, VALUE_BF16 = 0, 1
@@ -43,6 +43,7 @@ SIGNATURES = {
     "hffn_reduce_tiles": [_P, _U32, _U32, _U32, _U32, _U32, _P, _P, _P, _P, _P],
     "hffn_adamw": [_P] * 4 + [_U32] + [ctypes.c_float] * 8 + [_P],
     "hffn_gather_values": [_P, _P, _P, _U32, _P],
+    "hffn_read_probe": [_P, _U64, _P, _U32, _U32, _P],
     "hffn_output_major_workspace": [_U32, _U32, ctypes.POINTER(_U64)],
     "hffn_output_major": [_I, _P, _P, _P, _U32, _U32, _U32, _P, _P, _P, _P, _U64, _P],
     "hffn_mfma_supported": [_U32, _U32],

@@ -829,4 +829,14 @@ int hffn_gather_values(const float* src, const int32_t* pos, float* dst, uint32_
     return launched(hffn::launch_gather_values(src, pos, dst, count, static_cast<hipStream_t>(stream)), "gather_values");
 }
 
+int hffn_read_probe(const void* data, uint64_t bytes, uint32_t* sink, uint32_t sink_words, uint32_t blocks, void* stream) {
+    if (!data || !sink) return fail(HFFN_ERROR_ARGUMENT, "read_probe: null pointer");
+    if (bytes == 0 || bytes % 16 != 0 || reinterpret_cast<uintptr_t>(data) % 16 != 0)
+        return fail(HFFN_ERROR_ARGUMENT, "read_probe: %llu bytes: a nonzero multiple of 16 bytes from a 16-byte aligned pointer",
+                    static_cast<unsigned long long>(bytes));
+    if (blocks == 0 || blocks > 65535 || static_cast<uint64_t>(sink_words) < 4ull * blocks)
+        return fail(HFFN_ERROR_ARGUMENT, "read_probe: %u blocks need 1-65535 blocks and 4 sink words each (%u given)", blocks, sink_words);
+    return launched(hffn::launch_read_probe(data, bytes, sink, blocks, static_cast<hipStream_t>(stream)), "read_probe");
+}
+
 }  // extern "C"

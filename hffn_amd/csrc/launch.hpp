@@ -156,4 +156,7 @@ hipError_t launch_tiles_forward(int vt, const float* x, const void* up_store, co
                                 const void* down_store, const int32_t* down_table, const float* b_down, float* act, float* work,
                                 float* y, uint32_t d, uint32_t h, uint64_t nnz_up, uint64_t nnz_down, uint32_t n, hipStream_t stream);
 
+// probe.hip
+hipError_t launch_read_probe(const void* data, uint64_t bytes, uint32_t* sink, uint32_t blocks, hipStream_t stream);
+
 }  // namespace hffn

@@ -27,7 +27,7 @@
 extern "C" {
 #endif
 
-#define HFFN_ABI_VERSION 16
+#define HFFN_ABI_VERSION 17
 
 #define HFFN_OK 0
 #define HFFN_ERROR_ARGUMENT (-1) /* invalid shape, mode, pointer or workspace */
@@ -349,6 +349,11 @@ int hffn_adamw(float* p, const float* g, float* m, float* v, uint32_t count, flo
 /* dst[j] = src[pos[j]]: the values of a transposed support refreshed from the compact array they index (the
  * reference reads them through the positions inside its kernels, kernels_train.py:142-150, 204-215). */
 int hffn_gather_values(const float* src, const int32_t* pos, float* dst, uint32_t count, void* stream);
+
+/* Measurement only, no counterpart in the reference: a plain streaming read of `bytes` (a nonzero multiple of 16 from
+ * a 16-byte aligned pointer) by `blocks` blocks of 4 waves, each wave one contiguous span, one word per wave written to
+ * sink (sink_words >= 4 blocks). The floor that the decode calls are measured against (bench.py's decode record). */
+int hffn_read_probe(const void* data, uint64_t bytes, uint32_t* sink, uint32_t sink_words, uint32_t blocks, void* stream);
 
 #ifdef __cplusplus
 }

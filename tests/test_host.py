@@ -202,6 +202,22 @@ def test_large_n_estimates():
 
 
 @pytest.mark.skipif(torch.cuda.is_available(), reason="uses placeholder pointers: never run where a launch could reach a GPU")
+def test_read_probe_refuses_bad_arguments():
+    """The plain-read probe of the decode measurements refuses null or misaligned data, a size that is not a nonzero
+    multiple of 16 bytes, a grid outside 1-65535 blocks and a sink smaller than 4 words per block, before any launch."""
+    lib = _lib.load()
+    p, odd, sink = ctypes.c_void_p(256), ctypes.c_void_p(264), ctypes.c_void_p(4096)
+    _expect_argument_error(lib.hffn_read_probe(None, 1024, sink, 16, 4, None), "null pointer")
+    _expect_argument_error(lib.hffn_read_probe(p, 1024, None, 16, 4, None), "null pointer")
+    _expect_argument_error(lib.hffn_read_probe(odd, 1024, sink, 16, 4, None), "multiple of 16")
+    _expect_argument_error(lib.hffn_read_probe(p, 1000, sink, 16, 4, None), "multiple of 16")
+    _expect_argument_error(lib.hffn_read_probe(p, 0, sink, 16, 4, None), "multiple of 16")
+    _expect_argument_error(lib.hffn_read_probe(p, 1024, sink, 16, 0, None), "blocks")
+    _expect_argument_error(lib.hffn_read_probe(p, 1024, sink, 15, 4, None), "blocks")
+    _expect_argument_error(lib.hffn_read_probe(p, 1024, sink, 1 << 20, 65536, None), "blocks")
+
+
+@pytest.mark.skipif(torch.cuda.is_available(), reason="uses placeholder pointers: never run where a launch could reach a GPU")
 def test_training_planes_entries_refuse_bad_arguments():
     """The planes training products: sized only where the streamed GEMM takes N; the forward with z and the backward
     refuse a small or misaligned workspace, a bad ld and misaligned or null buffers before any launch."""
