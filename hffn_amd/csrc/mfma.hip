@@ -239,10 +239,12 @@ __global__ __launch_bounds__(kDensThreads) void densify_kernel(const int32_t* __
 #pragma unroll
         for (int q = 0; q < kHeld; ++q) m = max(m, abs_bits(hw[q]));
     } else {
+        // a batch's loads all issued before the first is used: a slot past the row reads the row's last slot again
+        // (a value of the row: the maximum is unchanged)
         for (int32_t s0 = first; s0 < end; s0 += kBatch * kStride) {
             float w[kBatch];
 #pragma unroll
-            for (int q = 0; q < kBatch; ++q) w[q] = s0 + q * kStride < end ? value(s0 + q * kStride) : 0.0f;
+            for (int q = 0; q < kBatch; ++q) w[q] = value(min(s0 + q * kStride, end - 1));
 #pragma unroll
             for (int q = 0; q < kBatch; ++q) m = max(m, abs_bits(w[q]));
         }
@@ -267,10 +269,10 @@ __global__ __launch_bounds__(kDensThreads) void densify_kernel(const int32_t* __
             uint32_t c[kBatch];
             float w[kBatch];
 #pragma unroll
-            for (int q = 0; q < kBatch; ++q) {
-                const bool in = s0 + q * kStride < end;
-                c[q] = in ? static_cast<uint16_t>(idx[s0 + q * kStride]) : 0xFFFFFFFFu;
-                w[q] = in ? value(s0 + q * kStride) : 0.0f;
+            for (int q = 0; q < kBatch; ++q) {  // past the row: its last slot again (placed again, the same cell and value)
+                const int32_t at = min(s0 + q * kStride, end - 1);
+                c[q] = static_cast<uint16_t>(idx[at]);
+                w[q] = value(at);
             }
 #pragma unroll
             for (int q = 0; q < kBatch; ++q) place(c[q], w[q]);
@@ -1288,20 +1290,25 @@ __global__ __launch_bounds__(kThreads) void gather_dense_kernel(const float* __r
     const size_t plane = static_cast<size_t>(rows) * cols;
     const float* row = partials + static_cast<size_t>(o) * cols;
     const int32_t end = off[o + 1];
+    // a batch's loads all issued before the first is used (no branch between them): a slot past the row reads the
+    // row's last slot again, and its sum is not written
     for (int32_t q0 = off[o] + static_cast<int32_t>(lane); q0 < end; q0 += kBatch * kWave) {
         uint32_t c[kBatch];
         float v[kBatch];
 #pragma unroll
-        for (int j = 0; j < kBatch; ++j) c[j] = q0 + j * kWave < end ? static_cast<uint16_t>(idx[q0 + j * kWave]) : 0u;
+        for (int j = 0; j < kBatch; ++j) c[j] = static_cast<uint16_t>(idx[min(q0 + j * static_cast<int32_t>(kWave), end - 1)]);
 #pragma unroll
-        for (int j = 0; j < kBatch; ++j) v[j] = q0 + j * kWave < end ? row[c[j]] : 0.0f;
-        for (uint32_t sp = 1; sp < splits; ++sp)
+        for (int j = 0; j < kBatch; ++j) v[j] = row[c[j]];
+        for (uint32_t sp = 1; sp < splits; ++sp) {
+            float u[kBatch];
 #pragma unroll
-            for (int j = 0; j < kBatch; ++j)
-                if (q0 + j * kWave < end) v[j] += row[sp * plane + c[j]];
+            for (int j = 0; j < kBatch; ++j) u[j] = row[sp * plane + c[j]];
+#pragma unroll
+            for (int j = 0; j < kBatch; ++j) v[j] += u[j];
+        }
 #pragma unroll
         for (int j = 0; j < kBatch; ++j)
-            if (q0 + j * kWave < end) g[q0 + j * kWave] = v[j];
+            if (q0 + j * static_cast<int32_t>(kWave) < end) g[q0 + j * kWave] = v[j];
     }
 }
 

@@ -81,28 +81,35 @@ constexpr bool shape_fits() {
 }
 
 // One 8-slot piece of a row of the compact store, slots [8 q, 8 q + 8): its 8 indices (one 16-byte load) and values
-// (one or two 16-byte loads); a piece across the end of the arrays is read slot by slot, the slots past nnz zero.
+// (one or two 16-byte loads), without branches, so that a wave's pieces are in flight together. A piece across the end
+// of the arrays (the store's last, when nnz is not a multiple of 8) loads piece 0 here (nnz >= 8), and load_tail then
+// reads it slot by slot, the slots past nnz zero.
 template <typename V>
 __device__ __forceinline__ void load_piece(const int16_t* __restrict__ idx, const V* __restrict__ val, int32_t q, int32_t nnz,
                                            uint4 (&pc)[1 + Planes<V>::count]) {
     constexpr uint32_t P = Planes<V>::count;
+    const int32_t s = 8 * q, at = s + 8 <= nnz ? s : 0;
+    pc[0] = *reinterpret_cast<const uint4*>(idx + at);
+#pragma unroll
+    for (uint32_t p = 0; p < P; ++p) pc[1 + p] = reinterpret_cast<const uint4*>(val + at)[p];
+}
+
+template <typename V>
+__device__ __forceinline__ void load_tail(const int16_t* __restrict__ idx, const V* __restrict__ val, int32_t q, int32_t nnz,
+                                          uint4 (&pc)[1 + Planes<V>::count]) {
+    // composed in 32-bit words (two 16-bit indices or bfloat16 values per word, one float32 value), as the whole-piece
+    // loads deliver them
     const int32_t s = 8 * q;
-    if (s + 8 <= nnz) {
-        pc[0] = *reinterpret_cast<const uint4*>(idx + s);
-#pragma unroll
-        for (uint32_t p = 0; p < P; ++p) pc[1 + p] = reinterpret_cast<const uint4*>(val + s)[p];
-    } else {
-        uint16_t ids[8] = {0, 0, 0, 0, 0, 0, 0, 0};
-        V vals[8] = {V(0), V(0), V(0), V(0), V(0), V(0), V(0), V(0)};
-        for (int u = 0; u < 8; ++u)
-            if (s + u < nnz) {
-                ids[u] = static_cast<uint16_t>(idx[s + u]);
-                vals[u] = val[s + u];
-            }
-        pc[0] = *reinterpret_cast<const uint4*>(ids);
-#pragma unroll
-        for (uint32_t p = 0; p < P; ++p) pc[1 + p] = reinterpret_cast<const uint4*>(vals)[p];
-    }
+    uint32_t ids[4] = {0, 0, 0, 0}, vals[8] = {0, 0, 0, 0, 0, 0, 0, 0};
+    for (int u = 0; u < 8; ++u)
+        if (s + u < nnz) {
+            ids[u / 2] |= static_cast<uint32_t>(static_cast<uint16_t>(idx[s + u])) << (16 * (u % 2));
+            if constexpr (Planes<V>::count == 1) vals[u / 2] |= static_cast<uint32_t>(val[s + u]) << (16 * (u % 2));
+            else vals[u] = __float_as_uint(val[s + u]);
+        }
+    pc[0] = make_uint4(ids[0], ids[1], ids[2], ids[3]);
+    pc[1] = make_uint4(vals[0], vals[1], vals[2], vals[3]);
+    if constexpr (Planes<V>::count == 2) pc[2] = make_uint4(vals[4], vals[5], vals[6], vals[7]);
 }
 
 // Value u (0..7) of a piece: float32 (fields 4 per uint4) or bfloat16 bits.
@@ -244,10 +251,14 @@ __global__ __launch_bounds__(kThreads) void tiles_kernel(const float* __restrict
                 if (g >= cum[t]) tr = t;
             q = q0[tr] + (g - cum[tr]);
         };
+        // without branches: a lane past the wave's pieces loads the wave's last piece again (and places nothing); a
+        // piece across nnz is completed by fix_tail
         auto fetch = [&](int32_t g, int& tr, int32_t& q, uint4 (&part)[3]) {
-            if (g >= pieces) return;
-            locate(g, tr, q);
-            load_piece(cidx, cval, q, nnz, reinterpret_cast<uint4(&)[1 + P]>(part));
+            locate(min(g, max(pieces, 1) - 1), tr, q);
+            if (nnz >= 8) load_piece(cidx, cval, q, nnz, reinterpret_cast<uint4(&)[1 + P]>(part));
+        };
+        auto fix_tail = [&](int32_t g, int32_t q, uint4 (&part)[3]) {
+            if (g < pieces && (nnz < 8 || 8 * q + 8 > nnz)) load_tail(cidx, cval, q, nnz, reinterpret_cast<uint4(&)[1 + P]>(part));
         };
         // 2'. scatter: a piece's slots inside its row's range, at (row, index - kb); float32 weights split into fp16
         // hi + lo = w 2^-e(row), as the tile would hold them from any source
@@ -274,8 +285,23 @@ __global__ __launch_bounds__(kThreads) void tiles_kernel(const float* __restrict
         uint4 pa[3], pb[3];
         int tra = 0, trb = 0;
         int32_t qa = 0, qb = 0;
-        fetch(ga_at, tra, qa, pa);
-        fetch(gb_at, trb, qb, pb);
+        locate(min(ga_at, max(pieces, 1) - 1), tra, qa);
+        locate(min(gb_at, max(pieces, 1) - 1), trb, qb);
+        if (nnz >= 8) {  // both rounds' pieces in one block of loads, none of them used before all are requested
+            load_piece(cidx, cval, qa, nnz, reinterpret_cast<uint4(&)[1 + P]>(pa));
+            load_piece(cidx, cval, qb, nnz, reinterpret_cast<uint4(&)[1 + P]>(pb));
+            __builtin_amdgcn_sched_barrier(0);
+        }
+        bool tail = false;  // wave-uniform: some row's pieces reach past the last whole piece of the store
+#pragma unroll
+        for (int tr = 0; tr < TR; ++tr) {
+            const int32_t count = (tr + 1 < TR ? cum[tr + 1] : pieces) - cum[tr];
+            tail |= count > 0 && 8 * (q0[tr] + count) > (nnz & ~7);
+        }
+        if (tail) {
+            fix_tail(ga_at, qa, pa);
+            fix_tail(gb_at, qb, pb);
+        }
         for (uint32_t i = threadIdx.x; i < kTileBytes / 16; i += kThreads) reinterpret_cast<uint4*>(tile)[i] = make_uint4(0, 0, 0, 0);
         __syncthreads();  // the tile is zero (this waits for the LDS only: the loads stay in flight)
         place(ga_at, tra, qa, pa);
@@ -285,6 +311,7 @@ __global__ __launch_bounds__(kThreads) void tiles_kernel(const float* __restrict
             int tr = 0;
             int32_t q = 0;
             fetch(g, tr, q, pc);
+            fix_tail(g, q, pc);
             place(g, tr, q, pc);
         }
         __syncthreads();

@@ -333,8 +333,26 @@ def _layer_with_empty_items() -> synth.CompactLayer:
                               offsets, idx, val, np.zeros(d_model, np.float32))
 
 
+def _layer_with_few_slots() -> synth.CompactLayer:
+    """d_model 16, d_ff 8 and 5 slots on each side: fewer than one 8-slot piece, so every piece of the compact rows is
+    the store's last, read slot by slot."""
+    rng = np.random.default_rng(5)
+    d_model, d_ff = 16, 8
+    degrees = np.array([1, 0, 2, 0, 0, 1, 1, 0])
+    offsets = np.zeros(d_ff + 1, np.int32)
+    offsets[1:] = np.cumsum(degrees)
+    idx = np.concatenate([np.sort(rng.choice(d_model, k, replace=False)) for k in degrees]).astype(np.int16)
+    val = rng.standard_normal(offsets[-1]).astype(np.float32)
+    return synth.CompactLayer(d_model, d_ff, synth._groups(d_ff), offsets, idx, val, np.full(d_ff, 0.1, np.float32),
+                              offsets, idx, val, np.full(d_model, -0.1, np.float32))
+
+
+def _special_layer(dims: str) -> synth.CompactLayer:
+    return _layer_with_empty_items() if dims == "empty" else _layer_with_few_slots()
+
+
 @pytest.mark.parametrize("shape", [("irreg_512_2048", None), ("odd_f32", (48, 520, 37, "float32")),
-                                   ("odd_bf16", (64, 1032, 300, "bf16")), ("empty_items", "empty")])
+                                   ("odd_bf16", (64, 1032, 300, "bf16")), ("empty_items", "empty"), ("few_slots", "few")])
 def test_tiled_store_bitwise(shape, test_layers, device):
     """The tiled stores built on the device equal their host restatement bit for bit, on both sides: a reference test
     layer (512 x 2048, four sub-chunks), two odd shapes (rows not a multiple of 16, K not a multiple of 512, float32
@@ -343,8 +361,8 @@ def test_tiled_store_bitwise(shape, test_layers, device):
     name, dims = shape
     if dims is None:
         compact, _, layer = test_layers[name]
-    elif dims == "empty":
-        compact = _layer_with_empty_items()
+    elif dims in ("empty", "few"):
+        compact = _special_layer(dims)
         layer = hip_layer(compact)
     else:
         d_model, d_ff, degree, dtype = dims
@@ -371,7 +389,7 @@ def test_tiled_store_bitwise(shape, test_layers, device):
 
 
 @pytest.mark.parametrize("shape", [("irreg_512_2048", None), ("odd_f32", (48, 520, 37, "float32")),
-                                   ("odd_bf16", (64, 1032, 60, "bf16")), ("empty_items", "empty"),
+                                   ("odd_bf16", (64, 1032, 60, "bf16")), ("empty_items", "empty"), ("few_slots", "few"),
                                    ("pythia1p4b_d20_bf16", "workload")])
 def test_tiles_on_the_compact_rows_equal_the_tiled_store(shape, test_layers, device):
     """With tiled=False the tiles path reads the compact rows through the table of row bounds: the same dense tiles,
@@ -381,8 +399,8 @@ def test_tiles_on_the_compact_rows_equal_the_tiled_store(shape, test_layers, dev
     name, dims = shape
     if dims is None:
         compact, _, layer = test_layers[name]
-    elif dims == "empty":
-        compact = _layer_with_empty_items()
+    elif dims in ("empty", "few"):
+        compact = _special_layer(dims)
         layer = hip_layer(compact)
     elif dims == "workload":
         compact = synth.make_workload_layer(synth.WORKLOADS[name])
@@ -394,7 +412,8 @@ def test_tiles_on_the_compact_rows_equal_the_tiled_store(shape, test_layers, dev
     tiled, rows = HFFNRuntime([layer], device), PreparedRuntime([layer], device, tiled=False)
     tiled.force("tiles", "tiles")
     rows.force("tiles", "tiles")
-    assert rows.tiles_bytes() < 0.5 * tiled.tiles_bytes()
+    if dims != "few":  # (a 16 x 8 layer's tables weigh as much as its few groups)
+        assert rows.tiles_bytes() < 0.5 * tiled.tiles_bytes()
     if dims == "workload":  # a real layer (1.4B shape, bfloat16, 20 %): the tables are 1.1 % of its compact store
         assert rows.tiles_bytes() <= 0.015 * layer.model_bytes()
     for n in (1, 2, 7, 16, 17, 33, 64):
