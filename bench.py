@@ -58,8 +58,9 @@ def parse() -> argparse.Namespace:
                              "up under load: 20 steps after 5 warm-up steps measured 0.141 ms per step, 200 after 20 "
                              "0.122 ms)")
     parser.add_argument("--no-decode", action="store_true", help="skip the decode record")
-    parser.add_argument("--untiled", action="store_true",
-                        help="the runtime without tiled copies of the stores (tiled=False: the tiles path reads the compact rows)")
+    parser.add_argument("--tiled", action="store_true",
+                        help="the runtime with tiled copies of the stores (tiled=True: the tiles path reads interleaved "
+                             "copies instead of the compact rows)")
     parser.add_argument("--decode-rotations", type=int, default=20, help="passes over the copies per decode entry")
     parser.add_argument("--copy-probe-mb", type=int, default=0,
                         help="after the run, copy a buffer of this many MiB 3 times (the plain copy kernel that "
@@ -283,7 +284,8 @@ def decode_record(runtime, base, device, rotations: int, steps: int) -> dict:
     from hffn_amd.prepared_runtime import PreparedRuntime
     from hffn_amd.runtime import HFFNRuntime
 
-    record = {"rotation": f"{rotations} passes over each layer's copies after one untimed pass; HIP events around all"}
+    record = {"rotation": f"{rotations} passes over each layer's copies after one untimed pass; HIP events around all",
+              "tiled": runtime.tiled}
     copies = len(runtime.layers)
     floor = read_floor(base, copies, rotations, device)
     record["pythia410m_d50_read_floor"] = floor
@@ -292,14 +294,14 @@ def decode_record(runtime, base, device, rotations: int, steps: int) -> dict:
     workload = synth.WORKLOADS["pythia1p4b_d20_bf16"]
     compact = synth.make_workload_layer(workload)
     count = max(1, math.ceil(MALL_BYTES / layer_costs(compact, 1)["model_bytes"]))
-    bf16 = HFFNRuntime(device_copies(hip_layer(compact, device), count), device)
+    bf16 = HFFNRuntime(device_copies(hip_layer(compact, device), count), device, tiled=runtime.tiled)
     bf16_floor = read_floor(compact, count, rotations, device)
     record["pythia1p4b_d20_bf16_read_floor"] = bf16_floor
     record["pythia1p4b_d20_bf16"] = [decode_entry(bf16, workload, compact, n, count, rotations, device, bf16_floor)
                                      for n in DECODE_TOKENS["pythia1p4b_d20_bf16"]]
     del bf16
     layers = runtime.layers + device_copies(runtime.layers[0], DECODE_STEP_LAYERS - copies + 1)[1:]
-    model = PreparedRuntime(layers[:DECODE_STEP_LAYERS], device)
+    model = PreparedRuntime(layers[:DECODE_STEP_LAYERS], device, tiled=runtime.tiled)
     record["pythia410m_model_step"] = [bench_decode.measure(model, [base] * DECODE_STEP_LAYERS, batch, steps)
                                        for batch in DECODE_STEP_BATCHES]
     for entry in record["pythia410m_model_step"]:  # against the plain read of every layer's stores, two launches each
@@ -372,7 +374,7 @@ def main() -> int:
     base = synth.make_workload_layer(workload)
     costs = layer_costs(base, n)
     copies = args.copies or max(1, math.ceil(MALL_BYTES / costs["model_bytes"]))
-    runtime = HFFNRuntime(device_copies(hip_layer(base, device), copies), device, tiled=not args.untiled)
+    runtime = HFFNRuntime(device_copies(hip_layer(base, device), copies), device, tiled=args.tiled)
     x_np = synth.make_input(workload, n)
     x = torch.from_numpy(x_np).to(device)
 

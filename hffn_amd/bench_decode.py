@@ -102,10 +102,11 @@ def main(argv: list[str] | None = None) -> int:
     parser.add_argument("--batch", default="1,8,16")
     parser.add_argument("--steps", type=int, default=50)
     parser.add_argument("--layers", type=int, default=24)
+    parser.add_argument("--tiled", action="store_true", help="the runtime with tiled copies of the stores")
     args = parser.parse_args(argv)
     device = torch.device("cuda", 0)
     compacts = [synth.make_workload_layer(WORKLOAD, seed=WORKLOAD.seed * 1000 + i) for i in range(args.layers)]
-    runtime = PreparedRuntime([hip_layer(c, device) for c in compacts], device)
+    runtime = PreparedRuntime([hip_layer(c, device) for c in compacts], device, tiled=args.tiled)
     for batch in (int(b) for b in args.batch.split(",")):
         print(json.dumps(measure(runtime, compacts, batch, args.steps)), flush=True)
     return 0

@@ -28,7 +28,7 @@ _GATHER = ("edges", "rows")
 class PreparedRuntime(HFFNRuntime):
     """``HFFNRuntime`` whose gather-mode calls launch from per-(layer, N) plans of the HIP library."""
 
-    def __init__(self, layers, device="cuda", dense: bool | None = None, tiled: bool = True) -> None:
+    def __init__(self, layers, device="cuda", dense: bool | None = None, tiled: bool = False) -> None:
         self._plans: dict = {}
         super().__init__(layers, device, dense, tiled)
         self._stream_of = getattr(torch._C, "_cuda_getCurrentRawStream", None)

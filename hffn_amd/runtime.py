@@ -9,9 +9,10 @@ the chosen shapes need.
 Kernel shapes (the build's own policy, ``up_mode``/``down_mode``):
 
 * ``edges`` - lanes over a row's slots, tokens in registers, input staged in LDS; decode-sized N (N <= 32).
-* ``tiles`` - the compact-store MFMA path (up and down together, 1-64 tokens): each side read once from its tiled
-  store (the compact slots regrouped at load by 16-row tile and 512-wide sub-chunk of K, interleaved 16-bit fields),
-  densified per block in LDS and multiplied on 16x16x32 MFMAs.
+* ``tiles`` - the compact-store MFMA path (up and down together, 1-64 tokens): each side read once, from the compact
+  rows through a table of row bounds (default) or from a tiled copy (``tiled=True``: the compact slots regrouped at
+  load by 16-row tile and 512-wide sub-chunk of K, interleaved 16-bit fields), densified per block in LDS and
+  multiplied on 16x16x32 MFMAs.
 * ``rows``  - lanes over tokens (1, 2 or 4 per lane), slots walked in order; large N on layers without the MFMA path.
 * ``mfma``  - tile-densified split-fp16 MFMA GEMMs over dense planes (up and down together) on high-density layers
   (density at least ``MFMA_MIN_DENSITY``, ``d_model`` and ``d_ff`` multiples of 256), above 64 tokens.
@@ -255,13 +256,14 @@ class HFFNRuntime:
     """``HFFNRuntime`` of ``runtime/gpu/nvidia/common/kernels/hffn_cuda/runtime.py:76-163`` on the HIP library."""
 
     def __init__(self, layers: list[HFFNLayer], device: str | torch.device = "cuda", dense: bool | None = None,
-                 tiled: bool = True) -> None:
+                 tiled: bool = False) -> None:
         """``dense``: build the dense planes of the MFMA path and the decode GEMVs (``d_model`` and ``d_ff`` multiples of
         256, distinct sorted indices per row): None (default) for layers of at least ``MFMA_MIN_DENSITY`` only, True
         whenever the shapes qualify (the policy still takes them only at that density), False never. ``tiled``: the
-        tiles path reads a tiled copy of each layer's store (True, the default: its interleaved groups make the decode
-        kernels 8-35 % faster) or the compact rows themselves through a small table of row bounds (False: the same
-        bits, and no second copy of the store)."""
+        tiles path reads the compact rows themselves through a small table of row bounds (False, the default: one
+        resident copy of each store, the layer's own) or a tiled copy of each layer's store built at construction
+        (True: its interleaved groups make the tiles calls 5-9 % faster, for a second copy of the store); both give the
+        same bits."""
         self.device = _device(device)
         self.tiled = tiled
         self.layers = layers

@@ -368,7 +368,7 @@ def test_tiled_store_bitwise(shape, test_layers, device):
         d_model, d_ff, degree, dtype = dims
         compact = synth.make_workload_layer(synth.Workload(name, d_model, d_ff, min(degree, d_model), 7, value_dtype=dtype))
         layer = hip_layer(compact)
-    runtime = HFFNRuntime([layer], device, dense=True)
+    runtime = HFFNRuntime([layer], device, dense=True, tiled=True)
     bf16 = layer.up_val.dtype == torch.bfloat16
     tiles = runtime._tiles[0]
     for side, rows, k, names in (("up", compact.d_ff, compact.d_model, ("up_offsets", "up_idx", "up_val")),
@@ -392,9 +392,9 @@ def test_tiled_store_bitwise(shape, test_layers, device):
                                    ("odd_bf16", (64, 1032, 60, "bf16")), ("empty_items", "empty"), ("few_slots", "few"),
                                    ("pythia1p4b_d20_bf16", "workload")])
 def test_tiles_on_the_compact_rows_equal_the_tiled_store(shape, test_layers, device):
-    """With tiled=False the tiles path reads the compact rows through the table of row bounds: the same dense tiles,
-    so the same bits as the tiled store at every token count (eager and planned); the layer then holds its compact
-    store plus tables of row bounds (about 1 % of a real layer's store)."""
+    """By default (tiled=False) the tiles path reads the compact rows through the table of row bounds: the same dense
+    tiles, so the same bits as the tiled store (tiled=True) at every token count (eager and planned); the layer then
+    holds its compact store plus tables of row bounds (about 1 % of a real layer's store)."""
     from hffn_amd.prepared_runtime import PreparedRuntime
     name, dims = shape
     if dims is None:
@@ -409,7 +409,7 @@ def test_tiles_on_the_compact_rows_equal_the_tiled_store(shape, test_layers, dev
         d_model, d_ff, degree, dtype = dims
         compact = synth.make_workload_layer(synth.Workload(name, d_model, d_ff, min(degree, d_model), 7, value_dtype=dtype))
         layer = hip_layer(compact)
-    tiled, rows = HFFNRuntime([layer], device), PreparedRuntime([layer], device, tiled=False)
+    tiled, rows = HFFNRuntime([layer], device, tiled=True), PreparedRuntime([layer], device)
     tiled.force("tiles", "tiles")
     rows.force("tiles", "tiles")
     if dims != "few":  # (a 16 x 8 layer's tables weigh as much as its few groups)

@@ -260,12 +260,13 @@ def test_transposed_supports_are_positions_into_the_runtime_arrays(device):
     assert np.array_equal(s["hid_offsets"], np.concatenate([[0], np.cumsum(np.bincount(out_hidden, minlength=d_ff))]))
 
 
-def test_inference_after_training_reads_the_updated_values(device):
-    """After steps, the runtime's MFMA path (densified planes, rebuilt in place) and its tiles path (tiled stores, rebuilt
-    in place) agree with its gather path."""
+@pytest.mark.parametrize("tiled", (False, True))
+def test_inference_after_training_reads_the_updated_values(tiled, device):
+    """After steps, the runtime's MFMA path (densified planes, rebuilt in place) and its tiles path (the compact rows'
+    powers of two, or the tiled stores, rebuilt in place) agree with its gather path."""
     case = synth.Case("mfma_256_1024", 256, 1024, 128, 128, False, 1005)
     layer = synth.make_layer(case)
-    runtime = HFFNRuntime([hip_layer(layer)], device, dense=True)
+    runtime = HFFNRuntime([hip_layer(layer)], device, dense=True, tiled=tiled)
     assert runtime.mfma_available
     train = HFFNTrainRuntime(runtime, **dict(HYPER, lr=1e-2))
     n = 256
@@ -281,7 +282,7 @@ def test_inference_after_training_reads_the_updated_values(device):
     y_rows = runtime.forward(0, x).clone()
     scale = float(y_rows.abs().max())
     assert float((y_mfma - y_rows).abs().max()) <= 1e-5 * max(1.0, scale)
-    # the tiled stores, rebuilt in place before the decode path next reads them, agree with the gathers too
+    # the tiles path's tables or stores, rebuilt in place before the decode path next reads them, agree with the gathers
     few = x[:16].contiguous()
     y_few = runtime.forward(0, few).clone()
     runtime.force("tiles", "tiles")
