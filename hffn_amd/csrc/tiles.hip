@@ -684,8 +684,12 @@ uint32_t items_of(uint32_t rows, uint32_t K) { return ((rows + kRows - 1) / kRow
 // timestamps of the 410M (float32, 50 %) and 1.4B (bfloat16, 20 %) sides at 16 tokens on MI355X: the loads take
 // 0.8 us + 25 ns per KB of groups and inputs (the inputs of the 16 token rows of the chunk, 32 S KB), the products
 // 0.3 + 0.4 S us (the inputs' split dominates), the epilogue 0.6 + 0.15 TR us; rounds of blocks over the CUs add up,
-// and a side whose blocks split K pays a reduce pass (3 us).
+// and a side whose blocks split K pays a reduce pass (3 us). A block of a side split over K reads each of its 16 TR
+// rows' slots in the chunk as a separate run of the compact arrays (the runs of a block that spans K are consecutive):
+// 0.1 us per run, from the compact-row blocks' timestamps (the 1.4B down side's loads and scatter 2.5 us with 64 runs
+// of 205 slots, 1.4 us from the tiled store's 4 ranges). Both stores take the same shape, so they give the same bits.
 TilesShape tiles_shape(int vt, uint32_t rows, uint32_t K, uint64_t nnz) {
+    constexpr double kRunUs = 0.1;
     const uint32_t planes = planes_of(vt), slot_bytes = vt == kBF16 ? 4 : 6;
     const uint32_t tiles = (rows + kRows - 1) / kRows, subchunks = (K + kSub - 1) / kSub;
     const double density = static_cast<double>(nnz) / (static_cast<double>(rows) * K);
@@ -698,7 +702,8 @@ TilesShape tiles_shape(int vt, uint32_t rows, uint32_t K, uint64_t nnz) {
             const double rounds = std::ceil(static_cast<double>(blocks) * chunks / kCUs);
             const double width = std::min<double>(s * kSub, K);
             const double load_kb = (kRows * tr * width * density * slot_bytes + kTokenTile * width * 4) / 1024;
-            const double block_us = 0.8 + 0.025 * load_kb + 0.3 + 0.4 * s + 0.6 + 0.15 * tr;
+            const double runs = chunks > 1 ? kRows * tr : 0.0;
+            const double block_us = 0.8 + 0.025 * load_kb + 0.3 + 0.4 * s + 0.6 + 0.15 * tr + kRunUs * runs;
             const double us = rounds * block_us + (chunks > 1 ? 3.0 : 0.0);
             if (us < best_us) {
                 best_us = us;
