@@ -27,9 +27,9 @@ larger layers, e.g. the 1.4B layer at 20 %, 59 against 223 us at 65 tokens and 1
 lane-per-token kernels the smallest, e.g. the 70M layer at 20 % from 128 tokens on, 53 against 63 us). The dense
 planes (4 bytes per weight for float32 values, 2 for bfloat16) are built only for layers of at least
 ``MFMA_MIN_DENSITY`` unless asked for (``dense=True``). Per call on the Pythia-410M layer at 50 % (12 rotating
-copies, MI355X, HFFNRuntime.forward): N = 1: tiles 17.4 us, edges 17.6; N = 4: edges 15.3, tiles 17.2; N = 16:
-tiles 18.4, edges 40.6; N = 64: tiles 30.0; N = 2048: mfma 152 us. On the 1.4B layer (bfloat16, 20 %): tiles 21.3,
-22.0, 24.3, 44.9 us at N = 1, 4, 16, 64 (edges 21.6, 25.5, 62.2 at 1, 4, 16).
+copies, MI355X, HFFNRuntime.forward, forced pairs, compact rows): N = 1: edges 12.6 us, tiles 17.3; N = 4: edges
+15.8, tiles 16.6; N = 16: tiles 17.9, edges 40.4; N = 32: tiles 21.7; N = 2048: mfma 110-116 us. On the 1.4B layer
+(bfloat16, 20 %): tiles 18.9, 19.3, 23.2, 31.7 us at N = 1, 4, 16, 32 (edges 15.4, 25.4, 63.2 at 1, 4, 16).
 
 Model arrays stay on the device. Work buffers are dense, shared by all layers, sized for the largest N seen and
 reused. Kernels are queued on PyTorch's current stream of the device, so they run in call order with the PyTorch
