@@ -108,10 +108,11 @@ def test_abi_refuses_bad_shapes_before_launching():
     # 410M shape, 16 tokens: the up side in one chunk, the down side's 64 row tiles over 4 chunks of K
     assert lib.hffn_tiles_workspace(0, 16, 1024, 4096, 2_097_152, 2_097_152, ctypes.byref(tiles_bytes)) == _lib.OK
     assert tiles_bytes.value == 4 * 16 * 1024 * 4
-    # 1.4B shape, bf16, 20 %, 16 tokens: the up side in 256 blocks of 32 rows x 2048 k, the down side in 32 blocks of
-    # 64 rows per chunk of 1024 (8 chunks)
+    # 1.4B shape, bf16, 20 %, 16 tokens: the up side in 256 blocks of 32 rows x 2048 k, the down side in 64 blocks of
+    # 32 rows per chunk of 2048 (4 chunks: the shape model prices the 32 row runs a block reads, against 64 runs of
+    # 4 x 1024 in 8 chunks)
     assert lib.hffn_tiles_workspace(1, 16, 2048, 8192, 3_358_720, 3_358_720, ctypes.byref(tiles_bytes)) == _lib.OK
-    assert tiles_bytes.value == 8 * 16 * 2048 * 4
+    assert tiles_bytes.value == 4 * 16 * 2048 * 4
     _expect_argument_error(lib.hffn_tiles_workspace(1, 16, 2048, 8192, 1 << 40, 0, ctypes.byref(tiles_bytes)), "nnz_up")
     _expect_argument_error(lib.hffn_tiles_workspace(0, 65, 1024, 4096, 0, 0, ctypes.byref(tiles_bytes)), "n=65")
     _expect_argument_error(lib.hffn_tiles_workspace(0, 16, 1000, 4096, 0, 0, ctypes.byref(tiles_bytes)), "multiple of 16")
