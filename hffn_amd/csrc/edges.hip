@@ -155,11 +155,13 @@ hipError_t allow_lds(size_t lds) {
 }
 
 // Every block stages x of its NT tokens (d * NT floats from L2): from 4 tokens on, blocks of 16 waves (a quarter as
-// many blocks) cut that traffic by 4.
+// many blocks) cut that traffic by 4. Below 4 tokens a row of one wave (P = 1) is the wave's only row, so that no
+// wave's second row waits behind its first: 4-wave blocks up to 4096 rows, 16-wave blocks above (at most 512 blocks
+// staging x; on the 1.4B shape at one token 7.4 -> 6.3 us against two rows per wave of 4-wave blocks).
 template <int NT, int P, typename V, int WAVES, bool GRAD>
 hipError_t up_waves(const float* x, const int32_t* off, const int16_t* idx, const V* w, const float* b, float* act, float* z, uint32_t d,
                     uint32_t h, uint32_t n, uint32_t ld, uint32_t nnz, hipStream_t stream) {
-    const uint32_t per = rows_per_block(h, P, WAVES, WAVES == kWaves ? 1024 : 256);
+    const uint32_t per = NT < 4 && P == 1 ? WAVES : rows_per_block(h, P, WAVES, WAVES == kWaves ? 1024 : 256);
     const size_t lds = (static_cast<size_t>(d) * NT + WAVES * NT) * sizeof(float);
     if (const hipError_t status = allow_lds<up_edges_kernel<NT, P, V, WAVES, GRAD>>(lds); status != hipSuccess) return status;
     hipLaunchKernelGGL((up_edges_kernel<NT, P, V, WAVES, GRAD>), dim3(ceil_div(h, per)), dim3(WAVES * kWave), lds, stream, x, off, idx, w, b,
@@ -171,6 +173,7 @@ template <int NT, int P, typename V, bool GRAD>
 hipError_t up_shape(const float* x, const int32_t* off, const int16_t* idx, const V* w, const float* b, float* act, float* z,
                     uint32_t d, uint32_t h, uint32_t n, uint32_t ld, uint32_t nnz, hipStream_t stream) {
     if constexpr (NT >= 4) return up_waves<NT, P, V, 16, GRAD>(x, off, idx, w, b, act, z, d, h, n, ld, nnz, stream);
+    else if (P == 1 && h > 4096) return up_waves<NT, P, V, 16, GRAD>(x, off, idx, w, b, act, z, d, h, n, ld, nnz, stream);
     else return up_waves<NT, P, V, kWaves, GRAD>(x, off, idx, w, b, act, z, d, h, n, ld, nnz, stream);
 }
 
