@@ -15,9 +15,11 @@ constexpr uint32_t kMaxTokens = 1u << 18;  // largest n of any entry point
 // Tokens per pass of the lane-per-slot ("edges") kernels: 1, 2, 4, or 8 for n > 4.
 constexpr uint32_t kEdgesMaxTokens = 8;
 inline uint32_t edges_tokens(uint32_t n) { return n <= 1 ? 1 : n <= 2 ? 2 : n <= 4 ? 4 : 8; }
-// The down edges kernel stages act of its tokens in LDS up to this many bytes (else gathers it from L2). Measured on
-// the 410M layer: staging 64-128 KB per block costs more than the L2 gathers it saves (4-8 tokens).
-constexpr size_t kEdgesStageBytes = 32768;
+// The down edges kernel stages act of its tokens in LDS up to this many bytes (else gathers it from L2): one block of
+// 16 waves per CU, so the stage may take most of the CU's 160 KB. Staged by DMA with every transfer issued before one
+// wait, 64-128 KB per block beat the L2 gathers (edges pair, MI355X: 410M layer at 4 / 8 tokens 15.9 -> 15.1 /
+// 24.7 -> 22.7 us; 1.4B bf16 layer at 2 / 4 tokens 19.8 -> 16.6 / 25.4 -> 21.4 us).
+constexpr size_t kEdgesStageBytes = 131072;
 
 // x[rows, cols] (row stride in_ld) -> out[cols, rows] (row stride out_ld).
 hipError_t launch_transpose(const float* in, float* out, uint32_t rows, uint32_t cols, uint32_t in_ld,

@@ -61,7 +61,7 @@ MFMA_MIN_DENSITY = 0.5    # the lowest support density whose layers get dense pl
 # MFMA path: TILES_BASE_US + TILES_SLOT_US per stored slot, plus up to (TILES_FILL_US + TILES_FILL_SLOT_US per slot)
 # as the first 16-token tile fills, plus (TILES_TILE_US + TILES_TILE_SLOT_US per slot) per further 16-token tile.
 EDGES_CALL_US, EDGES_PASS_US, EDGES_SLOT_US = 6.0, 4.0, 3.5e-6
-EDGES_PASS_WEIGHT = {1: 0.42, 2: 0.49, 4: 0.52, 8: 1.0}
+EDGES_PASS_WEIGHT = {1: 0.42, 2: 0.44, 4: 0.52, 8: 1.0}
 TILES_BASE_US, TILES_SLOT_US = 12.7, 1.11e-6
 TILES_FILL_US, TILES_FILL_SLOT_US = 2.0, 0.07e-6
 TILES_TILE_US, TILES_TILE_SLOT_US = 4.5, 0.17e-6
