@@ -559,7 +559,7 @@ def test_70m_config(device):
     assert float((y.double().cpu() - torch.from_numpy(reference.forward(compact, x_np))).abs().max()) <= ATOL
 
 
-@pytest.mark.parametrize("n", [1, 4, 16])
+@pytest.mark.parametrize("n", [1, 2, 4, 16])
 def test_1p4b_bf16(n, device):
     """Pythia-1.4B shape, 20 %, bf16 weights with fp32 accumulation, against the float64 oracle on the same
     (bf16-exact) weights: within the fp32 bound 1e-5 (the stated bf16 bound is 2e-2)."""

@@ -61,6 +61,37 @@ def test_prepared_forced_pairs(pair, runtimes, device):
     assert prepared._plans == {}
 
 
+@pytest.mark.parametrize("name", ["irreg_512_2048", "homog_256_1024"])
+def test_prepared_tiles_on_the_tiled_store(name, runtimes, device):
+    """With tiled=True the planned launches (hffn_plan_tiles) read the tiled copies: bit-identical to the eager calls of
+    a tiled runtime and to the default runtime's calls on the compact rows (one block shape, the same tiles), and the
+    plans see the copies rebuilt after an update of the compact values."""
+    compact, case, control, _ = runtimes[name]
+    tiled_control = HFFNRuntime([hip_layer(compact)], device, tiled=True)
+    tiled_prepared = PreparedRuntime([hip_layer(compact)], device, tiled=True)
+    for runtime in (control, tiled_control, tiled_prepared):
+        runtime.force("tiles", "tiles")
+    try:
+        for n in (1, 4, 7, 24, 33, 64):
+            x = torch.from_numpy(synth.make_input(case, n)).to(device)
+            expected = control.forward(0, x).clone()
+            assert torch.equal(tiled_control.forward(0, x), expected), (name, n)
+            for repeat in range(2):  # the second call runs from the plan the first one built
+                assert torch.equal(tiled_prepared.forward(0, x), expected), (name, n, repeat)
+            assert tiled_prepared._plans[(0, n)][1:] == ("tiles", "tiles")
+        x = torch.from_numpy(synth.make_input(case, 16)).to(device)
+        before = tiled_prepared.forward(0, x).clone()
+        for runtime in (tiled_control, tiled_prepared):
+            runtime._tensors[0]["up_val"].mul_(0.5)
+            runtime.invalidate_planes(0)  # marks the tiled copies stale as well
+        after = tiled_prepared.forward(0, x).clone()  # launched from the plan made before the update
+        assert torch.equal(after, tiled_control.forward(0, x))
+        assert not torch.equal(after, before)
+    finally:
+        for runtime in (control, tiled_control, tiled_prepared):
+            runtime.force(None, None)
+
+
 def test_plans_follow_the_buffers(device):
     """A larger N reallocates the work buffers: the plans made before are released and rebuilt on the new buffers;
     the calls counter counts plan launches like control calls; an input that is a row-offset view works."""
