@@ -122,19 +122,50 @@ __global__ __launch_bounds__(kBlock) void down_rows_kernel(const float* __restri
 }
 
 // ------------------------------------------------------------------------------------------ transpose
+// out[c, r] = in[r, c] through an LDS tile of kTransRows x kTransCols (padded by one float per row). A full tile whose
+// rows start on 16-byte boundaries on both sides (strides multiples of 4 floats, aligned pointers) moves float4s: thread
+// t reads 16 bytes of input rows t / 16 and t / 16 + 16 (16 threads per 256-byte row run) and writes 16 bytes of output
+// rows t / 8 and t / 8 + 32 (4 input rows each), every load issued before the first LDS write; any other tile moves
+// floats. 256 blocks for a 512 x 1024 transpose, one per CU.
+constexpr uint32_t kTransRows = 32, kTransCols = 64;
 __global__ __launch_bounds__(kBlock) void transpose_kernel(const float* __restrict__ in, float* __restrict__ out,
-                                                          uint32_t rows, uint32_t cols, uint32_t in_ld, uint32_t out_ld) {
-    __shared__ float tile[64][65];
-    const uint32_t r0 = blockIdx.y * 64, c0 = blockIdx.x * 64;
-    const uint32_t tx = threadIdx.x % 64, ty = threadIdx.x / 64;
-    for (uint32_t k = ty; k < 64; k += kWaves) {
-        const uint32_t r = r0 + k, c = c0 + tx;
-        if (r < rows && c < cols) tile[k][tx] = in[static_cast<size_t>(r) * in_ld + c];
+                                                          uint32_t rows, uint32_t cols, uint32_t in_ld, uint32_t out_ld,
+                                                          uint32_t vectors) {
+    static_assert(kBlock == 256 && kTransRows * kTransCols / 4 == 2 * kBlock, "two float4 per thread each way");
+    __shared__ float tile[kTransRows][kTransCols + 1];
+    const uint32_t r0 = blockIdx.y * kTransRows, c0 = blockIdx.x * kTransCols, t = threadIdx.x;
+    if (vectors && r0 + kTransRows <= rows && c0 + kTransCols <= cols) {
+        float4 v[2];
+#pragma unroll
+        for (int j = 0; j < 2; ++j) {
+            const uint32_t r = t / 16 + 16 * j, c = (t % 16) * 4;
+            v[j] = *reinterpret_cast<const float4*>(in + static_cast<size_t>(r0 + r) * in_ld + c0 + c);
+        }
+#pragma unroll
+        for (int j = 0; j < 2; ++j) {
+            const uint32_t r = t / 16 + 16 * j, c = (t % 16) * 4;
+            tile[r][c] = v[j].x;
+            tile[r][c + 1] = v[j].y;
+            tile[r][c + 2] = v[j].z;
+            tile[r][c + 3] = v[j].w;
+        }
+        __syncthreads();
+#pragma unroll
+        for (int j = 0; j < 2; ++j) {
+            const uint32_t c = t / 8 + 32 * j, r = (t % 8) * 4;
+            const float4 w = make_float4(tile[r][c], tile[r + 1][c], tile[r + 2][c], tile[r + 3][c]);
+            *reinterpret_cast<float4*>(out + static_cast<size_t>(c0 + c) * out_ld + r0 + r) = w;
+        }
+        return;
+    }
+    for (uint32_t k = t; k < kTransRows * kTransCols; k += kBlock) {
+        const uint32_t r = k / kTransCols, c = k % kTransCols;
+        if (r0 + r < rows && c0 + c < cols) tile[r][c] = in[static_cast<size_t>(r0 + r) * in_ld + c0 + c];
     }
     __syncthreads();
-    for (uint32_t k = ty; k < 64; k += kWaves) {
-        const uint32_t c = c0 + k, r = r0 + tx;
-        if (c < cols && r < rows) out[static_cast<size_t>(c) * out_ld + r] = tile[tx][k];
+    for (uint32_t k = t; k < kTransRows * kTransCols; k += kBlock) {
+        const uint32_t c = k / kTransRows, r = k % kTransRows;
+        if (c0 + c < cols && r0 + r < rows) out[static_cast<size_t>(c0 + c) * out_ld + r0 + r] = tile[r][c];
     }
 }
 
@@ -172,8 +203,10 @@ hipError_t down_rows_typed(const float* act, const int32_t* off, const int16_t* 
 
 hipError_t launch_transpose(const float* in, float* out, uint32_t rows, uint32_t cols, uint32_t in_ld, uint32_t out_ld,
                             hipStream_t stream) {
-    hipLaunchKernelGGL(transpose_kernel, dim3(ceil_div(cols, 64), ceil_div(rows, 64)), dim3(kBlock), 0, stream, in, out, rows,
-                       cols, in_ld, out_ld);
+    const uint32_t vectors = in_ld % 4 == 0 && out_ld % 4 == 0 && reinterpret_cast<uintptr_t>(in) % 16 == 0 &&
+                             reinterpret_cast<uintptr_t>(out) % 16 == 0;
+    hipLaunchKernelGGL(transpose_kernel, dim3(ceil_div(cols, kTransCols), ceil_div(rows, kTransRows)), dim3(kBlock), 0, stream, in,
+                       out, rows, cols, in_ld, out_ld, vectors);
     return hipGetLastError();
 }
 

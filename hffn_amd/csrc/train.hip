@@ -116,22 +116,44 @@ __global__ __launch_bounds__(kBlock) void reduce_tiles_kernel(const float* __res
     else gb_up[j - c3] = s;
 }
 
-// Compact AdamW, one thread per entry, in the order of PyTorch's AdamW (kernels_train.py:233-247): decoupled decay,
-// then the moments, then the bias-corrected step; the step-dependent scalars come from the host (float64 there).
+// Compact AdamW in the order of PyTorch's AdamW (kernels_train.py:233-247): decoupled decay, then the moments, then
+// the bias-corrected step; the step-dependent scalars come from the host (float64 there). A thread takes four
+// consecutive entries with 16-byte loads and stores (the first `quads` threads, when all four arrays are 16-byte
+// aligned), one entry otherwise (the rest); the same arithmetic per entry either way.
+struct AdamScalars {
+    float lr_decay, beta1, one_minus_beta1, beta2, one_minus_beta2, step_size, bias2_sqrt, eps;
+};
+
+__device__ __forceinline__ void adamw_entry(float& p, float g, float& m, float& v, const AdamScalars& a) {
+    p -= a.lr_decay * p;
+    m = a.beta1 * m + a.one_minus_beta1 * g;
+    v = a.beta2 * v + a.one_minus_beta2 * g * g;
+    p = p - a.step_size * m / (sqrtf(v) / a.bias2_sqrt + a.eps);
+}
+
 __global__ __launch_bounds__(kBlock) void adamw_kernel(float* __restrict__ p, const float* __restrict__ g, float* __restrict__ m,
-                                                      float* __restrict__ v, uint32_t count, float lr_decay, float beta1,
-                                                      float one_minus_beta1, float beta2, float one_minus_beta2, float step_size,
-                                                      float bias2_sqrt, float eps) {
+                                                      float* __restrict__ v, uint32_t count, uint32_t quads, AdamScalars a) {
     const uint32_t i = blockIdx.x * kBlock + threadIdx.x;
-    if (i >= count) return;
-    const float gi = g[i];
-    float pi = p[i];
-    pi -= lr_decay * pi;
-    const float mi = beta1 * m[i] + one_minus_beta1 * gi;
-    const float vi = beta2 * v[i] + one_minus_beta2 * gi * gi;
-    m[i] = mi;
-    v[i] = vi;
-    p[i] = pi - step_size * mi / (sqrtf(vi) / bias2_sqrt + eps);
+    if (i < quads) {
+        float4 pi = reinterpret_cast<const float4*>(p)[i];
+        const float4 gi = reinterpret_cast<const float4*>(g)[i];
+        float4 mi = reinterpret_cast<const float4*>(m)[i], vi = reinterpret_cast<const float4*>(v)[i];
+        adamw_entry(pi.x, gi.x, mi.x, vi.x, a);
+        adamw_entry(pi.y, gi.y, mi.y, vi.y, a);
+        adamw_entry(pi.z, gi.z, mi.z, vi.z, a);
+        adamw_entry(pi.w, gi.w, mi.w, vi.w, a);
+        reinterpret_cast<float4*>(m)[i] = mi;
+        reinterpret_cast<float4*>(v)[i] = vi;
+        reinterpret_cast<float4*>(p)[i] = pi;
+        return;
+    }
+    const uint32_t j = 4 * quads + (i - quads);
+    if (j >= count) return;
+    float pj = p[j], mj = m[j], vj = v[j];
+    adamw_entry(pj, g[j], mj, vj, a);
+    m[j] = mj;
+    v[j] = vj;
+    p[j] = pj;
 }
 
 __global__ __launch_bounds__(kBlock) void gather_values_kernel(const float* __restrict__ src, const int32_t* __restrict__ pos,
@@ -171,8 +193,11 @@ hipError_t launch_reduce_tiles(const float* ws, uint32_t stride, uint32_t tiles,
 hipError_t launch_adamw(float* p, const float* g, float* m, float* v, uint32_t count, float lr_decay, float beta1,
                         float one_minus_beta1, float beta2, float one_minus_beta2, float step_size, float bias2_sqrt, float eps,
                         hipStream_t stream) {
-    hipLaunchKernelGGL(adamw_kernel, dim3(ceil_div(count, kBlock)), dim3(kBlock), 0, stream, p, g, m, v, count, lr_decay, beta1,
-                       one_minus_beta1, beta2, one_minus_beta2, step_size, bias2_sqrt, eps);
+    const bool aligned = (reinterpret_cast<uintptr_t>(p) | reinterpret_cast<uintptr_t>(g) | reinterpret_cast<uintptr_t>(m) |
+                          reinterpret_cast<uintptr_t>(v)) % 16 == 0;
+    const uint32_t quads = aligned ? count / 4 : 0, threads = quads + (count - 4 * quads);
+    const AdamScalars a{lr_decay, beta1, one_minus_beta1, beta2, one_minus_beta2, step_size, bias2_sqrt, eps};
+    hipLaunchKernelGGL(adamw_kernel, dim3(ceil_div(threads, kBlock)), dim3(kBlock), 0, stream, p, g, m, v, count, quads, a);
     return hipGetLastError();
 }
 
