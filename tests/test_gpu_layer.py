@@ -473,6 +473,26 @@ def test_stack_of_layers(test_layers, device):
         assert float((y.double().cpu() - torch.from_numpy(reference.forward(compact, x_np))).abs().max()) <= ATOL
 
 
+@pytest.mark.parametrize("rows,cols,in_ld,out_ld,offset", [(512, 1024, 1024, 512, 0), (70, 130, 132, 72, 0),
+                                                          (33, 65, 65, 33, 0), (64, 128, 128, 64, 1), (5, 1000, 1003, 9, 0)])
+def test_transpose_bitwise(rows, cols, in_ld, out_ld, offset, device):
+    """hffn_transpose, bit for bit against the transposed input, padding of the output rows untouched: full 32 x 64
+    tiles with 16-byte rows (float4 path), ragged edge tiles, odd strides and a misaligned pointer (float path)."""
+    from hffn_amd import _lib
+    lib = _lib.load()
+    rng = np.random.default_rng(rows * 7 + cols)
+    source = torch.from_numpy(rng.standard_normal(rows * in_ld + offset).astype(np.float32)).to(device)
+    out = torch.full((cols * out_ld + offset,), -7.0, device=device)
+    stream = torch.cuda.current_stream(device).cuda_stream
+    status = lib.hffn_transpose(source.data_ptr() + 4 * offset, out.data_ptr() + 4 * offset, rows, cols, in_ld, out_ld, stream)
+    assert status == _lib.OK
+    torch.cuda.synchronize(device)
+    given = source[offset:].view(rows, in_ld)[:, :cols]
+    got = out[offset:].view(cols, out_ld)
+    assert torch.equal(got[:, :rows], given.t())
+    assert bool((got[:, rows:] == -7.0).all()) and bool((out[:offset] == -7.0).all())
+
+
 def test_input_validation(test_layers, device):
     _, case, layer = test_layers["homog_256_1024"]
     runtime = HFFNRuntime([layer], device, dense=True)
