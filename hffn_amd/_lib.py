@@ -10,7 +10,7 @@ import ctypes
 from pathlib import Path
 
 LIBRARY = Path(__file__).resolve().with_name("libhffn_amd.so")
-ABI_VERSION = 17
+ABI_VERSION = 18
 
 OK = 0
 VALUE_F32, VALUE_BF16 = 0, 1

@@ -76,11 +76,12 @@ int hffn_transpose(const float* in, float* out, uint32_t rows, uint32_t cols, ui
 }
 
 namespace {
-// The edges kernels read 4 slots at a time: 8-byte aligned indices, 16-byte (fp32) or 8-byte (bf16) aligned values.
+// The edges kernels read groups of slots in 16-byte value loads: float32 4 slots (8-byte index loads), bfloat16 8
+// slots (16-byte index loads).
 int check_store_alignment(const int16_t* idx, const void* val, int value_type) {
-    const uintptr_t value_align = value_type == HFFN_VALUE_BF16 ? 8 : 16;
-    if (reinterpret_cast<uintptr_t>(idx) % 8 != 0 || reinterpret_cast<uintptr_t>(val) % value_align != 0)
-        return fail(HFFN_ERROR_ARGUMENT, "edges mode: index/value arrays must be 8/%u-byte aligned", static_cast<unsigned>(value_align));
+    const uintptr_t index_align = value_type == HFFN_VALUE_BF16 ? 16 : 8;
+    if (reinterpret_cast<uintptr_t>(idx) % index_align != 0 || reinterpret_cast<uintptr_t>(val) % 16 != 0)
+        return fail(HFFN_ERROR_ARGUMENT, "edges mode: index/value arrays must be %u/16-byte aligned", static_cast<unsigned>(index_align));
     return HFFN_OK;
 }
 }  // namespace

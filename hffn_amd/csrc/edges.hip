@@ -3,16 +3,20 @@
 // Up:   act[r, t] = gelu(b_up[r] + sum_e w[e] x[t, idx[e]]),   one row per neuron r (up store).
 // Down: y[t, o]   = b_down[o] + sum_q v[q] act[hid[q], t],     one row per output o (output-major store).
 //
-// A row is read as groups of 4 consecutive slots per lane (16-byte value and 8-byte index loads, i.e. 1 KB and
-// 512 B per wave instruction; groups are aligned to 4 slots, so a group may straddle the row's ends and its outside
-// slots are skipped). A wave requests its first 3 groups per lane (768 slots) before its block stages the inputs in
-// LDS (by DMA, every transfer issued before any is waited for), so the store streams while the block waits: one
-// memory round trip for the row offsets, then one for the slots and the inputs together.
-// Long rows are split over P waves of the block (each takes a contiguous segment cut on the 4-slot grid); the P
+// A row is read as groups of consecutive slots per lane, each value load 16 bytes (1 KB of one contiguous range per
+// wave instruction): float32 groups of 4 slots with an 8-byte index load, bfloat16 groups of 8 with a 16-byte index
+// load (half the instructions of 4-slot groups: the 1.4B-shape pair at one token 14.0 -> 13.0 us). Groups are aligned
+// to the group size, so a group may straddle the row's ends and its outside slots are skipped. A wave requests its
+// first G groups per lane (1-3 rounds of 64 groups, from the average segment) before its block stages the
+// inputs in LDS (by DMA, every transfer issued before any is waited for), so the store streams while the block waits:
+// one memory round trip for the row offsets, then one for the slots and the inputs together.
+// Long rows are split over P waves of the block (each takes a contiguous segment cut on the group grid); the P
 // partial sums are added in segment order. Within a wave the 64 lane partials are added by a fixed xor butterfly. Inputs are
 // staged in LDS when they fit (x for up, act for down at small n), otherwise act is gathered from L2.
 // Tokens are processed NT at a time (NT = 1, 2, 4 or 8); every activation and output is written by one lane: no
 // atomics, bitwise repeatable, and a token's result does not depend on the other tokens of the call.
+#include <algorithm>
+
 #include "common.hpp"
 #include "edges.hpp"
 #include "launch.hpp"
@@ -26,7 +30,7 @@ constexpr uint32_t kBlock = 256;
 constexpr uint32_t kWaves = kBlock / kWave;
 
 // ------------------------------------------------------------------------------------------------- up
-template <int NT, int P, typename V, int WAVES, bool GRAD = false>
+template <int NT, int P, typename V, int WAVES, bool GRAD, int G>
 __global__ __launch_bounds__(WAVES * kWave) void up_edges_kernel(const float* __restrict__ x, const int32_t* __restrict__ off,
                                                                 const int16_t* __restrict__ idx, const V* __restrict__ w,
                                                                 const float* __restrict__ b, float* __restrict__ act,
@@ -43,7 +47,7 @@ __global__ __launch_bounds__(WAVES * kWave) void up_edges_kernel(const float* __
     for (uint32_t c0 = 0; c0 < n; c0 += NT) {
         const uint32_t tokens = min(n - c0, static_cast<uint32_t>(NT));
         // the first row's slots (and bias) are requested before the block stages x and waits for it
-        Slots<V> cur;
+        Slots<V, G> cur;
         request_row<P>(cur, off, idx, w, r0 + row_in_pass, r1, part, nnz, lane);
         float b_cur = GRAD ? 0.0f : row_bias(b, r0 + row_in_pass, r1);
         if (c0) __syncthreads();
@@ -54,7 +58,7 @@ __global__ __launch_bounds__(WAVES * kWave) void up_edges_kernel(const float* __
         for (uint32_t base = r0; base < r1; base += kRowsPerPass) {  // uniform trip count across the block
             const uint32_t r = base + row_in_pass;
             // the wave's next row is requested before this row's sums, so its slots stream meanwhile
-            Slots<V> next;
+            Slots<V, G> next;
             request_row<P>(next, off, idx, w, r + kRowsPerPass, r1, part, nnz, lane);
             const float b_next = GRAD ? 0.0f : row_bias(b, r + kRowsPerPass, r1);
             float acc[NT];
@@ -82,7 +86,7 @@ __global__ __launch_bounds__(WAVES * kWave) void up_edges_kernel(const float* __
 }
 
 // ----------------------------------------------------------------------------------------------- down
-template <int NT, int P, typename V, bool STAGE, int WAVES>
+template <int NT, int P, typename V, bool STAGE, int WAVES, int G>
 __global__ __launch_bounds__(WAVES * kWave) void down_edges_kernel(const float* __restrict__ act, const int32_t* __restrict__ off,
                                                            const int16_t* __restrict__ hid, const V* __restrict__ v,
                                                            const float* __restrict__ bias, float* __restrict__ y, uint32_t d,
@@ -97,7 +101,7 @@ __global__ __launch_bounds__(WAVES * kWave) void down_edges_kernel(const float* 
     const uint32_t o1 = min(d, o0 + per_block);
     for (uint32_t c0 = 0; c0 < n; c0 += NT) {
         const uint32_t tokens = min(n - c0, static_cast<uint32_t>(NT));
-        Slots<V> cur;
+        Slots<V, G> cur;
         request_row<P>(cur, off, hid, v, o0 + row_in_pass, o1, part, nnz, lane);
         float b_cur = row_bias(bias, o0 + row_in_pass, o1);
         if constexpr (STAGE) {
@@ -108,7 +112,7 @@ __global__ __launch_bounds__(WAVES * kWave) void down_edges_kernel(const float* 
         }
         for (uint32_t base = o0; base < o1; base += kRowsPerPass) {
             const uint32_t o = base + row_in_pass;
-            Slots<V> next;
+            Slots<V, G> next;
             request_row<P>(next, off, hid, v, o + kRowsPerPass, o1, part, nnz, lane);
             const float b_next = row_bias(bias, o + kRowsPerPass, o1);
             float acc[NT];
@@ -135,6 +139,15 @@ int parts_for(uint32_t nnz, uint32_t rows) {
     return average >= 1536 ? 4 : average >= 768 ? 2 : 1;
 }
 
+// Groups a lane holds at once: as many rounds of 64 groups as a wave's average segment takes, 1 to 3 (a longer
+// segment's rest is loaded a chunk at a time after the first chunk's sums; a lane's group past its segment is a load
+// of the store's group 0). The lanes meet their slots in the same order for any count: it does not change the bits.
+template <typename V>
+int groups_for(uint32_t nnz, uint32_t rows, int parts) {
+    const uint64_t average = rows ? nnz / (static_cast<uint64_t>(rows) * parts) : 0, round = Group<V>::kSlots * kWave;
+    return static_cast<int>(std::min<uint64_t>(3, std::max<uint64_t>(1, (average + round - 1) / round)));
+}
+
 // Rows per block: about `blocks` blocks, a multiple of the rows one pass of the block takes.
 uint32_t rows_per_block(uint32_t rows, int parts, uint32_t waves = kWaves, uint32_t blocks = 1024) {
     const uint32_t pass = waves / parts;
@@ -158,15 +171,25 @@ hipError_t allow_lds(size_t lds) {
 // many blocks) cut that traffic by 4. Below 4 tokens a row of one wave (P = 1) is the wave's only row, so that no
 // wave's second row waits behind its first: 4-wave blocks up to 4096 rows, 16-wave blocks above (at most 512 blocks
 // staging x; on the 1.4B shape at one token 7.4 -> 6.3 us against two rows per wave of 4-wave blocks).
+template <int NT, int P, typename V, int WAVES, bool GRAD, int G>
+hipError_t up_launch(const float* x, const int32_t* off, const int16_t* idx, const V* w, const float* b, float* act, float* z, uint32_t d,
+                     uint32_t h, uint32_t n, uint32_t ld, uint32_t nnz, hipStream_t stream) {
+    const uint32_t per = NT < 4 && P == 1 ? WAVES : rows_per_block(h, P, WAVES, WAVES == kWaves ? 1024 : 256);
+    const size_t lds = (static_cast<size_t>(d) * NT + WAVES * NT) * sizeof(float);
+    if (const hipError_t status = allow_lds<up_edges_kernel<NT, P, V, WAVES, GRAD, G>>(lds); status != hipSuccess) return status;
+    hipLaunchKernelGGL((up_edges_kernel<NT, P, V, WAVES, GRAD, G>), dim3(ceil_div(h, per)), dim3(WAVES * kWave), lds, stream, x, off, idx, w,
+                       b, act, z, d, h, n, ld, static_cast<int32_t>(nnz), per);
+    return hipGetLastError();
+}
+
 template <int NT, int P, typename V, int WAVES, bool GRAD>
 hipError_t up_waves(const float* x, const int32_t* off, const int16_t* idx, const V* w, const float* b, float* act, float* z, uint32_t d,
                     uint32_t h, uint32_t n, uint32_t ld, uint32_t nnz, hipStream_t stream) {
-    const uint32_t per = NT < 4 && P == 1 ? WAVES : rows_per_block(h, P, WAVES, WAVES == kWaves ? 1024 : 256);
-    const size_t lds = (static_cast<size_t>(d) * NT + WAVES * NT) * sizeof(float);
-    if (const hipError_t status = allow_lds<up_edges_kernel<NT, P, V, WAVES, GRAD>>(lds); status != hipSuccess) return status;
-    hipLaunchKernelGGL((up_edges_kernel<NT, P, V, WAVES, GRAD>), dim3(ceil_div(h, per)), dim3(WAVES * kWave), lds, stream, x, off, idx, w, b,
-                       act, z, d, h, n, ld, static_cast<int32_t>(nnz), per);
-    return hipGetLastError();
+    switch (groups_for<V>(nnz, h, P)) {
+        case 1: return up_launch<NT, P, V, WAVES, GRAD, 1>(x, off, idx, w, b, act, z, d, h, n, ld, nnz, stream);
+        case 2: return up_launch<NT, P, V, WAVES, GRAD, 2>(x, off, idx, w, b, act, z, d, h, n, ld, nnz, stream);
+        default: return up_launch<NT, P, V, WAVES, GRAD, 3>(x, off, idx, w, b, act, z, d, h, n, ld, nnz, stream);
+    }
 }
 
 template <int NT, int P, typename V, bool GRAD>
@@ -179,24 +202,34 @@ hipError_t up_shape(const float* x, const int32_t* off, const int16_t* idx, cons
 
 // With act staged in LDS (small n), blocks of 16 waves take 4x the rows of 4-wave blocks, so each block's staging
 // of the whole act serves 4x the slots.
-template <int NT, int P, typename V>
-hipError_t down_shape(const float* act, const int32_t* off, const int16_t* hid, const V* v, const float* bias, float* y,
-                      uint32_t d, uint32_t h, uint32_t n, uint32_t ld, uint32_t nnz, hipStream_t stream) {
+template <int NT, int P, typename V, int G>
+hipError_t down_launch(const float* act, const int32_t* off, const int16_t* hid, const V* v, const float* bias, float* y,
+                       uint32_t d, uint32_t h, uint32_t n, uint32_t ld, uint32_t nnz, hipStream_t stream) {
     const bool stage = static_cast<size_t>(h) * NT * sizeof(float) <= kEdgesStageBytes;
     if (stage) {
         constexpr uint32_t waves = 16;
         const uint32_t per = rows_per_block(d, P, waves, 256);
         const size_t lds = (static_cast<size_t>(h) * NT + waves * NT) * sizeof(float);
-        if (const hipError_t status = allow_lds<down_edges_kernel<NT, P, V, true, waves>>(lds); status != hipSuccess) return status;
-        hipLaunchKernelGGL((down_edges_kernel<NT, P, V, true, waves>), dim3(ceil_div(d, per)), dim3(waves * kWave), lds, stream,
+        if (const hipError_t status = allow_lds<down_edges_kernel<NT, P, V, true, waves, G>>(lds); status != hipSuccess) return status;
+        hipLaunchKernelGGL((down_edges_kernel<NT, P, V, true, waves, G>), dim3(ceil_div(d, per)), dim3(waves * kWave), lds, stream,
                            act, off, hid, v, bias, y, d, h, n, ld, static_cast<int32_t>(nnz), per);
     } else {
         const uint32_t per = rows_per_block(d, P);
         const size_t lds = static_cast<size_t>(kWaves) * NT * sizeof(float);
-        hipLaunchKernelGGL((down_edges_kernel<NT, P, V, false, kWaves>), dim3(ceil_div(d, per)), dim3(kBlock), lds, stream, act,
+        hipLaunchKernelGGL((down_edges_kernel<NT, P, V, false, kWaves, G>), dim3(ceil_div(d, per)), dim3(kBlock), lds, stream, act,
                            off, hid, v, bias, y, d, h, n, ld, static_cast<int32_t>(nnz), per);
     }
     return hipGetLastError();
+}
+
+template <int NT, int P, typename V>
+hipError_t down_shape(const float* act, const int32_t* off, const int16_t* hid, const V* v, const float* bias, float* y,
+                      uint32_t d, uint32_t h, uint32_t n, uint32_t ld, uint32_t nnz, hipStream_t stream) {
+    switch (groups_for<V>(nnz, d, P)) {
+        case 1: return down_launch<NT, P, V, 1>(act, off, hid, v, bias, y, d, h, n, ld, nnz, stream);
+        case 2: return down_launch<NT, P, V, 2>(act, off, hid, v, bias, y, d, h, n, ld, nnz, stream);
+        default: return down_launch<NT, P, V, 3>(act, off, hid, v, bias, y, d, h, n, ld, nnz, stream);
+    }
 }
 
 template <int NT, typename V, bool GRAD>

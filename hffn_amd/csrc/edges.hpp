@@ -1,8 +1,11 @@
-// Device pieces of the lane-per-slot ("edges") kernels (edges.hip): a row's slots read in
-// groups of 4 consecutive slots per lane (a 16-byte value load and an 8-byte index load per group for float32, 8 bytes
-// for bfloat16), the groups of a wave strided by 4 * 64 slots, the lane partials of NT tokens added by a fixed xor
-// butterfly, and a long row split in P segments (one wave each) added in segment order. Every kernel that runs a row
-// through these pieces with the same P produces the same bits.
+// Device pieces of the lane-per-slot ("edges") kernels (edges.hip): a row's slots read in groups of consecutive slots
+// per lane, every value load 16 bytes and each wave instruction 1 KB of one contiguous range: float32 groups of 4 slots
+// (a 16-byte value load and an 8-byte index load), bfloat16 groups of 8 (a 16-byte value load and a 16-byte index
+// load: half the load instructions of 4-slot groups; 8 float32 values per lane would split a wave's value loads into
+// two 2 KB ranges of half-used lines). The groups of a wave are strided by 64 groups, the lane partials of NT tokens
+// are added by a fixed xor butterfly, and a long row split in P segments (one wave each) is added in segment order.
+// Every kernel that runs a row through these pieces with the same P produces the same bits (the number of groups a
+// lane holds at once does not change them).
 #pragma once
 
 #include "common.hpp"
@@ -10,22 +13,53 @@
 namespace hffn {
 namespace edges {
 
+__device__ __forceinline__ uint32_t word_at(const uint4& q, int w) { return w == 0 ? q.x : w == 1 ? q.y : w == 2 ? q.z : q.w; }
+__device__ __forceinline__ uint32_t word_at(const uint2& q, int w) { return w == 0 ? q.x : q.y; }
+
+// A group of a value type: its slots, its value and index loads, value s and index s of a loaded group, and a group
+// composed slot by slot (the store's last, partial group).
 template <typename V> struct Group;
 template <> struct Group<float> {
+    static constexpr int kSlots = 4;
     using type = float4;
-    __device__ static float at(const float4& g, int s) { return s == 0 ? g.x : s == 1 ? g.y : s == 2 ? g.z : g.w; }
+    using ids = uint2;
+    __device__ static type load(const float* p) { return *reinterpret_cast<const float4*>(p); }
+    __device__ static float at(const type& g, int s) { return s == 0 ? g.x : s == 1 ? g.y : s == 2 ? g.z : g.w; }
+    __device__ static type compose(const float (&v)[kSlots]) { return make_float4(v[0], v[1], v[2], v[3]); }
 };
 template <> struct Group<uint16_t> {
-    using type = uint2;
-    __device__ static float at(const uint2& g, int s) {
-        const uint32_t word = s < 2 ? g.x : g.y;
+    static constexpr int kSlots = 8;
+    using type = uint4;
+    using ids = uint4;
+    __device__ static type load(const uint16_t* p) { return *reinterpret_cast<const uint4*>(p); }
+    __device__ static float at(const type& g, int s) {
+        const uint32_t word = word_at(g, s / 2);
         return __uint_as_float((s % 2 == 0 ? word << 16 : word & 0xffff0000u));
+    }
+    __device__ static type compose(const uint16_t (&v)[kSlots]) {
+        uint32_t w[4];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) w[i] = v[2 * i] | (static_cast<uint32_t>(v[2 * i + 1]) << 16);
+        return make_uint4(w[0], w[1], w[2], w[3]);
     }
 };
 
-__device__ __forceinline__ uint32_t index_at(const uint2& g, int s) {
-    const uint32_t word = s < 2 ? g.x : g.y;
+template <typename Ids>
+__device__ __forceinline__ uint32_t index_at(const Ids& g, int s) {
+    const uint32_t word = word_at(g, s / 2);
     return s % 2 == 0 ? (word & 0xffffu) : (word >> 16);
+}
+
+// The index group of `S` slots from 16-bit indices packed two per word.
+template <int S>
+__device__ __forceinline__ auto compose_ids(const uint16_t (&i)[S]) {
+    if constexpr (S == 4) {
+        return make_uint2(i[0] | (static_cast<uint32_t>(i[1]) << 16), i[2] | (static_cast<uint32_t>(i[3]) << 16));
+    } else {
+        static_assert(S == 8, "groups of 4 or 8 slots");
+        return make_uint4(i[0] | (static_cast<uint32_t>(i[1]) << 16), i[2] | (static_cast<uint32_t>(i[3]) << 16),
+                          i[4] | (static_cast<uint32_t>(i[5]) << 16), i[6] | (static_cast<uint32_t>(i[7]) << 16));
+    }
 }
 
 // Where a token's input for feature i lives: LDS [i][NT] (staged) or global [i * ld] + t (act of the down kernel).
@@ -41,47 +75,49 @@ struct GlobalInput {
     }
 };
 
-// A wave's slots of one row segment [pb, pe), held in registers: up to G groups of 4 slots per lane, loaded before
-// the inputs are staged so that the store's bytes are in flight while the block waits for its inputs.
+// A wave's slots of one row segment [pb, pe), held in registers: up to G groups per lane, loaded before the inputs are
+// staged so that the store's bytes are in flight while the block waits for its inputs.
 template <typename V, int G>
 struct Segment {
     typename Group<V>::type vals[G];
-    uint2 ids[G];
+    typename Group<V>::ids ids[G];
     int32_t first;  // slot of this lane's group 0
 };
 
-// Issues the loads of groups [chunk * G, chunk * G + G) of this lane (4-slot groups strided by the wave). The whole
-// groups (below pe and nnz) are loaded as one value and one index load each, all issued back to back with no branch
-// between them, so they are in flight together (a lane without a whole group reads the store's group 0, which it never
-// uses). A group that crosses nnz is loaded slot by slot, only in a wave whose segment reaches past the last whole group
-// of the store (nnz not a multiple of 4).
+// Issues the loads of groups [chunk * G, chunk * G + G) of this lane (groups strided by the wave). The whole groups
+// (below pe and nnz) are loaded as one value and one index load each, all issued back to back with no branch between
+// them, so they are in flight together (a lane without a whole group reads the store's group 0, which it never uses).
+// A group that crosses nnz is loaded slot by slot, only in a wave whose segment reaches past the last whole group of
+// the store (nnz not a multiple of the group).
 template <typename V, int G>
 __device__ __forceinline__ void load_segment(Segment<V, G>& seg, const int16_t* __restrict__ idx, const V* __restrict__ val,
                                              int32_t pb, int32_t pe, int32_t nnz, uint32_t lane, uint32_t chunk) {
-    seg.first = (pb & ~3) + 4 * static_cast<int32_t>(lane) + static_cast<int32_t>(chunk) * G * 4 * kWave;
-    if (nnz >= 4) {
+    constexpr int S = Group<V>::kSlots;
+    using Ids = typename Group<V>::ids;
+    seg.first = (pb & ~(S - 1)) + S * static_cast<int32_t>(lane) + static_cast<int32_t>(chunk) * G * S * kWave;
+    if (nnz >= S) {
 #pragma unroll
         for (int k = 0; k < G; ++k) {
-            const int32_t g = seg.first + k * 4 * kWave;
-            const int32_t at = g < pe && g + 4 <= nnz ? g : 0;
-            seg.vals[k] = *reinterpret_cast<const typename Group<V>::type*>(val + at);
-            seg.ids[k] = *reinterpret_cast<const uint2*>(idx + at);
+            const int32_t g = seg.first + k * S * kWave;
+            const int32_t at = g < pe && g + S <= nnz ? g : 0;
+            seg.vals[k] = Group<V>::load(val + at);
+            seg.ids[k] = *reinterpret_cast<const Ids*>(idx + at);
         }
     }
-    if (pe > (nnz & ~3)) {
+    if (pe > (nnz & ~(S - 1))) {
 #pragma unroll
         for (int k = 0; k < G; ++k) {
-            const int32_t g = seg.first + k * 4 * kWave;
-            if (g < pe && g + 4 > nnz) {
-                uint16_t i4[4] = {0, 0, 0, 0};
-                V v4[4] = {V(0), V(0), V(0), V(0)};
-                for (int s = 0; s < 4; ++s)
+            const int32_t g = seg.first + k * S * kWave;
+            if (g < pe && g + S > nnz) {
+                uint16_t is[S] = {};
+                V vs[S] = {};
+                for (int s = 0; s < S; ++s)
                     if (g + s < nnz) {
-                        i4[s] = static_cast<uint16_t>(idx[g + s]);
-                        v4[s] = val[g + s];
+                        is[s] = static_cast<uint16_t>(idx[g + s]);
+                        vs[s] = val[g + s];
                     }
-                seg.ids[k] = make_uint2(i4[0] | (static_cast<uint32_t>(i4[1]) << 16), i4[2] | (static_cast<uint32_t>(i4[3]) << 16));
-                seg.vals[k] = *reinterpret_cast<const typename Group<V>::type*>(v4);
+                seg.ids[k] = compose_ids<S>(is);
+                seg.vals[k] = Group<V>::compose(vs);
             }
         }
     }
@@ -109,12 +145,13 @@ __device__ __forceinline__ void stage_inputs(float* lds, const float* src, uint3
 template <int NT, typename V, int G, typename Input>
 __device__ __forceinline__ void accumulate_segment(const Segment<V, G>& seg, int32_t pb, int32_t pe, const Input& input,
                                                    float (&acc)[NT]) {
+    constexpr int S = Group<V>::kSlots;
 #pragma unroll
     for (int k = 0; k < G; ++k) {
-        const int32_t g = seg.first + k * 4 * kWave;
+        const int32_t g = seg.first + k * S * kWave;
         if (g < pe) {
 #pragma unroll
-            for (int s = 0; s < 4; ++s) {
+            for (int s = 0; s < S; ++s) {
                 if (g + s >= pb && g + s < pe) {
                     float xv[NT];
                     input.template load<NT>(index_at(seg.ids[k], s), xv);
@@ -127,21 +164,20 @@ __device__ __forceinline__ void accumulate_segment(const Segment<V, G>& seg, int
     }
 }
 
-// Groups per lane held at once (768 slots per wave); longer segments take several chunks.
-constexpr int kGroups = 3;
-
-// Partial sums of one wave over slots [pb, pe) of a row, NT tokens: the first chunk's loads come from `first`
-// (issued by the caller before the inputs were staged); the next chunks are loaded here.
-template <int NT, typename V, typename Input>
-__device__ __forceinline__ void row_partials(const Segment<V, kGroups>& first, const int16_t* __restrict__ idx,
+// Partial sums of one wave over slots [pb, pe) of a row, NT tokens, G groups per lane at a time (a chunk of 64 G
+// groups): the first chunk's loads come from `first` (issued by the caller before the inputs were staged); the next
+// chunks are loaded here.
+template <int NT, typename V, int G, typename Input>
+__device__ __forceinline__ void row_partials(const Segment<V, G>& first, const int16_t* __restrict__ idx,
                                              const V* __restrict__ val, int32_t pb, int32_t pe, int32_t nnz,
                                              const Input& input, uint32_t lane, float (&acc)[NT]) {
 #pragma unroll
     for (int t = 0; t < NT; ++t) acc[t] = 0.0f;
     accumulate_segment<NT>(first, pb, pe, input, acc);
-    const int32_t span = kGroups * 4 * kWave;
-    for (uint32_t chunk = 1; (pb & ~3) + static_cast<int32_t>(chunk) * span < pe; ++chunk) {
-        Segment<V, kGroups> seg;
+    constexpr int S = Group<V>::kSlots;
+    const int32_t span = G * S * kWave;
+    for (uint32_t chunk = 1; (pb & ~(S - 1)) + static_cast<int32_t>(chunk) * span < pe; ++chunk) {
+        Segment<V, G> seg;
         load_segment(seg, idx, val, pb, pe, nnz, lane, chunk);
         accumulate_segment<NT>(seg, pb, pe, input, acc);
     }
@@ -173,16 +209,16 @@ __device__ __forceinline__ float row_total(float (&acc)[NT], uint32_t lane, uint
     return mine;
 }
 
-// Segment [pb, pe) of part `part` of a row [begin, end) split in P: the parts cut the row on the 4-slot grid, so
-// each starts on a group boundary and no group is shared by two waves.
-template <int P>
+// Segment [pb, pe) of part `part` of a row [begin, end) split in P: the parts cut the row on the grid of S-slot
+// groups, so each starts on a group boundary and no group is shared by two waves.
+template <int P, int S>
 __device__ __forceinline__ void segment(int32_t begin, int32_t end, uint32_t part, int32_t& pb, int32_t& pe) {
     if constexpr (P == 1) {
         pb = begin;
         pe = end;
     } else {
-        const int32_t base = begin & ~3;
-        const int32_t seg = ((end - base + P - 1) / P + 3) & ~3;
+        const int32_t base = begin & ~(S - 1);
+        const int32_t seg = ((end - base + P - 1) / P + S - 1) & ~(S - 1);
         const int32_t start = base + static_cast<int32_t>(part) * seg;
         pb = max(begin, min(end, start));
         pe = min(end, start + seg);
@@ -196,19 +232,19 @@ __device__ __forceinline__ float row_bias(const float* __restrict__ b, uint32_t 
 }
 
 // A wave's first chunk of one row segment, requested ahead of its use.
-template <typename V>
+template <typename V, int G>
 struct Slots {
-    Segment<V, kGroups> seg;
+    Segment<V, G> seg;
     int32_t pb = 0, pe = 0;  // empty unless requested
 };
 
 // Requests the first chunk of part `part` of row r (nothing when r >= rows).
-template <int P, typename V>
-__device__ __forceinline__ void request_row(Slots<V>& s, const int32_t* __restrict__ off, const int16_t* __restrict__ idx,
+template <int P, typename V, int G>
+__device__ __forceinline__ void request_row(Slots<V, G>& s, const int32_t* __restrict__ off, const int16_t* __restrict__ idx,
                                             const V* __restrict__ val, uint32_t r, uint32_t rows, uint32_t part, int32_t nnz,
                                             uint32_t lane) {
     if (r < rows) {
-        segment<P>(off[r], off[r + 1], part, s.pb, s.pe);
+        segment<P, Group<V>::kSlots>(off[r], off[r + 1], part, s.pb, s.pe);
         load_segment(s.seg, idx, val, s.pb, s.pe, nnz, lane, 0);
     }
 }

@@ -27,7 +27,7 @@
 extern "C" {
 #endif
 
-#define HFFN_ABI_VERSION 17
+#define HFFN_ABI_VERSION 18
 
 #define HFFN_OK 0
 #define HFFN_ERROR_ARGUMENT (-1) /* invalid shape, mode, pointer or workspace */
@@ -36,8 +36,9 @@ extern "C" {
 #define HFFN_VALUE_F32 0
 #define HFFN_VALUE_BF16 1
 
-/* Kernel shapes. EDGES: lanes over a row's slots, 4 slots per lane per load (index arrays 8-byte aligned, value
- * arrays 16-byte (fp32) or 8-byte (bf16) aligned; nnz bounds the grouped loads), long rows split over up to 4 waves,
+/* Kernel shapes. EDGES: lanes over a row's slots in groups of consecutive slots, 16-byte value loads (fp32: 4 slots,
+ * index arrays 8-byte aligned; bf16: 8 slots, index arrays 16-byte aligned; value arrays 16-byte aligned; nnz bounds
+ * the grouped loads), long rows split over up to 4 waves,
  * tokens taken nt at a time (nt = 1, 2, 4 for n <= 4, else 8; ld must be a multiple of nt; the up input of nt tokens
  * is staged in LDS). ROWS: one wave per neuron/output, lanes over tokens. nnz_up / nnz_down: slots of each store. */
 #define HFFN_UP_EDGES 1
