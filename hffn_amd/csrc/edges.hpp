@@ -131,6 +131,15 @@ template <int NT, int WAVES>
 __device__ __forceinline__ void stage_inputs(float* lds, const float* src, uint32_t rows, uint32_t rstride, uint32_t tstride,
                                              uint32_t tokens, uint32_t wave, uint32_t lane) {
     const uint32_t total = rows * NT;
+    // Inputs already in LDS order (one token's contiguous row, or tokens interleaved with stride NT, as the packed
+    // activations are), from a 16-byte aligned source, a multiple of 4 floats: 16 bytes per lane, a quarter of the
+    // transfers.
+    const bool contiguous = (NT == 1 && rstride == 1) || (rstride == NT && tstride == 1 && tokens == NT);
+    if (contiguous && total % 4 == 0 && reinterpret_cast<uintptr_t>(src) % 16 == 0) {
+        for (uint32_t base = wave * kWave * 4; base < total; base += WAVES * kWave * 4)
+            if (base + lane * 4 < total) dma16(src + base, lane * 16, lds + base);
+        return;
+    }
     for (uint32_t base = wave * kWave; base < total; base += WAVES * kWave) {
         const uint32_t r0 = base / NT;  // the piece's first row: its address is the wave-uniform base of the transfer
         const float* from = src + static_cast<size_t>(r0) * rstride;
