@@ -133,8 +133,9 @@ __device__ __forceinline__ void stage_inputs(float* lds, const float* src, uint3
     const uint32_t total = rows * NT;
     // Inputs already in LDS order (one token's contiguous row, or tokens interleaved with stride NT, as the packed
     // activations are), from a 16-byte aligned source, a multiple of 4 floats: 16 bytes per lane, a quarter of the
-    // transfers.
-    const bool contiguous = (NT == 1 && rstride == 1) || (rstride == NT && tstride == 1 && tokens == NT);
+    // transfers. With fewer tokens than NT the padded tokens' columns are staged as they lie (never written by the up
+    // kernel): only the padded tokens' sums read them, and those are never written.
+    const bool contiguous = (NT == 1 && rstride == 1) || (rstride == NT && tstride == 1);
     if (contiguous && total % 4 == 0 && reinterpret_cast<uintptr_t>(src) % 16 == 0) {
         for (uint32_t base = wave * kWave * 4; base < total; base += WAVES * kWave * 4)
             if (base + lane * 4 < total) dma16(src + base, lane * 16, lds + base);
