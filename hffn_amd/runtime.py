@@ -38,6 +38,7 @@ operations around them (the reference requires the default stream; any current s
 from __future__ import annotations
 
 import ctypes
+import math
 from collections import Counter
 from dataclasses import dataclass
 
@@ -56,13 +57,18 @@ EDGES_PASS_TOKENS = 8     # tokens one pass of the lane-per-slot kernels takes
 MFMA_MIN_DENSITY = 0.5    # the lowest support density whose layers get dense planes by default (the MFMA path)
 # The policy's time estimates (µs per call), fitted to forced-pair timings of HFFNRuntime.forward on MI355X (layer
 # copies rotated so that every call reads HBM; the 70M/20 %, 410M/10 % and 50 %, 1.4B/20 % bf16 and 2.8B/80 % bf16
-# layers). Lane-per-slot kernels: EDGES_CALL_US per call, plus per pass of up to 8 tokens (EDGES_PASS_US +
-# EDGES_SLOT_US per stored slot of both sides) weighted by EDGES_PASS_WEIGHT of the pass's token width. Compact-store
-# MFMA path: TILES_BASE_US + TILES_SLOT_US per stored slot, plus up to (TILES_FILL_US + TILES_FILL_SLOT_US per slot)
-# as the first 16-token tile fills, plus (TILES_TILE_US + TILES_TILE_SLOT_US per slot) per further 16-token tile.
-EDGES_CALL_US, EDGES_PASS_US, EDGES_SLOT_US = 6.0, 4.0, 3.5e-6
-EDGES_PASS_WEIGHT = {1: 0.42, 2: 0.44, 4: 0.52, 8: 1.0}
-TILES_BASE_US, TILES_SLOT_US = 12.7, 1.11e-6
+# layers at 1-32 tokens: the faster path at every one of the 50 points). Lane-per-slot kernels, per pass of up to 8
+# tokens (a pass's width: 1, 2, 4 or 8): the larger of a floor of round trips and launches (EDGES_FLOOR_US of the
+# width, plus EDGES_SLOT_TOKEN_US per stored slot of both sides and token of the width) and the stores' stream
+# (EDGES_BYTE_US per stored byte, ~3.2 TB/s); a pass whose activations exceed the down kernel's LDS stage
+# (EDGES_STAGE_BYTES) gathers them from L2, EDGES_GATHER times slower. Compact-store MFMA path: the larger of a floor
+# that grows with the width of the layer (TILES_FLOOR_US + TILES_WIDTH_US per doubling of d_ff from 1024) and the
+# stores' stream (TILES_BYTE_US per byte, ~2.5 TB/s), plus up to (TILES_FILL_US + TILES_FILL_SLOT_US per slot) as the
+# first 16-token tile fills, plus (TILES_TILE_US + TILES_TILE_SLOT_US per slot) per further 16-token tile.
+EDGES_FLOOR_US = {1: 11.8, 2: 11.8, 4: 11.8, 8: 13.2}
+EDGES_SLOT_TOKEN_US, EDGES_BYTE_US = 0.2e-6, 0.315e-6
+EDGES_STAGE_BYTES, EDGES_GATHER = 131072, 2.3
+TILES_FLOOR_US, TILES_WIDTH_US, TILES_BYTE_US = 11.9, 2.47, 0.406e-6
 TILES_FILL_US, TILES_FILL_SLOT_US = 2.0, 0.07e-6
 TILES_TILE_US, TILES_TILE_SLOT_US = 4.5, 0.17e-6
 TILES_TIE = 1.05  # the tiles path wins estimates within 5 % of the lane-per-slot kernels' (its cost is flat in N)
@@ -97,42 +103,60 @@ def edges_supported(d_model: int, n: int) -> bool:
     return bool(_lib.load().hffn_edges_supported(d_model, n))
 
 
-def edges_us(n: int, slots: int) -> float:
-    """Estimated µs of a call on the lane-per-slot kernels (``slots``: stored slots of both sides)."""
-    full = EDGES_PASS_US + EDGES_SLOT_US * slots
-    passes, rest = divmod(n, EDGES_PASS_TOKENS)
-    edges = EDGES_CALL_US + passes * full
-    if rest:
-        edges += EDGES_PASS_WEIGHT[1 << (rest - 1).bit_length()] * full  # the pass's token width: 1, 2, 4 or 8
-    return edges
+@dataclass(frozen=True)
+class StoreShape:
+    """What the path estimates read of a layer: the stored slots of both sides, their bytes (int16 indices and the
+    values) and d_ff (the activations the down kernels read, the width of the tiles path's blocks)."""
+    slots: int
+    bytes: int
+    d_ff: int
 
 
-def tiles_us(n: int, slots: int) -> float:
-    """Estimated µs of a call on the compact-store MFMA path (N <= 64; ``slots``: stored slots of both sides)."""
-    return (TILES_BASE_US + TILES_SLOT_US * slots + (TILES_FILL_US + TILES_FILL_SLOT_US * slots) * min(n - 1, 15) / 15
-            + (TILES_TILE_US + TILES_TILE_SLOT_US * slots) * ((n - 1) // 16))
+def _width(tokens: int) -> int:
+    return 1 << (tokens - 1).bit_length()  # 1, 2, 4 or 8 tokens per lane-per-slot pass
 
 
-def rows_us(n: int, slots: int) -> float:
-    """Estimated µs of a call on the lane-per-token kernels above 64 tokens (``slots``: stored slots of both sides)."""
-    return ROWS_CALL_US + ROWS_SLOT_US * slots * n
+def edges_us(n: int, shape: StoreShape) -> float:
+    """Estimated µs of a call on the lane-per-slot kernels: passes of up to 8 tokens."""
+    total = 0.0
+    while n > 0:
+        tokens = min(n, EDGES_PASS_TOKENS)
+        width = _width(tokens)
+        cost = max(EDGES_FLOOR_US[width] + EDGES_SLOT_TOKEN_US * shape.slots * width, EDGES_BYTE_US * shape.bytes)
+        if shape.d_ff * width * 4 > EDGES_STAGE_BYTES:
+            cost *= EDGES_GATHER
+        total += cost
+        n -= tokens
+    return total
 
 
-def pieces_us(n: int, slots: int) -> float:
+def tiles_us(n: int, shape: StoreShape) -> float:
+    """Estimated µs of a call on the compact-store MFMA path (N <= 64)."""
+    floor = TILES_FLOOR_US + TILES_WIDTH_US * math.log2(max(shape.d_ff, 1024) / 1024)
+    return (max(floor, TILES_BYTE_US * shape.bytes) + (TILES_FILL_US + TILES_FILL_SLOT_US * shape.slots) * min(n - 1, 15) / 15
+            + (TILES_TILE_US + TILES_TILE_SLOT_US * shape.slots) * ((n - 1) // 16))
+
+
+def rows_us(n: int, shape: StoreShape) -> float:
+    """Estimated µs of a call on the lane-per-token kernels above 64 tokens."""
+    return ROWS_CALL_US + ROWS_SLOT_US * shape.slots * n
+
+
+def pieces_us(n: int, shape: StoreShape) -> float:
     """Estimated µs of N tokens on the tiles path, in calls of up to ``TILES_MAX_TOKENS`` tokens."""
     whole, rest = divmod(n, TILES_MAX_TOKENS)
-    return whole * tiles_us(TILES_MAX_TOKENS, slots) + (tiles_us(rest, slots) if rest else 0.0)
+    return whole * tiles_us(TILES_MAX_TOKENS, shape) + (tiles_us(rest, shape) if rest else 0.0)
 
 
-def decode_mode(n: int, slots: int, edges: bool, tiles: bool) -> str | None:
+def decode_mode(n: int, shape: StoreShape, edges: bool, tiles: bool) -> str | None:
     """The compact-store path of least estimated time for N <= 64 tokens: ``edges`` (up to ``EDGES_MAX_TOKENS``, when
     ``edges``: its LDS stage fits) or ``tiles`` (when ``tiles``: the layer has tiled stores; it also takes estimates
     within ``TILES_TIE`` of the lane-per-slot kernels'); None when neither applies."""
     options = {}
     if edges and n <= EDGES_MAX_TOKENS:
-        options["edges"] = edges_us(n, slots)
+        options["edges"] = edges_us(n, shape)
     if tiles and n <= TILES_MAX_TOKENS:
-        options["tiles"] = tiles_us(n, slots) / TILES_TIE
+        options["tiles"] = tiles_us(n, shape) / TILES_TIE
     return min(options, key=options.get) if options else None
 
 
@@ -291,6 +315,7 @@ class HFFNRuntime:
             self._nnz.append((tensors["up_idx"].numel(), tensors["out_hidden"].numel()))
         self._slots = max(layer.up_idx.numel() + layer.out_hidden.numel() for layer in layers)
         self.density = self._slots / (2 * self.d_model * self.d_ff)
+        self._store = StoreShape(self._slots, self._slots * (2 + self._tensors[0]["up_val"].element_size()), self.d_ff)
         self._planes: list[dict] | None = None
         self._stale: set[int] = set()   # layers whose values changed since their planes were built
         self._tiles_stale: set[int] = set()  # ... since their tiled stores were built
@@ -464,12 +489,12 @@ class HFFNRuntime:
         edges = edges_supported(self.d_model, n)
         if self.forced_up is None and self.forced_down is None:
             if n <= TILES_MAX_TOKENS:
-                mode = decode_mode(n, self._slots, edges, self._tiles is not None)
+                mode = decode_mode(n, self._store, edges, self._tiles is not None)
                 if mode == "tiles":
                     return mode, mode
             elif self._planes is not None and self.density >= MFMA_MIN_DENSITY and mfma_streamed(n, self.d_model, self.d_ff):
                 return "mfma", "mfma"
-            elif self._tiles is not None and pieces_us(n, self._slots) < rows_us(n, self._slots):
+            elif self._tiles is not None and pieces_us(n, self._store) < rows_us(n, self._store):
                 return "tiles", "tiles"
         up = self.forced_up or up_mode(n, self.d_model)
         if up == "edges" and not edges:

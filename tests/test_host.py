@@ -156,32 +156,47 @@ def test_policy():
     assert [runtime.leading_dim(n) for n in (1, 2, 3, 4, 5, 8, 9, 2048, 2049)] == [4, 4, 4, 4, 8, 8, 16, 2048, 2056]
 
 
+# Stored slots (both sides) and bytes of the layers the policy's estimates were fitted to: int16 indices and float32
+# (6 bytes a slot) or bfloat16 (4 bytes) values.
+S410 = runtime.StoreShape(2 * 4096 * 512, 6 * 2 * 4096 * 512, 4096)
+S410_D10 = runtime.StoreShape(2 * 4096 * 102, 6 * 2 * 4096 * 102, 4096)
+S1P4 = runtime.StoreShape(2 * 8192 * 410, 4 * 2 * 8192 * 410, 8192)
+S70 = runtime.StoreShape(2 * 2048 * 102, 6 * 2 * 2048 * 102, 2048)
+S2P8 = runtime.StoreShape(41_836_593, 4 * 41_836_593, 10240)
+
+
 def test_decode_policy():
     """Up to 64 tokens the policy reads the compact store; the estimated crossovers land where the forced-pair timings
-    put them: the 410M/50 % layer on the lane-per-slot kernels at 1-4 tokens and on the tiles path from 8, the
-    1.4B/20 % bf16 layer on the lane-per-slot kernels at 1-2 tokens (measured 14.2 against 18.8 us and 16.6 against
-    19.1 us) and on the tiles path from 4 (19.3 against 21.4 us: the tiles path takes estimates within 5 % of the
-    other's), the
-    narrow 70M/20 % layer on the lane-per-slot kernels up to 8 tokens, the 2.8B/80 % layer on the tiles path at every
-    count; above 32 tokens only the tiles path remains; without tiled stores the lane-per-slot kernels or nothing."""
-    s410, s1p4, s70, s2p8 = 2 * 4096 * 512, 2 * 8192 * 410, 2 * 2048 * 102, 2 * 10240 * 2048
-    assert [runtime.decode_mode(n, s410, True, True) for n in (1, 2, 4, 8, 16, 32, 64)] == \
-        ["edges", "edges", "edges", "tiles", "tiles", "tiles", "tiles"]
-    assert [runtime.decode_mode(n, s1p4, True, True) for n in (1, 2, 4, 8, 16, 32, 64)] == ["edges"] * 2 + ["tiles"] * 5
-    assert [runtime.decode_mode(n, s70, True, True) for n in (1, 4, 8, 16, 32)] == ["edges", "edges", "edges", "tiles", "tiles"]
-    assert all(runtime.decode_mode(n, s2p8, True, True) == "tiles" for n in (1, 4, 16, 64))
-    assert runtime.decode_mode(33, s410, True, False) is None and runtime.decode_mode(32, s410, True, False) == "edges"
-    assert runtime.decode_mode(65, s410, True, True) is None
-    assert runtime.decode_mode(4, s410, False, True) == "tiles"
+    put them (MI355X, 12 rotating copies, µs per call, lane-per-slot against tiles): the 410M/50 % layer on the
+    lane-per-slot kernels at 1-4 tokens (14.3 against 17.5 at 4) and on the tiles path from 6 (20.5 against 17.0); the
+    410M/10 % and 70M/20 % layers on the lane-per-slot kernels up to 8 tokens (15.0 against 17.3; 13.4 against 13.9)
+    and on the tiles path from 12; the 1.4B/20 % bf16 layer on the lane-per-slot kernels at 1-4 tokens (17.9 against
+    19.3 at 4) and on the tiles path from 6, where its activations no longer fit the down kernel's LDS stage (34.1
+    against 19.7); the 2.8B/80 % bf16 layer on the lane-per-slot kernels at 1-2 tokens (52.6 against 67.9 at 1) and
+    on the tiles path from 3 (124.8 against 69.0); above 32 tokens only the tiles path remains; without tiled stores
+    the lane-per-slot kernels or nothing."""
+    mode = lambda shape, ns: [runtime.decode_mode(n, shape, True, True) for n in ns]  # noqa: E731
+    assert mode(S410, (1, 2, 3, 4, 6, 8, 16, 32, 64)) == ["edges"] * 4 + ["tiles"] * 5
+    assert mode(S410_D10, (1, 4, 6, 8, 12, 16, 32)) == ["edges"] * 4 + ["tiles"] * 3
+    assert mode(S1P4, (1, 2, 3, 4, 6, 8, 16, 32, 64)) == ["edges"] * 4 + ["tiles"] * 5
+    assert mode(S70, (1, 4, 6, 8, 12, 16, 32)) == ["edges"] * 4 + ["tiles"] * 3
+    assert mode(S2P8, (1, 2, 3, 4, 16, 64)) == ["edges"] * 2 + ["tiles"] * 4
+    assert runtime.decode_mode(33, S410, True, False) is None and runtime.decode_mode(32, S410, True, False) == "edges"
+    assert runtime.decode_mode(65, S410, True, True) is None
+    assert runtime.decode_mode(4, S410, False, True) == "tiles"
 
 
-def test_tiles_estimate():
-    """The tiles path's estimate against the forced-pair timings it was fitted to (within 20 %)."""
-    measured = {(2 * 4096 * 512, 1): 17.4, (2 * 4096 * 512, 16): 18.4, (2 * 4096 * 512, 64): 30.0,
-                (2 * 8192 * 410, 1): 21.3, (2 * 8192 * 410, 16): 24.3, (2 * 8192 * 410, 64): 44.9,
-                (2 * 2048 * 102, 16): 16.5, (2 * 10240 * 2048, 1): 59.3, (2 * 10240 * 2048, 64): 99.3}
-    for (slots, n), us in measured.items():
-        assert abs(runtime.tiles_us(n, slots) / us - 1) < 0.2, (slots, n)
+def test_path_estimates():
+    """The estimates against the forced-pair timings they were fitted to (µs per call, within 20 %): the tiles path
+    at 1, 16 and 32 tokens, the lane-per-slot kernels where their activations fit the down kernel's stage."""
+    tiles = {(S410, 1): 17.8, (S410, 16): 17.8, (S410, 32): 21.5, (S1P4, 1): 19.0, (S1P4, 16): 23.0, (S1P4, 32): 31.5,
+             (S70, 16): 15.7, (S2P8, 1): 67.9, (S2P8, 32): 87.6, (S410_D10, 1): 17.2}
+    for (shape, n), us in tiles.items():
+        assert abs(runtime.tiles_us(n, shape) / us - 1) < 0.2, (shape, n)
+    edges = {(S410, 1): 12.9, (S410, 4): 14.3, (S410, 8): 20.5, (S410, 16): 39.0, (S1P4, 1): 13.0, (S1P4, 2): 14.4,
+             (S1P4, 4): 17.9, (S70, 8): 13.4, (S410_D10, 8): 15.0, (S2P8, 1): 52.6, (S2P8, 2): 55.8, (S2P8, 4): 125.1}
+    for (shape, n), us in edges.items():
+        assert abs(runtime.edges_us(n, shape) / us - 1) < 0.2, (shape, n)
 
 
 def test_large_n_estimates():
@@ -190,17 +205,16 @@ def test_large_n_estimates():
     the tiles path at every count (65: 59 against 223; 512: 332 against 500; 2048: 1321 against 1998), the 410M/50 %
     layer too (128: 57 against 203), the 70M/20 % layer on the lane-per-token kernels from 128 tokens (53 against 63;
     2048: 145 against 998); the rows estimate within 30 % of those timings from 128 tokens on."""
-    s410, s1p4, s70 = 2 * 4096 * 512, 2 * 8192 * 410, 2 * 2048 * 102
-    faster = lambda n, slots: "tiles" if runtime.pieces_us(n, slots) < runtime.rows_us(n, slots) else "rows"
-    assert [faster(n, s1p4) for n in (65, 128, 512, 2048)] == ["tiles"] * 4
-    assert [faster(n, s410) for n in (65, 128, 2048)] == ["tiles"] * 3
-    assert [faster(n, s70) for n in (128, 256, 2048)] == ["rows"] * 3
-    assert runtime.pieces_us(128, s70) == 2 * runtime.tiles_us(64, s70)
-    assert runtime.pieces_us(65, s70) == runtime.tiles_us(64, s70) + runtime.tiles_us(1, s70)
-    rows_measured = {(s70, 128): 52.6, (s70, 512): 69.1, (s70, 2048): 145.2, (s1p4, 512): 499.8, (s1p4, 2048): 1997.7,
-                     (s410, 512): 313.4, (s410, 2048): 1085.7, (s1p4, 128): 234.7}
-    for (slots, n), us in rows_measured.items():
-        assert abs(runtime.rows_us(n, slots) / us - 1) < 0.3, (slots, n)
+    faster = lambda n, shape: "tiles" if runtime.pieces_us(n, shape) < runtime.rows_us(n, shape) else "rows"  # noqa: E731
+    assert [faster(n, S1P4) for n in (65, 128, 512, 2048)] == ["tiles"] * 4
+    assert [faster(n, S410) for n in (65, 128, 2048)] == ["tiles"] * 3
+    assert [faster(n, S70) for n in (128, 256, 2048)] == ["rows"] * 3
+    assert runtime.pieces_us(128, S70) == 2 * runtime.tiles_us(64, S70)
+    assert runtime.pieces_us(65, S70) == runtime.tiles_us(64, S70) + runtime.tiles_us(1, S70)
+    rows_measured = {(S70, 128): 52.6, (S70, 512): 69.1, (S70, 2048): 145.2, (S1P4, 512): 499.8, (S1P4, 2048): 1997.7,
+                     (S410, 512): 313.4, (S410, 2048): 1085.7, (S1P4, 128): 234.7}
+    for (shape, n), us in rows_measured.items():
+        assert abs(runtime.rows_us(n, shape) / us - 1) < 0.3, (shape, n)
 
 
 @pytest.mark.skipif(torch.cuda.is_available(), reason="uses placeholder pointers: never run where a launch could reach a GPU")
