@@ -62,9 +62,10 @@ MFMA_MIN_DENSITY = 0.5    # the lowest support density whose layers get dense pl
 # width, plus EDGES_SLOT_TOKEN_US per stored slot of both sides and token of the width) and the stores' stream
 # (EDGES_BYTE_US per stored byte, ~3.2 TB/s); a pass whose activations exceed the down kernel's LDS stage
 # (EDGES_STAGE_BYTES) gathers them from L2, EDGES_GATHER times slower. Compact-store MFMA path: the larger of a floor
-# that grows with the width of the layer (TILES_FLOOR_US + TILES_WIDTH_US per doubling of d_ff from 1024) and the
-# stores' stream (TILES_BYTE_US per byte, ~2.5 TB/s), plus up to (TILES_FILL_US + TILES_FILL_SLOT_US per slot) as the
-# first 16-token tile fills, plus (TILES_TILE_US + TILES_TILE_SLOT_US per slot) per further 16-token tile.
+# that grows with the width of the layer (TILES_FLOOR_US + TILES_WIDTH_US per doubling of d_ff from 1024; below
+# 2048, the narrowest fitted, that layer's floor) and the stores' stream (TILES_BYTE_US per byte, ~2.5 TB/s), plus up
+# to (TILES_FILL_US + TILES_FILL_SLOT_US per slot) as the first 16-token tile fills, plus (TILES_TILE_US +
+# TILES_TILE_SLOT_US per slot) per further 16-token tile.
 EDGES_FLOOR_US = {1: 11.8, 2: 11.8, 4: 11.8, 8: 13.2}
 EDGES_SLOT_TOKEN_US, EDGES_BYTE_US = 0.2e-6, 0.315e-6
 EDGES_STAGE_BYTES, EDGES_GATHER = 131072, 2.3
@@ -132,7 +133,7 @@ def edges_us(n: int, shape: StoreShape) -> float:
 
 def tiles_us(n: int, shape: StoreShape) -> float:
     """Estimated µs of a call on the compact-store MFMA path (N <= 64)."""
-    floor = TILES_FLOOR_US + TILES_WIDTH_US * math.log2(max(shape.d_ff, 1024) / 1024)
+    floor = TILES_FLOOR_US + TILES_WIDTH_US * math.log2(max(shape.d_ff, 2048) / 1024)
     return (max(floor, TILES_BYTE_US * shape.bytes) + (TILES_FILL_US + TILES_FILL_SLOT_US * shape.slots) * min(n - 1, 15) / 15
             + (TILES_TILE_US + TILES_TILE_SLOT_US * shape.slots) * ((n - 1) // 16))
 
