@@ -65,16 +65,83 @@ __device__ __forceinline__ void walk_row(const float* __restrict__ base, const i
     }
 }
 
+// The same walk for one token per lane, pipelined over chunks of 64 slots: lane l holds slot c0 + l's index and
+// weight; chunk k + 1's input rows and chunk k + 2's slots are requested before chunk k's products are added, so each
+// chunk costs one memory round trip, overlapped with the previous chunk's adds (two chunks of inputs in registers,
+// 128 VGPRs: the lane-per-token kernels run few waves per CU). The sum is the same running sum in stored slot order.
+template <typename V>
+__device__ __forceinline__ float walk_row_pipelined(const float* __restrict__ base, const int16_t* __restrict__ idx,
+                                                    const V* __restrict__ w, int32_t begin, int32_t end, uint32_t ld,
+                                                    uint32_t lane) {
+    float acc = 0.0f;
+    if (begin >= end) return acc;
+    const int32_t last = end - 1;
+    const auto slot = [&](int32_t c0) { return min(c0 + static_cast<int32_t>(lane), last); };
+    const auto request = [&](float (&xv)[kWave], int32_t my_i, int32_t c0) {
+        const int32_t count = min(static_cast<int32_t>(kWave), end - c0);
+#pragma unroll
+        for (int32_t u = 0; u < kWave; ++u) {
+            const uint32_t i = static_cast<uint32_t>(__builtin_amdgcn_readlane(my_i, min(u, count - 1)));
+            xv[u] = base[static_cast<size_t>(i) * ld];
+        }
+    };
+    const auto add = [&](const float (&xv)[kWave], float my_w, int32_t c0) {
+        const int32_t count = min(static_cast<int32_t>(kWave), end - c0);
+#pragma unroll
+        for (int32_t u = 0; u < kWave; ++u)
+            if (u < count) acc = fmaf(__int_as_float(__builtin_amdgcn_readlane(__float_as_int(my_w), u)), xv[u], acc);
+    };
+    float xa[kWave], xb[kWave];
+    int32_t c0 = begin;
+    int32_t i_a = static_cast<uint16_t>(idx[slot(c0)]);
+    float w_a = widen(w[slot(c0)]);
+    request(xa, i_a, c0);
+    int32_t i_b = static_cast<uint16_t>(idx[slot(c0 + kWave)]);  // the next chunk's slots, behind this chunk's inputs
+    float w_b = widen(w[slot(c0 + kWave)]);
+    while (true) {
+        // chunk c0's inputs requested into xa (its weights w_a), the next chunk's slots into (i_b, w_b)
+        const bool more = c0 + kWave < end;
+        int32_t i_c = 0;
+        float w_c = 0.0f;
+        if (more) {
+            request(xb, i_b, c0 + kWave);
+            i_c = static_cast<uint16_t>(idx[slot(c0 + 2 * kWave)]);
+            w_c = widen(w[slot(c0 + 2 * kWave)]);
+        }
+        add(xa, w_a, c0);
+        if (!more) break;
+        c0 += kWave;
+        // chunk c0's inputs in xb (weights w_b), the next chunk's slots in (i_c, w_c): the same with the buffers' roles
+        // exchanged
+        const bool again = c0 + kWave < end;
+        int32_t i_d = 0;
+        float w_d = 0.0f;
+        if (again) {
+            request(xa, i_c, c0 + kWave);
+            i_d = static_cast<uint16_t>(idx[slot(c0 + 2 * kWave)]);
+            w_d = widen(w[slot(c0 + 2 * kWave)]);
+        }
+        add(xb, w_b, c0);
+        if (!again) break;
+        c0 += kWave;
+        w_a = w_c;  // chunk c0's inputs in xa, requested with i_c
+        i_b = i_d;
+        w_b = w_d;
+    }
+    return acc;
+}
+
 // ------------------------------------------------------------------------------------------- up, rows
 // EPI kGelu: act = gelu(b + acc), and z = b + acc where z is not null (the training forward keeps it). EPI kGeluGrad
 // (the backward's gz): act = acc * gelu'(z), z read, b unused.
 enum RowsEpilogue : int { kGelu = 0, kGeluGrad = 1 };
 
-template <int TPL, typename V, int EPI>
+template <int TPL, typename V, int EPI, bool PIPE = false>
 __global__ __launch_bounds__(kBlock) void up_rows_kernel(const float* __restrict__ x_t, const int32_t* __restrict__ off,
                                                         const int16_t* __restrict__ idx, const V* __restrict__ w,
                                                         const float* __restrict__ b, float* __restrict__ act,
                                                         float* __restrict__ z, uint32_t h, uint32_t n, uint32_t ld) {
+    static_assert(!PIPE || TPL == 1, "the pipelined walk takes one token per lane");
     const uint32_t r = blockIdx.x * kWaves + uniform(threadIdx.x / kWave);
     if (r >= h) return;
     // every lane walks (the slots are spread over the wave's lanes); a lane past the tokens reads token 0 and stores nothing
@@ -82,7 +149,8 @@ __global__ __launch_bounds__(kBlock) void up_rows_kernel(const float* __restrict
     const bool live = t0 < n;
     const float bias = EPI == kGelu ? b[r] : 0.0f;  // requested with the row's first slots
     float acc[TPL];
-    walk_row<TPL>(x_t + (live ? t0 : 0), idx, w, off[r], off[r + 1], ld, threadIdx.x % kWave, acc);
+    if constexpr (PIPE) acc[0] = walk_row_pipelined(x_t + (live ? t0 : 0), idx, w, off[r], off[r + 1], ld, threadIdx.x % kWave);
+    else walk_row<TPL>(x_t + (live ? t0 : 0), idx, w, off[r], off[r + 1], ld, threadIdx.x % kWave, acc);
     if (!live) return;
     float* out = act + static_cast<size_t>(r) * ld + t0;
     float* zr = z ? z + static_cast<size_t>(r) * ld + t0 : nullptr;
@@ -102,18 +170,20 @@ __global__ __launch_bounds__(kBlock) void up_rows_kernel(const float* __restrict
 }
 
 // ----------------------------------------------------------------------------------------- down, rows
-template <int TPL, typename V>
+template <int TPL, typename V, bool PIPE = false>
 __global__ __launch_bounds__(kBlock) void down_rows_kernel(const float* __restrict__ act, const int32_t* __restrict__ off,
                                                           const int16_t* __restrict__ hid, const V* __restrict__ v,
                                                           const float* __restrict__ bias, float* __restrict__ y_t,
                                                           uint32_t d, uint32_t n, uint32_t ld) {
+    static_assert(!PIPE || TPL == 1, "the pipelined walk takes one token per lane");
     const uint32_t o = blockIdx.x * kWaves + uniform(threadIdx.x / kWave);
     if (o >= d) return;
     const uint32_t t0 = (blockIdx.y * kWave + threadIdx.x % kWave) * TPL;
     const bool live = t0 < n;
     const float bo = bias ? bias[o] : 0.0f;  // no bias: the backward's gx; requested with the row's first slots
     float acc[TPL];
-    walk_row<TPL>(act + (live ? t0 : 0), hid, v, off[o], off[o + 1], ld, threadIdx.x % kWave, acc);
+    if constexpr (PIPE) acc[0] = walk_row_pipelined(act + (live ? t0 : 0), hid, v, off[o], off[o + 1], ld, threadIdx.x % kWave);
+    else walk_row<TPL>(act + (live ? t0 : 0), hid, v, off[o], off[o + 1], ld, threadIdx.x % kWave, acc);
     if (!live) return;
     float* out = y_t + static_cast<size_t>(o) * ld + t0;
 #pragma unroll
@@ -171,12 +241,21 @@ __global__ __launch_bounds__(kBlock) void transpose_kernel(const float* __restri
 
 uint32_t ceil_div(uint32_t a, uint32_t b) { return (a + b - 1) / b; }
 
+// Below 256 tokens: the pipelined walk (one token per lane) where the grid's waves fit one round at its occupancy (3
+// waves per SIMD on 256 CUs, 150 VGPRs): there each wave's chain of round trips bounds the kernel (the 70M layer's 512
+// outputs at 128 tokens: its down kernel 1024 waves, the call 44.1 -> 38.9 us); with more waves the plain walk's
+// occupancy (8 per SIMD) hides the latency better (the 1.4B layer at 128 tokens: 222 us plain, 267 us pipelined).
+constexpr uint64_t kPipelinedWaves = 3 * 4 * 256;
+bool pipelined(uint32_t rows, uint32_t n) { return static_cast<uint64_t>(rows) * ceil_div(n, kWave) <= kPipelinedWaves; }
+
 template <typename V, int EPI>
 hipError_t up_rows_typed(const float* x_t, const int32_t* off, const int16_t* idx, const V* w, const float* b, float* act,
                          float* z, uint32_t h, uint32_t n, uint32_t ld, hipStream_t stream) {
     const dim3 block(kBlock);
     if (n >= 256) {
         hipLaunchKernelGGL((up_rows_kernel<4, V, EPI>), dim3(ceil_div(h, kWaves), ceil_div(n, 4 * kWave)), block, 0, stream, x_t, off, idx, w, b, act, z, h, n, ld);
+    } else if (pipelined(h, n)) {
+        hipLaunchKernelGGL((up_rows_kernel<1, V, EPI, true>), dim3(ceil_div(h, kWaves), ceil_div(n, kWave)), block, 0, stream, x_t, off, idx, w, b, act, z, h, n, ld);
     } else if (n >= 128) {
         hipLaunchKernelGGL((up_rows_kernel<2, V, EPI>), dim3(ceil_div(h, kWaves), ceil_div(n, 2 * kWave)), block, 0, stream, x_t, off, idx, w, b, act, z, h, n, ld);
     } else {
@@ -191,6 +270,8 @@ hipError_t down_rows_typed(const float* act, const int32_t* off, const int16_t* 
     const dim3 block(kBlock);
     if (n >= 256) {
         hipLaunchKernelGGL((down_rows_kernel<4, V>), dim3(ceil_div(d, kWaves), ceil_div(n, 4 * kWave)), block, 0, stream, act, off, hid, v, bias, y_t, d, n, ld);
+    } else if (pipelined(d, n)) {
+        hipLaunchKernelGGL((down_rows_kernel<1, V, true>), dim3(ceil_div(d, kWaves), ceil_div(n, kWave)), block, 0, stream, act, off, hid, v, bias, y_t, d, n, ld);
     } else if (n >= 128) {
         hipLaunchKernelGGL((down_rows_kernel<2, V>), dim3(ceil_div(d, kWaves), ceil_div(n, 2 * kWave)), block, 0, stream, act, off, hid, v, bias, y_t, d, n, ld);
     } else {
