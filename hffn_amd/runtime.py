@@ -76,7 +76,7 @@ TILES_TIE = 1.05  # the tiles path wins estimates within 5 % of the lane-per-slo
 # Lane-per-token kernels above 64 tokens: ROWS_CALL_US per call plus ROWS_SLOT_US per stored slot (both sides) and token
 # (each slot reads its input row of every token from L2), fitted to forced-pair timings of the 70M/20 %, 410M/50 % and
 # 1.4B/20 % bf16 layers at 65-2048 tokens; against it the tiles path in pieces of 64 tokens (one tiles_us each).
-ROWS_CALL_US, ROWS_SLOT_US = 45.0, 0.14e-6
+ROWS_CALL_US, ROWS_SLOT_US = 30.0, 0.148e-6
 MAX_TOKENS = 1 << 18      # runtime/gpu/nvidia/common/kernels/hffn_cuda/runtime.py:26
 # The reference's policy constants (runtime.py:24-25), with this policy's meaning: COOP_MAX_TOKENS, the largest N the
 # policy may run on the cooperative (lane-per-slot, wave-reduced) kernels; BLOCK_MAX_WIDTH, the widest d_ff up to which
