@@ -23,13 +23,14 @@ The policy reads the compact store up to 64 tokens: ``edges`` (up to 32 tokens) 
 estimated time (``decode_mode``); above 64 tokens the MFMA path where the layer has planes, else ``tiles`` in pieces of
 64 tokens or ``rows``, whichever has the least estimated time (``pieces_us``, ``rows_us``: the tiles path reads the
 store once per piece, the lane-per-token kernels read an input row per slot and token, so the tiles path takes the
-larger layers, e.g. the 1.4B layer at 20 %, 59 against 223 us at 65 tokens and 1.32 against 2.00 ms at 2048, and the
-lane-per-token kernels the smallest, e.g. the 70M layer at 20 % from 128 tokens on, 53 against 63 us). The dense
+larger layers, e.g. the 1.4B layer at 20 %, 59 against 213 us at 65 tokens and 1.32 against 2.00 ms at 2048, and the
+lane-per-token kernels the smallest, e.g. the 70M layer at 20 % from 65 tokens on, 38.9 against 44.0 us). The dense
 planes (4 bytes per weight for float32 values, 2 for bfloat16) are built only for layers of at least
 ``MFMA_MIN_DENSITY`` unless asked for (``dense=True``). Per call on the Pythia-410M layer at 50 % (12 rotating
-copies, MI355X, HFFNRuntime.forward, forced pairs, compact rows): N = 1: edges 12.6 us, tiles 17.3; N = 4: edges
-15.8, tiles 16.6; N = 16: tiles 17.9, edges 40.4; N = 32: tiles 21.7; N = 2048: mfma 110-116 us. On the 1.4B layer
-(bfloat16, 20 %): tiles 18.9, 19.3, 23.2, 31.7 us at N = 1, 4, 16, 32 (edges 15.4, 25.4, 63.2 at 1, 4, 16).
+copies, MI355X, HFFNRuntime.forward, forced pairs, compact rows): N = 1: edges 12.9 us, tiles 17.8; N = 4: edges
+14.3, tiles 17.5; N = 16: tiles 17.8, edges 39.0; N = 32: tiles 21.5; N = 2048: mfma 110-116 us. On the 1.4B layer
+(bfloat16, 20 %): edges 13.0, 14.4, 17.9 us at N = 1, 2, 4 (tiles 19.0, 19.0, 19.3), tiles 23.0 and 31.5 us at 16
+and 32 (edges 59.5 at 16).
 
 Model arrays stay on the device. Work buffers are dense, shared by all layers, sized for the largest N seen and
 reused. Kernels are queued on PyTorch's current stream of the device, so they run in call order with the PyTorch
