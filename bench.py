@@ -286,6 +286,11 @@ def decode_record(runtime, base, device, rotations: int, steps: int) -> dict:
 
     record = {"rotation": f"{rotations} passes over each layer's copies after one untimed pass; HIP events around all",
               "tiled": runtime.tiled}
+    w410 = synth.WORKLOADS["pythia410m_d50"]
+    if (runtime.d_model, runtime.d_ff) != (w410.d_model, w410.d_ff):  # another headline layer: the 410M layer of its own
+        base = synth.make_workload_layer(w410)
+        count = max(1, math.ceil(MALL_BYTES / layer_costs(base, 1)["model_bytes"]))
+        runtime = HFFNRuntime(device_copies(hip_layer(base, device), count), device, tiled=runtime.tiled)
     copies = len(runtime.layers)
     floor = read_floor(base, copies, rotations, device)
     record["pythia410m_d50_read_floor"] = floor
