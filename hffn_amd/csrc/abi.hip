@@ -155,13 +155,12 @@ struct Plan {
 int check_forward(const Plan& p) {
     const float* some_x = reinterpret_cast<const float*>(uintptr_t{16});  // non-null, aligned: never dereferenced
     if (p.up_mode == HFFN_UP_ROWS && !p.x_t) return fail(HFFN_ERROR_ARGUMENT, "forward: null x_t workspace");
-    if (p.down_mode == HFFN_DOWN_ROWS && !p.y_t) return fail(HFFN_ERROR_ARGUMENT, "forward: null y_t workspace");
     const float* up_in = p.up_mode == HFFN_UP_ROWS ? p.x_t : some_x;
     if (int status = check_up(p.up_mode, p.value_type, up_in, p.up_offsets, p.up_idx, p.up_val, p.b_up, p.act, p.d_model, p.d_ff,
                               p.n, p.ld))
         return status;
-    return check_down(p.down_mode, p.value_type, p.act, p.out_offsets, p.out_hidden, p.out_val, p.b_down,
-                      p.down_mode == HFFN_DOWN_ROWS ? p.y_t : p.y, p.d_model, p.d_ff, p.n, p.ld);
+    return check_down(p.down_mode, p.value_type, p.act, p.out_offsets, p.out_hidden, p.out_val, p.b_down, p.y, p.d_model, p.d_ff,
+                      p.n, p.ld);
 }
 
 // hffn_forward after its checks. With z (the training forward) the pre-activations go to z and x_t is written for
@@ -178,12 +177,10 @@ int launch_forward(const Plan& p, const float* x, hipStream_t s, float* z = null
     if (int status = launch_up(p.up_mode, p.value_type, x, p.up_offsets, p.up_idx, p.up_val, p.b_up, p.act, p.d_model, p.d_ff,
                                p.nnz_up, p.n, act_ld, s, z))
         return status;
-    if (p.down_mode == HFFN_DOWN_ROWS) {
-        if (int status = launch_down(p.down_mode, p.value_type, p.act, p.out_offsets, p.out_hidden, p.out_val, p.b_down, p.y_t,
-                                     p.d_model, p.d_ff, p.nnz_down, p.n, p.ld, s))
-            return status;
-        return launched(hffn::launch_transpose(p.y_t, p.y, p.d_model, p.n, p.ld, p.d_model, s), "output transpose");
-    }
+    if (p.down_mode == HFFN_DOWN_ROWS)  // each output's lanes write y token-major: no output transpose
+        return launched(hffn::launch_down_rows(p.value_type, p.act, p.out_offsets, p.out_hidden, p.out_val, p.b_down, p.y, p.d_model,
+                                               p.n, p.ld, s, true),
+                        "down rows");
     return launch_down(p.down_mode, p.value_type, p.act, p.out_offsets, p.out_hidden, p.out_val, p.b_down, p.y, p.d_model, p.d_ff,
                        p.nnz_down, p.n, act_ld, s);
 }

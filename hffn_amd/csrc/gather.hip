@@ -173,8 +173,8 @@ __global__ __launch_bounds__(kBlock) void up_rows_kernel(const float* __restrict
 template <int TPL, typename V, bool PIPE = false>
 __global__ __launch_bounds__(kBlock) void down_rows_kernel(const float* __restrict__ act, const int32_t* __restrict__ off,
                                                           const int16_t* __restrict__ hid, const V* __restrict__ v,
-                                                          const float* __restrict__ bias, float* __restrict__ y_t,
-                                                          uint32_t d, uint32_t n, uint32_t ld) {
+                                                          const float* __restrict__ bias, float* __restrict__ y,
+                                                          uint32_t d, uint32_t n, uint32_t ld, uint32_t os, uint32_t ts) {
     static_assert(!PIPE || TPL == 1, "the pipelined walk takes one token per lane");
     const uint32_t o = blockIdx.x * kWaves + uniform(threadIdx.x / kWave);
     if (o >= d) return;
@@ -185,10 +185,10 @@ __global__ __launch_bounds__(kBlock) void down_rows_kernel(const float* __restri
     if constexpr (PIPE) acc[0] = walk_row_pipelined(act + (live ? t0 : 0), hid, v, off[o], off[o + 1], ld, threadIdx.x % kWave);
     else walk_row<TPL>(act + (live ? t0 : 0), hid, v, off[o], off[o + 1], ld, threadIdx.x % kWave, acc);
     if (!live) return;
-    float* out = y_t + static_cast<size_t>(o) * ld + t0;
+    float* out = y + static_cast<size_t>(o) * os + static_cast<size_t>(t0) * ts;  // y[o, t] at o os + t ts
 #pragma unroll
     for (int j = 0; j < TPL; ++j)
-        if (t0 + j < n) out[j] = acc[j] + bo;
+        if (t0 + j < n) out[static_cast<size_t>(j) * ts] = acc[j] + bo;
 }
 
 // ------------------------------------------------------------------------------------------ transpose
@@ -266,16 +266,16 @@ hipError_t up_rows_typed(const float* x_t, const int32_t* off, const int16_t* id
 
 template <typename V>
 hipError_t down_rows_typed(const float* act, const int32_t* off, const int16_t* hid, const V* v, const float* bias, float* y_t,
-                           uint32_t d, uint32_t n, uint32_t ld, hipStream_t stream) {
+                           uint32_t d, uint32_t n, uint32_t ld, uint32_t os, uint32_t ts, hipStream_t stream) {
     const dim3 block(kBlock);
     if (n >= 256) {
-        hipLaunchKernelGGL((down_rows_kernel<4, V>), dim3(ceil_div(d, kWaves), ceil_div(n, 4 * kWave)), block, 0, stream, act, off, hid, v, bias, y_t, d, n, ld);
+        hipLaunchKernelGGL((down_rows_kernel<4, V>), dim3(ceil_div(d, kWaves), ceil_div(n, 4 * kWave)), block, 0, stream, act, off, hid, v, bias, y_t, d, n, ld, os, ts);
     } else if (pipelined(d, n)) {
-        hipLaunchKernelGGL((down_rows_kernel<1, V, true>), dim3(ceil_div(d, kWaves), ceil_div(n, kWave)), block, 0, stream, act, off, hid, v, bias, y_t, d, n, ld);
+        hipLaunchKernelGGL((down_rows_kernel<1, V, true>), dim3(ceil_div(d, kWaves), ceil_div(n, kWave)), block, 0, stream, act, off, hid, v, bias, y_t, d, n, ld, os, ts);
     } else if (n >= 128) {
-        hipLaunchKernelGGL((down_rows_kernel<2, V>), dim3(ceil_div(d, kWaves), ceil_div(n, 2 * kWave)), block, 0, stream, act, off, hid, v, bias, y_t, d, n, ld);
+        hipLaunchKernelGGL((down_rows_kernel<2, V>), dim3(ceil_div(d, kWaves), ceil_div(n, 2 * kWave)), block, 0, stream, act, off, hid, v, bias, y_t, d, n, ld, os, ts);
     } else {
-        hipLaunchKernelGGL((down_rows_kernel<1, V>), dim3(ceil_div(d, kWaves), ceil_div(n, kWave)), block, 0, stream, act, off, hid, v, bias, y_t, d, n, ld);
+        hipLaunchKernelGGL((down_rows_kernel<1, V>), dim3(ceil_div(d, kWaves), ceil_div(n, kWave)), block, 0, stream, act, off, hid, v, bias, y_t, d, n, ld, os, ts);
     }
     return hipGetLastError();
 }
@@ -303,9 +303,10 @@ hipError_t launch_grad_hidden_rows(const float* gy_t, const int32_t* off, const 
 }
 
 hipError_t launch_down_rows(int vt, const float* act, const int32_t* off, const int16_t* hid, const void* v,
-                            const float* bias, float* y_t, uint32_t d, uint32_t n, uint32_t ld, hipStream_t stream) {
-    if (vt == kBF16) return down_rows_typed(act, off, hid, static_cast<const uint16_t*>(v), bias, y_t, d, n, ld, stream);
-    return down_rows_typed(act, off, hid, static_cast<const float*>(v), bias, y_t, d, n, ld, stream);
+                            const float* bias, float* y, uint32_t d, uint32_t n, uint32_t ld, hipStream_t stream, bool token_major) {
+    const uint32_t os = token_major ? 1 : ld, ts = token_major ? d : 1;  // y [n, d] or [d, ld]
+    if (vt == kBF16) return down_rows_typed(act, off, hid, static_cast<const uint16_t*>(v), bias, y, d, n, ld, os, ts, stream);
+    return down_rows_typed(act, off, hid, static_cast<const float*>(v), bias, y, d, n, ld, os, ts, stream);
 }
 
 }  // namespace hffn

@@ -48,9 +48,10 @@ hipError_t launch_grad_hidden_rows(const float* gy_t, const int32_t* off, const 
 hipError_t launch_down_edges(int vt, const float* act, const int32_t* off, const int16_t* hid, const void* v,
                              const float* bias, float* y, uint32_t d, uint32_t h, uint32_t n, uint32_t ld, uint32_t nnz,
                              hipStream_t stream);
+// down rows: y feature-major [d, ld], or token-major [n, d] (token_major: the forward's output, no transpose after).
 hipError_t launch_down_rows(int vt, const float* act, const int32_t* off, const int16_t* hid, const void* v,
-                            const float* bias, float* y_t, uint32_t d, uint32_t n, uint32_t ld,
-                            hipStream_t stream);
+                            const float* bias, float* y, uint32_t d, uint32_t n, uint32_t ld,
+                            hipStream_t stream, bool token_major = false);
 
 // Training (train.hip). Token tiles of kGradTile tokens; with more than one tile the SDDMM kernels write tile
 // partials (row k of a [tiles, stride] workspace) that launch_reduce_tiles adds in tile order.

@@ -81,7 +81,8 @@ int hffn_down(int mode, int value_type, const float* act, const int32_t* out_off
               uint32_t n, uint32_t ld, void* stream);
 
 /* The whole layer for x[n, d_model] -> y[n, d_model]: the transposes the modes need, up, down.
- * x_t and y_t may be NULL when the modes do not use them. act is a workspace here: for one or two tokens on the
+ * x_t may be NULL when the up mode is not ROWS; y_t is not written (the ROWS down kernel writes y token-major itself)
+ * and may be NULL. act is a workspace here: for one or two tokens on the
  * EDGES/EDGES pair it holds the activations packed [d_ff, n] (its first n d_ff floats). Replaces HFFNRuntime._launch
  * (runtime/gpu/nvidia/common/kernels/hffn_cuda/runtime.py:134-163). */
 int hffn_forward(int up_mode, int down_mode, int value_type, const float* x, const int32_t* up_offsets,
