@@ -245,6 +245,8 @@ uint32_t ceil_div(uint32_t a, uint32_t b) { return (a + b - 1) / b; }
 // waves per SIMD on 256 CUs, 150 VGPRs): there each wave's chain of round trips bounds the kernel (the 70M layer's 512
 // outputs at 128 tokens: its down kernel 1024 waves, the call 44.1 -> 38.9 us); with more waves the plain walk's
 // occupancy (8 per SIMD) hides the latency better (the 1.4B layer at 128 tokens: 222 us plain, 267 us pipelined).
+// Two tokens per lane pipelined in 32-slot chunks, where only that grid fits one round, measured slower (the 410M
+// outputs at 200 tokens 259 -> 281 us, the 1.4B outputs at 128 tokens 221 -> 242 us) or no faster (the 70M neurons at 128).
 constexpr uint64_t kPipelinedWaves = 3 * 4 * 256;
 bool pipelined(uint32_t rows, uint32_t n) { return static_cast<uint64_t>(rows) * ceil_div(n, kWave) <= kPipelinedWaves; }
 
