@@ -853,16 +853,15 @@ __global__ __launch_bounds__(64 * kDmaWaves) void gemm_dma_kernel(
             }
         }
     };
-    // The down GEMM's waves take a higher issue priority (s_setprio) for their MFMA runs, so that of the two waves of a
-    // SIMD the one with products ready issues ahead of the other's LDS reads and transfers (same box, alternating
-    // builds: the 2.8B layer's down GEMM 466-468 -> 450-451 us, the 410M layer's 57.9 -> 57.3 us; the up GEMMs measured
-    // no gain, 2.8B 421 -> 430 us, and keep their schedule).
-    const auto raise_priority = [] { if constexpr (EPI == Epi::Down) __builtin_amdgcn_s_setprio(1); };
+    // A wave raises its issue priority (s_setprio) for the MFMA run that carries the stage's transfers, so that of the two
+    // waves of a SIMD the one with products ready issues ahead of the other's LDS reads (same box, alternating builds:
+    // the 2.8B layer's up GEMM 415-427 -> 401-402 us and down GEMM 466-468 -> 444-458 us, the 410M layer's up GEMM
+    // ~56 -> 54.5 us; the raised priority around the other MFMA run gave nothing on the down GEMM and lost ~2 % on the
+    // up GEMM).
+    const auto raise_priority = [] { __builtin_amdgcn_s_setprio(1); };
     const auto lower_priority = [] {
-        if constexpr (EPI == Epi::Down) {
-            __builtin_amdgcn_sched_barrier(0);  // the MFMA run ends here
-            __builtin_amdgcn_s_setprio(0);
-        }
+        __builtin_amdgcn_sched_barrier(0);  // the MFMA run ends here
+        __builtin_amdgcn_s_setprio(0);
     };
     Frags f0, f1;
     load(f0, 0, 0);
@@ -875,9 +874,7 @@ __global__ __launch_bounds__(64 * kDmaWaves) void gemm_dma_kernel(
         wait_loads<63>();  // this step's reads, issued a step ago, are in: the next reads do not hold its MFMAs
         load(f1, slot, 1);
         __builtin_amdgcn_sched_barrier(0);
-        raise_priority();
         multiply(f0);
-        lower_priority();
         if (kt + 2 < k_end) wait_loads<kLoads>();  // stage kt + 1 has landed, kt + 2 may be in flight
         else wait_loads<0>();
         wait_loads<63>();  // the same LDS wait on every path, where the compiler's wait tracking sees it
