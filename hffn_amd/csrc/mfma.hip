@@ -638,6 +638,7 @@ constexpr int kDmaStages = 3;
 constexpr int kDmaBM = 256, kDmaBN = 128;
 constexpr int kDmaWaves = 8;  // waves per block: two per SIMD, 64 x 64 outputs each
 constexpr uint32_t kDmaMaxActBlocks = 40;  // activation blocks of one down split held in LDS (int8 binades)
+constexpr uint32_t kDmaLoRuns = 32;        // activation blocks more per ring slot with bfloat16 weights (its B lo plane)
 
 // Workgroup barrier without the memory fence of __syncthreads (whose release would also wait for every LDS DMA in
 // flight); LDS visibility is ensured by the wait_loads before it.
@@ -661,7 +662,9 @@ __global__ __launch_bounds__(64 * kDmaWaves) void gemm_dma_kernel(
     float* __restrict__ out,                // Down: y [M, Ncol] (splits == 1) or partials [splits, M, Ncol]; UpSplit: partials
     _Float16* __restrict__ out_planes,      // Up: activation planes [Ncol / 32][8][rows_pad][8]
     int32_t* __restrict__ out_exp,          // Up: [Ncol / BN, rows_pad] activation block binades (act_exp_at)
-    uint32_t M, uint32_t rows_pad, uint32_t Ncol, uint32_t K, uint32_t splits) {
+    uint32_t M, uint32_t rows_pad, uint32_t Ncol, uint32_t K, uint32_t splits,
+    uint32_t whole_n,                       // Down: column tiles below whole_n take all of K and write y into `out`
+    float* __restrict__ part) {             // Down, whole_n > 0: the other column tiles' partials [splits, M, Ncol - whole_n BN]
     // 8 waves in 4 x 2, 64 x 64 outputs each (two waves per SIMD)
     constexpr int W = kDmaWaves, MI = 2, NI = 2, BM = kDmaBM, BN = kDmaBN, S = kDmaStages;
     constexpr uint32_t kT = 64 * W, kWaveRows = 32 * MI, kHalf = W / 2;
@@ -669,29 +672,47 @@ __global__ __launch_bounds__(64 * kDmaWaves) void gemm_dma_kernel(
     static_assert(kHalf * kWave == BM, "the upper half of the waves holds a thread per block row");
     static_assert(LIVE == BM || LIVE == 128 || LIVE == 64, "live rows: the whole tile, its first half or first quarter");
     constexpr uint32_t kStage = kRuns * (BM + BN) * 8;  // halves per stage
+    // Down: the activation binades of up to kDmaMaxActBlocks blocks sit in e_tab; with bfloat16 weights the B lo plane of
+    // every ring slot (8 KB, never transferred) holds 32 blocks more, so that a tile can take all of a wide K
+    constexpr uint32_t kLoRegion = kRuns * BM * 8 + kRuns / 2 * BN * 8, kLoRuns = kRuns / 2 * BN * 8 * 2 / BM;
+    constexpr uint32_t kMaxActBlocks = LO_B ? kDmaMaxActBlocks : kDmaMaxActBlocks + S * kLoRuns;
+    static_assert(kLoRuns == kDmaLoRuns, "the host's plan counts the ring's spare runs alike");
     constexpr int kRowRuns = LIVE / 64;                  // 64-row runs of A transferred per (part, chunk)
     // runs of B transferred per k-tile: both planes, or the hi plane alone when the lo plane is not read (LO_B false)
     constexpr int kRunsB = LO_B ? kRuns : kRuns / 2;
     constexpr int kLoadsA = kRowRuns * kRuns / W, kLoadsB = BN * kRunsB / kWave / W;  // DMA instructions per wave
     static_assert(kLoadsA * W == kRowRuns * kRuns && kLoadsB * W == BN * kRunsB / kWave, "the transfers divide over the waves");
     constexpr int kLoads = kLoadsA + kLoadsB;
-    static_assert(kLoads * S + (kDmaMaxActBlocks + W - 1) / W < 64, "the prologue's transfers of a wave fit vmcnt");
+    static_assert(kLoads * S + (kMaxActBlocks + W - 1) / W < 64, "the prologue's transfers of a wave fit vmcnt");
     // multiplied 32-row tiles of a live wave (its rows start at wm * kWaveRows; LIVE is a multiple of kWaveRows)
     constexpr int MIL = LIVE >= static_cast<int>(kWaveRows) ? MI : LIVE / 32;
 
     __shared__ __attribute__((aligned(16))) _Float16 smem[S * kStage];
     __shared__ __attribute__((aligned(16))) int32_t e_row[1][BM];  // Up: x binades
     __shared__ __attribute__((aligned(16))) int8_t e_tab[EPI == Epi::Down ? kDmaMaxActBlocks : 1][EPI == Epi::Down ? BM : 1];  // Down: [block][row]
+    // Down: the BM binades of the k range's activation block c (c < kMaxActBlocks): a row of e_tab, or a 256-byte run in
+    // the unused B lo plane of ring slot (c - kDmaMaxActBlocks) / kLoRuns
+    const auto etab = [&](uint32_t c) -> int8_t* {
+        if (LO_B || c < kDmaMaxActBlocks) return &e_tab[c][0];
+        const uint32_t o = c - kDmaMaxActBlocks;
+        return reinterpret_cast<int8_t*>(smem + (o / kLoRuns) * kStage + kLoRegion) + (o % kLoRuns) * BM;
+    };
 
     const uint32_t tid = threadIdx.x, lane = tid % kWave, wave = uniform(tid / kWave);
     const uint32_t wm = wave / 2, wn = wave % 2;
     // wave-uniform: this wave's rows hold tokens (a constant for a full tile)
     const bool live = LIVE == BM || wm * kWaveRows < static_cast<uint32_t>(LIVE);
     const uint32_t tiles_m = rows_pad / BM, tiles_n = Ncol / BN;
-    const Tile tile = tile_of(blockIdx.x, tiles_m, tiles_n, splits);
+    // the first tiles_m * whole_n blocks: column tiles 0 .. whole_n - 1 over all of K (one round of long blocks first);
+    // the others: the remaining column tiles, K split `splits` ways (whole_n 0: every tile split alike)
+    const uint32_t whole_blocks = tiles_m * whole_n;
+    const bool whole = blockIdx.x < whole_blocks;
+    Tile tile = whole ? tile_of(blockIdx.x, tiles_m, whole_n, 1) : tile_of(blockIdx.x - whole_blocks, tiles_m, tiles_n - whole_n, splits);
+    if (!whole) tile.n += whole_n;
+    const uint32_t nsplit = whole ? 1 : splits;
     const uint32_t m0 = tile.m * BM, n0 = tile.n * BN;
     const uint32_t ktiles = K / kBK;
-    const uint32_t k_begin = tile.split * ktiles / splits, k_end = (tile.split + 1) * ktiles / splits;
+    const uint32_t k_begin = tile.split * ktiles / nsplit, k_end = (tile.split + 1) * ktiles / nsplit;
     const uint32_t kb0 = k_begin / kKtPerActBlock;
 
     // piece q of wave w's share of a stage: a run of 64 rows (1 KB) of A (pieces below kLoadsA), then of B; its
@@ -737,7 +758,7 @@ __global__ __launch_bounds__(64 * kDmaWaves) void gemm_dma_kernel(
         const uint32_t blocks = (k_end - k_begin) / kKtPerActBlock;  // at least one: K is split on activation blocks
         const int8_t* tab = act_exps(a_exp);
         for (uint32_t c = wave; c < blocks; c += W)
-            dma4(tab + act_exp_at(rows_pad, m0, kb0 + c), lane * 4, &e_tab[c][0]);
+            dma4(tab + act_exp_at(rows_pad, m0, kb0 + c), lane * 4, etab(c));
     } else {
         if (wave == 0) dma16(a_exp + m0, lane * 16, &e_row[0][0]);
     }
@@ -834,14 +855,14 @@ __global__ __launch_bounds__(64 * kDmaWaves) void gemm_dma_kernel(
             const uint32_t kb = kt / kKtPerActBlock - kb0;
             if (kt % kKtPerActBlock != 0 || kt == k_begin || !live) return;
             const uint32_t own = wm * kWaveRows + lane;
-            if (__builtin_amdgcn_ballot_w64(e_tab[kb - 1][own] != e_tab[kb][own]) != 0) {
+            if (__builtin_amdgcn_ballot_w64(etab(kb - 1)[own] != etab(kb)[own]) != 0) {
 #pragma unroll
                 for (int i = 0; i < MIL; ++i)
 #pragma unroll
                     for (int g = 0; g < 4; ++g) {
                         const uint32_t m = wave_row<kWaveRows>(wm, i, 4 * g, lane);
-                        const uint32_t before = *reinterpret_cast<const uint32_t*>(&e_tab[kb - 1][m]);
-                        const uint32_t now = *reinterpret_cast<const uint32_t*>(&e_tab[kb][m]);
+                        const uint32_t before = *reinterpret_cast<const uint32_t*>(etab(kb - 1) + m);
+                        const uint32_t now = *reinterpret_cast<const uint32_t*>(etab(kb) + m);
 #pragma unroll
                         for (int b = 0; b < 4; ++b) {
                             const int d = static_cast<int8_t>(before >> (8 * b)) - static_cast<int8_t>(now >> (8 * b));
@@ -953,6 +974,13 @@ __global__ __launch_bounds__(64 * kDmaWaves) void gemm_dma_kernel(
         static_assert(BM * kLd * sizeof(float) <= sizeof(smem), "the epilogue tile fits the staging LDS");
         float* tile_v = reinterpret_cast<float*>(smem);
         const uint32_t kb_last = (k_end - 1) / kKtPerActBlock - kb0;
+        // the last activation block's binades held in a ring slot (a wide k range), which the tile below overwrites,
+        // are first copied to e_row (block-uniform condition)
+        const bool last_in_ring = EPI == Epi::Down && kb_last >= kDmaMaxActBlocks;
+        if (last_in_ring) {
+            if (tid < BM) e_row[0][tid] = etab(kb_last)[tid];
+            __syncthreads();
+        }
 #pragma unroll
         for (int j = 0; j < NI; ++j) {
             const uint32_t c = wn * (BN / 2) + j * 32 + lane % 32;
@@ -962,13 +990,16 @@ __global__ __launch_bounds__(64 * kDmaWaves) void gemm_dma_kernel(
 #pragma unroll
                 for (int r = 0; r < 16; ++r) {
                     const uint32_t m = wave_row<kWaveRows>(wm, i, r, lane);
-                    const int ea = EPI == Epi::Down ? static_cast<int>(e_tab[kb_last][m]) : e_row[0][m];
+                    const int ea = EPI == Epi::Down && !last_in_ring ? static_cast<int>(e_tab[kb_last][m]) : e_row[0][m];
                     tile_v[m * kLd + c] = ldexpf(acc[i][j][r], ea + ce);
                 }
         }
         __syncthreads();
-        float* target = out + (splits > 1 ? static_cast<size_t>(tile.split) * M * Ncol : 0);
-        const bool add_bias = EPI == Epi::Down && splits == 1 && bias != nullptr;  // no bias: the training gx product
+        // y (whole k range) or this split's partial: [splits, M, Ncol], or with whole_n > 0 [splits, M, Ncol - whole_n BN]
+        // over the split column tiles only
+        const uint32_t ld = nsplit > 1 && whole_n > 0 ? Ncol - whole_n * BN : Ncol, c0 = n0 - (ld == Ncol ? 0 : whole_n * BN);
+        float* target = nsplit == 1 ? out : (whole_n > 0 ? part : out) + static_cast<size_t>(tile.split) * M * ld;
+        const bool add_bias = EPI == Epi::Down && nsplit == 1 && bias != nullptr;  // no bias: the training gx product
         for (uint32_t q = tid; q < BM * (BN / 4); q += kT) {
             const uint32_t m = q / (BN / 4), c = (q % (BN / 4)) * 4;
             if (m0 + m >= M) break;  // rows ascend with q
@@ -977,17 +1008,20 @@ __global__ __launch_bounds__(64 * kDmaWaves) void gemm_dma_kernel(
                 const float4 b = *reinterpret_cast<const float4*>(bias + n0 + c);
                 v.x += b.x; v.y += b.y; v.z += b.z; v.w += b.w;
             }
-            *reinterpret_cast<float4*>(target + static_cast<size_t>(m0 + m) * Ncol + n0 + c) = v;
+            *reinterpret_cast<float4*>(target + static_cast<size_t>(m0 + m) * ld + c0 + c) = v;
         }
     }
 }
 
-// y[m, :] = sum over splits (in split order) of partials[s, m, :] + bias; 4 columns per thread.
+// y[m, c0 + c] = sum over splits (in split order) of partials[s, m, c] + bias[c0 + c] for the partials' width columns
+// (y rows of Ncol); 4 columns per thread.
 __global__ __launch_bounds__(kThreads) void reduce_splits_kernel(const float* __restrict__ partials, const float* __restrict__ bias,
-                                                                float* __restrict__ y, uint32_t M, uint32_t Ncol, uint32_t splits) {
-    const size_t quads = static_cast<size_t>(M) * Ncol / 4;
+                                                                float* __restrict__ y, uint32_t M, uint32_t Ncol, uint32_t splits,
+                                                                uint32_t width, uint32_t c0) {
+    const size_t quads = static_cast<size_t>(M) * width / 4;
     const size_t i = static_cast<size_t>(blockIdx.x) * kThreads + threadIdx.x;
     if (i >= quads) return;
+    const size_t m = i / (width / 4), c = c0 + (i % (width / 4)) * 4;
     const float4* p = reinterpret_cast<const float4*>(partials);
     float4 t = p[i];
     for (uint32_t s0 = 1; s0 < splits; s0 += 8) {  // 8 loads in flight, added in split order
@@ -1002,10 +1036,10 @@ __global__ __launch_bounds__(kThreads) void reduce_splits_kernel(const float* __
             }
     }
     if (bias != nullptr) {  // none for the training gx product
-        const float4 b = *reinterpret_cast<const float4*>(bias + (i * 4) % Ncol);
+        const float4 b = *reinterpret_cast<const float4*>(bias + c);
         t.x += b.x; t.y += b.y; t.z += b.z; t.w += b.w;
     }
-    reinterpret_cast<float4*>(y)[i] = t;
+    *reinterpret_cast<float4*>(y + m * Ncol + c) = t;
 }
 
 // Activation planes from the up GEMM's k-split partial sums (Epi::UpSplit): v = gelu(sum over the splits, in split
@@ -1263,6 +1297,40 @@ uint32_t dma_down_splits(uint32_t m, uint32_t ncol, uint32_t k) {
     return best;
 }
 
+// The streamed down GEMM's plan: `splits` k splits of every column tile (whole_n 0), or, where that is estimated faster,
+// the first whole_n column tiles over all of K (one round of long blocks, writing y) and the others in `splits` k
+// splits, whose partials cover only their columns. A wide K takes the whole-K tiles only where a tile holds all of its
+// activation blocks' binades in LDS (bfloat16 weights leave the ring's B lo plane free for them). Priced as
+// dma_down_splits: the split blocks that the CUs without a whole tile finish meanwhile, then whole rounds of the rest.
+// MI355X, 2.8B shape at 4096 tokens (16 x 20 tiles, 320 k-tiles): 16 whole column tiles and 4 column tiles in 4 splits
+// (256 + 256 blocks) against 4 splits of all 20 (1280 blocks), a fifth of the partials.
+struct DownPlan {
+    uint32_t splits, whole_n;
+};
+DownPlan dma_down_plan(uint32_t m, uint32_t ncol, uint32_t k, bool bf16) {
+    const uint32_t uniform = dma_down_splits(m, ncol, k);
+    DownPlan plan{uniform, 0};
+    const uint32_t tiles_m = rows_padded(m) / kDmaBM, tiles_n = ncol / kDmaBN, ktiles = k / kBK;
+    const uint32_t max_blocks = bf16 ? kDmaMaxActBlocks + kDmaStages * kDmaLoRuns : kDmaMaxActBlocks;
+    if (uniform == 0 || k % kActBlock != 0 || k / kActBlock > max_blocks) return plan;
+    const double partial_us = 8.0 * rows_padded(m) / kPartialBytesPerUs;  // per split and column
+    double best_us = ceil_div(tiles_m * tiles_n * uniform, kCus) * (static_cast<double>(ktiles) / uniform * kDmaKtileUs + kDmaBlockUs) +
+                     (uniform > 1 ? partial_us * uniform * ncol + kReduceUs : 0.0);
+    const double whole_us = ktiles * kDmaKtileUs + kDmaBlockUs;
+    for (uint32_t whole_n = 1; whole_n < tiles_n && tiles_m * whole_n <= kCus; ++whole_n)
+        for (uint32_t splits = 2; splits <= kDmaMaxSplits; splits *= 2) {
+            if (k % (kActBlock * splits) != 0 || k / kActBlock / splits > kDmaMaxActBlocks) continue;
+            const double split_us = static_cast<double>(ktiles) / splits * kDmaKtileUs + kDmaBlockUs;
+            const uint32_t free_cus = kCus - tiles_m * whole_n, pieces = tiles_m * (tiles_n - whole_n) * splits;
+            const uint32_t meanwhile = free_cus * static_cast<uint32_t>(whole_us / split_us);
+            const double span = pieces <= meanwhile ? max(whole_us, ceil_div(pieces, free_cus) * split_us)
+                                                    : whole_us + ceil_div(pieces - meanwhile, kCus) * split_us;
+            const double us = span + partial_us * splits * (tiles_n - whole_n) * kDmaBN + kReduceUs;
+            if (us < best_us) plan = {splits, whole_n}, best_us = us;
+        }
+    return plan;
+}
+
 // Splits of the streamed up GEMM: 1 when its tiles alone fill the chip, else doubled (up to 8, each split at least
 // one k-tile) until ~192 blocks; the partial sums then go through act_planes_kernel. 0: not streamed.
 constexpr uint32_t kDmaMaxUpSplits = 8;
@@ -1328,32 +1396,37 @@ __global__ __launch_bounds__(kThreads) void gather_dense_kernel(const float* __r
 template <Epi EPI, bool LO_B>
 hipError_t launch_dma(const _Float16* a_planes, const int32_t* a_exp, const _Float16* b_planes, const int32_t* b_exp,
                       const float* bias, float* out, _Float16* out_planes, int32_t* out_exp, uint32_t M, uint32_t Ncol, uint32_t K,
-                      uint32_t splits, hipStream_t stream) {
-    const dim3 grid(dma_tiles(M, Ncol) * splits), block(64 * kDmaWaves);
+                      uint32_t splits, hipStream_t stream, uint32_t whole_n = 0, float* part = nullptr) {
+    const uint32_t tiles_m = rows_padded(M) / kDmaBM, tiles_n = Ncol / kDmaBN;
+    const dim3 grid(tiles_m * whole_n + tiles_m * (tiles_n - whole_n) * splits), block(64 * kDmaWaves);
     const uint32_t rows_pad = rows_padded(M), live = rows_live(M);
     if (live == 64)
         hipLaunchKernelGGL((gemm_dma_kernel<EPI, LO_B, 64>), grid, block, 0, stream, a_planes, a_exp, b_planes, b_exp, bias, out,
-                           out_planes, out_exp, M, rows_pad, Ncol, K, splits);
+                           out_planes, out_exp, M, rows_pad, Ncol, K, splits, whole_n, part);
     else if (live == 128)
         hipLaunchKernelGGL((gemm_dma_kernel<EPI, LO_B, 128>), grid, block, 0, stream, a_planes, a_exp, b_planes, b_exp, bias, out,
-                           out_planes, out_exp, M, rows_pad, Ncol, K, splits);
+                           out_planes, out_exp, M, rows_pad, Ncol, K, splits, whole_n, part);
     else
         hipLaunchKernelGGL((gemm_dma_kernel<EPI, LO_B, kDmaBM>), grid, block, 0, stream, a_planes, a_exp, b_planes, b_exp, bias, out,
-                           out_planes, out_exp, M, rows_pad, Ncol, K, splits);
+                           out_planes, out_exp, M, rows_pad, Ncol, K, splits, whole_n, part);
     return hipGetLastError();
 }
 
 template <bool LO_B>
-hipError_t dma_down(uint32_t splits, const _Float16* a_planes, const int32_t* a_exp, const _Float16* b_planes, const int32_t* b_exp,
+hipError_t dma_down(DownPlan plan, const _Float16* a_planes, const int32_t* a_exp, const _Float16* b_planes, const int32_t* b_exp,
                     const float* bias, float* y, float* partials, uint32_t M, uint32_t Ncol, uint32_t K, hipStream_t stream) {
-    if (splits == 1)
+    if (plan.splits == 1)
         return launch_dma<Epi::Down, LO_B>(a_planes, a_exp, b_planes, b_exp, bias, y, nullptr, nullptr, M, Ncol, K, 1, stream);
     const hipError_t status =
-        launch_dma<Epi::Down, LO_B>(a_planes, a_exp, b_planes, b_exp, bias, partials, nullptr, nullptr, M, Ncol, K, splits, stream);
+        plan.whole_n > 0 ? launch_dma<Epi::Down, LO_B>(a_planes, a_exp, b_planes, b_exp, bias, y, nullptr, nullptr, M, Ncol, K,
+                                                       plan.splits, stream, plan.whole_n, partials)
+                         : launch_dma<Epi::Down, LO_B>(a_planes, a_exp, b_planes, b_exp, bias, partials, nullptr, nullptr, M, Ncol, K,
+                                                       plan.splits, stream);
     if (status != hipSuccess) return status;
-    const size_t quads = static_cast<size_t>(M) * Ncol / 4;
+    const uint32_t c0 = plan.whole_n * kDmaBN, width = Ncol - c0;
+    const size_t quads = static_cast<size_t>(M) * width / 4;
     hipLaunchKernelGGL(reduce_splits_kernel, dim3(static_cast<uint32_t>((quads + kThreads - 1) / kThreads)), dim3(kThreads), 0, stream,
-                       partials, bias, y, M, Ncol, splits);
+                       partials, bias, y, M, Ncol, plan.splits, width, c0);
     return hipGetLastError();
 }
 
@@ -1374,6 +1447,10 @@ size_t partial_floats(uint32_t m, uint32_t d, uint32_t h) {
     for (uint32_t rows = kRowPad; rows <= rows_padded(m); rows += kRowPad) {
         const size_t tokens = min(m, rows);
         most = max(most, static_cast<size_t>(dma_down_splits(rows, d, h)) * tokens * d);
+        for (const bool bf16 : {false, true}) {
+            const DownPlan plan = dma_down_plan(rows, d, h, bf16);
+            most = max(most, static_cast<size_t>(plan.splits) * tokens * (d - plan.whole_n * kDmaBN));
+        }
         const uint32_t up = dma_up_splits(rows, h, d);
         if (up > 1) most = max(most, static_cast<size_t>(up) * tokens * h);
     }
@@ -1536,10 +1613,10 @@ hipError_t launch_mfma_down(int vt, const void* planes, const int32_t* v_exp, co
     const auto* act_planes = reinterpret_cast<const _Float16*>(bytes + w.act_planes);
     float* partials = reinterpret_cast<float*>(bytes + w.partials);
     const auto* p = static_cast<const _Float16*>(planes);
-    if (const uint32_t splits = dma_down_splits(n, d, h)) {
+    if (const DownPlan plan = dma_down_plan(n, d, h, vt == kBF16); plan.splits != 0) {
         if (vt == kBF16)
-            return dma_down<false>(splits, act_planes, words + w.act_binades, p, v_exp, b_down, y, partials, n, d, h, stream);
-        return dma_down<true>(splits, act_planes, words + w.act_binades, p, v_exp, b_down, y, partials, n, d, h, stream);
+            return dma_down<false>(plan, act_planes, words + w.act_binades, p, v_exp, b_down, y, partials, n, d, h, stream);
+        return dma_down<true>(plan, act_planes, words + w.act_binades, p, v_exp, b_down, y, partials, n, d, h, stream);
     }
     const Shape shape = down_shape(n, d, h);
     if (vt == kBF16)
