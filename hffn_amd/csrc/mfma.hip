@@ -23,7 +23,7 @@
 //
 // Two GEMM kernels: the streamed one (gemm_dma_kernel: 256 x 128 tiles whose k-tiles go from global memory straight
 // into LDS, K split 2-32 ways by an estimate of the rounds of blocks and the partials' cost, partials added by
-// separate passes) takes every
+// separate passes; a down GEMM may take its first column tiles over all of K and split only the others) takes every
 // shape whose tiles and splits give enough blocks; the register-staged one below (gemm_planes_kernel) remains for
 // narrower layers at small N.
 //
